@@ -1,0 +1,83 @@
+/*
+ * mxs_nf4 — C ABI of the MI355X (gfx950) NF4 quantized-linear hot path.
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t, allocates nothing,
+ * launches asynchronously on `stream`, and returns MXS_OK (0), a negative MXS_ERR_* code for a
+ * rejected argument (nothing launched), or a positive hipError_t from the launch.
+ *
+ * Data layout (bitsandbytes' NF4 QuantState as the reference reads it,
+ * solution/linear4bit.py:36-40):
+ *   packed   u8  [(N*K)/2]       byte i = value 2i (high nibble) and 2i+1 (low nibble),
+ *                                 values flattened row-major over W [N, K]
+ *   absmax8  u8  [N*K/64]        8-bit code of each 64-value block's absmax
+ *   code     f32 [256]           second-level code book (state2.code)
+ *   absmax2  f32 [ceil(N*K/64/256)]  second-level scale per 256 blocks (state2.absmax)
+ *   offset   f32 [1]             mean added back (state.offset), a device pointer
+ *   block scale = fma(code[absmax8[b]], absmax2[b >> 8], offset); value = fp16(NF4[q] * scale)
+ */
+#ifndef MXS_NF4_H
+#define MXS_NF4_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXS_OK 0
+#define MXS_ERR_ARG (-1)    /* null pointer or negative size */
+#define MXS_ERR_DTYPE (-2)  /* unsupported output dtype */
+#define MXS_ERR_ALIGN (-3)  /* pointer alignment the entry point requires */
+#define MXS_ERR_SIZE (-4)   /* shape outside what the kernels take */
+
+#define MXS_DTYPE_F16 0
+#define MXS_DTYPE_F32 1
+
+/* Dense W from packed NF4.  Replaces unpack_nf4 (solution/nf4.py:138-155) with its
+ * wide/one-byte dispatch (solution/nf4.py:145-154): the wide kernel when n_bytes % 32 == 0 and
+ * packed/out are 16-byte aligned, else the one-byte kernel.  absmax8 != NULL selects the nested
+ * (double-quantized) form with code/absmax2/offset; absmax8 == NULL takes fp32 absmax_f32
+ * [n_bytes/32] (the reference's non-nested branch, solution/nf4.py:74-75).
+ * out: fp16 or fp32 [2*n_bytes] (out_dtype MXS_DTYPE_F16 / MXS_DTYPE_F32). */
+int mxs_nf4_dequant(const void* packed, int64_t n_bytes, const void* absmax8, const float* code,
+                    const float* absmax2, const float* offset, const float* absmax_f32,
+                    void* out, int out_dtype, hipStream_t stream);
+
+/* The one-byte-per-lane kernel, launched directly: nf4_unpack_kernel (solution/nf4.py:31-51) as
+ * solution/test_nf4.py:68-82 launches it.  Same arguments and result as mxs_nf4_dequant. */
+int mxs_nf4_dequant_bytewise(const void* packed, int64_t n_bytes, const void* absmax8,
+                             const float* code, const float* absmax2, const float* offset,
+                             const float* absmax_f32, void* out, int out_dtype,
+                             hipStream_t stream);
+
+/* Several NF4 weights stored back to back, decoded by one launch to fp16 stored back to back.
+ * Replaces launch_layer / nf4_layer_kernel (solution/nf4.py:158-162, 89-110).
+ * Module m owns blocks [block0[m], block0[m+1]) of packed/absmax8/out, code
+ * [m*256, m*256+256), absmax2 from index scale0[m], and offset[m].
+ * block0: device int64 [n_modules + 1] ascending, block0[0] = 0, block0[n_modules] = n_blocks;
+ * scale0: device int64 [n_modules].  packed and out must be 16-byte aligned. */
+int mxs_nf4_dequant_layer(const void* packed, int64_t n_blocks, const void* absmax8,
+                          const float* code, const float* absmax2, const float* offset,
+                          const int64_t* block0, const int64_t* scale0, int n_modules,
+                          void* out, hipStream_t stream);
+
+/* Workspace bytes mxs_nf4_quantize needs for n_values (device memory, 8-byte aligned). */
+int mxs_nf4_quantize_workspace_bytes(int64_t n_values);
+
+/* NF4 quantizer with double-quantized absmax (upstream of the path: it makes the packed
+ * weights).  Stands in for bitsandbytes' quantize_4bit(w, blocksize=64, quant_type="nf4",
+ * compress_statistics=True) as the reference calls it (solution/test_nf4.py:33,
+ * tools/bench_nf4.py:30-35).  w_f16 [n_values] (16-byte aligned, n_values % 64 == 0) ->
+ * packed u8 [n/2], absmax_f32 [n/64] (first level, kept for checks), absmax8 u8 [n/64],
+ * absmax2 f32 [ceil(n/64/256)], offset f32 [1]; code f32 [256] is the second-level code book
+ * (ascending).  Deterministic. */
+int mxs_nf4_quantize(const void* w_f16, int64_t n_values, const float* code, void* packed,
+                     float* absmax_f32, void* absmax8, float* absmax2, float* offset,
+                     void* workspace, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MXS_NF4_H */

@@ -1,0 +1,54 @@
+"""mindxsoup_amd — MI355X-native (gfx950) NF4 quantized-linear hot path.
+
+Drop-in for the reference's `solution` package on the NF4 path: `apply()` installs the patches
+and `FEATURES` holds the switches under the reference's names (solution/__init__.py:32-83,
+113-171).  Only the NF4 switches act here; the reference's other switches are kept as keys so a
+configuration written for it still loads, and are inert (their subsystems are not part of this
+build).
+
+    import mindxsoup_amd as solution
+    solution.apply()
+"""
+
+from . import direct
+
+FEATURES = {
+    # --- NF4 path (acted on) -------------------------------------------------------------
+    "nf4": True,             # HIP NF4 unpack with fused double-dequant of absmax
+    "nf4_direct": True,      # Linear4bit: HIP path directly, no bitsandbytes dispatch layers
+    "nf4_cache_fp16": False,  # each NF4 weight unpacked once and kept in fp16
+    "layer_unpack": False,   # all weights of a layer unpacked by one launch
+    "direct_nograd": True,   # no Function.apply wrappers when no graph is recorded (direct.py)
+    "nf4_fused_gemm": True,  # dequant fused into the GEMM main loop (else HIP unpack + F.linear)
+    "nf4_fused_lora": True,  # LoRA branch fused into the GEMM epilogues (LoraLinear4bit)
+    # --- reference switches outside the NF4 path (inert here) ------------------------------
+    "startup_cache": False, "example_swiglu": False, "mlp_fp16": False, "adam_host": False,
+    "cublas_workspace": None, "fused_layer_input": False, "fused_head_acc": False,
+    "lean_draw": False, "mlp_gateup_recompute": False, "mlp_tail": False, "rmsnorm": False,
+    "fused_ce": False, "rope": False, "fp16_embedding": False, "head_stream": False,
+    "head_slice": 4096, "attention_fp16": False, "unpad": False, "recompute": False,
+    "recompute_fp16_inputs": False, "recompute_host_inputs": False,
+    "recompute_group_tokens": 0, "recompute_no_rerun": False, "offload_activations": False,
+    "stream_weights": False, "warmup": False,
+}
+
+PROFILE = "rules_fast"
+PROFILES = {
+    "rules_fast": {"layer_unpack": True},
+    "rules_time": {"nf4_cache_fp16": True},
+    "rules_memory": {},
+}
+FEATURES.update(PROFILES[PROFILE])
+
+
+def apply():
+    """Install the NF4 patches named by FEATURES (solution/__init__.py:113-171, NF4 part)."""
+    from . import linear4bit, nf4
+
+    direct.enabled = FEATURES["direct_nograd"]
+    linear4bit.FUSED_GEMM = FEATURES["nf4_fused_gemm"]
+    linear4bit.FUSED_LORA = FEATURES["nf4_fused_lora"]
+    if FEATURES["nf4"]:
+        nf4.patch_bnb_nf4()
+        if FEATURES["nf4_direct"]:
+            linear4bit.patch_bnb_linear4bit(cache_weights=FEATURES["nf4_cache_fp16"])

@@ -1,0 +1,84 @@
+"""ctypes binding of libmxs_nf4.so (the C ABI declared in include/mxs_nf4.h).
+
+This is the only way the Python side reaches the GPU kernels.  There is no fallback: if the
+library is missing or fails to load, every call raises MxsLibraryError, naming the build command.
+Tensors are passed as raw device pointers; launches go to torch's current HIP stream.
+"""
+
+import ctypes
+import os
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmxs_nf4.so")
+
+MXS_DTYPE_F16 = 0
+MXS_DTYPE_F32 = 1
+
+_ERRORS = {-1: "bad argument (null pointer or negative size)", -2: "unsupported dtype",
+           -3: "pointer alignment", -4: "shape outside what the kernels take"}
+
+
+class MxsLibraryError(RuntimeError):
+    pass
+
+
+_lib = None
+
+P = ctypes.c_void_p
+I64 = ctypes.c_int64
+I32 = ctypes.c_int
+F32 = ctypes.c_float
+
+# name -> argtypes (all return int)
+_SIGNATURES = {
+    "mxs_nf4_dequant": [P, I64, P, P, P, P, P, P, I32, P],
+    "mxs_nf4_dequant_bytewise": [P, I64, P, P, P, P, P, P, I32, P],
+    "mxs_nf4_dequant_layer": [P, I64, P, P, P, P, P, P, I32, P, P],
+    "mxs_nf4_quantize_workspace_bytes": [I64],
+    "mxs_nf4_quantize": [P, I64, P, P, P, P, P, P, P, P],
+}
+
+
+def lib():
+    """The loaded library; raises MxsLibraryError when it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MxsLibraryError(
+                f"{LIB_PATH} is not built: run `python -m mindxsoup_amd.build` (hipcc, gfx950)")
+        try:
+            L = ctypes.CDLL(LIB_PATH)
+        except OSError as e:
+            raise MxsLibraryError(f"cannot load {LIB_PATH}: {e}") from e
+        for name, args in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGNATURES)
+
+
+def ptr(t):
+    """Raw device pointer of a tensor, or None."""
+    if t is None:
+        return None
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(device=None):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def check(rc, name):
+    if rc != 0:
+        why = _ERRORS.get(rc, f"hipError_t {rc}")
+        raise RuntimeError(f"{name} failed: {why}")
+
+
+def call(name, *args):
+    check(getattr(lib(), name)(*args), name)

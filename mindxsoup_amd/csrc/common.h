@@ -1,0 +1,55 @@
+// Shared definitions for the gfx950 NF4 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mxs {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float float16_t __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// The 16 NF4 code values (QLoRA, arXiv 2305.14314, Appendix E), fp32, ascending; index 7 is 0.
+__device__ __constant__ static const float kNF4[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f,
+    0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,
+    0.7229568362236023f, 1.0f};
+
+constexpr int kBlock = 64;      // NF4 values per first-level absmax
+constexpr int kGroup = 256;     // first-level blocks per second-level absmax
+
+// Two fp32 values -> two fp16 (round to nearest even) packed low-first in a dword.
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+  float2_t v = {lo, hi};
+  half2_t h = __builtin_convertvector(v, half2_t);
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+// Decoded block scale of the double-quantized absmax: code[q8] * absmax2 + offset, one fused
+// multiply-add in fp32 (the contraction Triton applies to the reference kernel).
+__device__ __forceinline__ float nested_scale(float code_q8, float absmax2, float offset) {
+  return __builtin_fmaf(code_q8, absmax2, offset);
+}
+
+// Eight NF4 values of one packed dword (byte j holds values 2j high nibble, 2j+1 low nibble)
+// times `s`, as eight fp16 in four dwords.  `tab` is the NF4 table in LDS.
+__device__ __forceinline__ u32x4 decode8(uint32_t w, float s, const float* tab) {
+  u32x4 r;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t hi = (w >> (8 * j + 4)) & 15u;
+    const uint32_t lo = (w >> (8 * j)) & 15u;
+    r[j] = pack_f16x2(tab[hi] * s, tab[lo] * s);
+  }
+  return r;
+}
+
+}  // namespace mxs

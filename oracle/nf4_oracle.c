@@ -1,0 +1,303 @@
+/*
+ * CPU oracle for the NF4 quantized-linear hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker the HIP path is compared
+ * against (tests/, the smoke check and the CPU-baseline leg of the bench).  The
+ * product library never links, loads or calls it.
+ *
+ * Every function restates the reference's algorithm in plain scalar C, citing
+ * the reference file:line it follows (paths relative to the MindXSoup tree).
+ *
+ * Pinning (what checks each function independently of this restatement):
+ *   nf4_table            - recomputed from the normal-quantile definition
+ *                          (scipy norm.ppf) and the QLoRA paper's table.
+ *   f32_to_f16_rne       - numpy's IEEE float16 conversion over every class of
+ *                          input (normals, subnormals, ties, overflow, NaN).
+ *   dequant_nf4          - closed-form special cases (code index 7 -> +-0,
+ *                          index 15 -> +s), a brute force over all 256 byte
+ *                          values, the fused/unfused 1-ulp bound, an
+ *                          independent numpy vectorised restatement, and the
+ *                          quantize -> dequantize error bound, which fails for
+ *                          a swapped nibble order or a wrong block index.
+ *   quantize_nf4 / quantize_absmax_256 / dynamic_map
+ *                        - round-trip bounds and the nearest-code property
+ *                          (brute force over every candidate code).
+ *   The GEMM / LoRA references live in oracle/oracle.py (numpy) and are pinned
+ *   against float64 torch autograd.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+#include <stdlib.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* The 16 NF4 values, QLoRA (Dettmers et al. 2023, arXiv 2305.14314) Appendix E;
+ * bitsandbytes' get_4bit_type("nf4") returns the same list (called at
+ * solution/nf4.py:116-123). Index 7 is the exact zero. */
+static const float NF4[16] = {
+    -1.0f, -0.6961928009986877f, -0.5250730514526367f, -0.39491748809814453f,
+    -0.28444138169288635f, -0.18477343022823334f, -0.09105003625154495f, 0.0f,
+    0.07958029955625534f, 0.16093020141124725f, 0.24611230194568634f,
+    0.33791524171829224f, 0.44070982933044434f, 0.5626170039176941f,
+    0.7229568362236023f, 1.0f};
+
+void oracle_nf4_table(float *out) { memcpy(out, NF4, sizeof(NF4)); }
+
+/* IEEE-754 binary32 -> binary16, round to nearest, ties to even, with
+ * subnormals, overflow to infinity and NaN kept quiet.  This is the rounding
+ * Triton's `.to(tl.float16)` applies at solution/nf4.py:50 and :80. */
+uint16_t oracle_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t exp = (x >> 23) & 0xffu;
+    uint32_t man = x & 0x7fffffu;
+    if (exp == 0xffu) { /* inf / nan */
+        return (uint16_t)(sign | 0x7c00u | (man ? (0x200u | (man >> 13)) : 0));
+    }
+    int e = (int)exp - 127 + 15; /* biased half exponent */
+    if (e >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (e <= 0) {
+        /* subnormal half (or zero): value = man_full * 2^(exp-150); half ulp = 2^-24 */
+        if (e < -10) return (uint16_t)sign; /* below half of the smallest subnormal */
+        uint32_t full = man | 0x800000u;
+        uint32_t shift = (uint32_t)(14 - e); /* 24-bit significand -> 10-bit field */
+        uint32_t q = full >> shift;
+        uint32_t rem = full & ((1u << shift) - 1u);
+        uint32_t half = 1u << (shift - 1u);
+        if (rem > half || (rem == half && (q & 1u))) q++;
+        return (uint16_t)(sign | q); /* q may carry into the exponent field: correct */
+    }
+    uint32_t q = ((uint32_t)e << 10) | (man >> 13);
+    uint32_t rem = man & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (q & 1u))) q++; /* carry into exponent ok */
+    return (uint16_t)(sign | q);
+}
+
+float oracle_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t exp = (h >> 10) & 0x1fu;
+    uint32_t man = h & 0x3ffu;
+    uint32_t x;
+    if (exp == 0) {
+        if (man == 0) {
+            x = sign;
+        } else { /* subnormal: normalise */
+            int e = -1;
+            do { man <<= 1; e++; } while (!(man & 0x400u));
+            man &= 0x3ffu;
+            x = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+        }
+    } else if (exp == 31) {
+        x = sign | 0x7f800000u | (man << 13);
+    } else {
+        x = sign | ((exp - 15 + 127) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &x, 4);
+    return f;
+}
+
+/* Block scale of the double-quantized absmax: solution/nf4.py:40-43 / :70-73,
+ * code[q8] * absmax2[blk // 256] + offset in fp32.  Triton contracts the
+ * multiply-add into one FMA by default (the "one fp16 ulp" note at
+ * solution/test_nf4.py:41); `fused` selects that (1) or the two roundings (0). */
+static inline float block_scale(const uint8_t *absmax8, const float *code,
+                                const float *absmax2, float offset, int64_t blk, int fused) {
+    float c = code[absmax8[blk]];
+    float a2 = absmax2[blk >> 8];
+    if (fused) return fmaf(c, a2, offset);
+    volatile float prod = c * a2; /* force the separate rounding */
+    return prod + offset;
+}
+
+/* One-byte restatement of nf4_unpack_kernel (solution/nf4.py:31-51) which the
+ * wide kernel (:54-86) must match bit for bit: byte i holds values 2i (high
+ * nibble) and 2i+1 (low nibble); block = i // 32; out = fp16(NF4[q] * scale).
+ * nested != 0: scale from (absmax8, code, absmax2, offset); else absmax_f32[blk]
+ * (solution/nf4.py:44-45).  Output is fp16 bit patterns, 2*n_bytes of them. */
+void oracle_dequant_nf4(const uint8_t *packed, int64_t n_bytes, const uint8_t *absmax8,
+                        const float *code, const float *absmax2, float offset,
+                        const float *absmax_f32, int nested, int fused, uint16_t *out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n_bytes; i++) {
+        int64_t blk = i >> 5;
+        float s = nested ? block_scale(absmax8, code, absmax2, offset, blk, fused)
+                         : absmax_f32[blk];
+        uint8_t b = packed[i];
+        out[2 * i] = oracle_f32_to_f16(NF4[b >> 4] * s);
+        out[2 * i + 1] = oracle_f32_to_f16(NF4[b & 15] * s);
+    }
+}
+
+/* fp32 output variant (unpack_nf4's dtype=torch.float32 case, nf4.py:166). */
+void oracle_dequant_nf4_f32(const uint8_t *packed, int64_t n_bytes, const uint8_t *absmax8,
+                            const float *code, const float *absmax2, float offset,
+                            const float *absmax_f32, int nested, int fused, float *out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n_bytes; i++) {
+        int64_t blk = i >> 5;
+        float s = nested ? block_scale(absmax8, code, absmax2, offset, blk, fused)
+                         : absmax_f32[blk];
+        uint8_t b = packed[i];
+        out[2 * i] = NF4[b >> 4] * s;
+        out[2 * i + 1] = NF4[b & 15] * s;
+    }
+}
+
+/* The grouped (whole-layer) form of solution/nf4.py:89-110: several weights,
+ * each with its own code book, second-level scales and offset, decoded in one
+ * call.  Here simply a loop over the per-weight form. */
+void oracle_dequant_nf4_grouped(int n_weights, const uint8_t *const *packed,
+                                const int64_t *n_bytes, const uint8_t *const *absmax8,
+                                const float *const *code, const float *const *absmax2,
+                                const float *offset, uint16_t *const *out) {
+    for (int w = 0; w < n_weights; w++)
+        oracle_dequant_nf4(packed[w], n_bytes[w], absmax8[w], code[w], absmax2[w], offset[w],
+                           NULL, 1, 1, out[w]);
+}
+
+/* ---------------------------------------------------------------------------
+ * Quantizer (upstream of the path: makes synthetic NF4 weights).  Restates the
+ * published bitsandbytes algorithm behind quantize_4bit(..., quant_type="nf4",
+ * compress_statistics=True) as the reference calls it (solution/test_nf4.py:33,
+ * tools/bench_nf4.py:30-35).  Exact equality with bitsandbytes is not required:
+ * the path's contract starts at the packed tensors.
+ * ------------------------------------------------------------------------- */
+
+/* Signed dynamic-tree code book, 8 bits, 7 exponent bits (Dettmers, "8-bit
+ * approximations for parallelism in deep learning", arXiv 1511.04561): for
+ * decade i = 0..6 the 2^i midpoints of an even split of [0.1, 1] scaled by
+ * 10^(i-6), both signs, plus 0 and 1; sorted ascending. */
+void oracle_dynamic_map(float *out) {
+    float v[256];
+    int n = 0;
+    for (int i = 0; i < 7; i++) {
+        int items = (1 << i) + 1; /* boundaries in [0.1, 1] */
+        double scale = pow(10.0, (double)(i - 6));
+        for (int j = 0; j + 1 < items; j++) {
+            /* boundaries as fp32 like a float32 linspace, midpoint in fp32 */
+            float b0 = (float)(0.1 + 0.9 * (double)j / (double)(items - 1));
+            float b1 = (float)(0.1 + 0.9 * (double)(j + 1) / (double)(items - 1));
+            float mid = (b0 + b1) / 2.0f;
+            v[n++] = (float)(scale * (double)mid);
+            v[n++] = (float)(-scale * (double)mid);
+        }
+    }
+    v[n++] = 0.0f;
+    v[n++] = 1.0f;
+    /* n == 256 */
+    for (int i = 1; i < n; i++) { /* insertion sort */
+        float key = v[i];
+        int j = i - 1;
+        while (j >= 0 && v[j] > key) { v[j + 1] = v[j]; j--; }
+        v[j + 1] = key;
+    }
+    memcpy(out, v, sizeof(float) * 256);
+}
+
+/* Nearest NF4 index of a value already divided by the block absmax: the index
+ * of the first table entry whose upper midpoint is >= x (ties go down). */
+static inline int nf4_nearest(float x) {
+    int q = 0;
+    for (int i = 0; i < 15; i++) {
+        float mid = (float)(((double)NF4[i] + (double)NF4[i + 1]) * 0.5);
+        if (x > mid) q = i + 1;
+    }
+    return q;
+}
+
+/* Per-64 absmax and packed nibbles, high nibble first.  w: fp16 bit patterns,
+ * n a multiple of 64 (all Qwen2.5-1.5B shapes are). */
+void oracle_quantize_nf4(const uint16_t *w, int64_t n, uint8_t *packed, float *absmax) {
+    int64_t n_blocks = n / 64;
+#pragma omp parallel for schedule(static)
+    for (int64_t b = 0; b < n_blocks; b++) {
+        float m = 0.0f;
+        for (int j = 0; j < 64; j++) {
+            float a = fabsf(oracle_f16_to_f32(w[b * 64 + j]));
+            if (a > m) m = a;
+        }
+        absmax[b] = m;
+        float inv = m > 0.0f ? 1.0f / m : 0.0f;
+        for (int j = 0; j < 64; j += 2) {
+            int hi = nf4_nearest(oracle_f16_to_f32(w[b * 64 + j]) * inv);
+            int lo = nf4_nearest(oracle_f16_to_f32(w[b * 64 + j + 1]) * inv);
+            packed[b * 32 + j / 2] = (uint8_t)((hi << 4) | lo);
+        }
+    }
+}
+
+/* Mean of the block absmax values (bitsandbytes: absmax.mean()), summed in double in a fixed
+ * order: spans of 4096 blocks, each summed by 256 lane-strided partials combined pairwise
+ * (d = 128, 64, ..., 1), then the span sums in index order.  A fixed order makes the quantizer
+ * reproducible; the order itself is a choice of this build, not of the reference. */
+float oracle_absmax_mean(const float *absmax, int64_t n_blocks) {
+    double total = 0.0;
+    for (int64_t base = 0; base < n_blocks; base += 4096) {
+        double lane[256];
+        for (int t = 0; t < 256; t++) {
+            double acc = 0.0;
+            for (int i = t; i < 4096; i += 256)
+                if (base + i < n_blocks) acc += (double)absmax[base + i];
+            lane[t] = acc;
+        }
+        for (int d = 128; d > 0; d >>= 1)
+            for (int t = 0; t < d; t++) lane[t] += lane[t + d];
+        total += lane[0];
+    }
+    return (float)(total / (double)n_blocks);
+}
+
+/* Index of the code entry nearest to x (code sorted ascending; ties -> lower). */
+static inline int code_nearest(const float *code, float x) {
+    int lo = 0, hi = 255;
+    while (hi - lo > 1) { /* largest index with code[idx] <= x */
+        int mid = (lo + hi) >> 1;
+        if (code[mid] <= x) lo = mid; else hi = mid;
+    }
+    if (x <= code[0]) return 0;
+    if (x >= code[255]) return 255;
+    float dlo = x - code[lo], dhi = code[hi] - x;
+    return dhi < dlo ? hi : lo;
+}
+
+/* Second level: (absmax - offset) quantized blockwise (256 per block) with the
+ * signed dynamic code book: absmax2 = max |v| per 256-block, q8 = nearest code
+ * of v / absmax2.  Decoded scale = code[q8] * absmax2 + offset (nf4.py:70-73). */
+void oracle_quantize_absmax_256(const float *absmax, int64_t n_blocks, float offset,
+                                const float *code, uint8_t *q8, float *absmax2) {
+    int64_t n_groups = (n_blocks + 255) / 256;
+#pragma omp parallel for schedule(static)
+    for (int64_t g = 0; g < n_groups; g++) {
+        int64_t b0 = g * 256, b1 = b0 + 256 < n_blocks ? b0 + 256 : n_blocks;
+        float m = 0.0f;
+        for (int64_t b = b0; b < b1; b++) {
+            float a = fabsf(absmax[b] - offset);
+            if (a > m) m = a;
+        }
+        absmax2[g] = m;
+        float inv = m > 0.0f ? 1.0f / m : 0.0f;
+        for (int64_t b = b0; b < b1; b++) q8[b] = (uint8_t)code_nearest(code, (absmax[b] - offset) * inv);
+    }
+}
+
+/* Threads the OpenMP loops above use (1 without OpenMP). */
+int oracle_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+void oracle_set_num_threads(int n) {
+#ifdef _OPENMP
+    omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}

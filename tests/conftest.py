@@ -1,0 +1,26 @@
+"""pytest setup: the `gpu` marker, import paths and shared fixtures."""
+
+import os
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) GPU and the built HIP library")
+
+
+@pytest.fixture(scope="session")
+def cuda():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from mindxsoup_amd import _lib
+
+    _lib.lib()  # raises if the HIP library is not built: GPU tests never run without it
+    return torch.device("cuda:0")

@@ -1,0 +1,271 @@
+"""Pins of the CPU oracle (no GPU): each check is independent of the oracle's own code, chosen
+so that a plausible mistake (wrong table value, swapped nibbles, wrong block index, a missing or
+extra rounding, a sign or transposition error in the LoRA gradients) fails one of them."""
+
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+
+# --- NF4 table ----------------------------------------------------------------------------
+
+def test_nf4_table_is_the_normal_quantile_code():
+    """NF4 = normalised quantiles of N(0,1): 8 positive from linspace(0.9677083, 0.5, 9), 7
+    negative from linspace(0.9677083, 0.5, 8), plus 0 (QLoRA, arXiv 2305.14314, Sec. 3 / App. E;
+    the offset 0.9677083 = (1 - 1/(2*15) + 1 - 1/(2*16)) / 2)."""
+    from scipy.stats import norm
+
+    off = 0.9677083
+    pos = norm.ppf(np.linspace(off, 0.5, 9)[:-1])
+    neg = -norm.ppf(np.linspace(off, 0.5, 8)[:-1])
+    vals = np.sort(np.concatenate([pos, neg, [0.0]]))
+    vals = vals / vals.max()
+    table = O.nf4_table()
+    assert table.dtype == np.float32 and table.shape == (16,)
+    np.testing.assert_allclose(table, vals, rtol=0, atol=2e-7)
+    assert table[7] == 0.0 and table[0] == -1.0 and table[15] == 1.0
+    assert np.all(np.diff(table) > 0)
+
+
+def test_product_table_matches_oracle_table():
+    from mindxsoup_amd.nf4 import NF4_VALUES
+
+    assert np.array_equal(NF4_VALUES.view(np.uint32), O.nf4_table().view(np.uint32))
+
+
+# --- fp16 rounding ------------------------------------------------------------------------
+
+def test_f32_to_f16_matches_numpy_rne():
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal(20000) * 10.0 ** rng.integers(-9, 6, 20000)).astype(np.float32)
+    bits = rng.integers(0, 2 ** 32, 5000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    bits = bits[np.isfinite(bits)]
+    edge = np.array([0.0, -0.0, 65504, 65519.996, 65520, 2 ** -24, 2 ** -25, 3 * 2 ** -26,
+                     2 ** -14, 2 ** -14 - 2 ** -25, 1 + 2 ** -11, 1 + 3 * 2 ** -11, np.inf,
+                     -np.inf, 1e-30], np.float32)
+    allx = np.concatenate([x, bits, edge]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        want = allx.astype(np.float16).view(np.uint16)
+    got = O.f32_to_f16_bits(allx)
+    assert np.array_equal(got, want)
+
+
+# --- dequant: closed forms ----------------------------------------------------------------
+
+def _one_block_case(code_val, absmax2_val, offset, byte_values):
+    packed = np.asarray(byte_values, np.uint8)
+    n_blocks = (packed.size + 31) // 32
+    code = np.zeros(256, np.float32)
+    code[3] = code_val
+    absmax8 = np.full(n_blocks, 3, np.uint8)
+    absmax2 = np.full((n_blocks + 255) // 256, absmax2_val, np.float32)
+    return O.dequant(packed=packed, absmax8=absmax8, code=code, absmax2=absmax2, offset=offset)
+
+
+def test_dequant_zero_code_and_unit_code():
+    # scale = 0.5 * 2 + 0.25 = 1.25 exactly; byte 0x7F -> (NF4[7] = 0, NF4[15] = 1) * 1.25
+    out = _one_block_case(0.5, 2.0, 0.25, [0x7F] * 32)
+    assert out.dtype == np.float16
+    assert np.all(out[0::2] == 0.0) and np.all(out[1::2] == np.float16(1.25))
+    # 0xF0 -> high nibble first: (1.25, -1.25)
+    out = _one_block_case(0.5, 2.0, 0.25, [0xF0] * 32)
+    assert np.all(out[0::2] == np.float16(1.25)) and np.all(out[1::2] == np.float16(-1.25))
+    # code[q8] = 0: the scale is the offset alone
+    out = _one_block_case(0.0, 123.0, 0.5, [0xF0] * 32)
+    assert np.all(out[0::2] == np.float16(0.5))
+
+
+def test_dequant_all_bytes_brute_force():
+    """Every byte value: value 2i from the high nibble, 2i+1 from the low, times the scale, one
+    rounding to fp16 (numpy's own float32 -> float16 conversion)."""
+    table = O.nf4_table()
+    for scale_parts in [(0.75, 0.03125, 0.0), (-0.3, 0.07, 0.051), (1.0, 1e-3, 2e-4)]:
+        packed = np.arange(256, dtype=np.uint8)
+        out = _one_block_case(*scale_parts, packed)
+        c, a2, off = (np.float32(v) for v in scale_parts)
+        s = np.float32(Fraction(float(c)) * Fraction(float(a2)) + Fraction(float(off)))
+        hi = (table[packed >> 4] * s).astype(np.float16)
+        lo = (table[packed & 15] * s).astype(np.float16)
+        assert np.array_equal(out[0::2].view(np.uint16), hi.view(np.uint16))
+        assert np.array_equal(out[1::2].view(np.uint16), lo.view(np.uint16))
+
+
+def test_dequant_block_and_group_indexing():
+    """Block b (32 bytes) takes absmax8[b]; absmax2 advances every 256 blocks.  With distinct
+    powers of two per block and per group the output names its own block and group."""
+    n_blocks = 600
+    packed = np.full(32 * n_blocks, 0xFF, np.uint8)  # every value NF4[15] = 1.0
+    code = (2.0 ** -np.arange(256)).astype(np.float32)[::-1].copy()  # ascending, exact
+    absmax8 = (np.arange(n_blocks) % 200 + 40).astype(np.uint8)
+    absmax2 = np.array([1.0, 4.0, 16.0], np.float32)
+    out = O.dequant(packed=packed, absmax8=absmax8, code=code, absmax2=absmax2, offset=0.0)
+    want_block = code[absmax8] * absmax2[np.arange(n_blocks) // 256]
+    want = np.repeat(want_block, 64).astype(np.float16)
+    assert np.array_equal(out.view(np.uint16), want.view(np.uint16))
+
+
+def _fma32(a, b, c):
+    return np.float32(Fraction(float(a)) * Fraction(float(b)) + Fraction(float(c)))
+
+
+def test_dequant_scale_is_one_fused_multiply_add():
+    """Against exact rational arithmetic: the fused scale is RN(c*a2 + off); the unfused one is
+    RN(RN(c*a2) + off).  Cases are picked where the two differ, so a dropped FMA shows."""
+    rng = np.random.default_rng(3)
+    found = 0
+    for _ in range(4000):
+        c, a2, off = (np.float32(v) for v in rng.uniform(-1, 1, 3))
+        fused = _fma32(c, a2, off)
+        unfused = np.float32(np.float32(c * a2) + off)
+        if fused == unfused:
+            continue
+        found += 1
+        code = np.zeros(256, np.float32)
+        code[9] = c
+        packed = np.full(32, 0xF7, np.uint8)  # values (1.0, 0.0) * scale
+        got_f = O.dequant(packed=packed, absmax8=np.array([9], np.uint8), code=code,
+                          absmax2=np.array([a2], np.float32), offset=float(off),
+                          out_dtype=np.float32)
+        got_u = O.dequant(packed=packed, absmax8=np.array([9], np.uint8), code=code,
+                          absmax2=np.array([a2], np.float32), offset=float(off),
+                          out_dtype=np.float32, fused=False)
+        assert got_f[0] == fused and got_u[0] == unfused
+        if found > 40:
+            break
+    assert found > 10
+
+
+def test_fused_and_unfused_differ_by_at_most_one_ulp():
+    """solution/test_nf4.py:41-42: the two absmax decodes give fp16 values at most one ulp apart."""
+    rng = np.random.default_rng(5)
+    w = (rng.standard_normal((256, 512)) * 0.05).astype(np.float16)
+    q = O.quantize(w)
+    a = O.dequant(q).view(np.uint16).astype(np.int32)
+    b = O.dequant(q, fused=False).view(np.uint16).astype(np.int32)
+    assert np.abs(a - b).max() <= 1
+
+
+def test_dequant_numpy_restatement():
+    """An independent vectorised numpy decode (whole arrays, no per-byte loop) agrees bit for
+    bit with the scalar C oracle on a random double-quantized weight."""
+    rng = np.random.default_rng(11)
+    n_blocks = 1000
+    packed = rng.integers(0, 256, 32 * n_blocks, dtype=np.uint8)
+    absmax8 = rng.integers(0, 256, n_blocks, dtype=np.uint8)
+    code = np.sort(rng.uniform(-1, 1, 256).astype(np.float32))
+    absmax2 = rng.uniform(0.01, 0.1, (n_blocks + 255) // 256).astype(np.float32)
+    offset = np.float32(0.031)
+    got = O.dequant(packed=packed, absmax8=absmax8, code=code, absmax2=absmax2,
+                    offset=float(offset))
+    blk = np.arange(n_blocks)
+    scale = np.array([_fma32(c, a, offset) for c, a in zip(code[absmax8], absmax2[blk // 256])],
+                     np.float32)
+    nib = np.stack([packed >> 4, packed & 15], axis=1).reshape(-1)
+    want = (O.nf4_table()[nib] * np.repeat(scale, 64)).astype(np.float16)
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+# --- quantizer ----------------------------------------------------------------------------
+
+def test_quantize_roundtrip_error_bound():
+    """|w - deq(quant(w))| <= absmax_b * (largest half-gap of NF4) + second-level error: fails
+    for a swapped nibble order or a wrong block index on either side."""
+    rng = np.random.default_rng(0)
+    w = (rng.standard_normal((512, 256)) * 0.02).astype(np.float16)
+    q = O.quantize(w)
+    d = O.dequant(q).astype(np.float32).reshape(-1)
+    table = O.nf4_table().astype(np.float64)
+    half_gap = np.max(np.diff(table)) / 2
+    blk_absmax = np.repeat(q.absmax_f32, 64)
+    scale = np.repeat(q.code[q.absmax8] * q.absmax2[np.arange(q.absmax8.size) // 256] + q.offset,
+                      64)
+    err = np.abs(d - w.reshape(-1).astype(np.float32))
+    bound = blk_absmax * half_gap + np.abs(scale - blk_absmax) + 1e-3 * np.abs(d) + 1e-7
+    assert np.all(err <= bound)
+    # and much better than chance: relative RMS error of NF4 on Gaussian data is ~10 %
+    rel = np.sqrt(np.mean(err ** 2)) / np.sqrt(np.mean(w.astype(np.float32) ** 2))
+    assert rel < 0.15
+
+
+def test_quantize_picks_nearest_codes():
+    rng = np.random.default_rng(1)
+    w = (rng.standard_normal((64, 128)) * 0.02).astype(np.float16)
+    q = O.quantize(w)
+    table = O.nf4_table()
+    x = w.reshape(-1, 64).astype(np.float32) / q.absmax_f32[:, None]
+    nib = np.stack([q.packed >> 4, q.packed & 15], 1).reshape(-1, 64)
+    d_got = np.abs(x - table[nib])
+    d_best = np.abs(x[..., None] - table[None, None, :]).min(-1)
+    assert np.all(d_got <= d_best + 1e-6)
+    v = (q.absmax_f32 - q.offset) / q.absmax2[np.arange(q.absmax8.size) // 256]
+    assert np.all(np.abs(v - q.code[q.absmax8]) <= np.abs(v[:, None] - q.code[None]).min(1) + 1e-7)
+
+
+def test_dynamic_map_properties_and_product_copy():
+    from mindxsoup_amd.quant import dynamic_map
+
+    code = O.dynamic_map()
+    assert code.shape == (256,) and np.all(np.diff(code) >= 0)
+    assert code[-1] == 1.0 and 0.0 in code and (code < 0).sum() == 127
+    assert np.isclose(code.min(), -0.99296875, atol=1e-7)
+    assert np.array_equal(dynamic_map().view(np.uint32), code.view(np.uint32))
+
+
+def test_absmax_mean_close_to_exact_mean():
+    rng = np.random.default_rng(2)
+    a = rng.uniform(0, 0.1, 300000).astype(np.float32)
+    exact = math.fsum(float(v) for v in a) / a.size
+    assert abs(O.absmax_mean(a) - exact) <= 1e-7 * exact
+
+
+# --- GEMM / LoRA references ---------------------------------------------------------------
+
+def _lora_case(seed, m=24, k=64, n=40, r=16, p=0.25):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float16)
+    a = (rng.standard_normal((r, k)) * 0.1).astype(np.float16)
+    b = (rng.standard_normal((n, r)) * 0.1).astype(np.float16)
+    dy = rng.standard_normal((m, n)).astype(np.float16)
+    keep = (rng.uniform(size=(m, k)) > p).astype(np.uint8)
+    return x, w, a, b, dy, keep, p
+
+
+def test_lora_reference_matches_torch_autograd():
+    """The hand-written backward (dX, dA, dB) against float64 torch autograd of the forward."""
+    x, w, a, b, dy, keep, p = _lora_case(0)
+    s = 2.0
+    xt = torch.tensor(x.astype(np.float64), requires_grad=True)
+    at = torch.tensor(a.astype(np.float64), requires_grad=True)
+    bt = torch.tensor(b.astype(np.float64), requires_grad=True)
+    # dropout on the fp16 input as the reference rounds it (the mask and scale are constants)
+    xd = torch.tensor(O.dropout_fp16(x, keep, p).astype(np.float64))
+    mask_scale = torch.tensor(np.where(keep != 0, float(np.float32(1 / (1 - p))), 0.0))
+    # forward with the dropped input expressed through x so autograd sees d(xd)/dx
+    xd_graph = xt * mask_scale + (xd - (torch.tensor(x.astype(np.float64)) * mask_scale))
+    y = xt @ torch.tensor(w.astype(np.float64)).T + s * (xd_graph @ at.T) @ bt.T
+    y.backward(torch.tensor(dy.astype(np.float64)))
+    y_ref = O.lora_fwd(x, w, a, b, s, keep, p)
+    dx, da, db = O.lora_bwd(dy, x, w, a, b, s, keep, p)
+    np.testing.assert_allclose(y_ref, y.detach().numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dx, xt.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(da, at.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(db, bt.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_lora_forward_merged_weight_identity():
+    """Without dropout, base + s*B(A(x)) equals x @ (W + s*B@A)^T (peft's merge formula)."""
+    x, w, a, b, _, _, _ = _lora_case(1)
+    s = 2.0
+    merged = w.astype(np.float64) + s * b.astype(np.float64) @ a.astype(np.float64)
+    np.testing.assert_allclose(O.lora_fwd(x, w, a, b, s),
+                               x.astype(np.float64) @ merged.T, rtol=1e-10, atol=1e-10)
+
+
+def test_max_rel_definition():
+    assert O.max_rel([1.0, 2.0], [1.0, 4.0]) == pytest.approx(0.5)
