@@ -56,11 +56,21 @@ int mxs_nf4_dequant_bytewise(const void* packed, int64_t n_bytes, const void* ab
  * Module m owns blocks [block0[m], block0[m+1]) of packed/absmax8/out, code
  * [m*256, m*256+256), absmax2 from index scale0[m], and offset[m].
  * block0: device int64 [n_modules + 1] ascending, block0[0] = 0, block0[n_modules] = n_blocks;
- * scale0: device int64 [n_modules].  packed and out must be 16-byte aligned. */
+ * scale0: device int64 [n_modules].  packed and out must be 16-byte aligned.
+ * wg_module: device int16 map from mxs_nf4_dequant_layer_plan (the counterpart of the
+ * reference's per-program `module_of`, solution/stream.py:125-133), or NULL to look each
+ * block's module up in the kernel (slower). */
 int mxs_nf4_dequant_layer(const void* packed, int64_t n_blocks, const void* absmax8,
                           const float* code, const float* absmax2, const float* offset,
                           const int64_t* block0, const int64_t* scale0, int n_modules,
-                          void* out, hipStream_t stream);
+                          const int16_t* wg_module, void* out, hipStream_t stream);
+
+/* Host-side plan for mxs_nf4_dequant_layer: from HOST block0 [n_modules + 1], writes the module
+ * of each of the kernel's workgroups (-1 where one straddles two modules) into HOST wg_module
+ * [capacity] and returns the number of workgroups; with wg_module NULL it only returns that
+ * number.  Negative MXS_ERR_* on bad arguments. */
+int64_t mxs_nf4_dequant_layer_plan(const int64_t* block0, int n_modules, int16_t* wg_module,
+                                   int64_t capacity);
 
 /* Workspace bytes mxs_nf4_quantize needs for n_values (device memory, 8-byte aligned). */
 int mxs_nf4_quantize_workspace_bytes(int64_t n_values);

@@ -34,10 +34,14 @@ F32 = ctypes.c_float
 _SIGNATURES = {
     "mxs_nf4_dequant": [P, I64, P, P, P, P, P, P, I32, P],
     "mxs_nf4_dequant_bytewise": [P, I64, P, P, P, P, P, P, I32, P],
-    "mxs_nf4_dequant_layer": [P, I64, P, P, P, P, P, P, I32, P, P],
+    "mxs_nf4_dequant_layer": [P, I64, P, P, P, P, P, P, I32, P, P, P],
+    "mxs_nf4_dequant_layer_plan": [P, I32, P, I64],
     "mxs_nf4_quantize_workspace_bytes": [I64],
     "mxs_nf4_quantize": [P, I64, P, P, P, P, P, P, P, P],
 }
+
+
+_RESTYPES = {"mxs_nf4_dequant_layer_plan": ctypes.c_int64}
 
 
 def lib():
@@ -54,7 +58,7 @@ def lib():
         for name, args in _SIGNATURES.items():
             fn = getattr(L, name)
             fn.argtypes = args
-            fn.restype = ctypes.c_int
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
         _lib = L
     return _lib
 

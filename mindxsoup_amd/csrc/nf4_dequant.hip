@@ -29,6 +29,7 @@ struct DequantArgs {
   const float* absmax_f32; // non-nested first-level scales
   const int64_t* block0;   // [n_modules + 1] first block of each module (multi-module only)
   const int64_t* scale0;   // [n_modules] first absmax2 index of each module
+  const int16_t* wg_module;  // per workgroup: its module, or -1 if it straddles two (or NULL)
   int64_t n_chunks;
   int64_t n_blocks;
   int n_modules;
@@ -68,7 +69,10 @@ __global__ __launch_bounds__(kDqThreads) void k_dequant_wide(DequantArgs a) {
         int m = 0;
         int64_t first_blk = 0, first_a2 = 0;
         if (MULTI) {
-          m = find_module(a.block0, a.n_modules, blk);
+          // workgroup-uniform module from the plan; a binary search only where the workgroup
+          // straddles two modules (or no plan was given)
+          const int wm = a.wg_module ? (int)a.wg_module[blockIdx.x] : -1;
+          m = wm >= 0 ? wm : find_module(a.block0, a.n_modules, blk);
           first_blk = a.block0[m];
           first_a2 = a.scale0[m];
         }
@@ -172,11 +176,12 @@ int mxs_nf4_dequant_bytewise(const void* packed, int64_t n_bytes, const void* ab
                              const float* code, const float* absmax2, const float* offset,
                              const float* absmax_f32, void* out, int out_dtype,
                              hipStream_t stream) {
-  if (n_bytes < 0 || !packed || !out) return MXS_ERR_ARG;
+  if (n_bytes < 0) return MXS_ERR_ARG;
   if (out_dtype != MXS_DTYPE_F16 && out_dtype != MXS_DTYPE_F32) return MXS_ERR_DTYPE;
+  if (n_bytes == 0) return MXS_OK;  // empty tensors may carry null pointers
+  if (!packed || !out) return MXS_ERR_ARG;
   const bool nested = absmax8 != nullptr;
   if (nested ? (!code || !absmax2 || !offset) : !absmax_f32) return MXS_ERR_ARG;
-  if (n_bytes == 0) return MXS_OK;
   int64_t grid = (n_bytes + 1023) / 1024;
   if (grid > 65536) grid = 65536;
   const dim3 g((unsigned)grid), b(256);
@@ -198,8 +203,10 @@ int mxs_nf4_dequant_bytewise(const void* packed, int64_t n_bytes, const void* ab
 int mxs_nf4_dequant(const void* packed, int64_t n_bytes, const void* absmax8, const float* code,
                     const float* absmax2, const float* offset, const float* absmax_f32,
                     void* out, int out_dtype, hipStream_t stream) {
-  if (n_bytes < 0 || !packed || !out) return MXS_ERR_ARG;
+  if (n_bytes < 0) return MXS_ERR_ARG;
   if (out_dtype != MXS_DTYPE_F16 && out_dtype != MXS_DTYPE_F32) return MXS_ERR_DTYPE;
+  if (n_bytes == 0) return MXS_OK;  // empty tensors may carry null pointers
+  if (!packed || !out) return MXS_ERR_ARG;
   const bool nested = absmax8 != nullptr;
   if (nested ? (!code || !absmax2 || !offset) : !absmax_f32) return MXS_ERR_ARG;
   // The wide kernel needs whole 32-byte blocks, dword-aligned packed bytes and 16-byte aligned
@@ -223,10 +230,28 @@ int mxs_nf4_dequant(const void* packed, int64_t n_bytes, const void* absmax8, co
   return launch_wide(a, nested, false, out_dtype == MXS_DTYPE_F32, stream);
 }
 
+int64_t mxs_nf4_dequant_layer_plan(const int64_t* block0, int n_modules, int16_t* wg_module,
+                                   int64_t capacity) {
+  if (!block0 || n_modules < 1 || n_modules > 32767 || capacity < 0) return MXS_ERR_ARG;
+  const int64_t n_blocks = block0[n_modules];
+  const int64_t n_wg = (n_blocks + kDqBlocks - 1) / kDqBlocks;
+  if (!wg_module) return n_wg;
+  if (capacity < n_wg) return MXS_ERR_SIZE;
+  int m = 0;
+  for (int64_t g = 0; g < n_wg; g++) {
+    const int64_t first = g * kDqBlocks;
+    const int64_t last = (first + kDqBlocks < n_blocks ? first + kDqBlocks : n_blocks) - 1;
+    while (m + 1 <= n_modules && block0[m + 1] <= first) m++;
+    wg_module[g] = (int16_t)(last < block0[m + 1] ? m : -1);
+  }
+  return n_wg;
+}
+
 int mxs_nf4_dequant_layer(const void* packed, int64_t n_blocks, const void* absmax8,
                           const float* code, const float* absmax2, const float* offset,
                           const int64_t* block0, const int64_t* scale0, int n_modules,
-                          void* out, hipStream_t stream) {
+                          const int16_t* wg_module, void* out, hipStream_t stream) {
+  if (n_blocks == 0 && n_modules >= 1) return MXS_OK;
   if (n_blocks < 0 || n_modules < 1 || !packed || !out || !absmax8 || !code || !absmax2 ||
       !offset || !block0 || !scale0)
     return MXS_ERR_ARG;
@@ -240,6 +265,7 @@ int mxs_nf4_dequant_layer(const void* packed, int64_t n_blocks, const void* absm
   a.offset = offset;
   a.block0 = block0;
   a.scale0 = scale0;
+  a.wg_module = wg_module;
   a.n_chunks = n_blocks * 8;
   a.n_blocks = n_blocks;
   a.n_modules = n_modules;

@@ -113,10 +113,36 @@ def launch_layer(packed, out, absmax_8bit, code, absmax2, offset, module_of, blo
     if packed.numel() != 32 * n_blocks or out.numel() != 64 * n_blocks or \
             out.dtype != torch.float16:
         raise ValueError("packed/out sizes do not match the block count")
+    plan = layer_plan(block0)
     _lib.call("mxs_nf4_dequant_layer", _lib.ptr(packed), n_blocks, _lib.ptr(absmax_8bit),
               _lib.ptr(code), _lib.ptr(absmax2), _lib.ptr(offset), _lib.ptr(block0),
-              _lib.ptr(scale0), n_modules, _lib.ptr(out), _lib.stream_of(dev))
+              _lib.ptr(scale0), n_modules, _lib.ptr(plan), _lib.ptr(out), _lib.stream_of(dev))
     return out
+
+
+_PLANS = {}
+
+
+def layer_plan(block0):
+    """Device int16 map workgroup -> weight for the layer launch (the counterpart of the
+    reference's per-program `module_of`, solution/stream.py:125-133), built on the host once per
+    layout and cached by the block0 tensor's identity and version."""
+    key = (block0.data_ptr(), block0._version, block0.numel(), block0.device)
+    plan = _PLANS.get(key)
+    if plan is None:
+        b0 = np.ascontiguousarray(block0.cpu().numpy(), np.int64)
+        L = _lib.lib()
+        n = L.mxs_nf4_dequant_layer_plan(b0.ctypes.data, b0.size - 1, None, 0)
+        _lib.check(int(min(n, 0)), "mxs_nf4_dequant_layer_plan")
+        host = np.empty(max(n, 1), np.int16)
+        _lib.check(int(min(L.mxs_nf4_dequant_layer_plan(b0.ctypes.data, b0.size - 1,
+                                                         host.ctypes.data, n), 0)),
+                   "mxs_nf4_dequant_layer_plan")
+        plan = torch.from_numpy(host).to(block0.device)
+        if len(_PLANS) > 64:
+            _PLANS.clear()
+        _PLANS[key] = plan
+    return plan
 
 
 def _supported(packed, shape, blocksize, quant_type, dtype, nested_blocksize=256):

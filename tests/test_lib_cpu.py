@@ -12,7 +12,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def _declared():
     text = open(os.path.join(ROOT, "include", "mxs_nf4.h")).read()
-    return sorted(set(re.findall(r"^int\s+(mxs_\w+)\s*\(", text, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t)\s+(mxs_\w+)\s*\(", text, flags=re.M)))
 
 
 def test_header_declares_entry_points():
@@ -48,3 +48,19 @@ def test_error_codes_raise():
     with pytest.raises(RuntimeError, match="alignment"):
         _lib.check(-3, "x")
     _lib.check(0, "x")
+
+
+def test_layer_plan_marks_straddling_workgroups():
+    """The host-side plan of the layer launch: 128 blocks per workgroup; -1 where one straddles."""
+    import numpy as np
+
+    from mindxsoup_amd import _lib
+
+    L = _lib.lib()
+    block0 = np.array([0, 128, 300, 300, 640], np.int64)  # includes an empty module
+    n = L.mxs_nf4_dequant_layer_plan(block0.ctypes.data, 4, None, 0)
+    assert n == 5
+    out = np.zeros(n, np.int16)
+    assert L.mxs_nf4_dequant_layer_plan(block0.ctypes.data, 4, out.ctypes.data, n) == n
+    assert out.tolist() == [0, 1, -1, 3, 3]  # workgroup 2 spans blocks 256..383: modules 1 and 3
+    assert L.mxs_nf4_dequant_layer_plan(block0.ctypes.data, 4, out.ctypes.data, 2) < 0
