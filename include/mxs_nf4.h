@@ -86,6 +86,58 @@ int mxs_nf4_quantize(const void* w_f16, int64_t n_values, const float* code, voi
                      float* absmax_f32, void* absmax8, float* absmax2, float* offset,
                      void* workspace, hipStream_t stream);
 
+/* ---- Fused NF4 GEMMs (forward and input gradient of the frozen Linear4bit) ---------------
+ * cfg: tile configuration id (0: 256x128, 1: 128x128, 2: 128x256, 3: 256x256, 4: 64x128) or -1
+ * to let the library choose tiles and split-K for the shape; splits: reduction splits (used with
+ * cfg >= 0).  When the chosen plan splits the reduction, `workspace` must hold
+ * mxs_nf4_gemm_workspace_bytes(M, Nc, Kr, cfg, splits) bytes of device memory (else it may be
+ * NULL).  Shapes: in_features % 64 == 0, reduction % 64 == 0; x/dy 16-byte aligned. */
+int64_t mxs_nf4_gemm_workspace_bytes(int M, int Nc, int Kr, int cfg, int splits);
+
+/* Y[M,N] = X[M,K] . W[N,K]^T (+ bias[N]) (+ lora_h[M,r] . lora_b[N,r]^T), fp16 in/out, fp32
+ * accumulation, W decoded from NF4 inside the GEMM.  Replaces NF4LinearFunction.forward
+ * (solution/linear4bit.py:47-49: unpack, then F.linear) and adds peft's LoRA branch
+ * (solution/attention.py:197-199) as an epilogue: lora_h = s * H from mxs_lora_h, so the added
+ * term is s * B(A(drop(x))).  bias and lora_h may be NULL. */
+int mxs_nf4_linear_fwd(const void* x, int M, int K, int N, const void* packed,
+                       const void* absmax8, const float* code, const float* absmax2,
+                       const float* offset, const void* bias, const void* lora_h,
+                       const void* lora_b, int r, void* y, void* workspace, int cfg, int splits,
+                       hipStream_t stream);
+
+/* dX[M,K] = dY[M,N] . W[N,K] (+ mask[M,K] * mask_scale * (lora_dh[M,r] . lora_a[r,K])), with W
+ * decoded from NF4 inside the GEMM.  Replaces NF4LinearFunction.backward
+ * (solution/linear4bit.py:51-57: unpack again, then grad @ W) plus the LoRA branch's input
+ * gradient through the dropout (solution/dropout.py:62-69); lora_dh = s * dY . B from
+ * mxs_lora_dh.  mask: u8 keep mask [M,K] or NULL (no dropout); mask_scale = 1/(1-p). */
+int mxs_nf4_linear_bwd_dx(const void* dy, int M, int N, int K, const void* packed,
+                          const void* absmax8, const float* code, const float* absmax2,
+                          const float* offset, const void* lora_dh, const void* lora_a, int r,
+                          const void* mask, float mask_scale, void* dx, void* workspace, int cfg,
+                          int splits, hipStream_t stream);
+
+/* ---- LoRA side branch (peft lora.Linear around the 4-bit base, r % 16 == 0) --------------
+ * The transposed outputs/inputs (ht, dht) are fp16 [r, ldt] with ldt >= M, ldt % 8 == 0. */
+
+/* h = fp16(s * drop(x) . A^T) [M, r] and ht = its transpose: lora_A of peft's branch with the
+ * reference's dropout (solution/dropout.py:33-35, mask u8 [M,K] or NULL) and the scaling s
+ * folded in.  x [M,K] fp16, lora_a [r,K] fp16, K % 32 == 0. */
+int mxs_lora_h(const void* x, int M, int K, const void* lora_a, int r, const void* mask,
+               float mask_scale, float s, void* h, void* ht, int ldt, hipStream_t stream);
+
+/* dh = fp16(s * dY . B) [M, r] and dht = its transpose (the gradient reaching lora_B's output,
+ * times s).  dy [M,N] fp16, lora_b [N,r] fp16, N % 32 == 0. */
+int mxs_lora_dh(const void* dy, int M, int N, const void* lora_b, int r, float s, void* dh,
+                void* dht, int ldt, hipStream_t stream);
+
+/* dA[r,K] (fp32) = dh^T . drop(x): lora_A's weight gradient (autograd of peft's nn.Linear). */
+int mxs_lora_grad_a(const void* dht, int ldt, const void* x, int M, int K, int r,
+                    const void* mask, float mask_scale, float* da, hipStream_t stream);
+
+/* dB[N,r] (fp32) = dY^T . h (h = s * H): lora_B's weight gradient. */
+int mxs_lora_grad_b(const void* ht, int ldt, const void* dy, int M, int N, int r, float* db,
+                    hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,22 +1,31 @@
-"""Linear4bit forward/backward on the HIP NF4 path (mirror of solution/linear4bit.py).
+"""Linear4bit forward/backward on the HIP NF4 path (mirror of solution/linear4bit.py), and the
+LoRA-wrapped projection with its branch fused into the same kernels.
 
-NF4LinearFunction computes Y = x @ W^T + bias and, in backward, grad_x = grad @ W, with W the
-frozen NF4 weight (no weight or bias gradient), like the reference's Function
-(solution/linear4bit.py:43-57).  W is decoded by the HIP dequant kernel and multiplied by torch
-(rocBLAS/hipBLASLt); the fused HIP GEMMs take over where they are built (FUSED_GEMM).
+`NF4LinearFunction` keeps the reference's contract (solution/linear4bit.py:43-57): forward
+Y = x @ W^T + bias, backward grad_x = grad @ W, no gradient for the frozen W or bias.  With
+FUSED_GEMM the two products run as the fused dequant-GEMM kernels; otherwise W is decoded by the
+HIP dequant kernel and multiplied by torch (the reference's own structure).
+
+`Linear4bit` is a bitsandbytes-compatible module for when bitsandbytes is absent (same
+`forward(self, x)`, same `weight.quant_state` fields); `patch_bnb_linear4bit` installs the same
+forward on `bitsandbytes.nn.Linear4bit` when it is importable.  `LoraLinear4bit` has peft's
+attribute layout (base_layer, lora_A/lora_B/lora_dropout dicts, scaling, active_adapters,
+merged, disable_adapters) and computes base(x) + s * B(A(drop(x))) with `NF4LoraFunction`.
 """
 
 import contextlib
+import math
 
 import torch
 
-from . import direct
+from . import direct, kernels
 from .nf4 import _supported, unpack_nf4
+from .quant import quantize_4bit
 
 _enabled = True
-cache_fp16 = False
-FUSED_GEMM = True
-FUSED_LORA = True
+cache_fp16 = False   # set by patch_bnb_linear4bit(cache_weights=...)
+FUSED_GEMM = True    # FEATURES["nf4_fused_gemm"]
+FUSED_LORA = True    # FEATURES["nf4_fused_lora"]
 
 
 @contextlib.contextmanager
@@ -37,29 +46,278 @@ def _unpack(packed, state, dtype, absmax_8bit=None):
                       code=state.state2.code, offset=state.offset)
 
 
+def _fused(state, x):
+    return FUSED_GEMM and x.dtype == torch.float16 and kernels.fused_shape_ok(state)
+
+
 class NF4LinearFunction(torch.autograd.Function):
-    """F.linear(x, unpack(W), bias); backward grad_x = grad @ unpack(W). W and bias frozen."""
+    """F.linear(x, unpack(W), bias); backward grad_x = grad @ unpack(W).  W and bias frozen."""
 
     @staticmethod
     def forward(ctx, x, packed, state, bias):
         ctx.packed, ctx.state = packed, state
+        if _fused(state, x):
+            lead = x.shape[:-1]
+            y = kernels.nf4_linear_fwd(x.reshape(-1, x.shape[-1]), packed, state, bias)
+            return y.view(*lead, y.shape[-1])
         return torch.nn.functional.linear(x, _unpack(packed, state, x.dtype), bias)
 
     @staticmethod
     def backward(ctx, grad):
         grad_x = None
         if ctx.needs_input_grad[0]:
-            grad_x = torch.matmul(grad, _unpack(ctx.packed, ctx.state, ctx.state.dtype)
-                                  .to(grad.dtype))
+            state = ctx.state
+            if _fused(state, grad):
+                lead = grad.shape[:-1]
+                g = kernels.nf4_linear_bwd_dx(grad.reshape(-1, grad.shape[-1]), ctx.packed,
+                                              state)
+                grad_x = g.view(*lead, g.shape[-1])
+            else:
+                grad_x = torch.matmul(grad, _unpack(ctx.packed, state, state.dtype)
+                                      .to(grad.dtype))
         return grad_x, None, None, None
 
 
+class NF4LoraFunction(torch.autograd.Function):
+    """base(x) + s * B(A(drop(x))) for a frozen NF4 base, fused:
+    forward:  Hs = s * drop(x) A^T (mxs_lora_h), Y = x W^T + bias + Hs B^T (one fused GEMM);
+    backward: dHs = s * dY B, dX = dY W + keep/(1-p) * dHs A (one fused GEMM),
+              dA = dHs^T drop(x), dB = dY^T Hs.
+    `keep` is the u8 dropout mask [M, K] (None without dropout); mask_scale = 1/(1-p)."""
+
+    @staticmethod
+    def forward(ctx, x2d, lora_a, lora_b, packed, state, bias, keep, mask_scale, s):
+        a16 = lora_a.to(torch.float16).contiguous()
+        b16 = lora_b.to(torch.float16).contiguous()
+        h, ht = kernels.lora_h(x2d, a16, s, keep, mask_scale)
+        y = kernels.nf4_linear_fwd(x2d, packed, state, bias, h, b16)
+        ctx.save_for_backward(x2d, keep, ht, a16, b16)
+        ctx.packed, ctx.state, ctx.mask_scale, ctx.s = packed, state, mask_scale, s
+        ctx.dtypes = (lora_a.dtype, lora_b.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2d, keep, ht, a16, b16 = ctx.saved_tensors
+        dy = dy.to(torch.float16).contiguous()
+        dh, dht = kernels.lora_dh(dy, b16, ctx.s)
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx = kernels.nf4_linear_bwd_dx(dy, ctx.packed, ctx.state, dh, a16, keep,
+                                           ctx.mask_scale)
+        da = db = None
+        if ctx.needs_input_grad[1]:
+            da = kernels.lora_grad_a(dht, x2d, keep, ctx.mask_scale).to(ctx.dtypes[0])
+        if ctx.needs_input_grad[2]:
+            db = kernels.lora_grad_b(ht, dy).to(ctx.dtypes[1])
+        return dx, da, db, None, None, None, None, None, None
+
+
+# ---------------------------------------------------------------------------------------------
+# Modules
+# ---------------------------------------------------------------------------------------------
+
+def _direct_ok(layer, x):
+    """When the HIP path takes a call (solution/linear4bit.py:112-129, without bitsandbytes'
+    small-M kernel heuristic: the HIP path takes every token count)."""
+    if not _enabled:
+        return False
+    weight = layer.weight
+    state = getattr(weight, "quant_state", None)
+    return (isinstance(x, torch.Tensor) and x.is_cuda and x.dtype == torch.float16
+            and getattr(layer, "compute_type_is_set", False)
+            and layer.compute_dtype == torch.float16
+            and state is not None and getattr(state, "nested", False)
+            and getattr(state, "state2", None) is not None
+            and state.state2.blocksize == 256 and state.dtype == torch.float16
+            and not getattr(state, "packing_format_for_cpu", False)
+            and len(state.shape) == 2 and x.shape[-1] == state.shape[1] and x.numel() > 0
+            and not weight.requires_grad
+            and (layer.bias is None or not layer.bias.requires_grad)
+            and _supported(weight.data, state.shape, state.blocksize, state.quant_type,
+                           x.dtype, state.state2.blocksize))
+
+
+def _cached_weight(layer, x):
+    """The weight unpacked once to fp16 and kept (solution/linear4bit.py:132-148); None unless
+    this call would take the direct path."""
+    weight16 = layer.__dict__.get("_mindx_weight16")
+    if weight16 is None:
+        if not _direct_ok(layer, x):
+            return None
+        packed = layer.weight.data.view(-1, 1)
+        weight16 = _unpack(packed, layer.weight.quant_state, torch.float16)
+        layer.__dict__["_mindx_weight16"] = weight16
+        return weight16
+    if not (_enabled and isinstance(x, torch.Tensor) and x.is_cuda and x.dtype == torch.float16
+            and x.numel() > 0 and x.shape[-1] == weight16.shape[1]):
+        return None
+    return weight16
+
+
+def _cast_bias_once(layer, x):
+    bias = layer.bias
+    if bias is not None and bias.dtype != x.dtype:  # what Linear4bit.forward does, once
+        bias.data = bias.data.to(x.dtype)
+    return bias
+
+
+def hip_forward(layer, x, original=None):
+    """The patched Linear4bit.forward (solution/linear4bit.py:161-179): fp16 cache, then the
+    direct HIP path, else `original` (bitsandbytes' forward when patched onto it)."""
+    if cache_fp16:
+        weight16 = _cached_weight(layer, x)
+        if weight16 is not None:
+            return torch.nn.functional.linear(x, weight16, _cast_bias_once(layer, x))
+    if not _direct_ok(layer, x):
+        if original is None:
+            raise ValueError("input not supported by the HIP NF4 path")
+        return original(layer, x)
+    bias = _cast_bias_once(layer, x)
+    if bias is not None:
+        bias = bias.to(layer.compute_dtype)
+    packed = layer.weight.data.view(-1, 1)  # canonical [(N*K+1)//2, 1]
+    return direct.run(NF4LinearFunction, x, packed, layer.weight.quant_state, bias)
+
+
+class Linear4bit(torch.nn.Module):
+    """Frozen NF4 linear layer with bitsandbytes' Linear4bit fields (weight.data = packed u8,
+    weight.quant_state, bias, compute_dtype, compute_type_is_set) for when bitsandbytes is not
+    installed.  Inputs the HIP path does not take (another dtype, CPU) are cast to the compute
+    dtype and back, like bitsandbytes' own forward; CPU inputs raise."""
+
+    def __init__(self, input_features, output_features, bias=True, compute_dtype=torch.float16,
+                 device=None):
+        super().__init__()
+        self.in_features = input_features
+        self.out_features = output_features
+        self.compute_dtype = compute_dtype
+        self.compute_type_is_set = True
+        self.weight = None
+        if bias:
+            self.bias = torch.nn.Parameter(torch.zeros(output_features, dtype=torch.float16,
+                                                       device=device), requires_grad=False)
+        else:
+            self.register_parameter("bias", None)
+
+    @classmethod
+    def from_weight(cls, weight, bias=None):
+        """Quantize an fp16 CUDA weight [N, K] (NF4, blocksize 64, nested absmax)."""
+        n, k = weight.shape
+        layer = cls(k, n, bias=bias is not None, device=weight.device)
+        packed, state = quantize_4bit(weight.to(torch.float16))
+        layer.set_quantized(packed, state)
+        if bias is not None:
+            layer.bias.data = bias.detach().to(device=weight.device).clone()
+        return layer
+
+    def set_quantized(self, packed, state):
+        w = torch.nn.Parameter(packed.view(-1, 1), requires_grad=False)
+        w.quant_state = state
+        self.weight = w
+
+    def forward(self, x):
+        if _direct_ok(self, x):
+            return hip_forward(self, x)
+        return _generic_forward(self, x)
+
+
+def _generic_forward(layer, x):
+    """Any other input on the GPU: to the compute dtype, the HIP path, back to the input dtype."""
+    if not x.is_cuda:
+        raise ValueError("the NF4 HIP path needs a GPU tensor")
+    inp_dtype = x.dtype
+    x16 = x.to(layer.compute_dtype)
+    state = layer.weight.quant_state
+    bias = layer.bias.to(layer.compute_dtype) if layer.bias is not None else None
+    packed = layer.weight.data.view(-1, 1)
+    return NF4LinearFunction.apply(x16, packed, state, bias).to(inp_dtype)
+
+
+class LoraLinear4bit(torch.nn.Module):
+    """peft's lora.bnb.Linear4bit layout around a 4-bit base: base_layer, lora_A / lora_B /
+    lora_dropout as ModuleDicts keyed by adapter name, scaling dict, active_adapters, merged,
+    disable_adapters.  forward = base(x) + s * B(A(drop(x))) (solution/test_unpad.py:28-29),
+    fused into the NF4 kernels when FUSED_LORA and the shapes allow it."""
+
+    def __init__(self, base_layer, r=16, lora_alpha=32, lora_dropout=0.05, adapter="default"):
+        super().__init__()
+        self.base_layer = base_layer
+        k, n = base_layer.in_features, base_layer.out_features
+        dev = base_layer.weight.device
+        self.r = {adapter: r}
+        self.lora_alpha = {adapter: lora_alpha}
+        self.scaling = {adapter: lora_alpha / r}
+        self.lora_A = torch.nn.ModuleDict(
+            {adapter: torch.nn.Linear(k, r, bias=False, device=dev)})
+        self.lora_B = torch.nn.ModuleDict(
+            {adapter: torch.nn.Linear(r, n, bias=False, device=dev)})
+        self.lora_dropout = torch.nn.ModuleDict(
+            {adapter: torch.nn.Dropout(lora_dropout) if lora_dropout > 0 else torch.nn.Identity()})
+        torch.nn.init.kaiming_uniform_(self.lora_A[adapter].weight, a=math.sqrt(5))
+        torch.nn.init.zeros_(self.lora_B[adapter].weight)
+        self.active_adapters = [adapter]
+        self.merged = False
+        self.disable_adapters = False
+        self.next_keep = None  # optional u8 keep mask for the next training forward (tests)
+
+    def _adapter(self):
+        if self.disable_adapters or self.merged or len(self.active_adapters) != 1:
+            return None
+        return self.active_adapters[0]
+
+    def draw_keep(self, x2d, p):
+        """The dropout keep mask [M, K] as u8 (a fresh Bernoulli(1 - p) draw)."""
+        if self.next_keep is not None:
+            keep, self.next_keep = self.next_keep, None
+            return keep
+        return torch.empty(x2d.shape, dtype=torch.uint8, device=x2d.device).bernoulli_(1.0 - p)
+
+    def forward(self, x):
+        name = self._adapter()
+        base = self.base_layer
+        if name is None:
+            return base(x)
+        a = self.lora_A[name].weight
+        b = self.lora_B[name].weight
+        drop = self.lora_dropout[name]
+        p = drop.p if isinstance(drop, torch.nn.Dropout) else 0.0
+        state = base.weight.quant_state
+        r = a.shape[0]
+        if not (FUSED_LORA and _direct_ok(base, x) and kernels.fused_shape_ok(state)
+                and r % 16 == 0 and not getattr(self, "_force_unfused", False)):
+            h = drop(x).to(x.dtype) if p > 0 else x
+            return base(x) + (h @ a.to(x.dtype).t() @ b.to(x.dtype).t()) * self.scaling[name]
+        lead = x.shape[:-1]
+        x2d = x.reshape(-1, x.shape[-1]).contiguous()
+        keep = None
+        mask_scale = 1.0
+        if self.training and p > 0:
+            keep = self.draw_keep(x2d, p)
+            mask_scale = 1.0 / (1.0 - p)
+        bias = _cast_bias_once(base, x)
+        y = NF4LoraFunction.apply(x2d, a, b, base.weight.data.view(-1, 1), state, bias, keep,
+                                  mask_scale, float(self.scaling[name]))
+        return y.view(*lead, y.shape[-1])
+
+
 def patch_bnb_linear4bit(cache_weights=False):
-    """Install the HIP forward on bitsandbytes.nn.Linear4bit when bitsandbytes is importable."""
+    """Install the HIP forward on bitsandbytes.nn.Linear4bit (solution/linear4bit.py:151-182)
+    when bitsandbytes is importable; returns whether it did."""
     global cache_fp16
     cache_fp16 = cache_weights
     try:
-        import bitsandbytes as bnb  # noqa: F401
+        import bitsandbytes as bnb
     except Exception:
         return False
-    return False
+    cls = bnb.nn.Linear4bit
+    if getattr(cls, "_mindx_direct", False):
+        return True
+    original = cls.forward
+
+    def forward(self, x):
+        return hip_forward(self, x, original)
+
+    cls.forward = forward
+    cls._mindx_direct = True
+    return True

@@ -1,0 +1,219 @@
+"""Fused NF4 GEMMs and the LoRA branch on the GPU against the CPU oracle.
+
+Bar (north star): GEMM outputs within max relative error 1e-2 (max|got - ref| / max|ref|, the
+measure of solution/test_attention.py:91-92) of dequant-then-matmul; the in-GEMM decode itself
+is checked bit for bit against the standalone dequant through one-hot inputs.  Shapes follow
+solution/test_linear4bit.py:37-59 (out_features x tokens) and BASELINE configs 3-4.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+
+
+def _layer(dev, n, k, seed, bias=False):
+    from mindxsoup_amd.linear4bit import Linear4bit
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    w = (torch.randn((n, k), device=dev, generator=g) * 0.02).half()
+    b = (torch.randn((n,), device=dev, generator=g) * 0.1).half() if bias else None
+    return Linear4bit.from_weight(w, b)
+
+
+def _w_oracle(layer):
+    """The exact fp16 W the oracle decodes from the layer's packed bytes."""
+    st = layer.weight.quant_state
+    q = O.NF4Weight(st.shape, layer.weight.data.view(-1).cpu().numpy(), st.absmax.cpu().numpy(),
+                    st.state2.code.cpu().numpy(), st.state2.absmax.cpu().numpy(),
+                    float(st.offset.item()))
+    return O.dequant(q)
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+@pytest.mark.parametrize("n,k", [(256, 1536), (1536, 1536), (192, 128)])
+@pytest.mark.parametrize("cfg,splits", [(-1, 1), (0, 1), (1, 2), (2, 1), (4, 3)])
+def test_in_gemm_decode_is_bit_exact(cuda, n, k, cfg, splits):
+    """One-hot rows: X = I gives Y = W^T and dY = I gives dX = W, each output a single exact
+    product, so the fused kernels must reproduce the standalone dequant bit for bit (also with
+    split-K, where the other splits add exact zeros)."""
+    from mindxsoup_amd import kernels
+    from mindxsoup_amd.linear4bit import _unpack
+
+    print(f"case decode n={n} k={k} cfg={cfg} splits={splits}", flush=True)
+    layer = _layer(cuda, n, k, 0)
+    st = layer.weight.quant_state
+    packed = layer.weight.data.view(-1, 1)
+    w = _unpack(packed, st, torch.float16)
+    eye_k = torch.eye(k, dtype=torch.float16, device=cuda)
+    y = kernels.nf4_linear_fwd(eye_k, packed, st, cfg=cfg, splits=splits)
+    assert torch.equal(y.view(torch.int16), w.t().contiguous().view(torch.int16))
+    eye_n = torch.eye(n, dtype=torch.float16, device=cuda)
+    dx = kernels.nf4_linear_bwd_dx(eye_n, packed, st, cfg=cfg, splits=splits)
+    assert torch.equal(dx.view(torch.int16), w.view(torch.int16))
+
+
+@pytest.mark.parametrize("out_features,bias", [(1536, True), (256, True), (8960, False),
+                                               (1536, False)])
+@pytest.mark.parametrize("tokens", [37, 300, 700, 1203, 2048])
+def test_linear4bit_fwd_bwd_matches_oracle(cuda, out_features, bias, tokens):
+    """solution/test_linear4bit.py:37-59 shapes: Y = x W^T + b and grad_x = grad W through the
+    module and autograd, against float64 dequant-then-matmul."""
+    print(f"case linear out={out_features} bias={bias} tokens={tokens}", flush=True)
+    layer = _layer(cuda, out_features, 1536, 1, bias)
+    torch.manual_seed(2)
+    x = torch.randn(1, tokens, 1536, device=cuda, dtype=torch.float16, requires_grad=True)
+    y = layer(x)
+    g = torch.randn_like(y)
+    y.backward(g)
+    w = _w_oracle(layer)
+    xb = _np(x)[0].astype(np.float16)
+    ref_y = O.linear_fwd(xb, w, None if not bias else _np(layer.bias))
+    ref_dx = O.linear_bwd_dx(_np(g)[0].astype(np.float16), w)
+    ey, edx = O.max_rel(_np(y)[0], ref_y), O.max_rel(_np(x.grad)[0], ref_dx)
+    print(f"  max_rel y={ey:.2e} dx={edx:.2e}", flush=True)
+    assert y.shape == (1, tokens, out_features) and y.dtype == torch.float16
+    assert ey < TOL and edx < TOL
+
+
+@pytest.mark.parametrize("cfg,splits", [(0, 1), (0, 4), (1, 1), (1, 3), (2, 2), (4, 1)])
+def test_tile_configs_agree_with_oracle(cuda, cfg, splits):
+    from mindxsoup_amd import kernels
+
+    print(f"case tiles cfg={cfg} splits={splits}", flush=True)
+    layer = _layer(cuda, 1536, 1536, 3, bias=True)
+    st = layer.weight.quant_state
+    packed = layer.weight.data.view(-1, 1)
+    torch.manual_seed(4)
+    x = torch.randn(300, 1536, device=cuda, dtype=torch.float16)
+    dy = torch.randn(300, 1536, device=cuda, dtype=torch.float16)
+    y = kernels.nf4_linear_fwd(x, packed, st, layer.bias, cfg=cfg, splits=splits)
+    dx = kernels.nf4_linear_bwd_dx(dy, packed, st, cfg=cfg, splits=splits)
+    w = _w_oracle(layer)
+    assert O.max_rel(_np(y), O.linear_fwd(_np(x).astype(np.float16), w, _np(layer.bias))) < TOL
+    assert O.max_rel(_np(dx), O.linear_bwd_dx(_np(dy).astype(np.float16), w)) < TOL
+
+
+def _lora_inputs(dev, M, K, N, seed, x_kind="normal", dy_std=1.0):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    if x_kind == "silu_mul":  # saved activations silu(g) * u
+        gg = torch.randn((M, K), device=dev, generator=g)
+        uu = torch.randn((M, K), device=dev, generator=g)
+        x = (torch.nn.functional.silu(gg) * uu).half()
+    else:
+        x = torch.randn((M, K), device=dev, generator=g).half()
+    bound = 1.0 / np.sqrt(K)  # kaiming_uniform(a=sqrt(5)) bound for fan_in K
+    a = ((torch.rand((16, K), device=dev, generator=g) * 2 - 1) * bound).half()
+    b = (torch.randn((N, 16), device=dev, generator=g) * 0.01).half()
+    dy = (torch.randn((M, N), device=dev, generator=g) * dy_std).half()
+    keep = (torch.rand((M, K), device=dev, generator=g) >= 0.05).to(torch.uint8)
+    return x, a, b, dy, keep
+
+
+@pytest.mark.parametrize("name,n,k,m,x_kind,dy_std", [
+    ("gate_proj (BASELINE config 3)", 8960, 1536, 1024, "normal", 1.0),
+    ("down_proj (BASELINE config 4)", 1536, 8960, 1024, "silu_mul", 1e-3),
+    ("k_proj ragged tokens", 256, 1536, 37, "normal", 1.0),
+])
+def test_fused_lora_fwd_bwd_matches_oracle(cuda, name, n, k, m, x_kind, dy_std):
+    """peft LoRA (r=16, alpha=32, dropout 0.05 with an explicit mask) around the NF4 base:
+    Y, dX, dA, dB against the float64 oracle (itself pinned against torch autograd)."""
+    from mindxsoup_amd.linear4bit import NF4LoraFunction
+
+    print(f"case lora {name} m={m}", flush=True)
+    layer = _layer(cuda, n, k, 5)
+    st = layer.weight.quant_state
+    packed = layer.weight.data.view(-1, 1)
+    x, a, b, dy, keep = _lora_inputs(cuda, m, k, n, 6, x_kind, dy_std)
+    p, s = 0.05, 2.0
+    a_p = a.float().requires_grad_(True)  # fp32 LoRA params, as peft keeps them
+    b_p = b.float().requires_grad_(True)
+    xg = x.clone().requires_grad_(True)
+    y = NF4LoraFunction.apply(xg, a_p, b_p, packed, st, None, keep, 1.0 / (1.0 - p), s)
+    y.backward(dy)
+    w = _w_oracle(layer)
+    xn, an, bn, dyn, kn = (_np(x).astype(np.float16), _np(a).astype(np.float16),
+                           _np(b).astype(np.float16), _np(dy).astype(np.float16),
+                           keep.cpu().numpy())
+    ref_y = O.lora_fwd(xn, w, an, bn, s, kn, p)
+    ref_dx, ref_da, ref_db = O.lora_bwd(dyn, xn, w, an, bn, s, kn, p)
+    errs = dict(y=O.max_rel(_np(y), ref_y), dx=O.max_rel(_np(xg.grad), ref_dx),
+                da=O.max_rel(_np(a_p.grad), ref_da), db=O.max_rel(_np(b_p.grad), ref_db))
+    print("  max_rel " + " ".join(f"{k_}={v:.2e}" for k_, v in errs.items()), flush=True)
+    assert all(v < TOL for v in errs.values()), errs
+    # the LoRA branch matters at this scale: dropping it moves Y beyond the tolerance's reach
+    assert O.max_rel(ref_y, O.linear_fwd(xn, w)) > 1e-4
+
+
+def test_lora_kernels_match_oracle(cuda):
+    from mindxsoup_amd import kernels
+
+    M, K, N = 300, 1536, 256
+    x, a, b, dy, keep = _lora_inputs(cuda, M, K, N, 7)
+    s, p = 2.0, 0.05
+    h, ht = kernels.lora_h(x, a, s, keep, 1 / (1 - p))
+    dh, dht = kernels.lora_dh(dy, b, s)
+    da = kernels.lora_grad_a(dht, x, keep, 1 / (1 - p))
+    db = kernels.lora_grad_b(ht, dy)
+    xn, an, bn, dyn, kn = (_np(x).astype(np.float16), _np(a).astype(np.float16),
+                           _np(b).astype(np.float16), _np(dy).astype(np.float16),
+                           keep.cpu().numpy())
+    ref_h = s * O.lora_h(xn, an, kn, p)
+    assert O.max_rel(_np(h), ref_h) < TOL
+    assert torch.equal(ht[:, :M].t(), h) and torch.all(ht[:, M:] == 0)
+    ref_dh = s * (dyn.astype(np.float64) @ bn.astype(np.float64))
+    assert O.max_rel(_np(dh), ref_dh) < TOL
+    xd = O.dropout_fp16(xn, kn, p).astype(np.float64)
+    assert O.max_rel(_np(da), _np(dh).astype(np.float64).T @ xd) < TOL
+    assert O.max_rel(_np(db), dyn.astype(np.float64).T @ _np(h).astype(np.float64)) < TOL
+
+
+def test_lora_module_forward_backward(cuda):
+    """LoraLinear4bit (peft layout) in training mode with a given mask equals the oracle; in
+    eval mode (no dropout) it equals the merged-weight product x (W + s B A)^T."""
+    from mindxsoup_amd.linear4bit import LoraLinear4bit
+
+    base = _layer(cuda, 1536, 1536, 8, bias=True)
+    mod = LoraLinear4bit(base, r=16, lora_alpha=32, lora_dropout=0.05)
+    torch.nn.init.normal_(mod.lora_B["default"].weight, std=0.02)
+    torch.manual_seed(9)
+    x = torch.randn(2, 150, 1536, device=cuda, dtype=torch.float16)
+    mod.eval()
+    y = mod(x)
+    w = _w_oracle(base).astype(np.float64)
+    a = _np(mod.lora_A["default"].weight).astype(np.float16).astype(np.float64)
+    b = _np(mod.lora_B["default"].weight).astype(np.float16).astype(np.float64)
+    merged = w + 2.0 * b @ a
+    ref = _np(x).reshape(-1, 1536).astype(np.float64) @ merged.T + _np(base.bias)
+    assert O.max_rel(_np(y).reshape(-1, 1536), ref) < TOL
+    mod.train()
+    keep = (torch.rand(300, 1536, device=cuda) >= 0.05).to(torch.uint8)
+    mod.next_keep = keep
+    xg = x.clone().requires_grad_(True)
+    y = mod(xg)
+    y.sum().backward()
+    assert mod.lora_A["default"].weight.grad is not None
+    assert mod.lora_B["default"].weight.grad.shape == (1536, 16)
+    assert xg.grad.shape == x.shape
+
+
+def test_empty_tokens(cuda):
+    from mindxsoup_amd import kernels
+
+    layer = _layer(cuda, 256, 1536, 10)
+    st = layer.weight.quant_state
+    packed = layer.weight.data.view(-1, 1)
+    x = torch.empty(0, 1536, device=cuda, dtype=torch.float16)
+    assert kernels.nf4_linear_fwd(x, packed, st).shape == (0, 256)
+    dy = torch.empty(0, 256, device=cuda, dtype=torch.float16)
+    assert kernels.nf4_linear_bwd_dx(dy, packed, st).shape == (0, 1536)
