@@ -9,9 +9,11 @@ at blocksize 64 with double-quantized absmax, decoded to fp16 by one launch over
 one launch; `value` is GB/s over the algorithmic bytes: packed + absmax8 + absmax2 + fp16 out =
 3 296 280 960 B per step.  Inputs are resident in HBM before timing.
 
-Also reported (not the headline): the fused NF4+LoRA projection stack when
-the fused kernels are built, and the CPU baseline (the C restatement of the reference's decode,
-OpenMP, timed on this host).  Prints ONE JSON line.
+Also reported under "fused_stack" (not the headline): the fused NF4+LoRA projections of BASELINE
+configs[2] (gate+up forward), configs[3] (down_proj backward) and configs[4] (all 196
+projections forward + backward at M = 1024, captured as one HIP graph per step), in TFLOP/s
+against the dense fp16 MFMA peak; and CPU baselines timed on this host (the oracle's C decode
+with OpenMP; for the GEMMs, one layer with torch CPU fp32 GEMMs).  Prints ONE JSON line.
 """
 
 import argparse
@@ -132,12 +134,212 @@ def cpu_baseline_dequant(m, budget_s=20.0):
                        f"torch threads {torch.get_num_threads()}")
 
 
+# ---------------------------------------------------------------------------------------------
+# Fused NF4 + LoRA projections (BASELINE configs[2..4])
+# ---------------------------------------------------------------------------------------------
+M_TOKENS, RANK, ALPHA, P_DROP = 1024, 16, 32, 0.05
+MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, MI355X spec
+
+
+def proj_flops(n, k, m=M_TOKENS, r=RANK, fwd=True, bwd=True):
+    """Algorithmic FLOPs of one NF4+LoRA projection: base 2MNK per direction; LoRA forward
+    2Mr(K+N) (H and its product with B), backward 4Mr(K+N) (dH, dX_lora, dA, dB)."""
+    f = 0
+    if fwd:
+        f += 2 * m * n * k + 2 * m * r * (k + n)
+    if bwd:
+        f += 2 * m * n * k + 4 * m * r * (k + n)
+    return f
+
+
+def make_proj(dev, g, n, k, x=None, x_kind="normal", dy_std=1.0):
+    """One projection's synthetic inputs: NF4 weight N(0,0.02), LoRA A Kaiming-uniform, B
+    N(0,0.01), fp16; X [M,K] ~ N(0,1) (or silu(g)*u), dY ~ N(0, dy_std); keep mask Bernoulli(0.95)."""
+    from mindxsoup_amd.quant import quantize_4bit
+
+    w = (torch.randn((n, k), device=dev, generator=g) * 0.02).half()
+    packed, st = quantize_4bit(w)
+    st.absmax_f32 = None
+    del w
+    if x is None:
+        if x_kind == "silu_mul":
+            a_ = torch.randn((M_TOKENS, k), device=dev, generator=g)
+            b_ = torch.randn((M_TOKENS, k), device=dev, generator=g)
+            x = (torch.nn.functional.silu(a_) * b_).half()
+        else:
+            x = torch.randn((M_TOKENS, k), device=dev, generator=g).half()
+    bound = 1.0 / np.sqrt(k)
+    la = ((torch.rand((RANK, k), device=dev, generator=g) * 2 - 1) * bound).half()
+    lb = (torch.randn((n, RANK), device=dev, generator=g) * 0.01).half()
+    dy = (torch.randn((M_TOKENS, n), device=dev, generator=g) * dy_std).half()
+    keep = (torch.rand((M_TOKENS, k), device=dev, generator=g) >= P_DROP).to(torch.uint8)
+    return dict(packed=packed, st=st, x=x, a=la, b=lb, dy=dy, keep=keep, n=n, k=k)
+
+
+def proj_fwd(p, s=ALPHA / RANK):
+    from mindxsoup_amd import kernels
+
+    h, ht = kernels.lora_h(p["x"], p["a"], s, p["keep"], 1.0 / (1.0 - P_DROP))
+    y = kernels.nf4_linear_fwd(p["x"], p["packed"], p["st"], None, h, p["b"])
+    return y, ht
+
+
+def proj_bwd(p, ht, s=ALPHA / RANK):
+    from mindxsoup_amd import kernels
+
+    ms = 1.0 / (1.0 - P_DROP)
+    dh, dht = kernels.lora_dh(p["dy"], p["b"], s)
+    dx = kernels.nf4_linear_bwd_dx(p["dy"], p["packed"], p["st"], dh, p["a"], p["keep"], ms)
+    da = kernels.lora_grad_a(dht, p["x"], p["keep"], ms)
+    db = kernels.lora_grad_b(ht, p["dy"])
+    return dx, da, db
+
+
+def graph_time(fn, steps, warmup):
+    """Capture fn() in a HIP graph, replay: mean ms per replay (events on the capture stream's
+    replay stream) and the wall-clock mean."""
+    fn()  # eager warm-up (first launches set kernel attributes)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps * 1e3
+    return a.elapsed_time(b) / steps, wall
+
+
+def bench_fused(dev, steps, warmup):
+    g = torch.Generator(device=dev)
+    g.manual_seed(1)
+    out = {}
+    # config 3: forward of gate_proj and up_proj on one X [1024, 1536] (they share the input)
+    gate = make_proj(dev, g, 8960, 1536)
+    up = make_proj(dev, g, 8960, 1536, x=gate["x"])
+    ms, _ = graph_time(lambda: (proj_fwd(gate), proj_fwd(up)), steps, warmup)
+    fl = 2 * proj_flops(8960, 1536, bwd=False)
+    out["config3_fwd_gate_up"] = {"ms": round(ms, 4), "gflop": round(fl / 1e9, 3),
+                                  "tflops": round(fl / ms / 1e9, 1)}
+    # the dominant kernel alone: the fused forward GEMM with its LoRA epilogue (gate, up)
+    from mindxsoup_amd import kernels
+    hg, _ = kernels.lora_h(gate["x"], gate["a"], 2.0, gate["keep"], 1 / (1 - P_DROP))
+    hu, _ = kernels.lora_h(up["x"], up["a"], 2.0, up["keep"], 1 / (1 - P_DROP))
+    ms_k, _ = graph_time(lambda: (kernels.nf4_linear_fwd(gate["x"], gate["packed"], gate["st"],
+                                                         None, hg, gate["b"]),
+                                  kernels.nf4_linear_fwd(up["x"], up["packed"], up["st"], None,
+                                                         hu, up["b"])), steps, warmup)
+    fl_k = 2 * (2 * M_TOKENS * 8960 * 1536 + 2 * M_TOKENS * RANK * 8960)
+    out["gemm_fwd_kernel"] = {"ms_per_launch": round(ms_k / 2, 4),
+                              "tflops": round(fl_k / ms_k / 1e9, 1)}
+    del gate, up, hg, hu
+    # config 4: backward through down_proj (X = silu(g) * u saved, dY ~ N(0, 1e-3))
+    down = make_proj(dev, g, 1536, 8960, x_kind="silu_mul", dy_std=1e-3)
+    _, ht = proj_fwd(down)
+    ms, _ = graph_time(lambda: proj_bwd(down, ht), steps, warmup)
+    fl = proj_flops(1536, 8960, fwd=False)
+    out["config4_bwd_down"] = {"ms": round(ms, 4), "gflop": round(fl / 1e9, 3),
+                               "tflops": round(fl / ms / 1e9, 1)}
+    del down, ht
+    # config 5: forward + backward of all 28 layers x 7 projections, M = 1024
+    layers = []
+    for _ in range(LAYERS):
+        x_attn = torch.randn((M_TOKENS, 1536), device=dev, generator=g).half()
+        x_mlp = torch.randn((M_TOKENS, 1536), device=dev, generator=g).half()
+        projs = []
+        for name, n, k in PROJ:
+            x = x_attn if name in ("q", "k", "v") else x_mlp if name in ("gate", "up") else None
+            projs.append(make_proj(dev, g, n, k, x=x))
+        layers.append(projs)
+    torch.cuda.synchronize()
+    print("bench: projection stack inputs resident", file=sys.stderr, flush=True)
+
+    def step():
+        saved = []
+        for projs in layers:
+            saved.append([proj_fwd(p)[1] for p in projs])
+        for projs, hts in zip(reversed(layers), reversed(saved)):
+            for p, ht in zip(reversed(projs), reversed(hts)):
+                proj_bwd(p, ht)
+
+    ms, wall = graph_time(step, max(3, steps // 5), max(2, warmup // 5))
+    fl = LAYERS * sum(proj_flops(n, k) for _, n, k in PROJ)
+    tf = fl / ms / 1e9
+    out["config5_stack"] = {"ms_per_step": round(ms, 4), "wall_ms_per_step": round(wall, 4),
+                            "tflop_per_step": round(fl / 1e12, 4), "tflops": round(tf, 1),
+                            "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4),
+                            "launches": "one HIP graph per step"}
+    del layers
+    return out
+
+
+def cpu_baseline_layer(dev):
+    """One layer's 7 NF4+LoRA projections forward + backward on the host: the oracle's C decode,
+    then torch CPU fp32 GEMMs (x28 extrapolated to the step, labelled as such)."""
+    from oracle import oracle as O
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    O.set_num_threads(cores)
+    g = torch.Generator(device=dev)
+    g.manual_seed(3)
+    projs = [make_proj(dev, g, n, k) for _, n, k in PROJ]
+    host = []
+    for p in projs:
+        st = p["st"]
+        host.append(dict(
+            packed=p["packed"].view(-1).cpu().numpy(), absmax8=st.absmax.cpu().numpy(),
+            code=st.state2.code.cpu().numpy(), absmax2=st.state2.absmax.cpu().numpy(),
+            offset=float(st.offset.item()), shape=st.shape,
+            x=p["x"].float().cpu(), a=p["a"].float().cpu(), b=p["b"].float().cpu(),
+            dy=p["dy"].float().cpu(), keep=p["keep"].cpu().bool()))
+    del projs
+
+    def layer_pass():
+        for h in host:
+            w = torch.from_numpy(O.dequant(packed=h["packed"], absmax8=h["absmax8"],
+                                           code=h["code"], absmax2=h["absmax2"],
+                                           offset=h["offset"], shape=h["shape"])
+                                 .astype(np.float32))
+            xd = torch.where(h["keep"], h["x"] * (1 / (1 - P_DROP)), 0.0)
+            hh = xd @ h["a"].T * 2.0
+            _ = h["x"] @ w.T + hh @ h["b"].T
+            dh = h["dy"] @ h["b"] * 2.0
+            _ = h["dy"] @ w + torch.where(h["keep"], (dh @ h["a"]) * (1 / (1 - P_DROP)), 0.0)
+            _ = dh.T @ xd
+            _ = h["dy"].T @ hh
+
+    layer_pass()
+    times = []
+    start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - start < 10 and len(times) < 10):
+        t = time.perf_counter()
+        layer_pass()
+        times.append(time.perf_counter() - t)
+    sec = float(np.median(times))
+    fl = sum(proj_flops(n, k) for _, n, k in PROJ)
+    return {"value": round(fl / sec / 1e12, 4), "unit": "TFLOP/s", "cores": cores,
+            "kind": "port",
+            "sample": f"one layer (7 projections) fwd+bwd, M=1024: oracle decode + torch CPU fp32 "
+                      f"GEMMs, median {sec * 1e3:.1f} ms/layer; x28 extrapolated step "
+                      f"{sec * LAYERS * 1e3:.0f} ms"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-gemm", action="store_true", help="dequant only")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the hot path is "
@@ -152,6 +354,10 @@ def main():
           file=sys.stderr, flush=True)
     ms_step, ms_kernel, _ = bench_dequant(m, args.steps, args.warmup)
     print(f"bench: dequant timed, {ms_step:.4f} ms/step", file=sys.stderr, flush=True)
+    cpu_baseline_dequant_cached = None
+    if not args.no_cpu:
+        print("bench: CPU baseline (oracle decode)", file=sys.stderr, flush=True)
+        cpu_baseline_dequant_cached = cpu_baseline_dequant(m)
     nbytes = dequant_bytes(m)
     value = nbytes / (ms_step / 1e3) / 1e9
     achieved = nbytes / (ms_kernel / 1e3) / 1e9
@@ -169,9 +375,24 @@ def main():
                      "kernel": "k_dequant_wide<nested, multi, f16>",
                      "kernel_ms": round(ms_kernel, 4)},
     }
+    del m
+    torch.cuda.empty_cache()
+    if not args.no_gemm:
+        print("bench: fused NF4+LoRA projections", file=sys.stderr, flush=True)
+        fused = bench_fused(dev, args.steps, args.warmup)
+        st = fused["config5_stack"]
+        fused["roofline"] = {"bound": "mfma", "achieved": fused["gemm_fwd_kernel"]["tflops"],
+                             "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                             "frac": round(fused["gemm_fwd_kernel"]["tflops"] / MFMA_PEAK_TFLOPS, 4),
+                             "kernel": "k_nf4_gemm forward (gate/up, LoRA epilogue)"}
+        result["fused_stack"] = fused
+        print(f"bench: stack {st['ms_per_step']} ms/step, {st['tflops']} TFLOP/s",
+              file=sys.stderr, flush=True)
     if not args.no_cpu:
-        print("bench: CPU baseline (oracle decode)", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline_dequant(m)
+        result["cpu_baseline"] = cpu_baseline_dequant_cached
+        if not args.no_gemm:
+            print("bench: CPU baseline (one layer of projections)", file=sys.stderr, flush=True)
+            result["fused_stack"]["cpu_baseline"] = cpu_baseline_layer(dev)
     print(json.dumps(result), flush=True)
 
 

@@ -22,7 +22,6 @@
 namespace mxs {
 
 constexpr int kBK = 64;           // reduction indices per K-step (one NF4 block in forward)
-constexpr int kThreads = 256;     // 4 waves
 
 struct GemmArgs {
   const _Float16* A;        // [M, lda]
@@ -52,33 +51,306 @@ __device__ __forceinline__ int lds_off(int row, int seg) {
   return row * kBK + (((seg ^ row ^ (row >> 3)) & 7) << 3);
 }
 
-__device__ __forceinline__ float block_scale_at(const GemmArgs& a, int64_t blk) {
-  return nested_scale(a.code[a.absmax8[blk]], a.absmax2[blk >> 8], a.offset[0]);
-}
-
-template <int BM, int BN, int WAVES_M, bool BWD>
+template <int BM, int BN, int WAVES_M, int WAVES_N_, bool BWD>
 struct Tile {
-  static constexpr int WAVES_N = 4 / WAVES_M;
+  static constexpr int WAVES_N = WAVES_N_;
+  static constexpr int NT = 64 * WAVES_M * WAVES_N;  // threads per workgroup
   static constexpr int WM = BM / WAVES_M;
   static constexpr int WN = BN / WAVES_N;
   static constexpr int TM = WM / 32;               // 32x32 MFMA tiles per wave along M
   static constexpr int TN = WN / 32;
-  static constexpr int A_ITEMS = BM * 8 / kThreads;  // 16-byte A segments per thread
-  // forward B items: (row, half) = 32 NF4 values; backward: 4 W rows x 8 cols
-  static constexpr int B_ITEMS = BWD ? (BN / 8) * (kBK / 4) / kThreads : BN * 2 / kThreads;
+  static constexpr int A_ITEMS = BM * 8 / NT;      // 16-byte A segments per thread
+  // B work items: forward (row, half) = 32 NF4 values; backward 4 W rows x 8 cols.  Handed to
+  // threads 0..B_TOTAL-1 (B_TOTAL a multiple of 64, so whole waves take or skip them).
+  static constexpr int B_TOTAL = BWD ? (BN / 8) * (kBK / 4) : BN * 2;
+  static constexpr int B_ITEMS = (B_TOTAL + NT - 1) / NT;
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile");
-  static_assert(A_ITEMS >= 1 && B_ITEMS >= 1, "tile too small for 256 threads");
+  static_assert(A_ITEMS >= 1 && BM * 8 % NT == 0, "A tile vs threads");
+  static_assert(B_TOTAL % 64 == 0, "B items in whole waves");
   static constexpr int LDS_A = BM * kBK;            // halfs per buffer
   static constexpr int LDS_B = BN * kBK;
 };
 
-template <int BM, int BN, int WAVES_M, bool BWD>
-__global__ __launch_bounds__(kThreads, 1) void k_nf4_gemm(GemmArgs a) {
-  using T = Tile<BM, BN, WAVES_M, BWD>;
+// Epilogue of one wave's TM x TN tiles of 32x32 at output rows mb.., columns nb...  The MFMAs
+// take the W fragment as their first operand, so each tile is held transposed: lane l keeps row
+// m = mb + 32i + l%32 and, in register group g (4 registers), the 4 consecutive columns
+// n = nb + 32j + 8g + 4(l/32) .. +3 -> one 8-byte fp16 store (or 16-byte fp32 partial) per group.
+// Adds the LoRA term (one more MFMA per tile per 16 ranks, masked by the dropout keep mask in the
+// backward pass) and the bias; split-K partials go to the workspace instead.
+template <int TM, int TN, bool BWD>
+__device__ __forceinline__ void epilogue(const GemmArgs& a, float16_t (&acc)[TM][TN], int mb,
+                                         int nb, int lrow, int lseg) {
+  const bool first_split = blockIdx.z == 0;
+  const bool split = gridDim.z > 1;
+  const bool vec = (a.Nc % 4) == 0 && (a.ldc % 4) == 0;
+  if (a.lora_h && first_split) {
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const int m = mb + i * 32 + lrow;
+#pragma unroll
+      for (int j = 0; j < TN; j++) {
+        float16_t lacc = {};
+        const int ncol = nb + j * 32 + lrow;  // column this lane feeds as the W-side operand
+        for (int r0 = 0; r0 < a.r; r0 += 16) {
+          half8_t hf = {}, wf = {};
+          if (m < a.M) hf = *reinterpret_cast<const half8_t*>(a.lora_h + (int64_t)m * a.r + r0 + 8 * lseg);
+          if (ncol < a.Nc) {
+            if (!BWD) {
+              wf = *reinterpret_cast<const half8_t*>(a.lora_w + (int64_t)ncol * a.r + r0 + 8 * lseg);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; e++) wf[e] = a.lora_w[(int64_t)(r0 + 8 * lseg + e) * a.Nc + ncol];
+            }
+          }
+          lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, hf, lacc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int n = nb + j * 32 + 8 * g + 4 * lseg;
+          uint32_t keep = 0x01010101u;
+          if (BWD && a.mask) {
+            keep = 0;
+            if (m < a.M) {
+              if (vec && n + 3 < a.Nc) {
+                keep = *reinterpret_cast<const uint32_t*>(a.mask + (int64_t)m * a.Nc + n);
+              } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                  if (n + e < a.Nc) keep |= (uint32_t)a.mask[(int64_t)m * a.Nc + n + e] << (8 * e);
+              }
+            }
+          }
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            float l = lacc[4 * g + e];
+            if (BWD && a.mask) l = ((keep >> (8 * e)) & 0xffu) ? l * a.mask_scale : 0.0f;
+            acc[i][j][4 * g + e] += l;
+          }
+        }
+      }
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+    const int m = mb + i * 32 + lrow;
+    if (m >= a.M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int n = nb + j * 32 + 8 * g + 4 * lseg;
+        if (n >= a.Nc) continue;
+        float4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                      acc[i][j][4 * g + 3]};
+        const bool full = vec && n + 3 < a.Nc;
+        if (a.bias && first_split) {
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[e] += (n + e < a.Nc) ? (float)a.bias[n + e] : 0.0f;
+        }
+        if (split) {
+          float* w = a.ws + ((int64_t)blockIdx.z * a.M + m) * a.Nc + n;
+          if (full) {
+            *reinterpret_cast<float4_t*>(w) = v;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              if (n + e < a.Nc) w[e] = v[e];
+          }
+        } else {
+          _Float16* c = a.C + (int64_t)m * a.ldc + n;
+          if (full) {
+            *reinterpret_cast<half4_t*>(c) = __builtin_convertvector(v, half4_t);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+              if (n + e < a.Nc) c[e] = (_Float16)v[e];
+          }
+        }
+      }
+    }
+  }
+}
+
+// Global -> register staging and register -> LDS commit of one K-step's tiles, for NTP
+// loading threads (thread index p in [0, NTP)).
+//   A: BM rows x 64 fp16 (16-byte segments; rows past M clamped to the last row).
+//   B forward:  item (row n, half) = 32 NF4 values of W row n, one block scale.
+//   B backward: item (row group of 4 W rows, chunk of 8 output columns) = 32 values, 4 scales;
+//               decoded along W's rows so LDS holds B[n'][k'] with the reduction contiguous.
+// Columns past Nc are clamped to the last valid ones: they only reach outputs never stored.
+template <int BM, int BN, bool BWD, int NTP>
+struct Loader {
+  static constexpr int A_ITEMS = BM * 8 / NTP;
+  static constexpr int B_TOTAL = BWD ? (BN / 8) * (kBK / 4) : BN * 2;
+  static constexpr int B_ITEMS = (B_TOTAL + NTP - 1) / NTP;
+  static constexpr int NS = BWD ? 4 : 1;
+  static_assert(BM * 8 % NTP == 0 && A_ITEMS >= 1, "A tile vs loading threads");
+  static_assert(B_TOTAL % 64 == 0, "B items in whole waves");
+
+  struct Stage {
+    u32x4 a[A_ITEMS];
+    uint32_t w[B_ITEMS][4];
+    uint32_t q8[B_ITEMS][NS];
+    float a2[B_ITEMS][NS];
+  };
+
+  __device__ static __forceinline__ void issue(const GemmArgs& a, Stage& S, int p, int kt, int m0,
+                                               int n0) {
+    const int k0 = kt * kBK;
+#pragma unroll
+    for (int u = 0; u < B_ITEMS; u++) {
+      const int q = p + u * NTP;
+      if (q >= B_TOTAL) break;
+      if (!BWD) {
+        const int n = min(n0 + (q >> 1), a.Nc - 1);
+        const int64_t blk = ((int64_t)n * a.Kw + k0) >> 6;
+        S.q8[u][0] = a.absmax8[blk];
+        S.a2[u][0] = a.absmax2[blk >> 8];
+        const u32x4 w = *reinterpret_cast<const u32x4*>(
+            a.packed + (int64_t)n * (a.Kw / 2) + k0 / 2 + (q & 1) * 16);
+#pragma unroll
+        for (int j = 0; j < 4; j++) S.w[u][j] = w[j];
+      } else {
+        const int chunk = q % (BN / 8);
+        const int rg = q / (BN / 8);
+        const int col = min(n0 + chunk * 8, a.Nc - 8);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int64_t idx = (int64_t)(k0 + rg * 4 + i) * a.Kw + col;
+          S.q8[u][i] = a.absmax8[idx >> 6];
+          S.a2[u][i] = a.absmax2[idx >> 14];
+          S.w[u][i] = *reinterpret_cast<const uint32_t*>(a.packed + (idx >> 1));
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < A_ITEMS; u++) {
+      const int q = p + u * NTP;
+      const int m = min(m0 + (q >> 3), a.M - 1);
+      S.a[u] = *reinterpret_cast<const u32x4*>(a.A + (int64_t)m * a.lda + k0 + (q & 7) * 8);
+    }
+  }
+
+  // Part `part` (0..3) of the commit: a quarter of the A segments and of the B decode.
+  __device__ static __forceinline__ void commit(const Stage& S, _Float16* as, _Float16* bs, int p,
+                                                int part, const float2_t* s_pair,
+                                                const float* s_code, float offset) {
+    constexpr int APP = (A_ITEMS + 3) / 4;
+#pragma unroll
+    for (int v = 0; v < APP; v++) {
+      const int u = part * APP + v;
+      if (u < A_ITEMS) {
+        const int q = p + u * NTP;
+        *reinterpret_cast<u32x4*>(as + lds_off(q >> 3, q & 7)) = S.a[u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < B_ITEMS; u++) {
+      const int q = p + u * NTP;
+      if (q >= B_TOTAL) break;
+      if (!BWD) {
+        // dword `part`: 8 values, one LDS pair lookup per byte
+        const int row = q >> 1, half = q & 1;
+        const float sc = nested_scale(s_code[S.q8[u][0]], S.a2[u][0], offset);
+        const uint32_t w = S.w[u][part];
+        u32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float2_t pr = s_pair[(w >> (8 * j)) & 0xffu];
+          v[j] = pack_f16x2(pr[0] * sc, pr[1] * sc);
+        }
+        *reinterpret_cast<u32x4*>(bs + lds_off(row, half * 4 + part)) = v;
+      } else {
+        // byte `part` of each of the 4 rows: output columns 2*part (high nibble) and 2*part+1
+        const int chunk = q % (BN / 8);
+        const int rg = q / (BN / 8);
+        float2_t pr[4];
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          sc[i] = nested_scale(s_code[S.q8[u][i]], S.a2[u][i], offset);
+          pr[i] = s_pair[(S.w[u][i] >> (8 * part)) & 0xffu];
+        }
+#pragma unroll
+        for (int cc = 0; cc < 2; cc++) {
+          u32x2 v;
+          v[0] = pack_f16x2(pr[0][cc] * sc[0], pr[1][cc] * sc[1]);
+          v[1] = pack_f16x2(pr[2][cc] * sc[2], pr[3][cc] * sc[3]);
+          const int row = chunk * 8 + part * 2 + cc;
+          *reinterpret_cast<u32x2*>(bs + lds_off(row, rg >> 1) + (rg & 1) * 4) = v;
+        }
+      }
+    }
+  }
+};
+
+// LDS tables both kernels use: the byte -> (NF4[hi], NF4[lo]) pair table and the code book.
+__device__ __forceinline__ void fill_tables(const GemmArgs& a, float2_t* s_pair, float* s_code,
+                                            int t, int nthreads) {
+  for (int i = t; i < 256; i += nthreads) {
+    s_code[i] = a.code[i];
+    s_pair[i] = (float2_t){kNF4[i >> 4], kNF4[i & 15]};
+  }
+}
+
+// One wave's 32x32x16 MFMAs over one 64-deep K-step held in LDS (A rows wm0.., B rows wn0..),
+// with the operand fragments of sub-step kk+1 read while sub-step kk multiplies.
+template <int TM, int TN>
+__device__ __forceinline__ void mma_kstep(float16_t (&acc)[TM][TN], const _Float16* as,
+                                          const _Float16* bs, int wm0, int wn0, int lrow,
+                                          int lseg) {
+  half8_t af[2][TM], bf[2][TN];
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+    af[0][i] = *reinterpret_cast<const half8_t*>(as + lds_off(wm0 + i * 32 + lrow, lseg));
+#pragma unroll
+  for (int j = 0; j < TN; j++)
+    bf[0][j] = *reinterpret_cast<const half8_t*>(bs + lds_off(wn0 + j * 32 + lrow, lseg));
+#pragma unroll
+  for (int kk = 0; kk < kBK / 16; kk++) {
+    const int cur = kk & 1;
+    if (kk + 1 < kBK / 16) {
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        af[cur ^ 1][i] = *reinterpret_cast<const half8_t*>(
+            as + lds_off(wm0 + i * 32 + lrow, 2 * (kk + 1) + lseg));
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+        bf[cur ^ 1][j] = *reinterpret_cast<const half8_t*>(
+            bs + lds_off(wn0 + j * 32 + lrow, 2 * (kk + 1) + lseg));
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[cur][j], af[cur][i], acc[i][j], 0,
+                                                           0, 0);
+  }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void zero_acc(float16_t (&acc)[TM][TN]) {
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+}
+
+// All waves load, decode and multiply: K-step kt+2 is loaded while kt multiplies and kt+1 is
+// committed to the other LDS buffer in four parts between the MFMA sub-steps.
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool BWD>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void k_nf4_gemm(GemmArgs a) {
+  using T = Tile<BM, BN, WAVES_M, WAVES_N, BWD>;
+  constexpr int NTH = T::NT;
+  using L = Loader<BM, BN, BWD, NTH>;
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
   _Float16* As = smem;                      // [2][BM][64]
   _Float16* Bs = smem + 2 * T::LDS_A;       // [2][BN][64]
-  __shared__ float s_nf4[16];
+  __shared__ float2_t s_pair[256];
+  __shared__ float s_code[256];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -90,208 +362,248 @@ __global__ __launch_bounds__(kThreads, 1) void k_nf4_gemm(GemmArgs a) {
   const int n_steps = a.Kr / kBK;
   const int kt0 = blockIdx.z * a.steps_per_split;
   const int kt1 = min(n_steps, kt0 + a.steps_per_split);
-  if (t < 16) s_nf4[t] = kNF4[t];
+  const int lrow = lane & 31;
+  const int lseg = lane >> 5;
+  fill_tables(a, s_pair, s_code, t, NTH);
+  const float offset = a.offset[0];
 
-  // ---- prefetch registers ----
-  u32x4 a_pf[T::A_ITEMS];
-  uint32_t b_pf[T::B_ITEMS][4];
-  float b_sc[T::B_ITEMS][BWD ? 4 : 1];
+  float16_t acc[T::TM][T::TN];
+  zero_acc(acc);
 
-  auto load_tile = [&](int kt) {
+  auto mma = [&](int buf, int kk) {
+    const _Float16* as = As + buf * T::LDS_A;
+    const _Float16* bs = Bs + buf * T::LDS_B;
+    half8_t af[T::TM], bf[T::TN];
+#pragma unroll
+    for (int i = 0; i < T::TM; i++)
+      af[i] = *reinterpret_cast<const half8_t*>(as + lds_off(wm0 + i * 32 + lrow, 2 * kk + lseg));
+#pragma unroll
+    for (int j = 0; j < T::TN; j++)
+      bf[j] = *reinterpret_cast<const half8_t*>(bs + lds_off(wn0 + j * 32 + lrow, 2 * kk + lseg));
+#pragma unroll
+    for (int i = 0; i < T::TM; i++)
+#pragma unroll
+      for (int j = 0; j < T::TN; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
+  };
+
+  // K-step kt multiplies while kt+1 is committed between the MFMA sub-steps; kt+2 is issued
+  // after the commit (unconditionally, clamped) so counter waits never cover fresh loads.
+  auto step = [&](int buf, int kt, const typename L::Stage& next, typename L::Stage& later) {
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; kk++) {
+      mma(buf, kk);
+      if (kt + 1 < kt1)
+        L::commit(next, As + (buf ^ 1) * T::LDS_A, Bs + (buf ^ 1) * T::LDS_B, t, kk, s_pair,
+                  s_code, offset);
+    }
+    L::issue(a, later, t, min(kt + 2, kt1 - 1), m0, n0);
+    __syncthreads();
+  };
+
+  if (kt0 < kt1) {
+    typename L::Stage S0, S1;
+    L::issue(a, S0, t, kt0, m0, n0);
+    L::issue(a, S1, t, min(kt0 + 1, kt1 - 1), m0, n0);
+    __syncthreads();  // tables
+#pragma unroll
+    for (int part = 0; part < 4; part++)
+      L::commit(S0, As, Bs, t, part, s_pair, s_code, offset);
+    __syncthreads();
+    // two K-steps per trip with a fixed register assignment for both stages; odd tail after
+    int kt = kt0;
+    for (; kt + 1 < kt1; kt += 2) {
+      step(0, kt, S1, S0);
+      step(1, kt + 1, S0, S1);
+    }
+    if (kt < kt1) step(0, kt, S1, S0);
+  }
+
+  epilogue<T::TM, T::TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
+}
+
+// NF4 side of a K-step for the warp-specialized kernel's 256 producer threads.
+//   forward:  item = one packed dword of W row n (8 values, one block scale): BN * 8 items
+//   backward: item = 4 W rows x 8 output columns (4 block scales), decoded along W's rows
+template <int BN, bool BWD>
+struct BLoad {
+  static constexpr int NTP = 256;
+  static constexpr int TOTAL = BWD ? (BN / 8) * (kBK / 4) : BN * 8;
+  static constexpr int ITEMS = (TOTAL + NTP - 1) / NTP;
+  static constexpr int NW = BWD ? 4 : 1;
+  static_assert(TOTAL % 64 == 0, "B items in whole waves");
+
+  struct Stage {
+    uint32_t w[ITEMS][NW];
+    uint32_t q8[ITEMS][NW];
+    float a2[ITEMS][NW];
+  };
+
+  __device__ static __forceinline__ void issue(const GemmArgs& a, Stage& S, int p, int kt,
+                                               int n0) {
     const int k0 = kt * kBK;
 #pragma unroll
-    for (int u = 0; u < T::A_ITEMS; u++) {
-      const int q = t + u * kThreads;
-      const int row = q >> 3, seg = q & 7;
-      const int m = m0 + row;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (m < a.M) v = *reinterpret_cast<const u32x4*>(a.A + (int64_t)m * a.lda + k0 + seg * 8);
-      a_pf[u] = v;
-    }
-#pragma unroll
-    for (int u = 0; u < T::B_ITEMS; u++) {
-      const int q = t + u * kThreads;
+    for (int u = 0; u < ITEMS; u++) {
+      const int q = p + u * NTP;
+      if (q >= TOTAL) break;
       if (!BWD) {
-        // W row n = n0 + q/2, values k0 + 32*(q&1) .. +32 (16 bytes, inside one NF4 block)
-        const int n = n0 + (q >> 1);
-        const int half = q & 1;
-        if (n < a.Nc) {
-          const int64_t byte = (int64_t)n * (a.Kw / 2) + k0 / 2 + half * 16;
-          const u32x4 w = *reinterpret_cast<const u32x4*>(a.packed + byte);
-#pragma unroll
-          for (int j = 0; j < 4; j++) b_pf[u][j] = w[j];
-          b_sc[u][0] = block_scale_at(a, ((int64_t)n * a.Kw + k0) >> 6);
-        } else {
-#pragma unroll
-          for (int j = 0; j < 4; j++) b_pf[u][j] = 0x77777777u;  // NF4 index 7 = 0.0
-          b_sc[u][0] = 0.0f;
-        }
+        const int n = min(n0 + (q >> 3), a.Nc - 1);
+        const int64_t blk = ((int64_t)n * a.Kw + k0) >> 6;
+        S.q8[u][0] = a.absmax8[blk];
+        S.a2[u][0] = a.absmax2[blk >> 8];
+        S.w[u][0] = *reinterpret_cast<const uint32_t*>(
+            a.packed + (int64_t)n * (a.Kw / 2) + k0 / 2 + (q & 7) * 4);
       } else {
-        // W rows k0 + 4*rg .. +4 (reduction), cols n0 + 8*chunk .. +8 (output)
         const int chunk = q % (BN / 8);
         const int rg = q / (BN / 8);
-        const int col = n0 + chunk * 8;
+        const int col = min(n0 + chunk * 8, a.Nc - 8);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const int wrow = k0 + rg * 4 + i;
-          if (col < a.Nc) {
-            const int64_t idx = (int64_t)wrow * a.Kw + col;
-            b_pf[u][i] = *reinterpret_cast<const uint32_t*>(a.packed + (idx >> 1));
-            b_sc[u][i] = block_scale_at(a, idx >> 6);
-          } else {
-            b_pf[u][i] = 0x77777777u;
-            b_sc[u][i] = 0.0f;
+          const int64_t idx = (int64_t)(k0 + rg * 4 + i) * a.Kw + col;
+          S.q8[u][i] = a.absmax8[idx >> 6];
+          S.a2[u][i] = a.absmax2[idx >> 14];
+          S.w[u][i] = *reinterpret_cast<const uint32_t*>(a.packed + (idx >> 1));
+        }
+      }
+    }
+  }
+
+  __device__ static __forceinline__ void commit(const Stage& S, _Float16* bs, int p,
+                                                const float2_t* s_pair, const float* s_code,
+                                                float offset) {
+#pragma unroll
+    for (int u = 0; u < ITEMS; u++) {
+      const int q = p + u * NTP;
+      if (q >= TOTAL) break;
+      if (!BWD) {
+        const float sc = nested_scale(s_code[S.q8[u][0]], S.a2[u][0], offset);
+        const uint32_t w = S.w[u][0];
+        u32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float2_t pr = s_pair[(w >> (8 * j)) & 0xffu];
+          v[j] = pack_f16x2(pr[0] * sc, pr[1] * sc);
+        }
+        *reinterpret_cast<u32x4*>(bs + lds_off(q >> 3, q & 7)) = v;
+      } else {
+        const int chunk = q % (BN / 8);
+        const int rg = q / (BN / 8);
+        float sc[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) sc[i] = nested_scale(s_code[S.q8[u][i]], S.a2[u][i], offset);
+#pragma unroll
+        for (int part = 0; part < 4; part++) {
+          float2_t pr[4];
+#pragma unroll
+          for (int i = 0; i < 4; i++) pr[i] = s_pair[(S.w[u][i] >> (8 * part)) & 0xffu];
+#pragma unroll
+          for (int cc = 0; cc < 2; cc++) {
+            u32x2 v;
+            v[0] = pack_f16x2(pr[0][cc] * sc[0], pr[1][cc] * sc[1]);
+            v[1] = pack_f16x2(pr[2][cc] * sc[2], pr[3][cc] * sc[3]);
+            const int row = chunk * 8 + part * 2 + cc;
+            *reinterpret_cast<u32x2*>(bs + lds_off(row, rg >> 1) + (rg & 1) * 4) = v;
           }
         }
       }
     }
-  };
+  }
+};
 
-  auto store_tile = [&](int buf) {
-    _Float16* as = As + buf * T::LDS_A;
-    _Float16* bs = Bs + buf * T::LDS_B;
+// Direct global -> LDS copy of one K-step's A tile (BM rows x 64 fp16) by the producer waves:
+// each global_load_lds_dwordx4 writes 8 rows (64 lanes x 16 B, consecutive in LDS); lane l takes
+// the logical segment that the row's XOR swizzle places at its physical slot.
+template <int BM>
+__device__ __forceinline__ void dma_a_tile(const GemmArgs& a, _Float16* as, int pw, int lane,
+                                           int kt, int m0) {
+  const int k0 = kt * kBK;
 #pragma unroll
-    for (int u = 0; u < T::A_ITEMS; u++) {
-      const int q = t + u * kThreads;
-      *reinterpret_cast<u32x4*>(as + lds_off(q >> 3, q & 7)) = a_pf[u];
+  for (int g = pw; g < BM / 8; g += 4) {
+    const int row = g * 8 + (lane >> 3);
+    const int seg = ((lane & 7) ^ row ^ (row >> 3)) & 7;
+    const int m = min(m0 + row, a.M - 1);
+    const _Float16* src = a.A + (int64_t)m * a.lda + k0 + seg * 8;
+    __builtin_amdgcn_global_load_lds(src, as + g * 8 * kBK, 16, 0, 0);
+  }
+}
+
+// vmcnt(0) (gfx9 s_waitcnt encoding: expcnt and lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Warp-specialized kernel: 4 consumer waves (one per SIMD, CWM x CWN over the BM x BN tile)
+// only read LDS fragments and issue MFMAs; 4 producer waves (the other wave of each SIMD) copy
+// the A tile of K-step kt+2 straight into a 3-deep LDS ring, and decode the NF4 of kt+1 into
+// the other half of a 2-deep B buffer while the consumers multiply kt.  Everything a producer
+// issues in one K-step is waited for at the start of the next, and one workgroup barrier per
+// K-step hands the buffers over.
+template <int BM, int BN, int CWM, int CWN, bool BWD>
+__global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
+  constexpr int WM = BM / CWM, WN = BN / CWN, TM = WM / 32, TN = WN / 32;
+  static_assert(CWM * CWN == 4 && WM % 32 == 0 && WN % 32 == 0, "consumer wave tiles");
+  using B = BLoad<BN, BWD>;
+  constexpr int LDS_A = BM * kBK, LDS_B = BN * kBK;
+  extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
+  _Float16* As = smem;                      // [3][BM][64]
+  _Float16* Bs = smem + 3 * LDS_A;          // [2][BN][64]
+  __shared__ float2_t s_pair[256];
+  __shared__ float s_code[256];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int m0 = blockIdx.y * BM;
+  const int n0 = blockIdx.x * BN;
+  const int n_steps = a.Kr / kBK;
+  const int kt0 = blockIdx.z * a.steps_per_split;
+  const int kt1 = min(n_steps, kt0 + a.steps_per_split);
+  fill_tables(a, s_pair, s_code, t, 512);
+
+  if (t >= 256) {
+    // ---- producers ----
+    if (kt0 >= kt1) return;
+    const int p = t - 256;
+    const int pw = p >> 6;
+    const float offset = a.offset[0];
+    typename B::Stage S;
+    B::issue(a, S, p, kt0, n0);
+    dma_a_tile<BM>(a, As, pw, lane, kt0, m0);
+    __syncthreads();  // tables
+    wait_vmem_all();
+    B::commit(S, Bs, p, s_pair, s_code, offset);
+    if (kt0 + 1 < kt1) {
+      B::issue(a, S, p, kt0 + 1, n0);
+      dma_a_tile<BM>(a, As + LDS_A, pw, lane, kt0 + 1, m0);
     }
-#pragma unroll
-    for (int u = 0; u < T::B_ITEMS; u++) {
-      const int q = t + u * kThreads;
-      if (!BWD) {
-        const int row = q >> 1, half = q & 1;
-        const float s = b_sc[u][0];
-#pragma unroll
-        for (int d = 0; d < 4; d++)
-          *reinterpret_cast<u32x4*>(bs + lds_off(row, half * 4 + d)) = decode8(b_pf[u][d], s, s_nf4);
-      } else {
-        const int chunk = q % (BN / 8);
-        const int rg = q / (BN / 8);
-        // column c of the 8: values of rows rg*4 .. +4 -> 4 fp16 along the reduction dim
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-          const int sh = 8 * (c >> 1) + ((c & 1) ? 0 : 4);
-          u32x2 v;
-          v[0] = pack_f16x2(s_nf4[(b_pf[u][0] >> sh) & 15u] * b_sc[u][0],
-                            s_nf4[(b_pf[u][1] >> sh) & 15u] * b_sc[u][1]);
-          v[1] = pack_f16x2(s_nf4[(b_pf[u][2] >> sh) & 15u] * b_sc[u][2],
-                            s_nf4[(b_pf[u][3] >> sh) & 15u] * b_sc[u][3]);
-          const int row = chunk * 8 + c;
-          *reinterpret_cast<u32x2*>(bs + lds_off(row, rg >> 1) + (rg & 1) * 4) = v;
-        }
+    __syncthreads();  // K-step kt0 ready
+    for (int kt = kt0; kt < kt1; kt++) {
+      wait_vmem_all();  // K-step kt+1 (issued during the previous step) has landed
+      if (kt + 1 < kt1) B::commit(S, Bs + ((kt + 1 - kt0) & 1) * LDS_B, p, s_pair, s_code, offset);
+      if (kt + 2 < kt1) {
+        B::issue(a, S, p, kt + 2, n0);
+        dma_a_tile<BM>(a, As + ((kt + 2 - kt0) % 3) * LDS_A, pw, lane, kt + 2, m0);
       }
+      __syncthreads();
     }
-  };
+    return;
+  }
 
-  float16_t acc[T::TM][T::TN];
-#pragma unroll
-  for (int i = 0; i < T::TM; i++)
-#pragma unroll
-    for (int j = 0; j < T::TN; j++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
-
+  // ---- consumers ----
+  const int wave = t >> 6;
+  const int wm0 = (wave / CWN) * WM;
+  const int wn0 = (wave % CWN) * WN;
   const int lrow = lane & 31;
   const int lseg = lane >> 5;
-
+  float16_t acc[TM][TN];
+  zero_acc(acc);
   if (kt0 < kt1) {
-    load_tile(kt0);
-    __syncthreads();  // s_nf4 ready
-    store_tile(0);
-    __syncthreads();
+    __syncthreads();  // tables
+    __syncthreads();  // K-step kt0 ready
     for (int kt = kt0; kt < kt1; kt++) {
-      const int cur = (kt - kt0) & 1;
-      if (kt + 1 < kt1) load_tile(kt + 1);
-      const _Float16* as = As + cur * T::LDS_A;
-      const _Float16* bs = Bs + cur * T::LDS_B;
-#pragma unroll
-      for (int kk = 0; kk < kBK / 16; kk++) {
-        half8_t af[T::TM], bf[T::TN];
-#pragma unroll
-        for (int i = 0; i < T::TM; i++)
-          af[i] = *reinterpret_cast<const half8_t*>(as + lds_off(wm0 + i * 32 + lrow, 2 * kk + lseg));
-#pragma unroll
-        for (int j = 0; j < T::TN; j++)
-          bf[j] = *reinterpret_cast<const half8_t*>(bs + lds_off(wn0 + j * 32 + lrow, 2 * kk + lseg));
-#pragma unroll
-        for (int i = 0; i < T::TM; i++)
-#pragma unroll
-          for (int j = 0; j < T::TN; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-      }
-      if (kt + 1 < kt1) store_tile(cur ^ 1);
+      const int r = kt - kt0;
+      mma_kstep<TM, TN>(acc, As + (r % 3) * LDS_A, Bs + (r & 1) * LDS_B, wm0, wn0, lrow, lseg);
       __syncthreads();
     }
   }
-
-  // ---- epilogue ----
-  const bool first_split = blockIdx.z == 0;
-  const bool split = gridDim.z > 1;
-  // LoRA term: (s*H)[M, r] . lora_B[N, r]^T  (forward)  or  (s*dH)[M, r] . lora_A[r, N] (backward,
-  // times the dropout keep mask and 1/(1-p) when a mask is given).  One 32x32x16 MFMA per tile
-  // and 16 LoRA ranks, done one 32-row tile at a time to keep few registers live.
-  if (a.lora_h && first_split) {
-#pragma unroll
-    for (int i = 0; i < T::TM; i++) {
-      float16_t lacc[T::TN];
-#pragma unroll
-      for (int j = 0; j < T::TN; j++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) lacc[j][e] = 0.0f;
-      const int mrow = m0 + wm0 + i * 32 + lrow;
-      for (int r0 = 0; r0 < a.r; r0 += 16) {
-        half8_t hf = {};
-        if (mrow < a.M) hf = *reinterpret_cast<const half8_t*>(a.lora_h + (int64_t)mrow * a.r + r0 + 8 * lseg);
-#pragma unroll
-        for (int j = 0; j < T::TN; j++) {
-          const int n = n0 + wn0 + j * 32 + lrow;
-          half8_t wf = {};
-          if (n < a.Nc) {
-            if (!BWD) {
-              wf = *reinterpret_cast<const half8_t*>(a.lora_w + (int64_t)n * a.r + r0 + 8 * lseg);
-            } else {
-#pragma unroll
-              for (int e = 0; e < 8; e++) wf[e] = a.lora_w[(int64_t)(r0 + 8 * lseg + e) * a.Nc + n];
-            }
-          }
-          lacc[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(hf, wf, lacc[j], 0, 0, 0);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < T::TN; j++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          float l = lacc[j][e];
-          if (BWD && a.mask) {
-            const int m = m0 + wm0 + i * 32 + 8 * (e >> 2) + 4 * lseg + (e & 3);
-            const int n = n0 + wn0 + j * 32 + lrow;
-            const bool keep = m < a.M && n < a.Nc && a.mask[(int64_t)m * a.Nc + n] != 0;
-            l = keep ? l * a.mask_scale : 0.0f;
-          }
-          acc[i][j][e] += l;
-        }
-    }
-  }
-
-#pragma unroll
-  for (int j = 0; j < T::TN; j++) {
-    const int n = n0 + wn0 + j * 32 + lrow;
-    if (n >= a.Nc) continue;
-    const float b = (a.bias && first_split) ? (float)a.bias[n] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < T::TM; i++) {
-#pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const int m = m0 + wm0 + i * 32 + 8 * (e >> 2) + 4 * lseg + (e & 3);
-        if (m >= a.M) continue;
-        const float v = acc[i][j][e] + b;
-        if (split)
-          a.ws[((int64_t)blockIdx.z * a.M + m) * a.Nc + n] = v;
-        else
-          a.C[(int64_t)m * a.ldc + n] = (_Float16)v;
-      }
-    }
-  }
+  epilogue<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
 }
 
 // Sum of split-K partials -> fp16.  ws [splits, M, Nc] fp32.
@@ -319,9 +631,20 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
   }
 }
 
-template <int BM, int BN, int WAVES_M, bool BWD>
+static int launch_reduce(const GemmArgs& a, int splits, hipStream_t stream) {
+  const int64_t total = (int64_t)a.M * a.Nc;
+  int64_t blocks = (total / 4 + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  if (blocks < 1) blocks = 1;
+  hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)blocks), dim3(256), 0, stream, a.ws, splits,
+                     a.M, a.Nc, a.C, a.ldc);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MXS_OK : (int)e;
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, bool BWD>
 static int launch_cfg(const GemmArgs& a0, int splits, hipStream_t stream) {
-  using T = Tile<BM, BN, WAVES_M, BWD>;
+  using T = Tile<BM, BN, WAVES_M, WAVES_N, BWD>;
   GemmArgs a = a0;
   const int n_steps = a.Kr / kBK;
   if (splits < 1) splits = 1;
@@ -333,71 +656,87 @@ static int launch_cfg(const GemmArgs& a0, int splits, hipStream_t stream) {
   const size_t lds = (size_t)2 * (T::LDS_A + T::LDS_B) * sizeof(_Float16);
   static bool lds_set = false;  // idempotent attribute; a benign race between threads
   if (!lds_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_nf4_gemm<BM, BN, WAVES_M, BWD>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&k_nf4_gemm<BM, BN, WAVES_M, WAVES_N, BWD>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
     lds_set = true;
   }
-  hipLaunchKernelGGL((k_nf4_gemm<BM, BN, WAVES_M, BWD>), grid, dim3(kThreads), lds, stream, a);
+  hipLaunchKernelGGL((k_nf4_gemm<BM, BN, WAVES_M, WAVES_N, BWD>), grid, dim3(T::NT), lds, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  if (splits > 1) {
-    const int64_t total = (int64_t)a.M * a.Nc;
-    int64_t blocks = (total / 4 + 255) / 256;
-    if (blocks > 4096) blocks = 4096;
-    if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)blocks), dim3(256), 0, stream, a.ws, splits,
-                       a.M, a.Nc, a.C, a.ldc);
-    e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
-  }
-  return MXS_OK;
+  return splits > 1 ? launch_reduce(a, splits, stream) : MXS_OK;
 }
 
-// Tile configurations, by id (mxs_nf4_gemm_config_*): BM x BN, waves along M.
+template <int BM, int BN, int CWM, int CWN, bool BWD>
+static int launch_ws(const GemmArgs& a0, int splits, hipStream_t stream) {
+  GemmArgs a = a0;
+  const int n_steps = a.Kr / kBK;
+  if (splits < 1) splits = 1;
+  if (splits > n_steps) splits = n_steps > 0 ? n_steps : 1;
+  a.steps_per_split = (n_steps + splits - 1) / splits;
+  splits = n_steps > 0 ? (n_steps + a.steps_per_split - 1) / a.steps_per_split : 1;
+  if (splits > 1 && !a.ws) return MXS_ERR_ARG;
+  const dim3 grid((a.Nc + BN - 1) / BN, (a.M + BM - 1) / BM, splits);
+  const size_t lds = (size_t)(3 * BM + 2 * BN) * kBK * sizeof(_Float16);
+  static bool lds_set = false;  // idempotent attribute; a benign race between threads
+  if (!lds_set) {
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+    lds_set = true;
+  }
+  hipLaunchKernelGGL((k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD>), grid, dim3(512), lds, stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  return splits > 1 ? launch_reduce(a, splits, stream) : MXS_OK;
+}
+
+// Tile configurations, by id: BM x BN and the wave layout.
+//   0-4: all waves load, decode and multiply (WAVES_M x WAVES_N waves)
+//   6-9: warp-specialized, 4 producer + 4 consumer waves (consumers CWM x CWN)
 template <bool BWD>
 static int launch_by_id(int cfg, const GemmArgs& a, int splits, hipStream_t s) {
   switch (cfg) {
-    case 0: return launch_cfg<256, 128, 2, BWD>(a, splits, s);
-    case 1: return launch_cfg<128, 128, 2, BWD>(a, splits, s);
-    case 2: return launch_cfg<128, 256, 2, BWD>(a, splits, s);
-    case 3: return launch_cfg<256, 256, 2, BWD>(a, splits, s);
-    case 4: return launch_cfg<64, 128, 1, BWD>(a, splits, s);
+    case 0: return launch_cfg<256, 128, 2, 2, BWD>(a, splits, s);
+    case 1: return launch_cfg<128, 128, 2, 2, BWD>(a, splits, s);
+    case 2: return launch_cfg<256, 128, 4, 2, BWD>(a, splits, s);
+    case 3: return launch_cfg<128, 128, 2, 4, BWD>(a, splits, s);
+    case 4: return launch_cfg<64, 128, 1, 4, BWD>(a, splits, s);
+    case 6: return launch_ws<256, 128, 2, 2, BWD>(a, splits, s);
+    case 7: return launch_ws<256, 160, 4, 1, BWD>(a, splits, s);
+    case 8: return launch_ws<128, 128, 2, 2, BWD>(a, splits, s);
+    case 9: return launch_ws<256, 96, 4, 1, BWD>(a, splits, s);
     default: return MXS_ERR_ARG;
   }
 }
 
-static const int kCfgBM[] = {256, 128, 128, 256, 64};
-static const int kCfgBN[] = {128, 128, 256, 256, 128};
-constexpr int kNumCfg = 5;
+constexpr int kNumCfg = 10;
 
-// Tile and split choice for one GEMM: fill the 256 CUs with whole tiles where the shape allows,
-// else split the reduction (each split keeps at least 4 K-steps).
+// Tile and split choice for one GEMM (M x Nc output, Kr reduction), from measured sweeps on
+// MI355X at the Qwen2.5-1.5B projection shapes (M = 1024):
+//   wide outputs (Nc >= 4096): warp-specialized 256x160, one tile per CU, no split;
+//   narrow outputs with a long reduction (Kr >= 4096): warp-specialized 256x96, split-K 4;
+//   mid outputs (Nc >= 1024): 128x128 (2x4 waves), split-K 2;
+//   small outputs: 64x128, split-K 4 when the reduction is long enough.
+// Splits keep at least 8 K-steps each.
 static void choose(int M, int Nc, int Kr, int* cfg, int* splits) {
   const int n_steps = Kr / kBK;
-  const int order[] = {0, 2, 1, 4};
-  int best = 0, best_split = 1;
-  double best_score = -1.0;
-  for (int c : order) {
-    const int64_t tiles = (int64_t)((M + kCfgBM[c] - 1) / kCfgBM[c]) * ((Nc + kCfgBN[c] - 1) / kCfgBN[c]);
-    for (int sp = 1; sp <= 16; sp *= 2) {
-      if (sp > 1 && n_steps / sp < 4) break;
-      const int64_t wgs = tiles * sp;
-      const double waves = (double)wgs / 256.0;
-      const double fill = waves / ((double)((wgs + 255) / 256));
-      // efficiency: CU fill x tile-size factor (bigger tiles reuse more) x split-K overhead
-      const double tile_eff = (kCfgBM[c] * kCfgBN[c]) / (kCfgBM[c] + kCfgBN[c]) / 85.3;
-      const double split_pen = sp > 1 ? 1.0 / (1.0 + 0.08 * sp) : 1.0;
-      const double score = fill * (tile_eff > 1.0 ? 1.0 : tile_eff) * split_pen;
-      if (score > best_score + 1e-9) {
-        best_score = score;
-        best = c;
-        best_split = sp;
-      }
-    }
+  int c, sp;
+  if (Nc >= 4096) {
+    c = 7; sp = 1;
+  } else if (Kr >= 4096) {
+    c = 9; sp = 4;
+  } else if (Nc >= 1024) {
+    c = 3; sp = 2;
+  } else {
+    c = 4; sp = Kr >= 1024 ? 4 : 1;
   }
-  *cfg = best;
-  *splits = best_split;
+  (void)M;
+  while (sp > 1 && n_steps / sp < 8) sp >>= 1;
+  *cfg = c;
+  *splits = sp;
 }
 
 static int gemm_entry(bool bwd, const GemmArgs& a, int cfg, int splits, hipStream_t stream) {
@@ -413,7 +752,7 @@ static int gemm_entry(bool bwd, const GemmArgs& a, int cfg, int splits, hipStrea
   if (a.lora_h && (((uintptr_t)a.lora_h % 16) != 0 || (!bwd && ((uintptr_t)a.lora_w % 16) != 0)))
     return MXS_ERR_ALIGN;
   if (cfg < 0) choose(a.M, a.Nc, a.Kr, &cfg, &splits);
-  if (cfg >= kNumCfg) return MXS_ERR_ARG;
+  if (cfg >= kNumCfg || cfg == 5) return MXS_ERR_ARG;
   return bwd ? launch_by_id<true>(cfg, a, splits, stream)
              : launch_by_id<false>(cfg, a, splits, stream);
 }
