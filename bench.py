@@ -173,25 +173,42 @@ def make_proj(dev, g, n, k, x=None, x_kind="normal", dy_std=1.0):
     lb = (torch.randn((n, RANK), device=dev, generator=g) * 0.01).half()
     dy = (torch.randn((M_TOKENS, n), device=dev, generator=g) * dy_std).half()
     keep = (torch.rand((M_TOKENS, k), device=dev, generator=g) >= P_DROP).to(torch.uint8)
-    return dict(packed=packed, st=st, x=x, a=la, b=lb, dy=dy, keep=keep, n=n, k=k)
+    return dict(packed=packed, st=st, x=x, a=la, b=lb, dy=dy, keep=keep, n=n, k=k,
+                ws=shared_workspace(dev))
+
+
+_WS = {}
+
+
+def shared_workspace(dev):
+    """One workspace for every projection's kernels (they run in stream order), allocated before
+    any graph capture."""
+    from mindxsoup_amd import kernels
+
+    if dev not in _WS:
+        need = max(kernels.projection_workspace_bytes(M_TOKENS, k, n, RANK) for _, n, k in PROJ)
+        _WS[dev] = kernels.new_workspace(need, dev)
+    return _WS[dev]
 
 
 def proj_fwd(p, s=ALPHA / RANK):
     from mindxsoup_amd import kernels
 
-    h, ht = kernels.lora_h(p["x"], p["a"], s, p["keep"], 1.0 / (1.0 - P_DROP))
-    y = kernels.nf4_linear_fwd(p["x"], p["packed"], p["st"], None, h, p["b"])
-    return y, ht
+    h, ht, at = kernels.lora_h(p["x"], p["a"], s, p["keep"], 1.0 / (1.0 - P_DROP), ws=p["ws"],
+                               n_out=p["n"], want_at=True)
+    y = kernels.nf4_linear_fwd(p["x"], p["packed"], p["st"], None, h, p["b"], ws=p["ws"])
+    return y, (ht, at)
 
 
-def proj_bwd(p, ht, s=ALPHA / RANK):
+def proj_bwd(p, saved, s=ALPHA / RANK):
     from mindxsoup_amd import kernels
 
+    ht, at = saved
     ms = 1.0 / (1.0 - P_DROP)
-    dh, dht = kernels.lora_dh(p["dy"], p["b"], s)
-    dx = kernels.nf4_linear_bwd_dx(p["dy"], p["packed"], p["st"], dh, p["a"], p["keep"], ms)
-    da = kernels.lora_grad_a(dht, p["x"], p["keep"], ms)
-    db = kernels.lora_grad_b(ht, p["dy"])
+    dh, dht = kernels.lora_dh(p["dy"], p["b"], s, ws=p["ws"], k_in=p["k"])
+    dx = kernels.nf4_linear_bwd_dx(p["dy"], p["packed"], p["st"], dh, None, p["keep"], ms,
+                                   lora_at=at, ws=p["ws"])
+    da, db = kernels.lora_grads(dht, ht, p["x"], p["dy"], p["keep"], ms, ws=p["ws"])
     return dx, da, db
 
 
@@ -231,12 +248,14 @@ def bench_fused(dev, steps, warmup):
                                   "tflops": round(fl / ms / 1e9, 1)}
     # the dominant kernel alone: the fused forward GEMM with its LoRA epilogue (gate, up)
     from mindxsoup_amd import kernels
-    hg, _ = kernels.lora_h(gate["x"], gate["a"], 2.0, gate["keep"], 1 / (1 - P_DROP))
-    hu, _ = kernels.lora_h(up["x"], up["a"], 2.0, up["keep"], 1 / (1 - P_DROP))
+    hg, _ = kernels.lora_h(gate["x"], gate["a"], 2.0, gate["keep"], 1 / (1 - P_DROP),
+                           ws=gate["ws"])
+    hu, _ = kernels.lora_h(up["x"], up["a"], 2.0, up["keep"], 1 / (1 - P_DROP), ws=up["ws"])
     ms_k, _ = graph_time(lambda: (kernels.nf4_linear_fwd(gate["x"], gate["packed"], gate["st"],
-                                                         None, hg, gate["b"]),
+                                                         None, hg, gate["b"], ws=gate["ws"]),
                                   kernels.nf4_linear_fwd(up["x"], up["packed"], up["st"], None,
-                                                         hu, up["b"])), steps, warmup)
+                                                         hu, up["b"], ws=up["ws"])),
+                         steps, warmup)
     fl_k = 2 * (2 * M_TOKENS * 8960 * 1536 + 2 * M_TOKENS * RANK * 8960)
     out["gemm_fwd_kernel"] = {"ms_per_launch": round(ms_k / 2, 4),
                               "tflops": round(fl_k / ms_k / 1e9, 1)}

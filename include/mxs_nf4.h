@@ -87,11 +87,13 @@ int mxs_nf4_quantize(const void* w_f16, int64_t n_values, const float* code, voi
                      void* workspace, hipStream_t stream);
 
 /* ---- Fused NF4 GEMMs (forward and input gradient of the frozen Linear4bit) ---------------
- * cfg: tile configuration id (0: 256x128, 1: 128x128, 2: 128x256, 3: 256x256, 4: 64x128) or -1
- * to let the library choose tiles and split-K for the shape; splits: reduction splits (used with
- * cfg >= 0).  When the chosen plan splits the reduction, `workspace` must hold
- * mxs_nf4_gemm_workspace_bytes(M, Nc, Kr, cfg, splits) bytes of device memory (else it may be
- * NULL).  Shapes: in_features % 64 == 0, reduction % 64 == 0; x/dy 16-byte aligned. */
+ * cfg: tile configuration id (0-4: all-wave kernels, 6-9: producer/consumer kernels; 5 is
+ * invalid) or -1 to let the library choose tiles and split-K for the shape; splits: reduction
+ * splits (used with cfg >= 0).  When the plan splits the reduction, `workspace` must hold
+ * mxs_nf4_gemm_workspace_bytes(M, Nc, Kr, cfg, splits) bytes of device memory (fp32 partial
+ * sums, no initial contents needed; a return of 0 means no workspace is needed) and a second
+ * small kernel adds the partials in split order: results are deterministic.  Shapes:
+ * in_features % 64 == 0, reduction % 64 == 0; x/dy 16-byte aligned. */
 int64_t mxs_nf4_gemm_workspace_bytes(int M, int Nc, int Kr, int cfg, int splits);
 
 /* Y[M,N] = X[M,K] . W[N,K]^T (+ bias[N]) (+ lora_h[M,r] . lora_b[N,r]^T), fp16 in/out, fp32
@@ -105,38 +107,58 @@ int mxs_nf4_linear_fwd(const void* x, int M, int K, int N, const void* packed,
                        const void* lora_b, int r, void* y, void* workspace, int cfg, int splits,
                        hipStream_t stream);
 
-/* dX[M,K] = dY[M,N] . W[N,K] (+ mask[M,K] * mask_scale * (lora_dh[M,r] . lora_a[r,K])), with W
- * decoded from NF4 inside the GEMM.  Replaces NF4LinearFunction.backward
+/* dX[M,K] = dY[M,N] . W[N,K] (+ mask[M,K] * mask_scale * (lora_dh[M,r] . lora_at[K,r]^T)), with
+ * W decoded from NF4 inside the GEMM.  Replaces NF4LinearFunction.backward
  * (solution/linear4bit.py:51-57: unpack again, then grad @ W) plus the LoRA branch's input
  * gradient through the dropout (solution/dropout.py:62-69); lora_dh = s * dY . B from
- * mxs_lora_dh.  mask: u8 keep mask [M,K] or NULL (no dropout); mask_scale = 1/(1-p). */
+ * mxs_lora_dh, lora_at = lora_A transposed ([K, r]: the `at` output of mxs_lora_h, or
+ * mxs_transpose_f16).  mask: u8 keep mask
+ * [M,K] or NULL (no dropout); mask_scale = 1/(1-p). */
 int mxs_nf4_linear_bwd_dx(const void* dy, int M, int N, int K, const void* packed,
                           const void* absmax8, const float* code, const float* absmax2,
-                          const float* offset, const void* lora_dh, const void* lora_a, int r,
+                          const float* offset, const void* lora_dh, const void* lora_at, int r,
                           const void* mask, float mask_scale, void* dx, void* workspace, int cfg,
                           int splits, hipStream_t stream);
 
 /* ---- LoRA side branch (peft lora.Linear around the 4-bit base, r % 16 == 0) --------------
- * The transposed outputs/inputs (ht, dht) are fp16 [r, ldt] with ldt >= M, ldt % 8 == 0. */
+ * The transposed outputs/inputs (ht, dht) are fp16 [r, ldt] with ldt >= M, ldt % 8 == 0 (columns
+ * past M hold zeros).  Each call needs `workspace` of mxs_lora_workspace_bytes(M, K, N, r) bytes
+ * of device memory (fp32 partial sums, no initial contents needed; one buffer serves all calls
+ * of a projection when they run in order on one stream).  Each call is a partial-sum launch and
+ * a launch that adds the partials in a fixed order, so results are deterministic. */
+int64_t mxs_lora_workspace_bytes(int M, int K, int N, int r);
 
 /* h = fp16(s * drop(x) . A^T) [M, r] and ht = its transpose: lora_A of peft's branch with the
  * reference's dropout (solution/dropout.py:33-35, mask u8 [M,K] or NULL) and the scaling s
- * folded in.  x [M,K] fp16, lora_a [r,K] fp16, K % 32 == 0. */
+ * folded in.  x [M,K] fp16, lora_a [r,K] fp16, K % 32 == 0.  at: NULL or fp16 [K, r], which
+ * receives lora_a transposed (the operand mxs_nf4_linear_bwd_dx takes). */
 int mxs_lora_h(const void* x, int M, int K, const void* lora_a, int r, const void* mask,
-               float mask_scale, float s, void* h, void* ht, int ldt, hipStream_t stream);
+               float mask_scale, float s, void* h, void* ht, int ldt, void* at, void* workspace,
+               hipStream_t stream);
 
 /* dh = fp16(s * dY . B) [M, r] and dht = its transpose (the gradient reaching lora_B's output,
  * times s).  dy [M,N] fp16, lora_b [N,r] fp16, N % 32 == 0. */
 int mxs_lora_dh(const void* dy, int M, int N, const void* lora_b, int r, float s, void* dh,
-                void* dht, int ldt, hipStream_t stream);
+                void* dht, int ldt, void* workspace, hipStream_t stream);
 
 /* dA[r,K] (fp32) = dh^T . drop(x): lora_A's weight gradient (autograd of peft's nn.Linear). */
 int mxs_lora_grad_a(const void* dht, int ldt, const void* x, int M, int K, int r,
-                    const void* mask, float mask_scale, float* da, hipStream_t stream);
+                    const void* mask, float mask_scale, float* da, void* workspace,
+                    hipStream_t stream);
 
 /* dB[N,r] (fp32) = dY^T . h (h = s * H): lora_B's weight gradient. */
 int mxs_lora_grad_b(const void* ht, int ldt, const void* dy, int M, int N, int r, float* db,
-                    hipStream_t stream);
+                    void* workspace, hipStream_t stream);
+
+/* mxs_lora_grad_a and mxs_lora_grad_b in one pair of launches (either output may be NULL): the two
+ * weight gradients autograd computes for peft's lora_A and lora_B (solution/attention.py:197-199
+ * under torch.autograd).  M == 0 writes zero gradients. */
+int mxs_lora_grads(const void* dht, const void* ht, int ldt, const void* x, const void* dy, int M,
+                   int K, int N, int r, const void* mask, float mask_scale, float* da, float* db,
+                   void* workspace, hipStream_t stream);
+
+/* dst[cols, rows] = src[rows, cols]^T, fp16 (lora_A -> the [K, r] operand of the backward). */
+int mxs_transpose_f16(const void* src, int rows, int cols, void* dst, hipStream_t stream);
 
 #ifdef __cplusplus
 }

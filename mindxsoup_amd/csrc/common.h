@@ -52,4 +52,8 @@ __device__ __forceinline__ u32x4 decode8(uint32_t w, float s, const float* tab) 
   return r;
 }
 
+// vmcnt(0): every vector memory access this wave issued has completed (gfx9 s_waitcnt encoding,
+// expcnt and lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 }  // namespace mxs

@@ -36,7 +36,7 @@ struct GemmArgs {
   // epilogue
   const _Float16* bias;     // [Nc] (forward) or null
   const _Float16* lora_h;   // [M, r]: s*H (forward) or s*dH (backward), or null
-  const _Float16* lora_w;   // forward: lora_B [Nc, r]; backward: lora_A [r, Nc]
+  const _Float16* lora_w;   // [Nc, r]: forward lora_B; backward lora_A transposed
   int r;
   const uint8_t* mask;      // backward: dropout keep mask [M, Nc] or null
   float mask_scale;         // 1 / (1 - p)
@@ -84,48 +84,42 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float16_t (&acc)[TM]
   const bool split = gridDim.z > 1;
   const bool vec = (a.Nc % 4) == 0 && (a.ldc % 4) == 0;
   if (a.lora_h && first_split) {
+    // lora_w is [Nc, r] in both directions (the backward pass gets lora_A transposed), so the
+    // W-side operand is one 16-byte load per tile and 16 ranks.
+    const bool masked = BWD && a.mask;
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       const int m = mb + i * 32 + lrow;
 #pragma unroll
       for (int j = 0; j < TN; j++) {
-        float16_t lacc = {};
         const int ncol = nb + j * 32 + lrow;  // column this lane feeds as the W-side operand
+        float16_t lacc = {};
         for (int r0 = 0; r0 < a.r; r0 += 16) {
           half8_t hf = {}, wf = {};
           if (m < a.M) hf = *reinterpret_cast<const half8_t*>(a.lora_h + (int64_t)m * a.r + r0 + 8 * lseg);
-          if (ncol < a.Nc) {
-            if (!BWD) {
-              wf = *reinterpret_cast<const half8_t*>(a.lora_w + (int64_t)ncol * a.r + r0 + 8 * lseg);
-            } else {
-#pragma unroll
-              for (int e = 0; e < 8; e++) wf[e] = a.lora_w[(int64_t)(r0 + 8 * lseg + e) * a.Nc + ncol];
-            }
-          }
-          lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, hf, lacc, 0, 0, 0);
+          if (ncol < a.Nc) wf = *reinterpret_cast<const half8_t*>(a.lora_w + (int64_t)ncol * a.r + r0 + 8 * lseg);
+          if (masked)
+            lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, hf, lacc, 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, hf, acc[i][j], 0, 0, 0);
         }
+        if (!masked) continue;
 #pragma unroll
         for (int g = 0; g < 4; g++) {
           const int n = nb + j * 32 + 8 * g + 4 * lseg;
-          uint32_t keep = 0x01010101u;
-          if (BWD && a.mask) {
-            keep = 0;
-            if (m < a.M) {
-              if (vec && n + 3 < a.Nc) {
-                keep = *reinterpret_cast<const uint32_t*>(a.mask + (int64_t)m * a.Nc + n);
-              } else {
+          uint32_t keep = 0;
+          if (m < a.M) {
+            if (vec && n + 3 < a.Nc) {
+              keep = *reinterpret_cast<const uint32_t*>(a.mask + (int64_t)m * a.Nc + n);
+            } else {
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                  if (n + e < a.Nc) keep |= (uint32_t)a.mask[(int64_t)m * a.Nc + n + e] << (8 * e);
-              }
+              for (int e = 0; e < 4; e++)
+                if (n + e < a.Nc) keep |= (uint32_t)a.mask[(int64_t)m * a.Nc + n + e] << (8 * e);
             }
           }
 #pragma unroll
-          for (int e = 0; e < 4; e++) {
-            float l = lacc[4 * g + e];
-            if (BWD && a.mask) l = ((keep >> (8 * e)) & 0xffu) ? l * a.mask_scale : 0.0f;
-            acc[i][j][4 * g + e] += l;
-          }
+          for (int e = 0; e < 4; e++)
+            if ((keep >> (8 * e)) & 0xffu) acc[i][j][4 * g + e] += lacc[4 * g + e] * a.mask_scale;
         }
       }
     }
@@ -170,6 +164,36 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float16_t (&acc)[TM]
       }
     }
   }
+}
+
+// Split-K: C = fp16(sum over the split planes of ws), summed in split order (deterministic).
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int splits,
+                                                      int M, int Nc, _Float16* __restrict__ C,
+                                                      int64_t ldc) {
+  const int64_t plane = (int64_t)M * Nc;
+  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (e >= plane) return;
+  const int m = (int)(e / Nc), n = (int)(e % Nc);
+  if ((Nc % 4) == 0 && (ldc % 4) == 0) {
+    float4_t v = *reinterpret_cast<const float4_t*>(ws + e);
+    for (int z = 1; z < splits; z++) v += *reinterpret_cast<const float4_t*>(ws + z * plane + e);
+    *reinterpret_cast<half4_t*>(C + (int64_t)m * ldc + n) = __builtin_convertvector(v, half4_t);
+  } else {
+    for (int q = 0; q < 4 && e + q < plane; q++) {
+      const int mq = (int)((e + q) / Nc), nq = (int)((e + q) % Nc);
+      float v = ws[e + q];
+      for (int z = 1; z < splits; z++) v += ws[z * plane + e + q];
+      C[(int64_t)mq * ldc + nq] = (_Float16)v;
+    }
+  }
+}
+
+static int launch_reduce(const GemmArgs& a, int splits, hipStream_t stream) {
+  const int64_t quads = ((int64_t)a.M * a.Nc + 3) / 4;
+  hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
+                     a.ws, splits, a.M, a.Nc, a.C, (int64_t)a.ldc);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MXS_OK : (int)e;
 }
 
 // Global -> register staging and register -> LDS commit of one K-step's tiles, for NTP
@@ -527,9 +551,6 @@ __device__ __forceinline__ void dma_a_tile(const GemmArgs& a, _Float16* as, int 
   }
 }
 
-// vmcnt(0) (gfx9 s_waitcnt encoding: expcnt and lgkmcnt left at their maxima).
-__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
-
 // Warp-specialized kernel: 4 consumer waves (one per SIMD, CWM x CWN over the BM x BN tile)
 // only read LDS fragments and issue MFMAs; 4 producer waves (the other wave of each SIMD) copy
 // the A tile of K-step kt+2 straight into a 3-deep LDS ring, and decode the NF4 of kt+1 into
@@ -558,88 +579,53 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
   fill_tables(a, s_pair, s_code, t, 512);
 
   if (t >= 256) {
-    // ---- producers ----
-    if (kt0 >= kt1) return;
-    const int p = t - 256;
-    const int pw = p >> 6;
-    const float offset = a.offset[0];
-    typename B::Stage S;
-    B::issue(a, S, p, kt0, n0);
-    dma_a_tile<BM>(a, As, pw, lane, kt0, m0);
-    __syncthreads();  // tables
-    wait_vmem_all();
-    B::commit(S, Bs, p, s_pair, s_code, offset);
-    if (kt0 + 1 < kt1) {
-      B::issue(a, S, p, kt0 + 1, n0);
-      dma_a_tile<BM>(a, As + LDS_A, pw, lane, kt0 + 1, m0);
-    }
-    __syncthreads();  // K-step kt0 ready
-    for (int kt = kt0; kt < kt1; kt++) {
-      wait_vmem_all();  // K-step kt+1 (issued during the previous step) has landed
-      if (kt + 1 < kt1) B::commit(S, Bs + ((kt + 1 - kt0) & 1) * LDS_B, p, s_pair, s_code, offset);
-      if (kt + 2 < kt1) {
-        B::issue(a, S, p, kt + 2, n0);
-        dma_a_tile<BM>(a, As + ((kt + 2 - kt0) % 3) * LDS_A, pw, lane, kt + 2, m0);
+    // ---- producers (they stay to the end: every wave takes part in every barrier) ----
+    if (kt0 < kt1) {
+      const int p = t - 256;
+      const int pw = p >> 6;
+      const float offset = a.offset[0];
+      typename B::Stage S;
+      B::issue(a, S, p, kt0, n0);
+      dma_a_tile<BM>(a, As, pw, lane, kt0, m0);
+      __syncthreads();  // tables
+      wait_vmem_all();
+      B::commit(S, Bs, p, s_pair, s_code, offset);
+      if (kt0 + 1 < kt1) {
+        B::issue(a, S, p, kt0 + 1, n0);
+        dma_a_tile<BM>(a, As + LDS_A, pw, lane, kt0 + 1, m0);
       }
-      __syncthreads();
-    }
-    return;
-  }
-
-  // ---- consumers ----
-  const int wave = t >> 6;
-  const int wm0 = (wave / CWN) * WM;
-  const int wn0 = (wave % CWN) * WN;
-  const int lrow = lane & 31;
-  const int lseg = lane >> 5;
-  float16_t acc[TM][TN];
-  zero_acc(acc);
-  if (kt0 < kt1) {
-    __syncthreads();  // tables
-    __syncthreads();  // K-step kt0 ready
-    for (int kt = kt0; kt < kt1; kt++) {
-      const int r = kt - kt0;
-      mma_kstep<TM, TN>(acc, As + (r % 3) * LDS_A, Bs + (r & 1) * LDS_B, wm0, wn0, lrow, lseg);
-      __syncthreads();
-    }
-  }
-  epilogue<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
-}
-
-// Sum of split-K partials -> fp16.  ws [splits, M, Nc] fp32.
-__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int splits,
-                                                      int M, int Nc, _Float16* __restrict__ C,
-                                                      int64_t ldc) {
-  const int64_t total = (int64_t)M * Nc;
-  const int64_t plane = total;
-  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < total;
-       i += (int64_t)gridDim.x * 256 * 4) {
-    float4_t s = {0.f, 0.f, 0.f, 0.f};
-    const bool vec = (Nc % 4 == 0) && i + 3 < total;
-    if (vec) {
-      for (int z = 0; z < splits; z++) s += *reinterpret_cast<const float4_t*>(ws + z * plane + i);
-      const int64_t m = i / Nc, n = i % Nc;
-      half4_t h = __builtin_convertvector(s, half4_t);
-      *reinterpret_cast<half4_t*>(C + m * ldc + n) = h;
-    } else {
-      for (int64_t e = i; e < i + 4 && e < total; e++) {
-        float v = 0.f;
-        for (int z = 0; z < splits; z++) v += ws[z * plane + e];
-        C[(e / Nc) * ldc + e % Nc] = (_Float16)v;
+      __syncthreads();  // K-step kt0 ready
+      for (int kt = kt0; kt < kt1; kt++) {
+        wait_vmem_all();  // K-step kt+1 (issued during the previous step) has landed
+        if (kt + 1 < kt1)
+          B::commit(S, Bs + ((kt + 1 - kt0) & 1) * LDS_B, p, s_pair, s_code, offset);
+        if (kt + 2 < kt1) {
+          B::issue(a, S, p, kt + 2, n0);
+          dma_a_tile<BM>(a, As + ((kt + 2 - kt0) % 3) * LDS_A, pw, lane, kt + 2, m0);
+        }
+        __syncthreads();
       }
     }
+  } else {
+    // ---- consumers ----
+    const int wave = t >> 6;
+    const int wm0 = (wave / CWN) * WM;
+    const int wn0 = (wave % CWN) * WN;
+    const int lrow = lane & 31;
+    const int lseg = lane >> 5;
+    float16_t acc[TM][TN];
+    zero_acc(acc);
+    if (kt0 < kt1) {
+      __syncthreads();  // tables
+      __syncthreads();  // K-step kt0 ready
+      for (int kt = kt0; kt < kt1; kt++) {
+        const int r = kt - kt0;
+        mma_kstep<TM, TN>(acc, As + (r % 3) * LDS_A, Bs + (r & 1) * LDS_B, wm0, wn0, lrow, lseg);
+        __syncthreads();
+      }
+    }
+    epilogue<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
   }
-}
-
-static int launch_reduce(const GemmArgs& a, int splits, hipStream_t stream) {
-  const int64_t total = (int64_t)a.M * a.Nc;
-  int64_t blocks = (total / 4 + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)blocks), dim3(256), 0, stream, a.ws, splits,
-                     a.M, a.Nc, a.C, a.ldc);
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? MXS_OK : (int)e;
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool BWD>
@@ -651,8 +637,8 @@ static int launch_cfg(const GemmArgs& a0, int splits, hipStream_t stream) {
   if (splits > n_steps) splits = n_steps > 0 ? n_steps : 1;
   a.steps_per_split = (n_steps + splits - 1) / splits;
   splits = n_steps > 0 ? (n_steps + a.steps_per_split - 1) / a.steps_per_split : 1;
-  if (splits > 1 && !a.ws) return MXS_ERR_ARG;
   const dim3 grid((a.Nc + BN - 1) / BN, (a.M + BM - 1) / BM, splits);
+  if (splits > 1 && !a.ws) return MXS_ERR_ARG;
   const size_t lds = (size_t)2 * (T::LDS_A + T::LDS_B) * sizeof(_Float16);
   static bool lds_set = false;  // idempotent attribute; a benign race between threads
   if (!lds_set) {
@@ -676,8 +662,8 @@ static int launch_ws(const GemmArgs& a0, int splits, hipStream_t stream) {
   if (splits > n_steps) splits = n_steps > 0 ? n_steps : 1;
   a.steps_per_split = (n_steps + splits - 1) / splits;
   splits = n_steps > 0 ? (n_steps + a.steps_per_split - 1) / a.steps_per_split : 1;
-  if (splits > 1 && !a.ws) return MXS_ERR_ARG;
   const dim3 grid((a.Nc + BN - 1) / BN, (a.M + BM - 1) / BM, splits);
+  if (splits > 1 && !a.ws) return MXS_ERR_ARG;
   const size_t lds = (size_t)(3 * BM + 2 * BN) * kBK * sizeof(_Float16);
   static bool lds_set = false;  // idempotent attribute; a benign race between threads
   if (!lds_set) {
@@ -749,7 +735,7 @@ static int gemm_entry(bool bwd, const GemmArgs& a, int cfg, int splits, hipStrea
   if (a.lda % 8 != 0 || ((uintptr_t)a.A % 16) != 0 || ((uintptr_t)a.packed % 16) != 0)
     return MXS_ERR_ALIGN;
   if (a.lora_h && (!a.lora_w || a.r <= 0 || a.r % 16 != 0)) return MXS_ERR_SIZE;
-  if (a.lora_h && (((uintptr_t)a.lora_h % 16) != 0 || (!bwd && ((uintptr_t)a.lora_w % 16) != 0)))
+  if (a.lora_h && (((uintptr_t)a.lora_h % 16) != 0 || ((uintptr_t)a.lora_w % 16) != 0))
     return MXS_ERR_ALIGN;
   if (cfg < 0) choose(a.M, a.Nc, a.Kr, &cfg, &splits);
   if (cfg >= kNumCfg || cfg == 5) return MXS_ERR_ARG;
@@ -761,13 +747,18 @@ static int gemm_entry(bool bwd, const GemmArgs& a, int cfg, int splits, hipStrea
 
 using namespace mxs;
 
-extern "C" {
-
+// Split-K workspace: one fp32 partial plane per split.
 int64_t mxs_nf4_gemm_workspace_bytes(int M, int Nc, int Kr, int cfg, int splits) {
   if (cfg < 0) choose(M, Nc, Kr, &cfg, &splits);
   if (splits <= 1) return 0;
   return (int64_t)splits * M * Nc * (int64_t)sizeof(float);
 }
+
+static void set_workspace(GemmArgs& a, void* workspace) {
+  a.ws = static_cast<float*>(workspace);
+}
+
+extern "C" {
 
 int mxs_nf4_linear_fwd(const void* x, int M, int K, int N, const void* packed,
                        const void* absmax8, const float* code, const float* absmax2,
@@ -792,13 +783,13 @@ int mxs_nf4_linear_fwd(const void* x, int M, int K, int N, const void* packed,
   a.r = r;
   a.C = static_cast<_Float16*>(y);
   a.ldc = N;
-  a.ws = static_cast<float*>(workspace);
+  set_workspace(a, workspace);
   return gemm_entry(false, a, cfg, splits, stream);
 }
 
 int mxs_nf4_linear_bwd_dx(const void* dy, int M, int N, int K, const void* packed,
                           const void* absmax8, const float* code, const float* absmax2,
-                          const float* offset, const void* lora_dh, const void* lora_a, int r,
+                          const float* offset, const void* lora_dh, const void* lora_at, int r,
                           const void* mask, float mask_scale, void* dx, void* workspace, int cfg,
                           int splits, hipStream_t stream) {
   GemmArgs a{};
@@ -814,13 +805,13 @@ int mxs_nf4_linear_bwd_dx(const void* dy, int M, int N, int K, const void* packe
   a.Kr = N;
   a.Kw = K;
   a.lora_h = static_cast<const _Float16*>(lora_dh);
-  a.lora_w = static_cast<const _Float16*>(lora_a);
+  a.lora_w = static_cast<const _Float16*>(lora_at);
   a.r = r;
   a.mask = static_cast<const uint8_t*>(mask);
   a.mask_scale = mask_scale;
   a.C = static_cast<_Float16*>(dx);
   a.ldc = K;
-  a.ws = static_cast<float*>(workspace);
+  set_workspace(a, workspace);
   return gemm_entry(true, a, cfg, splits, stream);
 }
 

@@ -1,13 +1,34 @@
 """Tensor-level calls of the fused NF4 GEMM and LoRA kernels (C ABI in include/mxs_nf4.h).
 
-Every function checks shapes, dtypes and devices, allocates its outputs (and the split-K
-workspace) with torch's caching allocator, and launches on the current HIP stream.  Nothing here
-computes on the CPU or falls back to another implementation: an unsupported shape raises.
+Every function checks shapes, dtypes and devices, allocates its outputs with torch's caching
+allocator, and launches on the current HIP stream.  Nothing here computes on the CPU or falls
+back to another implementation: an unsupported shape raises.
+
+Workspaces: the split-K GEMMs and the LoRA kernels write fp32 partial sums to a workspace that
+a second small kernel adds up in a fixed order; its contents need no initialisation and are dead
+after the call, so one buffer serves any number of calls issued in order on one stream.  Calls
+take it as `ws` or allocate it from torch's caching allocator.
 """
 
 import torch
 
 from . import _lib
+
+
+def new_workspace(nbytes, device):
+    """A workspace of at least nbytes (u8 tensor; contents undefined)."""
+    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
+
+
+def _workspace(nbytes, device, ws):
+    if nbytes <= 0:
+        return None
+    if ws is None:
+        return new_workspace(nbytes, device)
+    if ws.numel() * ws.element_size() < nbytes:
+        raise ValueError(f"workspace holds {ws.numel() * ws.element_size()} bytes, "
+                         f"needs {nbytes}")
+    return ws
 
 
 def _c(t):
@@ -28,14 +49,26 @@ def fused_shape_ok(state, M=None):
             and k % 64 == 0 and n % 64 == 0)
 
 
-def _ws(M, Nc, Kr, dev, cfg, splits):
-    nbytes = _lib.lib().mxs_nf4_gemm_workspace_bytes(M, Nc, Kr, cfg, splits)
-    if nbytes <= 0:
-        return None
-    return torch.empty(nbytes // 4, dtype=torch.float32, device=dev)
+def gemm_workspace_bytes(M, Nc, Kr, cfg=-1, splits=1):
+    return int(_lib.lib().mxs_nf4_gemm_workspace_bytes(M, Nc, Kr, cfg, splits))
 
 
-def nf4_linear_fwd(x2d, packed, state, bias=None, lora_h=None, lora_b=None, cfg=-1, splits=1):
+def lora_workspace_bytes(M, K, N, r):
+    return int(_lib.lib().mxs_lora_workspace_bytes(M, K, N, r))
+
+
+def projection_workspace_bytes(M, K, N, r=16):
+    """Bytes one workspace needs for every call of a K -> N projection at M tokens."""
+    return max(gemm_workspace_bytes(M, N, K), gemm_workspace_bytes(M, K, N),
+               lora_workspace_bytes(M, K, N, r) if r else 0)
+
+
+def _ws(M, Nc, Kr, dev, cfg, splits, ws=None):
+    return _workspace(gemm_workspace_bytes(M, Nc, Kr, cfg, splits), dev, ws)
+
+
+def nf4_linear_fwd(x2d, packed, state, bias=None, lora_h=None, lora_b=None, cfg=-1, splits=1,
+                   ws=None):
     """Y = x2d @ W^T (+ bias) (+ lora_h @ lora_b^T), fp16 [M, N]; W decoded inside the GEMM."""
     n, k = state.shape
     if x2d.dtype != torch.float16 or x2d.dim() != 2 or x2d.shape[1] != k:
@@ -51,7 +84,7 @@ def nf4_linear_fwd(x2d, packed, state, bias=None, lora_h=None, lora_b=None, cfg=
         lora_h, lora_b = lora_h.contiguous(), lora_b.contiguous()
     if bias is not None:
         bias = bias.to(torch.float16).contiguous()
-    ws = _ws(M, n, k, x2d.device, cfg, splits)
+    ws = _ws(M, n, k, x2d.device, cfg, splits, ws)
     _lib.call("mxs_nf4_linear_fwd", _lib.ptr(x2d), M, k, n, *_nf4_args(packed, state),
               _lib.ptr(bias), _lib.ptr(lora_h), _lib.ptr(lora_b), r, _lib.ptr(y), _lib.ptr(ws),
               cfg, splits, _lib.stream_of(x2d.device))
@@ -59,8 +92,9 @@ def nf4_linear_fwd(x2d, packed, state, bias=None, lora_h=None, lora_b=None, cfg=
 
 
 def nf4_linear_bwd_dx(dy2d, packed, state, lora_dh=None, lora_a=None, mask=None,
-                      mask_scale=1.0, cfg=-1, splits=1):
-    """dX = dy2d @ W (+ mask * mask_scale * (lora_dh @ lora_a)), fp16 [M, K]."""
+                      mask_scale=1.0, cfg=-1, splits=1, lora_at=None, ws=None):
+    """dX = dy2d @ W (+ mask * mask_scale * (lora_dh @ lora_a)), fp16 [M, K].  The kernel takes
+    lora_A transposed ([K, r]); pass it as lora_at to skip the transpose."""
     n, k = state.shape
     if dy2d.dtype != torch.float16 or dy2d.dim() != 2 or dy2d.shape[1] != n:
         raise ValueError("dy must be fp16 [M, out_features]")
@@ -70,68 +104,115 @@ def nf4_linear_bwd_dx(dy2d, packed, state, lora_dh=None, lora_a=None, mask=None,
     r = 0
     if lora_dh is not None:
         r = lora_dh.shape[1]
-        if lora_a is None or lora_a.shape != (r, k) or lora_dh.shape[0] != M:
-            raise ValueError("lora_dh [M, r] needs lora_a [r, K]")
-        lora_dh, lora_a = lora_dh.contiguous(), lora_a.contiguous()
+        if lora_at is None:
+            if lora_a is None or lora_a.shape != (r, k):
+                raise ValueError("lora_dh [M, r] needs lora_a [r, K]")
+            lora_at = transpose(lora_a.to(torch.float16))
+        if lora_at.shape != (k, r) or lora_dh.shape[0] != M:
+            raise ValueError("lora_dh [M, r] needs lora_at [K, r]")
+        lora_dh, lora_at = lora_dh.contiguous(), lora_at.contiguous()
     if mask is not None:
         if mask.dtype != torch.uint8 or mask.shape != (M, k):
             raise ValueError("mask must be uint8 [M, K]")
         mask = mask.contiguous()
-    ws = _ws(M, k, n, dy2d.device, cfg, splits)
+    ws = _ws(M, k, n, dy2d.device, cfg, splits, ws)
     _lib.call("mxs_nf4_linear_bwd_dx", _lib.ptr(dy2d), M, n, k, *_nf4_args(packed, state),
-              _lib.ptr(lora_dh), _lib.ptr(lora_a), r, _lib.ptr(mask), float(mask_scale),
+              _lib.ptr(lora_dh), _lib.ptr(lora_at), r, _lib.ptr(mask), float(mask_scale),
               _lib.ptr(dx), _lib.ptr(ws), cfg, splits, _lib.stream_of(dy2d.device))
     return dx
+
+
+def transpose(t2d):
+    """[rows, cols] fp16 -> [cols, rows] fp16 on the GPU (mxs_transpose_f16)."""
+    t2d = t2d.contiguous()
+    rows, cols = t2d.shape
+    out = torch.empty((cols, rows), dtype=torch.float16, device=t2d.device)
+    _lib.call("mxs_transpose_f16", _lib.ptr(t2d), rows, cols, _lib.ptr(out),
+              _lib.stream_of(t2d.device))
+    return out
+
+
+def lora_workspace(M, K, N, r, device):
+    """A fresh workspace for the LoRA kernels of one K -> N projection at M tokens."""
+    return new_workspace(lora_workspace_bytes(M, K, N, r), device)
 
 
 def _ldt(M):
     return (M + 7) // 8 * 8
 
 
-def lora_h(x2d, lora_a, s, mask=None, mask_scale=1.0):
-    """(h, ht): h = fp16(s * drop(x) @ A^T) [M, r] and its transpose [r, ldt]."""
+def lora_h(x2d, lora_a, s, mask=None, mask_scale=1.0, ws=None, n_out=None, want_at=False):
+    """(h, ht[, at]): h = fp16(s * drop(x) @ A^T) [M, r], its transpose [r, ldt], and with
+    want_at lora_A transposed [K, r] (the operand of nf4_linear_bwd_dx), one launch."""
     x2d = x2d.contiguous()
     lora_a = lora_a.to(torch.float16).contiguous()
     M, K = x2d.shape
     r = lora_a.shape[0]
+    ws = _workspace(lora_workspace_bytes(M, K, n_out or K, r), x2d.device, ws)
     h = torch.empty((M, r), dtype=torch.float16, device=x2d.device)
     ht = torch.empty((r, _ldt(M)), dtype=torch.float16, device=x2d.device)
+    at = torch.empty((K, r), dtype=torch.float16, device=x2d.device) if want_at else None
     _lib.call("mxs_lora_h", _lib.ptr(x2d), M, K, _lib.ptr(lora_a), r, _lib.ptr(_c(mask)),
-              float(mask_scale), float(s), _lib.ptr(h), _lib.ptr(ht), ht.shape[1],
-              _lib.stream_of(x2d.device))
-    return h, ht
+              float(mask_scale), float(s), _lib.ptr(h), _lib.ptr(ht), ht.shape[1], _lib.ptr(at),
+              _lib.ptr(ws), _lib.stream_of(x2d.device))
+    return (h, ht, at) if want_at else (h, ht)
 
 
-def lora_dh(dy2d, lora_b, s):
+def lora_dh(dy2d, lora_b, s, ws=None, k_in=None):
     """(dh, dht): dh = fp16(s * dY @ B) [M, r] and its transpose [r, ldt]."""
     dy2d = dy2d.contiguous()
     lora_b = lora_b.to(torch.float16).contiguous()
     M, N = dy2d.shape
     r = lora_b.shape[1]
+    ws = _workspace(lora_workspace_bytes(M, k_in or N, N, r), dy2d.device, ws)
     dh = torch.empty((M, r), dtype=torch.float16, device=dy2d.device)
     dht = torch.empty((r, _ldt(M)), dtype=torch.float16, device=dy2d.device)
     _lib.call("mxs_lora_dh", _lib.ptr(dy2d), M, N, _lib.ptr(lora_b), r, float(s), _lib.ptr(dh),
-              _lib.ptr(dht), dht.shape[1], _lib.stream_of(dy2d.device))
+              _lib.ptr(dht), dht.shape[1], _lib.ptr(ws), _lib.stream_of(dy2d.device))
     return dh, dht
 
 
-def lora_grad_a(dht, x2d, mask=None, mask_scale=1.0):
+def lora_grads(dht, ht, x2d, dy2d, mask=None, mask_scale=1.0, want_a=True, want_b=True,
+               ws=None):
+    """(dA, dB) in one launch: dA = dh^T @ drop(x) fp32 [r, K], dB = dY^T @ h fp32 [N, r]
+    (None where not wanted)."""
+    x2d, dy2d = x2d.contiguous(), dy2d.contiguous()
+    M, K = x2d.shape
+    N = dy2d.shape[1]
+    r = dht.shape[0]
+    if dy2d.shape[0] != M or ht.shape != dht.shape:
+        raise ValueError("x, dy and the transposed LoRA activations disagree")
+    ws = _workspace(lora_workspace_bytes(M, K, N, r), x2d.device, ws)
+    da = torch.empty((r, K), dtype=torch.float32, device=x2d.device) if want_a else None
+    db = torch.empty((N, r), dtype=torch.float32, device=x2d.device) if want_b else None
+    if da is None and db is None:
+        return None, None
+    _lib.call("mxs_lora_grads", _lib.ptr(dht), _lib.ptr(ht), dht.shape[1], _lib.ptr(x2d),
+              _lib.ptr(dy2d), M, K, N, r, _lib.ptr(_c(mask)), float(mask_scale), _lib.ptr(da),
+              _lib.ptr(db), _lib.ptr(ws), _lib.stream_of(x2d.device))
+    return da, db
+
+
+def lora_grad_a(dht, x2d, mask=None, mask_scale=1.0, ws=None):
     """dA = dh^T @ drop(x), fp32 [r, K]."""
     x2d = x2d.contiguous()
     M, K = x2d.shape
     r = dht.shape[0]
+    ws = _workspace(lora_workspace_bytes(M, K, K, r), x2d.device, ws)
     da = torch.empty((r, K), dtype=torch.float32, device=x2d.device)
     _lib.call("mxs_lora_grad_a", _lib.ptr(dht), dht.shape[1], _lib.ptr(x2d), M, K, r,
-              _lib.ptr(_c(mask)), float(mask_scale), _lib.ptr(da), _lib.stream_of(x2d.device))
+              _lib.ptr(_c(mask)), float(mask_scale), _lib.ptr(da), _lib.ptr(ws),
+              _lib.stream_of(x2d.device))
     return da
 
 
-def lora_grad_b(ht, dy2d):
+def lora_grad_b(ht, dy2d, ws=None):
     """dB = dY^T @ h, fp32 [N, r] (h already carries the scaling s)."""
     dy2d = dy2d.contiguous()
     M, N = dy2d.shape
     r = ht.shape[0]
+    ws = _workspace(lora_workspace_bytes(M, N, N, r), dy2d.device, ws)
     db = torch.empty((N, r), dtype=torch.float32, device=dy2d.device)
     _lib.call("mxs_lora_grad_b", _lib.ptr(ht), ht.shape[1], _lib.ptr(dy2d), M, N, r,
-              _lib.ptr(db), _lib.stream_of(dy2d.device))
+              _lib.ptr(db), _lib.ptr(ws), _lib.stream_of(dy2d.device))
     return db

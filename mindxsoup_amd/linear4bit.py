@@ -89,27 +89,31 @@ class NF4LoraFunction(torch.autograd.Function):
     def forward(ctx, x2d, lora_a, lora_b, packed, state, bias, keep, mask_scale, s):
         a16 = lora_a.to(torch.float16).contiguous()
         b16 = lora_b.to(torch.float16).contiguous()
-        h, ht = kernels.lora_h(x2d, a16, s, keep, mask_scale)
+        n, k = state.shape
+        h, ht, at = kernels.lora_h(x2d, a16, s, keep, mask_scale, n_out=n, want_at=True)
         y = kernels.nf4_linear_fwd(x2d, packed, state, bias, h, b16)
-        ctx.save_for_backward(x2d, keep, ht, a16, b16)
+        ctx.save_for_backward(x2d, keep, ht, at, b16)
         ctx.packed, ctx.state, ctx.mask_scale, ctx.s = packed, state, mask_scale, s
         ctx.dtypes = (lora_a.dtype, lora_b.dtype)
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        x2d, keep, ht, a16, b16 = ctx.saved_tensors
+        x2d, keep, ht, at, b16 = ctx.saved_tensors
         dy = dy.to(torch.float16).contiguous()
-        dh, dht = kernels.lora_dh(dy, b16, ctx.s)
+        n, k = ctx.state.shape
+        dh, dht = kernels.lora_dh(dy, b16, ctx.s, k_in=k)
         dx = None
         if ctx.needs_input_grad[0]:
-            dx = kernels.nf4_linear_bwd_dx(dy, ctx.packed, ctx.state, dh, a16, keep,
-                                           ctx.mask_scale)
-        da = db = None
-        if ctx.needs_input_grad[1]:
-            da = kernels.lora_grad_a(dht, x2d, keep, ctx.mask_scale).to(ctx.dtypes[0])
-        if ctx.needs_input_grad[2]:
-            db = kernels.lora_grad_b(ht, dy).to(ctx.dtypes[1])
+            dx = kernels.nf4_linear_bwd_dx(dy, ctx.packed, ctx.state, dh, None, keep,
+                                           ctx.mask_scale, lora_at=at)
+        da, db = kernels.lora_grads(dht, ht, x2d, dy, keep, ctx.mask_scale,
+                                    want_a=ctx.needs_input_grad[1],
+                                    want_b=ctx.needs_input_grad[2])
+        if da is not None:
+            da = da.to(ctx.dtypes[0])
+        if db is not None:
+            db = db.to(ctx.dtypes[1])
         return dx, da, db, None, None, None, None, None, None
 
 

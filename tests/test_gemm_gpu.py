@@ -178,6 +178,78 @@ def test_lora_kernels_match_oracle(cuda):
     xd = O.dropout_fp16(xn, kn, p).astype(np.float64)
     assert O.max_rel(_np(da), _np(dh).astype(np.float64).T @ xd) < TOL
     assert O.max_rel(_np(db), dyn.astype(np.float64).T @ _np(h).astype(np.float64)) < TOL
+    # the one-launch pair and the A^T side output agree with the separate calls bit for bit
+    h2, ht2, at = kernels.lora_h(x, a, s, keep, 1 / (1 - p), want_at=True)
+    assert torch.equal(h2, h) and torch.equal(ht2, ht)
+    assert torch.equal(at, a.t().contiguous())
+    da2, db2 = kernels.lora_grads(dht, ht, x, dy, keep, 1 / (1 - p))
+    assert torch.equal(da2, da) and torch.equal(db2, db)
+    da3, none = kernels.lora_grads(dht, ht, x, dy, keep, 1 / (1 - p), want_b=False)
+    assert none is None and torch.equal(da3, da)
+
+
+@pytest.mark.parametrize("M", [1, 64, 1000])
+def test_lora_reductions_across_many_workgroups(cuda, M):
+    """Reductions longer than one slice (K = 8960: 18 slices of H; M = 1000: 16 token blocks of
+    dA/dB) are summed in a fixed order: repeated calls give the same bits."""
+    from mindxsoup_amd import kernels
+
+    K, N = 8960, 1536
+    x, a, b, dy, keep = _lora_inputs(cuda, M, K, N, 11)
+    s, p = 2.0, 0.1
+    h, ht = kernels.lora_h(x, a, s, keep, 1 / (1 - p))
+    dh, dht = kernels.lora_dh(dy, b, s)
+    da, db = kernels.lora_grads(dht, ht, x, dy, keep, 1 / (1 - p))
+    xn, an, bn, dyn, kn = (_np(x).astype(np.float16), _np(a).astype(np.float16),
+                           _np(b).astype(np.float16), _np(dy).astype(np.float16),
+                           keep.cpu().numpy())
+    assert O.max_rel(_np(h), s * O.lora_h(xn, an, kn, p)) < TOL
+    assert O.max_rel(_np(dh), s * (dyn.astype(np.float64) @ bn.astype(np.float64))) < TOL
+    xd = O.dropout_fp16(xn, kn, p).astype(np.float64)
+    assert O.max_rel(_np(da), _np(dh).astype(np.float64).T @ xd) < TOL
+    assert O.max_rel(_np(db), dyn.astype(np.float64).T @ _np(h).astype(np.float64)) < TOL
+    for _ in range(2):
+        h2, _ = kernels.lora_h(x, a, s, keep, 1 / (1 - p))
+        da2, db2 = kernels.lora_grads(dht, ht, x, dy, keep, 1 / (1 - p))
+        assert torch.equal(h2, h) and torch.equal(da2, da) and torch.equal(db2, db)
+
+
+def test_lora_grads_without_tokens(cuda):
+    from mindxsoup_amd import kernels
+
+    r, K, N = 16, 1536, 256
+    ht = torch.zeros((r, 0), dtype=torch.float16, device=cuda)
+    x = torch.empty((0, K), dtype=torch.float16, device=cuda)
+    dy = torch.empty((0, N), dtype=torch.float16, device=cuda)
+    da, db = kernels.lora_grads(ht, ht, x, dy)
+    assert torch.count_nonzero(da) == 0 and torch.count_nonzero(db) == 0
+    assert da.shape == (r, K) and db.shape == (N, r)
+
+
+@pytest.mark.parametrize("cfg,splits", [(-1, 1), (4, 4), (9, 4), (3, 2)])
+def test_split_k_is_deterministic_on_a_reused_workspace(cuda, cfg, splits):
+    """Split-K partials are summed in split order: repeated calls (and a call of another shape
+    in between, on the same workspace) give identical bits."""
+    from mindxsoup_amd import kernels
+
+    layer = _layer(cuda, 1536, 8960, 12)
+    st = layer.weight.quant_state
+    packed = layer.weight.data.view(-1, 1)
+    g = torch.Generator(device=cuda)
+    g.manual_seed(13)
+    x = torch.randn((700, 8960), device=cuda, generator=g).half()
+    dy = torch.randn((700, 1536), device=cuda, generator=g).half()
+    ws = kernels.new_workspace(max(kernels.gemm_workspace_bytes(700, 1536, 8960, cfg, splits),
+                                   kernels.gemm_workspace_bytes(700, 8960, 1536, cfg, splits)),
+                               cuda)
+    y0 = kernels.nf4_linear_fwd(x, packed, st, cfg=cfg, splits=splits, ws=ws)
+    dx0 = kernels.nf4_linear_bwd_dx(dy, packed, st, cfg=cfg, splits=splits, ws=ws)
+    for _ in range(2):
+        y = kernels.nf4_linear_fwd(x, packed, st, cfg=cfg, splits=splits, ws=ws)
+        dx = kernels.nf4_linear_bwd_dx(dy, packed, st, cfg=cfg, splits=splits, ws=ws)
+        assert torch.equal(y, y0) and torch.equal(dx, dx0)
+    w = _w_oracle(layer)
+    assert O.max_rel(_np(y0), O.linear_fwd(_np(x).astype(np.float16), w)) < TOL
 
 
 def test_lora_module_forward_backward(cuda):
