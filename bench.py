@@ -35,6 +35,39 @@ PROJ = [("q", 1536, 1536), ("k", 256, 1536), ("v", 256, 1536), ("o", 1536, 1536)
 HBM_PEAK_GBS = 8000.0
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "nf4_dequant_model_traffic.txt")
+
+
+def measured_traffic(path=TRAFFIC_FILE):
+    """HBM bytes per launch of the dequant kernel, from the committed rocprofv3 PMC summary
+    (FETCH_SIZE + WRITE_SIZE scaled by the copy-kernel calibration); None without it."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        pass
+    return None
+
+
+def calibrate(dev, nbytes=1 << 30, reps=5):
+    """A plain device-to-device copy of known size, for scaling the PMC byte counters: each of
+    the `reps` copy launches reads nbytes and writes nbytes."""
+    src = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / reps * 1e3
+    print(json.dumps({"calibration": "copy", "bytes_read_per_launch": nbytes,
+                      "bytes_written_per_launch": nbytes, "launches": reps,
+                      "ms_per_launch": round(ms, 4),
+                      "gbs": round(2 * nbytes / ms / 1e6, 1)}), flush=True)
+
+
 def model_weights(dev, seed=0):
     """All 196 NF4 weights back to back: N(0, 0.02) fp16 quantized on the GPU."""
     from mindxsoup_amd.quant import quantize_4bit
@@ -194,21 +227,21 @@ def shared_workspace(dev):
 def proj_fwd(p, s=ALPHA / RANK):
     from mindxsoup_amd import kernels
 
-    h, ht, at = kernels.lora_h(p["x"], p["a"], s, p["keep"], 1.0 / (1.0 - P_DROP), ws=p["ws"],
-                               n_out=p["n"], want_at=True)
+    h, ht, at, bt = kernels.lora_h(p["x"], p["a"], s, p["keep"], 1.0 / (1.0 - P_DROP),
+                                   want_at=True, lora_b=p["b"])
     y = kernels.nf4_linear_fwd(p["x"], p["packed"], p["st"], None, h, p["b"], ws=p["ws"])
-    return y, (ht, at)
+    return y, (ht, at, bt)
 
 
 def proj_bwd(p, saved, s=ALPHA / RANK):
     from mindxsoup_amd import kernels
 
-    ht, at = saved
+    ht, at, bt = saved
     ms = 1.0 / (1.0 - P_DROP)
-    dh, dht = kernels.lora_dh(p["dy"], p["b"], s, ws=p["ws"], k_in=p["k"])
+    dh, dht = kernels.lora_dh(p["dy"], None, s, lora_bt=bt)
     dx = kernels.nf4_linear_bwd_dx(p["dy"], p["packed"], p["st"], dh, None, p["keep"], ms,
                                    lora_at=at, ws=p["ws"])
-    da, db = kernels.lora_grads(dht, ht, p["x"], p["dy"], p["keep"], ms, ws=p["ws"])
+    da, db = kernels.lora_grads(dht, ht, p["x"], p["dy"], p["keep"], ms)
     return dx, da, db
 
 
@@ -248,9 +281,8 @@ def bench_fused(dev, steps, warmup):
                                   "tflops": round(fl / ms / 1e9, 1)}
     # the dominant kernel alone: the fused forward GEMM with its LoRA epilogue (gate, up)
     from mindxsoup_amd import kernels
-    hg, _ = kernels.lora_h(gate["x"], gate["a"], 2.0, gate["keep"], 1 / (1 - P_DROP),
-                           ws=gate["ws"])
-    hu, _ = kernels.lora_h(up["x"], up["a"], 2.0, up["keep"], 1 / (1 - P_DROP), ws=up["ws"])
+    hg, _ = kernels.lora_h(gate["x"], gate["a"], 2.0, gate["keep"], 1 / (1 - P_DROP))
+    hu, _ = kernels.lora_h(up["x"], up["a"], 2.0, up["keep"], 1 / (1 - P_DROP))
     ms_k, _ = graph_time(lambda: (kernels.nf4_linear_fwd(gate["x"], gate["packed"], gate["st"],
                                                          None, hg, gate["b"], ws=gate["ws"]),
                                   kernels.nf4_linear_fwd(up["x"], up["packed"], up["st"], None,
@@ -359,6 +391,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="dequant only")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only run a 1 GiB device copy (reference for the PMC byte counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the hot path is "
@@ -367,6 +401,9 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate:
+        calibrate(dev)
+        return
     m = model_weights(dev)
     torch.cuda.synchronize()
     print(f"bench: {len(m['nb'])} NF4 weights resident ({m['packed'].numel() / 1e9:.3f} GB packed)",
@@ -390,7 +427,8 @@ def main():
                    "bytes_per_step": nbytes, "weights": LAYERS * len(PROJ),
                    "packed_bytes": m["packed"].numel(), "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
                      "kernel": "k_dequant_wide<nested, multi, f16>",
                      "kernel_ms": round(ms_kernel, 4)},
     }

@@ -120,25 +120,26 @@ int mxs_nf4_linear_bwd_dx(const void* dy, int M, int N, int K, const void* packe
                           const void* mask, float mask_scale, void* dx, void* workspace, int cfg,
                           int splits, hipStream_t stream);
 
-/* ---- LoRA side branch (peft lora.Linear around the 4-bit base, r % 16 == 0) --------------
+/* ---- LoRA side branch (peft lora.Linear around the 4-bit base, r % 16 == 0, r <= 128) ------
  * The transposed outputs/inputs (ht, dht) are fp16 [r, ldt] with ldt >= M, ldt % 8 == 0 (columns
- * past M hold zeros).  Each call needs `workspace` of mxs_lora_workspace_bytes(M, K, N, r) bytes
- * of device memory (fp32 partial sums, no initial contents needed; one buffer serves all calls
- * of a projection when they run in order on one stream).  Each call is a partial-sum launch and
- * a launch that adds the partials in a fixed order, so results are deterministic. */
+ * past M hold zeros).  Each product is one launch that reduces inside its workgroups, in a
+ * fixed order: results are deterministic.  `workspace` is unused (may be NULL); the size query
+ * returns 0 and is kept so that callers size one buffer for every entry point. */
 int64_t mxs_lora_workspace_bytes(int M, int K, int N, int r);
 
 /* h = fp16(s * drop(x) . A^T) [M, r] and ht = its transpose: lora_A of peft's branch with the
  * reference's dropout (solution/dropout.py:33-35, mask u8 [M,K] or NULL) and the scaling s
- * folded in.  x [M,K] fp16, lora_a [r,K] fp16, K % 32 == 0.  at: NULL or fp16 [K, r], which
- * receives lora_a transposed (the operand mxs_nf4_linear_bwd_dx takes). */
+ * folded in.  x [M,K] fp16, lora_a [r,K] fp16, K % 32 == 0.  Side outputs for the backward
+ * (each optional, NULL to skip): at [K, r] = lora_a^T (the operand mxs_nf4_linear_bwd_dx takes)
+ * and bt [r, N] = lora_b^T for lora_b [N, r] (the operand mxs_lora_dh takes). */
 int mxs_lora_h(const void* x, int M, int K, const void* lora_a, int r, const void* mask,
-               float mask_scale, float s, void* h, void* ht, int ldt, void* at, void* workspace,
-               hipStream_t stream);
+               float mask_scale, float s, void* h, void* ht, int ldt, void* at,
+               const void* lora_b, int N, void* bt, void* workspace, hipStream_t stream);
 
 /* dh = fp16(s * dY . B) [M, r] and dht = its transpose (the gradient reaching lora_B's output,
- * times s).  dy [M,N] fp16, lora_b [N,r] fp16, N % 32 == 0. */
-int mxs_lora_dh(const void* dy, int M, int N, const void* lora_b, int r, float s, void* dh,
+ * times s).  dy [M,N] fp16, lora_bt = lora_B transposed [r, N] fp16 (the bt output of
+ * mxs_lora_h), N % 32 == 0. */
+int mxs_lora_dh(const void* dy, int M, int N, const void* lora_bt, int r, float s, void* dh,
                 void* dht, int ldt, void* workspace, hipStream_t stream);
 
 /* dA[r,K] (fp32) = dh^T . drop(x): lora_A's weight gradient (autograd of peft's nn.Linear). */
@@ -150,9 +151,9 @@ int mxs_lora_grad_a(const void* dht, int ldt, const void* x, int M, int K, int r
 int mxs_lora_grad_b(const void* ht, int ldt, const void* dy, int M, int N, int r, float* db,
                     void* workspace, hipStream_t stream);
 
-/* mxs_lora_grad_a and mxs_lora_grad_b in one pair of launches (either output may be NULL): the two
- * weight gradients autograd computes for peft's lora_A and lora_B (solution/attention.py:197-199
- * under torch.autograd).  M == 0 writes zero gradients. */
+/* mxs_lora_grad_a and mxs_lora_grad_b in one launch (either output may be NULL): the two weight
+ * gradients autograd computes for peft's lora_A and lora_B (solution/attention.py:197-199 under
+ * torch.autograd).  M == 0 writes zero gradients. */
 int mxs_lora_grads(const void* dht, const void* ht, int ldt, const void* x, const void* dy, int M,
                    int K, int N, int r, const void* mask, float mask_scale, float* da, float* db,
                    void* workspace, hipStream_t stream);

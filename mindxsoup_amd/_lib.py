@@ -43,7 +43,7 @@ _SIGNATURES = {
     "mxs_nf4_linear_bwd_dx": [P, I32, I32, I32, P, P, P, P, P, P, P, I32, P, F32, P, P, I32, I32,
                               P],
     "mxs_lora_workspace_bytes": [I32, I32, I32, I32],
-    "mxs_lora_h": [P, I32, I32, P, I32, P, F32, F32, P, P, I32, P, P, P],
+    "mxs_lora_h": [P, I32, I32, P, I32, P, F32, F32, P, P, I32, P, P, I32, P, P, P],
     "mxs_lora_dh": [P, I32, I32, P, I32, F32, P, P, I32, P, P],
     "mxs_lora_grad_a": [P, I32, P, I32, I32, I32, P, F32, P, P, P],
     "mxs_lora_grad_b": [P, I32, P, I32, I32, I32, P, P, P],

@@ -11,227 +11,236 @@
 // and dHs . A (= the LoRA part of dX before the dropout mask) without another multiply, and
 // dB = s * dY^T . H = dY^T . Hs.
 //
-// These products are thin (r = 16) and read a few MB each, so they are spread over many
-// workgroups: each computes a partial over one slice of the reduction with
-// v_mfma_f32_16x16x32_f16 and writes it to a workspace, and a small second kernel sums the slices
-// in a fixed order (deterministic) and writes the results.  (Summing in the last-arriving
-// workgroup instead needs agent-scope fences, which on the multi-XCD gfx950 write back and
-// invalidate whole L2s; measured, that cost more than the second launch.)
-//   rows kernel (Hs, dHs): workgroup = 16 tokens x one reduction slice, 4 waves in LDS sum.
-//   cols kernel (dA and dB in one launch):  reduction over tokens; each lane loads an 8-token x 8-column block
-//     of the row-major fp16 input and regroups it in registers into 8 MFMA operands (one per
-//     column), so a wave covers 128 columns per 32-token step without a transpose in memory.
+// These products are thin (r = 16) and read a few MB each; each is ONE launch with no partial
+// sums in memory: a workgroup owns a block of output rows (Hs, dHs: 16 tokens) or columns
+// (dA, dB: 32-128 columns) and splits the reduction over up to 16 waves, which add their
+// v_mfma_f32_16x16x32_f16 accumulators in LDS in a fixed order (deterministic).  Summing partials
+// across workgroups would need a second launch or agent-scope fences (on the multi-XCD gfx950,
+// write-back and invalidation of whole L2s): both measured slower than these kernels.
+//   rows kernel: lane (row l%16, k-group l/16) loads 16-byte fragments of X (plus 8 mask bytes)
+//     and of the r x K operand (lora_A, or lora_B transposed), four 32-wide chunks in flight.
+//   cols kernel: each lane loads an 8-token x CPL-column block of the row-major fp16 input and
+//     regroups it in registers into CPL MFMA operands (one per column), so a wave covers 16*CPL
+//     columns per 32-token step without a transpose in memory; dA and dB share one grid.
+//   The forward rows kernel also writes lora_A^T [K, r] and lora_B^T [r, N] for the backward
+//     (the dX epilogue's operand and the dHs kernel's operand), spread over its workgroups.
 #include "common.h"
 #include "mxs_nf4.h"
 
 namespace mxs {
 
-constexpr int kRowsWaves = 4;     // waves per rows-kernel workgroup
-constexpr int kRowsUnroll = 4;    // 32-wide reduction steps per wave and slice
-constexpr int kColsRows = 64;     // tokens per cols-kernel workgroup (2 waves x 32)
+constexpr int kMaxWaves = 16;        // waves per workgroup (1024 threads)
+constexpr int kMaxRB = 8;            // r <= 128 (r / 16 accumulator blocks)
+constexpr int kChunksInFlight = 4;   // 32-wide reduction chunks loaded per rows-kernel iteration
+constexpr int kColsLds = 64 * 1024;  // LDS budget for the cross-wave sums (bytes)
 
-__device__ __forceinline__ _Float16 drop1(_Float16 x, uint8_t keep, float scale) {
-  return keep ? (_Float16)((float)x * scale) : (_Float16)0.0f;
+__device__ __forceinline__ half8_t drop8(half8_t x, u32x2 keep, float scale) {
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const uint32_t k = (keep[e >> 2] >> (8 * (e & 3))) & 0xFFu;
+    x[e] = k ? (_Float16)((float)x[e] * scale) : (_Float16)0.0f;
+  }
+  return x;
 }
 
-// Reduction slice length (multiple of 32) for the rows kernel.
-constexpr int kRowsSlice = 32 * kRowsWaves * kRowsUnroll;
-static int rows_slices(int K) { return (K + kRowsSlice - 1) / kRowsSlice; }
-
 struct RowsArgs {
-  const _Float16* P;       // [M, K] row-major
+  const _Float16* P;      // [M, K] row-major
   int M, K;
-  const uint8_t* mask;     // [M, K] keep mask or null
+  const uint8_t* mask;    // [M, K] keep mask or null
   float mscale;
-  const _Float16* R;       // R(c, k) = R[c * rs_r + k * rs_k]
-  int64_t rs_r, rs_k;
+  const _Float16* R;      // [r, K] row-major
   int r, ldt;
   float s;
-  _Float16* out;           // [M, r]
-  _Float16* outT;          // [r, ldt], zeros past M
-  _Float16* rt;            // optional [K, r]: R transposed (rs_k == 1 only)
-  float* ws;               // [slices][ldt][r]
+  _Float16* out;          // [M, r]
+  _Float16* outT;         // [r, ldt], zeros past M
+  _Float16* rt;           // optional [K, r] = R^T
+  const _Float16* B;      // optional [N, r]; with bt, bt [r, N] = B^T
+  int N;
+  _Float16* bt;
 };
 
-// Partial of out[m][c] = s * sum_k P[m][k] * R(c, k) over reduction slice blockIdx.y, for the 16
-// rows of blockIdx.x: ws[slice][m][c] fp32.
-__global__ __launch_bounds__(64 * kRowsWaves) void k_lora_rows(RowsArgs a) {
-  __shared__ float red[kRowsWaves][16][17];
+// out[m][c] = fp16(s * sum_k drop(P)[m][k] * R[c][k]) for the 16 rows of blockIdx.x.
+__global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
+  extern __shared__ float red[];  // [waves][16][r + 1]
+  const int nw = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int m0 = blockIdx.x * 16;
-  const int slice = blockIdx.y;
   const int row = m0 + (lane & 15);
-  const int kg = 8 * (lane >> 4);
-  const int kbase = slice * kRowsSlice + wave * 32 * kRowsUnroll;
-  for (int r0 = 0; r0 < a.r; r0 += 16) {
-    const int rr = r0 + (lane & 15);
-    half8_t av[kRowsUnroll], bv[kRowsUnroll];
+  const int g = lane >> 4;
+  const int rbn = a.r >> 4;
+  const int chunks = a.K >> 5;
+  const bool row_ok = row < a.M;
+  const int64_t prow = (int64_t)(row_ok ? row : 0) * a.K + 8 * g;
+  float4_t acc[kMaxRB];
 #pragma unroll
-    for (int u = 0; u < kRowsUnroll; u++) {
-      const int k = kbase + u * 32 + kg;
-      half8_t x = {}, y = {};
-      if (k < a.K) {
-        if (row < a.M) {
-          x = *reinterpret_cast<const half8_t*>(a.P + (int64_t)row * a.K + k);
-          if (a.mask) {
-            const u32x2 mk = *reinterpret_cast<const u32x2*>(a.mask + (int64_t)row * a.K + k);
+  for (int b = 0; b < kMaxRB; b++) acc[b] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  for (int c0 = wave; c0 < chunks; c0 += kChunksInFlight * nw) {
+    half8_t x[kChunksInFlight];
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-              x[e] = drop1(x[e], (uint8_t)(mk[e >> 2] >> (8 * (e & 3))), a.mscale);
-          }
-        }
-        if (a.rs_k == 1) {
-          y = *reinterpret_cast<const half8_t*>(a.R + (int64_t)rr * a.rs_r + k);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; e++) y[e] = a.R[(int64_t)rr * a.rs_r + (int64_t)(k + e) * a.rs_k];
-        }
+    for (int u = 0; u < kChunksInFlight; u++) {
+      const int c = c0 + u * nw;
+      half8_t v = {};
+      if (c < chunks && row_ok) {
+        v = *reinterpret_cast<const half8_t*>(a.P + prow + 32 * c);
+        if (a.mask) v = drop8(v, *reinterpret_cast<const u32x2*>(a.mask + prow + 32 * c), a.mscale);
       }
-      av[u] = x;
-      bv[u] = y;
+      x[u] = v;
     }
-    float4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int u = 0; u < kRowsUnroll; u++)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[u], bv[u], acc, 0, 0, 0);
-    // acc[v] = C[row 4*(lane/16)+v][col lane%16]
+    for (int b = 0; b < kMaxRB; b++) {
+      if (b >= rbn) break;
+      const _Float16* rrow = a.R + (int64_t)(16 * b + (lane & 15)) * a.K + 8 * g;
+      half8_t y[kChunksInFlight];
 #pragma unroll
-    for (int v = 0; v < 4; v++) red[wave][4 * (lane >> 4) + v][lane & 15] = acc[v];
-    __syncthreads();
-    const int i = threadIdx.x >> 4, j = threadIdx.x & 15;
+      for (int u = 0; u < kChunksInFlight; u++) {
+        const int c = c0 + u * nw;
+        y[u] = c < chunks ? *reinterpret_cast<const half8_t*>(rrow + 32 * c) : (half8_t){};
+      }
+#pragma unroll
+      for (int u = 0; u < kChunksInFlight; u++)
+        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[u], y[u], acc[b], 0, 0, 0);
+    }
+  }
+  // acc[b][v] = C[row 4*g + v][column 16*b + lane%16]
+  const int ld = a.r + 1;
+#pragma unroll
+  for (int b = 0; b < kMaxRB; b++) {
+    if (b >= rbn) break;
+#pragma unroll
+    for (int v = 0; v < 4; v++)
+      red[(wave * 16 + 4 * g + v) * ld + 16 * b + (lane & 15)] = acc[b][v];
+  }
+  // side outputs, spread over the workgroups: R^T [K, r] and B^T [r, N]
+  if (a.rt) {
+    const int span = ((a.K + gridDim.x - 1) / gridDim.x + 7) & ~7;
+    const int k_beg = blockIdx.x * span, k_end = min(a.K, k_beg + span);
+    for (int i = threadIdx.x; i < (k_end - k_beg) * a.r; i += blockDim.x) {
+      const int k = k_beg + i / a.r, c = i % a.r;
+      a.rt[(int64_t)k * a.r + c] = a.R[(int64_t)c * a.K + k];
+    }
+  }
+  if (a.bt) {
+    const int span = ((a.N + gridDim.x - 1) / gridDim.x + 7) & ~7;
+    const int n_beg = blockIdx.x * span, n_end = min(a.N, n_beg + span);
+    for (int i = threadIdx.x; i < (n_end - n_beg) * a.r; i += blockDim.x) {
+      const int n = n_beg + i / a.r, c = i % a.r;
+      a.bt[(int64_t)c * a.N + n] = a.B[(int64_t)n * a.r + c];
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 16 * a.r; i += blockDim.x) {
+    const int rr = i / a.r, c = i % a.r;
+    const int m = m0 + rr;
+    if (m >= a.ldt) continue;
     float sum = 0.f;
-#pragma unroll
-    for (int w = 0; w < kRowsWaves; w++) sum += red[w][i][j];
-    if (m0 + i < a.ldt) a.ws[((int64_t)slice * a.ldt + m0 + i) * a.r + r0 + j] = sum;
-    __syncthreads();
+    for (int w = 0; w < nw; w++) sum += red[(w * 16 + rr) * ld + c];
+    const _Float16 h = m < a.M ? (_Float16)(a.s * sum) : (_Float16)0.0f;
+    if (m < a.M) a.out[(int64_t)m * a.r + c] = h;
+    a.outT[(int64_t)c * a.ldt + m] = h;
   }
-  // the first row block also writes this slice of R transposed
-  if (a.rt && blockIdx.x == 0) {
-    for (int idx = threadIdx.x; idx < kRowsSlice * a.r; idx += 64 * kRowsWaves) {
-      const int k = slice * kRowsSlice + idx / a.r, c = idx % a.r;
-      if (k < a.K) a.rt[(int64_t)k * a.r + c] = a.R[(int64_t)c * a.rs_r + k];
-    }
-  }
-}
-
-// out[m][c] = fp16(s * sum over slices of ws) for m < M; outT [r, ldt] with zeros past M.
-__global__ __launch_bounds__(256) void k_lora_rows_finish(RowsArgs a, int slices) {
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= a.ldt * a.r) return;
-  const int m = idx / a.r, c = idx % a.r;
-  float sum = 0.f;
-  for (int z = 0; z < slices; z++) sum += a.ws[((int64_t)z * a.ldt + m) * a.r + c];
-  const _Float16 h = m < a.M ? (_Float16)(a.s * sum) : (_Float16)0.0f;
-  if (m < a.M) a.out[(int64_t)m * a.r + c] = h;
-  a.outT[(int64_t)c * a.ldt + m] = h;
 }
 
 struct ColsProblem {
-  const _Float16* PT;      // [r, ldt] (transposed LoRA activations)
-  const _Float16* Q;       // [M, Nq] row-major
-  const uint8_t* mask;     // [M, Nq] keep mask or null
+  const _Float16* PT;     // [r, ldt] (transposed LoRA activations, zeros past M)
+  const _Float16* Q;      // [M, Nq] row-major
+  const uint8_t* mask;    // [M, Nq] keep mask or null
   float mscale;
   int Nq;
-  float* out;              // [r, Nq] (out_rn) or [Nq, r]
+  float* out;             // [r, Nq] (out_rn) or [Nq, r]
   int out_rn;
-  float* ws;               // [token blocks][r][Nq]
 };
 
-// Partial of out[j][n] = sum_m PT[j][m] * Q[m][n] over the 64 tokens of blockIdx.y, for problem
-// blockIdx.z (dA and dB share the launch): workgroup = 128 columns, 2 waves of 32 tokens, LDS
-// sum; ws[token block][j][n] fp32.
-__global__ __launch_bounds__(128) void k_lora_cols(ColsProblem p0, ColsProblem p1, int M, int ldt,
-                                                  int r) {
-  __shared__ float red[16][129];
-  const ColsProblem a = blockIdx.z == 0 ? p0 : p1;
-  const int nb = blockIdx.x * 128;
-  if (nb >= a.Nq) return;  // whole workgroup (the wider problem sets the grid)
+template <int CPL> struct ColsVec;
+template <> struct ColsVec<2> { typedef uint32_t T; typedef uint16_t MT; };
+template <> struct ColsVec<4> { typedef u32x2 T; typedef uint32_t MT; };
+template <> struct ColsVec<8> { typedef u32x4 T; typedef u32x2 MT; };
+
+// out[j][n] = sum_m PT[j][m] * Q[m][n] over all tokens, for the 16*CPL columns of this
+// workgroup: blockIdx.x < cb0 is problem p0 (dA), the rest p1 (dB).  Waves take 32-token steps
+// in turn and add their accumulators in LDS.
+template <int CPL>
+__global__ __launch_bounds__(1024) void k_lora_cols(ColsProblem p0, ColsProblem p1, int cb0, int M,
+                                                   int ldt, int r) {
+  typedef typename ColsVec<CPL>::T VT;
+  typedef typename ColsVec<CPL>::MT MT;
+  constexpr int WC = 16 * CPL;  // columns per workgroup
+  extern __shared__ float red[];  // [waves][r][WC + 1]
+  const bool second = (int)blockIdx.x >= cb0;
+  const ColsProblem a = second ? p1 : p0;
+  const int nb = (second ? (int)blockIdx.x - cb0 : (int)blockIdx.x) * WC;
+  const int nw = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int mblk = blockIdx.y;
-  const int ln = lane & 15;  // columns nb + 8*ln .. +8
-  const int lg = lane >> 4;  // tokens mb .. +8
-  const int col = nb + 8 * ln;
-  const int mb = mblk * kColsRows + wave * 32 + 8 * lg;
-  u32x4 rows[8];
+  const int ln = lane & 15;  // columns nb + CPL*ln .. +CPL
+  const int lg = lane >> 4;  // tokens t0 + 8*lg .. +8
+  const int col = nb + CPL * ln;
+  const bool col_ok = col < a.Nq;
+  const int ld = WC + 1;
+  for (int b = 0; b < (r >> 4); b++) {  // r-blocks of 16 (the input is re-read per block)
+    float4_t acc[CPL];
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const int m = mb + e;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (m < M && col < a.Nq) {
-      v = *reinterpret_cast<const u32x4*>(a.Q + (int64_t)m * a.Nq + col);
-      if (a.mask) {
-        const u32x2 mk = *reinterpret_cast<const u32x2*>(a.mask + (int64_t)m * a.Nq + col);
-        half8_t h = __builtin_bit_cast(half8_t, v);
+    for (int c = 0; c < CPL; c++) acc[c] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    for (int t0 = wave * 32; t0 < M; t0 += nw * 32) {
+      const int mb = t0 + 8 * lg;
+      half8_t av = {};
+      if (mb < ldt) av = *reinterpret_cast<const half8_t*>(a.PT + (int64_t)(16 * b + ln) * ldt + mb);
+      VT rows[8];
 #pragma unroll
-        for (int c = 0; c < 8; c++)
-          h[c] = drop1(h[c], (uint8_t)(mk[c >> 2] >> (8 * (c & 3))), a.mscale);
-        v = __builtin_bit_cast(u32x4, h);
+      for (int e = 0; e < 8; e++) {
+        const int m = mb + e;
+        VT v = {};
+        if (m < M && col_ok) {
+          v = *reinterpret_cast<const VT*>(a.Q + (int64_t)m * a.Nq + col);
+          if (a.mask) {
+            const MT mk = *reinterpret_cast<const MT*>(a.mask + (int64_t)m * a.Nq + col);
+            _Float16 h[CPL];
+            __builtin_memcpy(h, &v, sizeof(v));
+#pragma unroll
+            for (int c = 0; c < CPL; c++) {
+              uint32_t kb;
+              if constexpr (CPL == 8) kb = (mk[c >> 2] >> (8 * (c & 3))) & 0xFFu;
+              else kb = ((uint32_t)mk >> (8 * c)) & 0xFFu;
+              h[c] = kb ? (_Float16)((float)h[c] * a.mscale) : (_Float16)0.0f;
+            }
+            __builtin_memcpy(&v, h, sizeof(v));
+          }
+        }
+        rows[e] = v;
+      }
+      _Float16 hv[8][CPL];
+#pragma unroll
+      for (int e = 0; e < 8; e++) __builtin_memcpy(hv[e], &rows[e], sizeof(VT));
+#pragma unroll
+      for (int c = 0; c < CPL; c++) {
+        half8_t bv;
+#pragma unroll
+        for (int e = 0; e < 8; e++) bv[e] = hv[e][c];
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[c], 0, 0, 0);
       }
     }
-    rows[e] = v;
+    // acc[c][v] = C[j = 16*b + 4*lg + v][column nb + CPL*ln + c]
+#pragma unroll
+    for (int c = 0; c < CPL; c++)
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+        red[(wave * r + 16 * b + 4 * lg + v) * ld + CPL * ln + c] = acc[c][v];
   }
-  for (int r0 = 0; r0 < r; r0 += 16) {
-    half8_t av = {};
-    if (mb < ldt) av = *reinterpret_cast<const half8_t*>(a.PT + (int64_t)(r0 + ln) * ldt + mb);
-    float4_t acc[8];
-#pragma unroll
-    for (int c = 0; c < 8; c++) {
-      half8_t b;
-#pragma unroll
-      for (int e = 0; e < 8; e++) b[e] = __builtin_bit_cast(half8_t, rows[e])[c];
-      acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, (float4_t){0.f, 0.f, 0.f, 0.f}, 0,
-                                                      0, 0);
-    }
-    // acc[c][v] = C[j = 4*lg + v][column nb + 8*ln + c]; wave 1 stores, wave 0 adds
-    if (wave == 1) {
-#pragma unroll
-      for (int c = 0; c < 8; c++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) red[4 * lg + v][8 * ln + c] = acc[c][v];
-    }
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-      for (int c = 0; c < 8; c++)
-#pragma unroll
-        for (int v = 0; v < 4; v++) red[4 * lg + v][8 * ln + c] += acc[c][v];
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < 16 * 128; idx += 128) {
-      const int i = idx >> 7, j = idx & 127;
-      const int n = nb + j;
-      if (n < a.Nq) a.ws[((int64_t)mblk * r + r0 + i) * a.Nq + n] = red[i][j];
-    }
-    __syncthreads();
+  __syncthreads();
+  for (int i = threadIdx.x; i < r * WC; i += blockDim.x) {
+    const int j = i / WC, n = nb + i % WC;
+    if (n >= a.Nq) continue;
+    float sum = 0.f;
+    for (int w = 0; w < nw; w++) sum += red[(w * r + j) * ld + i % WC];
+    if (a.out_rn) a.out[(int64_t)j * a.Nq + n] = sum;
+    else a.out[(int64_t)n * r + j] = sum;
   }
-}
-
-// out = sum over token blocks of ws, laid out [r, Nq] (out_rn) or [Nq, r]; problem blockIdx.y.
-__global__ __launch_bounds__(256) void k_lora_cols_finish(ColsProblem p0, ColsProblem p1,
-                                                         int blocks, int r) {
-  const ColsProblem a = blockIdx.y == 0 ? p0 : p1;
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= r * a.Nq) return;
-  const int j = idx / a.Nq, n = idx % a.Nq;
-  float sum = 0.f;
-  for (int z = 0; z < blocks; z++) sum += a.ws[((int64_t)z * r + j) * a.Nq + n];
-  if (a.out_rn) a.out[(int64_t)j * a.Nq + n] = sum;
-  else a.out[(int64_t)n * r + j] = sum;
 }
 
 // dst[0, n) = 0 (a kernel, not hipMemsetAsync, so that the call can be captured in a graph).
 __global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ dst, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n) dst[i] = 0.f;
-}
-
-static int zero_f32(float* dst, int64_t n, hipStream_t stream) {
-  if (n <= 0) return MXS_OK;
-  hipLaunchKernelGGL(k_zero_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, dst, n);
-  const hipError_t e = hipGetLastError();
-  return e == hipSuccess ? MXS_OK : (int)e;
 }
 
 // dst [cols, rows] = src [rows, cols]^T (fp16).
@@ -249,42 +258,48 @@ static int check_launch() {
   return e == hipSuccess ? MXS_OK : (int)e;
 }
 
-static int64_t rows_ws_bytes(int K, int ldt, int r) {
-  return (int64_t)rows_slices(K) * ldt * r * (int64_t)sizeof(float);
-}
-
-static int64_t cols_ws_bytes(int M, int N, int r) {
-  const int blocks = (M + kColsRows - 1) / kColsRows;
-  return (int64_t)blocks * r * N * (int64_t)sizeof(float);
-}
-
-static int rows_launch(RowsArgs a, void* workspace, hipStream_t stream) {
-  a.ws = static_cast<float*>(workspace);
-  const int slices = rows_slices(a.K);
-  hipLaunchKernelGGL(k_lora_rows, dim3((a.ldt + 15) / 16, slices), dim3(64 * kRowsWaves), 0,
-                     stream, a);
-  hipLaunchKernelGGL(k_lora_rows_finish, dim3((a.ldt * a.r + 255) / 256), dim3(256), 0, stream, a,
-                     slices);
+static int zero_f32(float* dst, int64_t n, hipStream_t stream) {
+  if (n <= 0) return MXS_OK;
+  hipLaunchKernelGGL(k_zero_f32, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, dst, n);
   return check_launch();
 }
 
-// Partial and finish launches for one or two cols problems (p1 ignored when nprob == 1).
-static int cols_launch(ColsProblem p0, ColsProblem p1, int nprob, int M, int ldt, int r,
-                       void* workspace, hipStream_t stream) {
-  const int blocks = (M + kColsRows - 1) / kColsRows;
-  const int cb0 = (p0.Nq + 127) / 128, cb1 = nprob > 1 ? (p1.Nq + 127) / 128 : 0;
-  p0.ws = static_cast<float*>(workspace);
-  if (nprob > 1) {
-    p1.ws = p0.ws + (int64_t)blocks * r * p0.Nq;
-  } else {
-    p1 = p0;
-  }
-  hipLaunchKernelGGL(k_lora_cols, dim3(cb0 > cb1 ? cb0 : cb1, blocks, nprob), dim3(128), 0,
-                     stream, p0, p1, M, ldt, r);
-  const int nmax = p0.Nq > p1.Nq ? p0.Nq : p1.Nq;
-  hipLaunchKernelGGL(k_lora_cols_finish, dim3((r * nmax + 255) / 256, nprob), dim3(256), 0, stream,
-                     p0, p1, blocks, r);
+// Waves for a reduction of `steps` units: about three units per wave, 4..16 waves.
+static int waves_for(int steps) {
+  int w = (steps + 2) / 3;
+  return w < 4 ? 4 : w > kMaxWaves ? kMaxWaves : w;
+}
+
+static int rows_launch(const RowsArgs& a, hipStream_t stream) {
+  int nw = waves_for(a.K / 32);
+  while (nw > 1 && (size_t)nw * 16 * (a.r + 1) * sizeof(float) > (size_t)kColsLds) nw--;
+  const size_t lds = (size_t)nw * 16 * (a.r + 1) * sizeof(float);
+  hipLaunchKernelGGL(k_lora_rows, dim3((a.ldt + 15) / 16), dim3(64 * nw), lds, stream, a);
   return check_launch();
+}
+
+template <int CPL>
+static int cols_launch_t(const ColsProblem& p0, const ColsProblem& p1, int nprob, int M, int ldt,
+                         int r, hipStream_t stream) {
+  constexpr int WC = 16 * CPL;
+  const int cb0 = (p0.Nq + WC - 1) / WC, cb1 = nprob > 1 ? (p1.Nq + WC - 1) / WC : 0;
+  int nw = waves_for((M + 31) / 32);
+  const int per_wave = r * (WC + 1) * (int)sizeof(float);
+  while (nw > 1 && nw * per_wave > kColsLds) nw--;
+  if (nw * per_wave > kColsLds) return MXS_ERR_SIZE;
+  hipLaunchKernelGGL(k_lora_cols<CPL>, dim3(cb0 + cb1), dim3(64 * nw), (size_t)nw * per_wave,
+                     stream, p0, p1, cb0, M, ldt, r);
+  return check_launch();
+}
+
+// One launch for one or two cols problems (p1 ignored when nprob == 1).  Columns per lane: the
+// widest that still gives the launch enough workgroups.
+static int cols_launch(const ColsProblem& p0, const ColsProblem& p1, int nprob, int M, int ldt,
+                       int r, hipStream_t stream) {
+  const int n_tot = p0.Nq + (nprob > 1 ? p1.Nq : 0);
+  if (n_tot / 128 >= 160) return cols_launch_t<8>(p0, p1, nprob, M, ldt, r, stream);
+  if (n_tot / 64 >= 96) return cols_launch_t<4>(p0, p1, nprob, M, ldt, r, stream);
+  return cols_launch_t<2>(p0, p1, nprob, M, ldt, r, stream);
 }
 
 }  // namespace mxs
@@ -294,22 +309,18 @@ using namespace mxs;
 extern "C" {
 
 int64_t mxs_lora_workspace_bytes(int M, int K, int N, int r) {
-  const int ldt = (M + 7) / 8 * 8;
-  int64_t b = rows_ws_bytes(K, ldt, r);
-  const int64_t b2 = rows_ws_bytes(N, ldt, r);
-  if (b2 > b) b = b2;
-  const int64_t c = cols_ws_bytes(M, K, r) + cols_ws_bytes(M, N, r);
-  if (c > b) b = c;
-  return b;
+  (void)M; (void)K; (void)N; (void)r;
+  return 0;  // every LoRA product reduces inside its workgroups
 }
 
 int mxs_lora_h(const void* x, int M, int K, const void* lora_a, int r, const void* mask,
-               float mask_scale, float s, void* h, void* ht, int ldt, void* at, void* workspace,
-               hipStream_t stream) {
-  if (M < 0 || K < 0 || r <= 0) return MXS_ERR_ARG;
+               float mask_scale, float s, void* h, void* ht, int ldt, void* at,
+               const void* lora_b, int N, void* bt, void* workspace, hipStream_t stream) {
+  (void)workspace;
+  if (M < 0 || K < 0 || N < 0 || r <= 0) return MXS_ERR_ARG;
   if (M == 0) return MXS_OK;
-  if (!x || !lora_a || !h || !ht || !workspace) return MXS_ERR_ARG;
-  if (r % 16 || K % 32 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  if (!x || !lora_a || !h || !ht || (bt && !lora_b)) return MXS_ERR_ARG;
+  if (r % 16 || r > 16 * kMaxRB || K % 32 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
   if (((uintptr_t)x % 16) || ((uintptr_t)lora_a % 16) || (mask && ((uintptr_t)mask % 8)))
     return MXS_ERR_ALIGN;
   RowsArgs a{};
@@ -319,55 +330,56 @@ int mxs_lora_h(const void* x, int M, int K, const void* lora_a, int r, const voi
   a.mask = static_cast<const uint8_t*>(mask);
   a.mscale = mask_scale;
   a.R = static_cast<const _Float16*>(lora_a);
-  a.rs_r = K;
-  a.rs_k = 1;
   a.r = r;
   a.ldt = ldt;
   a.s = s;
   a.out = static_cast<_Float16*>(h);
   a.outT = static_cast<_Float16*>(ht);
   a.rt = static_cast<_Float16*>(at);
-  return rows_launch(a, workspace, stream);
+  a.B = static_cast<const _Float16*>(lora_b);
+  a.N = N;
+  a.bt = static_cast<_Float16*>(bt);
+  return rows_launch(a, stream);
 }
 
-int mxs_lora_dh(const void* dy, int M, int N, const void* lora_b, int r, float s, void* dh,
+int mxs_lora_dh(const void* dy, int M, int N, const void* lora_bt, int r, float s, void* dh,
                 void* dht, int ldt, void* workspace, hipStream_t stream) {
+  (void)workspace;
   if (M < 0 || N < 0 || r <= 0) return MXS_ERR_ARG;
   if (M == 0) return MXS_OK;
-  if (!dy || !lora_b || !dh || !dht || !workspace) return MXS_ERR_ARG;
-  if (r % 16 || N % 32 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
-  if ((uintptr_t)dy % 16) return MXS_ERR_ALIGN;
+  if (!dy || !lora_bt || !dh || !dht) return MXS_ERR_ARG;
+  if (r % 16 || r > 16 * kMaxRB || N % 32 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  if (((uintptr_t)dy % 16) || ((uintptr_t)lora_bt % 16)) return MXS_ERR_ALIGN;
   RowsArgs a{};
   a.P = static_cast<const _Float16*>(dy);
   a.M = M;
   a.K = N;
   a.mscale = 1.0f;
-  a.R = static_cast<const _Float16*>(lora_b);
-  a.rs_r = 1;
-  a.rs_k = r;
+  a.R = static_cast<const _Float16*>(lora_bt);
   a.r = r;
   a.ldt = ldt;
   a.s = s;
   a.out = static_cast<_Float16*>(dh);
   a.outT = static_cast<_Float16*>(dht);
-  return rows_launch(a, workspace, stream);
+  return rows_launch(a, stream);
 }
 
 int mxs_lora_grads(const void* dht, const void* ht, int ldt, const void* x, const void* dy, int M,
                    int K, int N, int r, const void* mask, float mask_scale, float* da, float* db,
                    void* workspace, hipStream_t stream) {
+  (void)workspace;
   if (M < 0 || K < 0 || N < 0 || r <= 0) return MXS_ERR_ARG;
   if (!da && !db) return MXS_ERR_ARG;
+  if (r % 16 || r > 16 * kMaxRB) return MXS_ERR_SIZE;
   if (M == 0) {  // empty reduction: zero gradients
     const int e = da ? zero_f32(da, (int64_t)r * K, stream) : MXS_OK;
     if (e != MXS_OK) return e;
     return db ? zero_f32(db, (int64_t)N * r, stream) : MXS_OK;
   }
-  if ((da && (!dht || !x)) || (db && (!ht || !dy)) || !workspace) return MXS_ERR_ARG;
-  if (r % 16 || K % 8 || N % 8 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
-  if ((x && ((uintptr_t)x % 16)) || (dy && ((uintptr_t)dy % 16)) ||
-      (mask && ((uintptr_t)mask % 8)) || (dht && ((uintptr_t)dht % 16)) ||
-      (ht && ((uintptr_t)ht % 16)))
+  if ((da && (!dht || !x)) || (db && (!ht || !dy))) return MXS_ERR_ARG;
+  if ((da && K % 8) || (db && N % 8) || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  if ((da && ((uintptr_t)x % 16 || (uintptr_t)dht % 16)) ||
+      (db && ((uintptr_t)dy % 16 || (uintptr_t)ht % 16)) || (mask && ((uintptr_t)mask % 8)))
     return MXS_ERR_ALIGN;
   ColsProblem pa{}, pb{};
   pa.PT = static_cast<const _Float16*>(dht);
@@ -384,9 +396,9 @@ int mxs_lora_grads(const void* dht, const void* ht, int ldt, const void* x, cons
   pb.out = db;
   pb.out_rn = 0;
   const bool a_on = da && K > 0, b_on = db && N > 0;
-  if (a_on && b_on) return cols_launch(pa, pb, 2, M, ldt, r, workspace, stream);
-  if (a_on) return cols_launch(pa, pa, 1, M, ldt, r, workspace, stream);
-  if (b_on) return cols_launch(pb, pb, 1, M, ldt, r, workspace, stream);
+  if (a_on && b_on) return cols_launch(pa, pb, 2, M, ldt, r, stream);
+  if (a_on) return cols_launch(pa, pa, 1, M, ldt, r, stream);
+  if (b_on) return cols_launch(pb, pb, 1, M, ldt, r, stream);
   return MXS_OK;
 }
 

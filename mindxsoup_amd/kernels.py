@@ -4,10 +4,11 @@ Every function checks shapes, dtypes and devices, allocates its outputs with tor
 allocator, and launches on the current HIP stream.  Nothing here computes on the CPU or falls
 back to another implementation: an unsupported shape raises.
 
-Workspaces: the split-K GEMMs and the LoRA kernels write fp32 partial sums to a workspace that
-a second small kernel adds up in a fixed order; its contents need no initialisation and are dead
-after the call, so one buffer serves any number of calls issued in order on one stream.  Calls
-take it as `ws` or allocate it from torch's caching allocator.
+Workspaces: the split-K GEMMs write fp32 partial sums to a workspace that a second small kernel
+adds up in a fixed order; its contents need no initialisation and are dead after the call, so
+one buffer serves any number of calls issued in order on one stream.  Calls take it as `ws` or
+allocate it from torch's caching allocator.  The LoRA kernels reduce inside their workgroups
+and need none (their `ws` argument is accepted and ignored).
 """
 
 import torch
@@ -132,43 +133,53 @@ def transpose(t2d):
     return out
 
 
-def lora_workspace(M, K, N, r, device):
-    """A fresh workspace for the LoRA kernels of one K -> N projection at M tokens."""
-    return new_workspace(lora_workspace_bytes(M, K, N, r), device)
-
-
 def _ldt(M):
     return (M + 7) // 8 * 8
 
 
-def lora_h(x2d, lora_a, s, mask=None, mask_scale=1.0, ws=None, n_out=None, want_at=False):
-    """(h, ht[, at]): h = fp16(s * drop(x) @ A^T) [M, r], its transpose [r, ldt], and with
-    want_at lora_A transposed [K, r] (the operand of nf4_linear_bwd_dx), one launch."""
+def lora_h(x2d, lora_a, s, mask=None, mask_scale=1.0, ws=None, n_out=None, want_at=False,
+           lora_b=None):
+    """(h, ht): h = fp16(s * drop(x) @ A^T) [M, r] and its transpose [r, ldt]; with want_at also
+    (at, bt): lora_A^T [K, r] and, given lora_b [N, r], lora_B^T [r, N] (else None) -- the
+    backward's operands, written by the same launch."""
     x2d = x2d.contiguous()
     lora_a = lora_a.to(torch.float16).contiguous()
     M, K = x2d.shape
     r = lora_a.shape[0]
-    ws = _workspace(lora_workspace_bytes(M, K, n_out or K, r), x2d.device, ws)
-    h = torch.empty((M, r), dtype=torch.float16, device=x2d.device)
-    ht = torch.empty((r, _ldt(M)), dtype=torch.float16, device=x2d.device)
-    at = torch.empty((K, r), dtype=torch.float16, device=x2d.device) if want_at else None
+    dev = x2d.device
+    h = torch.empty((M, r), dtype=torch.float16, device=dev)
+    ht = torch.empty((r, _ldt(M)), dtype=torch.float16, device=dev)
+    at = bt = None
+    N = 0
+    if want_at:
+        at = torch.empty((K, r), dtype=torch.float16, device=dev)
+        if lora_b is not None:
+            lora_b = lora_b.to(torch.float16).contiguous()
+            N = lora_b.shape[0]
+            if lora_b.shape != (N, r):
+                raise ValueError("lora_b must be [N, r]")
+            bt = torch.empty((r, N), dtype=torch.float16, device=dev)
     _lib.call("mxs_lora_h", _lib.ptr(x2d), M, K, _lib.ptr(lora_a), r, _lib.ptr(_c(mask)),
               float(mask_scale), float(s), _lib.ptr(h), _lib.ptr(ht), ht.shape[1], _lib.ptr(at),
-              _lib.ptr(ws), _lib.stream_of(x2d.device))
-    return (h, ht, at) if want_at else (h, ht)
+              _lib.ptr(lora_b if bt is not None else None), N, _lib.ptr(bt), _lib.ptr(ws),
+              _lib.stream_of(dev))
+    return (h, ht, at, bt) if want_at else (h, ht)
 
 
-def lora_dh(dy2d, lora_b, s, ws=None, k_in=None):
-    """(dh, dht): dh = fp16(s * dY @ B) [M, r] and its transpose [r, ldt]."""
+def lora_dh(dy2d, lora_b, s, ws=None, k_in=None, lora_bt=None):
+    """(dh, dht): dh = fp16(s * dY @ B) [M, r] and its transpose [r, ldt].  The kernel takes
+    lora_B transposed ([r, N], the bt output of lora_h); given only lora_b it is transposed here."""
     dy2d = dy2d.contiguous()
-    lora_b = lora_b.to(torch.float16).contiguous()
     M, N = dy2d.shape
-    r = lora_b.shape[1]
-    ws = _workspace(lora_workspace_bytes(M, k_in or N, N, r), dy2d.device, ws)
+    if lora_bt is None:
+        lora_bt = lora_b.to(torch.float16).t().contiguous()
+    r = lora_bt.shape[0]
+    if lora_bt.shape != (r, N):
+        raise ValueError("lora_bt must be [r, N]")
     dh = torch.empty((M, r), dtype=torch.float16, device=dy2d.device)
     dht = torch.empty((r, _ldt(M)), dtype=torch.float16, device=dy2d.device)
-    _lib.call("mxs_lora_dh", _lib.ptr(dy2d), M, N, _lib.ptr(lora_b), r, float(s), _lib.ptr(dh),
-              _lib.ptr(dht), dht.shape[1], _lib.ptr(ws), _lib.stream_of(dy2d.device))
+    _lib.call("mxs_lora_dh", _lib.ptr(dy2d), M, N, _lib.ptr(lora_bt.contiguous()), r, float(s),
+              _lib.ptr(dh), _lib.ptr(dht), dht.shape[1], _lib.ptr(ws), _lib.stream_of(dy2d.device))
     return dh, dht
 
 
@@ -182,7 +193,6 @@ def lora_grads(dht, ht, x2d, dy2d, mask=None, mask_scale=1.0, want_a=True, want_
     r = dht.shape[0]
     if dy2d.shape[0] != M or ht.shape != dht.shape:
         raise ValueError("x, dy and the transposed LoRA activations disagree")
-    ws = _workspace(lora_workspace_bytes(M, K, N, r), x2d.device, ws)
     da = torch.empty((r, K), dtype=torch.float32, device=x2d.device) if want_a else None
     db = torch.empty((N, r), dtype=torch.float32, device=x2d.device) if want_b else None
     if da is None and db is None:
@@ -198,7 +208,6 @@ def lora_grad_a(dht, x2d, mask=None, mask_scale=1.0, ws=None):
     x2d = x2d.contiguous()
     M, K = x2d.shape
     r = dht.shape[0]
-    ws = _workspace(lora_workspace_bytes(M, K, K, r), x2d.device, ws)
     da = torch.empty((r, K), dtype=torch.float32, device=x2d.device)
     _lib.call("mxs_lora_grad_a", _lib.ptr(dht), dht.shape[1], _lib.ptr(x2d), M, K, r,
               _lib.ptr(_c(mask)), float(mask_scale), _lib.ptr(da), _lib.ptr(ws),
@@ -211,7 +220,6 @@ def lora_grad_b(ht, dy2d, ws=None):
     dy2d = dy2d.contiguous()
     M, N = dy2d.shape
     r = ht.shape[0]
-    ws = _workspace(lora_workspace_bytes(M, N, N, r), dy2d.device, ws)
     db = torch.empty((N, r), dtype=torch.float32, device=dy2d.device)
     _lib.call("mxs_lora_grad_b", _lib.ptr(ht), ht.shape[1], _lib.ptr(dy2d), M, N, r,
               _lib.ptr(db), _lib.ptr(ws), _lib.stream_of(dy2d.device))

@@ -90,19 +90,19 @@ class NF4LoraFunction(torch.autograd.Function):
         a16 = lora_a.to(torch.float16).contiguous()
         b16 = lora_b.to(torch.float16).contiguous()
         n, k = state.shape
-        h, ht, at = kernels.lora_h(x2d, a16, s, keep, mask_scale, n_out=n, want_at=True)
+        h, ht, at, bt = kernels.lora_h(x2d, a16, s, keep, mask_scale, want_at=True,
+                                       lora_b=b16)
         y = kernels.nf4_linear_fwd(x2d, packed, state, bias, h, b16)
-        ctx.save_for_backward(x2d, keep, ht, at, b16)
+        ctx.save_for_backward(x2d, keep, ht, at, bt)
         ctx.packed, ctx.state, ctx.mask_scale, ctx.s = packed, state, mask_scale, s
         ctx.dtypes = (lora_a.dtype, lora_b.dtype)
         return y
 
     @staticmethod
     def backward(ctx, dy):
-        x2d, keep, ht, at, b16 = ctx.saved_tensors
+        x2d, keep, ht, at, bt = ctx.saved_tensors
         dy = dy.to(torch.float16).contiguous()
-        n, k = ctx.state.shape
-        dh, dht = kernels.lora_dh(dy, b16, ctx.s, k_in=k)
+        dh, dht = kernels.lora_dh(dy, None, ctx.s, lora_bt=bt)
         dx = None
         if ctx.needs_input_grad[0]:
             dx = kernels.nf4_linear_bwd_dx(dy, ctx.packed, ctx.state, dh, None, keep,

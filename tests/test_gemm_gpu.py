@@ -179,9 +179,11 @@ def test_lora_kernels_match_oracle(cuda):
     assert O.max_rel(_np(da), _np(dh).astype(np.float64).T @ xd) < TOL
     assert O.max_rel(_np(db), dyn.astype(np.float64).T @ _np(h).astype(np.float64)) < TOL
     # the one-launch pair and the A^T side output agree with the separate calls bit for bit
-    h2, ht2, at = kernels.lora_h(x, a, s, keep, 1 / (1 - p), want_at=True)
+    h2, ht2, at, bt = kernels.lora_h(x, a, s, keep, 1 / (1 - p), want_at=True, lora_b=b)
     assert torch.equal(h2, h) and torch.equal(ht2, ht)
-    assert torch.equal(at, a.t().contiguous())
+    assert torch.equal(at, a.t().contiguous()) and torch.equal(bt, b.t().contiguous())
+    dh2, _ = kernels.lora_dh(dy, None, s, lora_bt=bt)
+    assert torch.equal(dh2, dh)
     da2, db2 = kernels.lora_grads(dht, ht, x, dy, keep, 1 / (1 - p))
     assert torch.equal(da2, da) and torch.equal(db2, db)
     da3, none = kernels.lora_grads(dht, ht, x, dy, keep, 1 / (1 - p), want_b=False)
