@@ -56,4 +56,25 @@ __device__ __forceinline__ u32x4 decode8(uint32_t w, float s, const float* tab) 
 // expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Workgroup barrier that waits only for this wave's LDS operations (lgkmcnt(0)), not for its
+// global loads: __syncthreads() adds a workgroup fence that waits for every outstanding vector
+// memory instruction, which would drain a multi-stage load pipeline at each barrier.  The empty
+// asm statements keep the compiler from moving memory accesses across the barrier.  Use only
+// where no global store must become visible to the workgroup at this barrier, and wait for
+// direct-to-LDS loads (counted in vmcnt) explicitly before it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maxima
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// vmcnt(N): at most the N most recently issued vector memory instructions of this wave are still
+// outstanding (they complete in issue order).  gfx9 encoding: vmcnt bits 3:0 and 15:14.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N <= 63, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
 }  // namespace mxs

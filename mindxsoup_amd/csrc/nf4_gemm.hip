@@ -13,9 +13,10 @@
 // XOR-swizzled by the row index, so MFMA operand reads and the tile writes are bank-conflict
 // free.
 //
-// Epilogue: + bias, + the LoRA term as one more MFMA per 32x32 tile (K = r), dropout mask on the
-// LoRA term of the input gradient, fp16 store.  With split-K (gridDim.z > 1) each split writes
-// fp32 partials and k_splitk_reduce sums them (split 0 carries bias and LoRA).
+// The accumulators start at bias + the LoRA term (one more MFMA per 32x32 tile with K = r; in
+// the input gradient masked by the dropout keep mask), computed before the main loop; the
+// epilogue stores fp16.  With split-K (gridDim.z > 1) each split writes fp32 partials and
+// k_splitk_reduce sums them (split 0 carries bias and LoRA).
 #include "common.h"
 #include "mxs_nf4.h"
 
@@ -71,19 +72,27 @@ struct Tile {
   static constexpr int LDS_B = BN * kBK;
 };
 
-// Epilogue of one wave's TM x TN tiles of 32x32 at output rows mb.., columns nb...  The MFMAs
-// take the W fragment as their first operand, so each tile is held transposed: lane l keeps row
-// m = mb + 32i + l%32 and, in register group g (4 registers), the 4 consecutive columns
-// n = nb + 32j + 8g + 4(l/32) .. +3 -> one 8-byte fp16 store (or 16-byte fp32 partial) per group.
-// Adds the LoRA term (one more MFMA per tile per 16 ranks, masked by the dropout keep mask in the
-// backward pass) and the bias; split-K partials go to the workspace instead.
+// Accumulator layout of one wave's TM x TN tiles of 32x32 at output rows mb.., columns nb...:
+// the MFMAs take the W fragment as their first operand, so each tile is held transposed: lane l
+// keeps row m = mb + 32i + l%32 and, in register group g (4 registers), the 4 consecutive
+// columns n = nb + 32j + 8g + 4(l/32) .. +3.
+//
+// Accumulator start value: the terms that do not depend on the reduction, computed before the
+// main loop (their loads overlap the first tiles' arrival): bias, and the LoRA term as one MFMA
+// per tile per 16 ranks (masked by the dropout keep mask and scaled in the backward pass).  Only
+// the first split of a split-K launch carries them; the others start at zero.
 template <int TM, int TN, bool BWD>
-__device__ __forceinline__ void epilogue(const GemmArgs& a, float16_t (&acc)[TM][TN], int mb,
+__device__ __forceinline__ void init_acc(const GemmArgs& a, float16_t (&acc)[TM][TN], int mb,
                                          int nb, int lrow, int lseg) {
-  const bool first_split = blockIdx.z == 0;
-  const bool split = gridDim.z > 1;
+#pragma unroll
+  for (int i = 0; i < TM; i++)
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+  if (blockIdx.z != 0) return;
   const bool vec = (a.Nc % 4) == 0 && (a.ldc % 4) == 0;
-  if (a.lora_h && first_split) {
+  if (a.lora_h) {
     // lora_w is [Nc, r] in both directions (the backward pass gets lora_A transposed), so the
     // W-side operand is one 16-byte load per tile and 16 ranks.
     const bool masked = BWD && a.mask;
@@ -98,12 +107,12 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float16_t (&acc)[TM]
           half8_t hf = {}, wf = {};
           if (m < a.M) hf = *reinterpret_cast<const half8_t*>(a.lora_h + (int64_t)m * a.r + r0 + 8 * lseg);
           if (ncol < a.Nc) wf = *reinterpret_cast<const half8_t*>(a.lora_w + (int64_t)ncol * a.r + r0 + 8 * lseg);
-          if (masked)
-            lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, hf, lacc, 0, 0, 0);
-          else
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, hf, acc[i][j], 0, 0, 0);
+          lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, hf, lacc, 0, 0, 0);
         }
-        if (!masked) continue;
+        if (!masked) {
+          acc[i][j] = lacc;
+          continue;
+        }
 #pragma unroll
         for (int g = 0; g < 4; g++) {
           const int n = nb + j * 32 + 8 * g + 4 * lseg;
@@ -119,12 +128,35 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float16_t (&acc)[TM]
           }
 #pragma unroll
           for (int e = 0; e < 4; e++)
-            if ((keep >> (8 * e)) & 0xffu) acc[i][j][4 * g + e] += lacc[4 * g + e] * a.mask_scale;
+            acc[i][j][4 * g + e] = ((keep >> (8 * e)) & 0xffu) ? lacc[4 * g + e] * a.mask_scale : 0.0f;
         }
       }
     }
   }
+  if (a.bias) {
+#pragma unroll
+    for (int j = 0; j < TN; j++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int n = nb + j * 32 + 8 * g + 4 * lseg;
+        float b[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) b[e] = (n + e < a.Nc) ? (float)a.bias[n + e] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) acc[i][j][4 * g + e] += b[e];
+      }
+  }
+}
 
+// Epilogue: fp16 stores of the tiles (one 8-byte store per register group), or with split-K
+// fp32 partials (16 bytes per group) to the workspace.
+template <int TM, int TN, bool BWD>
+__device__ __forceinline__ void epilogue(const GemmArgs& a, float16_t (&acc)[TM][TN], int mb,
+                                         int nb, int lrow, int lseg) {
+  const bool split = gridDim.z > 1;
+  const bool vec = (a.Nc % 4) == 0 && (a.ldc % 4) == 0;
 #pragma unroll
   for (int i = 0; i < TM; i++) {
     const int m = mb + i * 32 + lrow;
@@ -138,10 +170,6 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float16_t (&acc)[TM]
         float4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
                       acc[i][j][4 * g + 3]};
         const bool full = vec && n + 3 < a.Nc;
-        if (a.bias && first_split) {
-#pragma unroll
-          for (int e = 0; e < 4; e++) v[e] += (n + e < a.Nc) ? (float)a.bias[n + e] : 0.0f;
-        }
         if (split) {
           float* w = a.ws + ((int64_t)blockIdx.z * a.M + m) * a.Nc + n;
           if (full) {
@@ -353,15 +381,6 @@ __device__ __forceinline__ void mma_kstep(float16_t (&acc)[TM][TN], const _Float
   }
 }
 
-template <int TM, int TN>
-__device__ __forceinline__ void zero_acc(float16_t (&acc)[TM][TN]) {
-#pragma unroll
-  for (int i = 0; i < TM; i++)
-#pragma unroll
-    for (int j = 0; j < TN; j++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
-}
 
 // All waves load, decode and multiply: K-step kt+2 is loaded while kt multiplies and kt+1 is
 // committed to the other LDS buffer in four parts between the MFMA sub-steps.
@@ -392,7 +411,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void k_nf4_gemm(GemmArgs a)
   const float offset = a.offset[0];
 
   float16_t acc[T::TM][T::TN];
-  zero_acc(acc);
+  init_acc<T::TM, T::TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
 
   auto mma = [&](int buf, int kk) {
     const _Float16* as = As + buf * T::LDS_A;
@@ -447,14 +466,97 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void k_nf4_gemm(GemmArgs a)
 }
 
 // NF4 side of a K-step for the warp-specialized kernel's 256 producer threads.
-//   forward:  item = one packed dword of W row n (8 values, one block scale): BN * 8 items
+//   forward:  item = 16 packed bytes of W row n (32 values, half of the row's block for this
+//             K-step, one block scale), 3 memory instructions each (dwordx4, absmax8 byte,
+//             absmax2 float); a 160-row tile adds one 4-byte item per lane for rows 128-159
 //   backward: item = 4 W rows x 8 output columns (4 block scales), decoded along W's rows
 template <int BN, bool BWD>
-struct BLoad {
+struct BLoad;
+
+template <int BN>
+struct BLoad<BN, false> {
+  // Rows [0, R16) as 16-byte items (2 lanes per row); for BN = 160 the last 32 rows as 4-byte
+  // items (8 lanes per row), so every producer lane decodes 40 values and no wave does a
+  // second 16-byte round alone.
   static constexpr int NTP = 256;
-  static constexpr int TOTAL = BWD ? (BN / 8) * (kBK / 4) : BN * 8;
+  static constexpr int R16 = BN >= 128 ? 128 : BN;
+  static constexpr int REST = BN - R16;
+  static_assert(REST == 0 || REST == 32, "B tile rows: <= 128, or 128 + 32");
+  static constexpr int TOTAL = R16 * 2;  // 16-byte items
+  static constexpr int VMEM = REST ? 6 : 3;  // memory instructions one issue() makes per lane
+  static_assert(TOTAL % 64 == 0, "B items in whole waves");
+
+  struct Stage {
+    u32x4 w;
+    uint32_t q8;
+    float a2;
+    uint32_t w4, q8b;  // 4-byte item (REST rows)
+    float a2b;
+  };
+
+  __device__ static __forceinline__ void issue(const GemmArgs& a, Stage& S, int p, int kt,
+                                               int n0) {
+    const int k0 = kt * kBK;
+    {
+      const int q = min(p, TOTAL - 1);  // lanes past TOTAL load a duplicate item
+      const int n = min(n0 + (q >> 1), a.Nc - 1);
+      const int64_t blk = ((int64_t)n * a.Kw + k0) >> 6;
+      S.q8 = a.absmax8[blk];
+      S.a2 = a.absmax2[blk >> 8];
+      S.w = *reinterpret_cast<const u32x4*>(a.packed + (int64_t)n * (a.Kw / 2) + k0 / 2 +
+                                             (q & 1) * 16);
+    }
+    if constexpr (REST > 0) {
+      const int n = min(n0 + R16 + (p >> 3), a.Nc - 1);
+      const int64_t blk = ((int64_t)n * a.Kw + k0) >> 6;
+      S.q8b = a.absmax8[blk];
+      S.a2b = a.absmax2[blk >> 8];
+      S.w4 = *reinterpret_cast<const uint32_t*>(a.packed + (int64_t)n * (a.Kw / 2) + k0 / 2 +
+                                                 (p & 7) * 4);
+    }
+  }
+
+  __device__ static __forceinline__ void commit(const Stage& S, _Float16* bs, int p,
+                                                const float2_t* s_pair, const float* s_code,
+                                                float offset) {
+    float2_t pr[4][4];  // all table lookups first: one LDS round trip
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
+    float2_t pb[4];
+    if constexpr (REST > 0) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) pb[j] = s_pair[(S.w4 >> (8 * j)) & 0xffu];
+    }
+    if (p < TOTAL) {
+      const float sc = nested_scale(s_code[S.q8], S.a2, offset);
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        u32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pr[d][j][0] * sc, pr[d][j][1] * sc);
+        *reinterpret_cast<u32x4*>(bs + lds_off(p >> 1, (p & 1) * 4 + d)) = v;
+      }
+    }
+    if constexpr (REST > 0) {
+      const float sc = nested_scale(s_code[S.q8b], S.a2b, offset);
+      u32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pb[j][0] * sc, pb[j][1] * sc);
+      *reinterpret_cast<u32x4*>(bs + lds_off(R16 + (p >> 3), p & 7)) = v;
+    }
+  }
+};
+
+template <int BN>
+struct BLoad<BN, true> {
+  static constexpr bool BWD = true;
+  static constexpr int NTP = 256;
+  static constexpr int TOTAL = (BN / 8) * (kBK / 4);
   static constexpr int ITEMS = (TOTAL + NTP - 1) / NTP;
-  static constexpr int NW = BWD ? 4 : 1;
+  static constexpr int NW = 4;
+  static constexpr int VMEM = 3 * NW * ITEMS;  // memory instructions one issue() makes per lane
   static_assert(TOTAL % 64 == 0, "B items in whole waves");
 
   struct Stage {
@@ -468,8 +570,7 @@ struct BLoad {
     const int k0 = kt * kBK;
 #pragma unroll
     for (int u = 0; u < ITEMS; u++) {
-      const int q = p + u * NTP;
-      if (q >= TOTAL) break;
+      const int q = min(p + u * NTP, TOTAL - 1);  // lanes past TOTAL load a duplicate item
       if (!BWD) {
         const int n = min(n0 + (q >> 3), a.Nc - 1);
         const int64_t blk = ((int64_t)n * a.Kw + k0) >> 6;
@@ -547,7 +648,17 @@ __device__ __forceinline__ void dma_a_tile(const GemmArgs& a, _Float16* as, int 
     const int seg = ((lane & 7) ^ row ^ (row >> 3)) & 7;
     const int m = min(m0 + row, a.M - 1);
     const _Float16* src = a.A + (int64_t)m * a.lda + k0 + seg * 8;
-    __builtin_amdgcn_global_load_lds(src, as + g * 8 * kBK, 16, 0, 0);
+    // Inline asm rather than __builtin_amdgcn_global_load_lds: the compiler cannot tell these
+    // LDS writes from the producers' table reads and would drain every outstanding load before
+    // each of those reads.  Completion is awaited explicitly (wait_vmcnt) before the barrier
+    // that hands the tile over.  M0 = this wave's LDS destination (the low 32 bits of a generic
+    // pointer into LDS are the LDS address); no other code in the kernel uses M0.
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as + g * 8 * kBK)));
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+                 :
+                 : "s"(dst), "v"(src)
+                 : "memory", "m0");
   }
 }
 
@@ -584,27 +695,43 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
       const int p = t - 256;
       const int pw = p >> 6;
       const float offset = a.offset[0];
-      typename B::Stage S;
-      B::issue(a, S, p, kt0, n0);
+      // NF4 tile of K-step kt is issued three steps ahead into register stage (kt - kt0) % 3
+      // and committed to LDS one step ahead; the A tile is copied two steps ahead into the LDS
+      // ring.  Every issue is unconditional (steps past the end re-load the last one), so the
+      // number of memory instructions in flight is a constant and each wait names exactly the
+      // group it needs.  Order within step kt: commit B(kt+1), A(kt+2), B(kt+3), wait A(kt+1).
+      constexpr int LB = B::VMEM;
+      constexpr int LA = BM / 32;  // dma_a_tile instructions per producer wave
+      const int last = kt1 - 1;
+      typename B::Stage S0, S1, S2;
+      B::issue(a, S0, p, kt0, n0);
       dma_a_tile<BM>(a, As, pw, lane, kt0, m0);
-      __syncthreads();  // tables
-      wait_vmem_all();
-      B::commit(S, Bs, p, s_pair, s_code, offset);
-      if (kt0 + 1 < kt1) {
-        B::issue(a, S, p, kt0 + 1, n0);
-        dma_a_tile<BM>(a, As + LDS_A, pw, lane, kt0 + 1, m0);
+      B::issue(a, S1, p, min(kt0 + 1, last), n0);
+      dma_a_tile<BM>(a, As + LDS_A, pw, lane, min(kt0 + 1, last), m0);
+      B::issue(a, S2, p, min(kt0 + 2, last), n0);
+      lds_barrier();  // tables
+      B::commit(S0, Bs, p, s_pair, s_code, offset);
+      wait_vmcnt<2 * LB + LA>();  // A(kt0): after it only B(kt0+1), A(kt0+1), B(kt0+2)
+      lds_barrier();  // K-step kt0 ready
+      auto step = [&](int kt, typename B::Stage& Sc, typename B::Stage& Si) {
+        const int r = kt - kt0;
+        // the compiler's own wait before this commit (B(kt+1) registers) also completes
+        // A(kt+1), issued after B(kt+1); B(kt+2) stays in flight
+        if (kt + 1 < kt1) B::commit(Sc, Bs + ((r + 1) & 1) * LDS_B, p, s_pair, s_code, offset);
+        dma_a_tile<BM>(a, As + ((r + 2) % 3) * LDS_A, pw, lane, min(kt + 2, last), m0);
+        B::issue(a, Si, p, min(kt + 3, last), n0);
+        wait_vmcnt<2 * LB + LA>();  // A(kt+1): after it only B(kt+2), A(kt+2), B(kt+3)
+        lds_barrier();
+      };
+      int kt = kt0;
+      for (; kt + 3 <= kt1; kt += 3) {
+        step(kt, S1, S0);
+        step(kt + 1, S2, S1);
+        step(kt + 2, S0, S2);
       }
-      __syncthreads();  // K-step kt0 ready
-      for (int kt = kt0; kt < kt1; kt++) {
-        wait_vmem_all();  // K-step kt+1 (issued during the previous step) has landed
-        if (kt + 1 < kt1)
-          B::commit(S, Bs + ((kt + 1 - kt0) & 1) * LDS_B, p, s_pair, s_code, offset);
-        if (kt + 2 < kt1) {
-          B::issue(a, S, p, kt + 2, n0);
-          dma_a_tile<BM>(a, As + ((kt + 2 - kt0) % 3) * LDS_A, pw, lane, kt + 2, m0);
-        }
-        __syncthreads();
-      }
+      if (kt < kt1) step(kt, S1, S0);
+      if (kt + 1 < kt1) step(kt + 1, S2, S1);
+      wait_vmem_all();  // no copy into LDS may be in flight when the workgroup ends
     }
   } else {
     // ---- consumers ----
@@ -614,14 +741,14 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
     const int lrow = lane & 31;
     const int lseg = lane >> 5;
     float16_t acc[TM][TN];
-    zero_acc(acc);
+    init_acc<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
     if (kt0 < kt1) {
-      __syncthreads();  // tables
-      __syncthreads();  // K-step kt0 ready
+      lds_barrier();  // tables
+      lds_barrier();  // K-step kt0 ready
       for (int kt = kt0; kt < kt1; kt++) {
         const int r = kt - kt0;
         mma_kstep<TM, TN>(acc, As + (r % 3) * LDS_A, Bs + (r & 1) * LDS_B, wm0, wn0, lrow, lseg);
-        __syncthreads();
+        lds_barrier();
       }
     }
     epilogue<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
