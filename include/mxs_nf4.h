@@ -122,9 +122,11 @@ int mxs_nf4_linear_bwd_dx(const void* dy, int M, int N, int K, const void* packe
 
 /* ---- LoRA side branch (peft lora.Linear around the 4-bit base, r % 16 == 0, r <= 128) ------
  * The transposed outputs/inputs (ht, dht) are fp16 [r, ldt] with ldt >= M, ldt % 8 == 0 (columns
- * past M hold zeros).  Each product is one launch that reduces inside its workgroups, in a
- * fixed order: results are deterministic.  `workspace` is unused (may be NULL); the size query
- * returns 0 and is kept so that callers size one buffer for every entry point. */
+ * past M hold zeros).  Results are deterministic (fixed summation order).  `workspace` may be
+ * NULL: each product is then one launch that reduces inside its workgroups.  With a workspace of
+ * mxs_lora_workspace_bytes(M, K, N, r) bytes (no initial contents needed; 0 means none is
+ * used) and ldt = M rounded up to 8, mxs_lora_h / mxs_lora_dh split reductions of 1024 or more
+ * over up to 4 slices of workgroups and add the slices in a second small launch. */
 int64_t mxs_lora_workspace_bytes(int M, int K, int N, int r);
 
 /* h = fp16(s * drop(x) . A^T) [M, r] and ht = its transpose: lora_A of peft's branch with the

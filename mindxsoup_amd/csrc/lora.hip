@@ -57,6 +57,7 @@ struct RowsArgs {
   const _Float16* B;      // optional [N, r]; with bt, bt [r, N] = B^T
   int N;
   _Float16* bt;
+  float* ws;              // with gridDim.y > 1: fp32 partials [slices][ldt][r]
 };
 
 // out[m][c] = fp16(s * sum_k drop(P)[m][k] * R[c][k]) for the 16 rows of blockIdx.x.
@@ -70,18 +71,22 @@ __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
   const int g = lane >> 4;
   const int rbn = a.r >> 4;
   const int chunks = a.K >> 5;
+  // reduction slice of this workgroup (blockIdx.y of gridDim.y): chunks [c_beg, c_end)
+  const int cps = (chunks + gridDim.y - 1) / gridDim.y;
+  const int c_beg = blockIdx.y * cps;
+  const int c_end = min(chunks, c_beg + cps);
   const bool row_ok = row < a.M;
   const int64_t prow = (int64_t)(row_ok ? row : 0) * a.K + 8 * g;
   float4_t acc[kMaxRB];
 #pragma unroll
   for (int b = 0; b < kMaxRB; b++) acc[b] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  for (int c0 = wave; c0 < chunks; c0 += kChunksInFlight * nw) {
+  for (int c0 = c_beg + wave; c0 < c_end; c0 += kChunksInFlight * nw) {
     half8_t x[kChunksInFlight];
 #pragma unroll
     for (int u = 0; u < kChunksInFlight; u++) {
       const int c = c0 + u * nw;
       half8_t v = {};
-      if (c < chunks && row_ok) {
+      if (c < c_end && row_ok) {
         v = *reinterpret_cast<const half8_t*>(a.P + prow + 32 * c);
         if (a.mask) v = drop8(v, *reinterpret_cast<const u32x2*>(a.mask + prow + 32 * c), a.mscale);
       }
@@ -95,7 +100,7 @@ __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
 #pragma unroll
       for (int u = 0; u < kChunksInFlight; u++) {
         const int c = c0 + u * nw;
-        y[u] = c < chunks ? *reinterpret_cast<const half8_t*>(rrow + 32 * c) : (half8_t){};
+        y[u] = c < c_end ? *reinterpret_cast<const half8_t*>(rrow + 32 * c) : (half8_t){};
       }
 #pragma unroll
       for (int u = 0; u < kChunksInFlight; u++)
@@ -112,17 +117,19 @@ __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
       red[(wave * 16 + 4 * g + v) * ld + 16 * b + (lane & 15)] = acc[b][v];
   }
   // side outputs, spread over the workgroups: R^T [K, r] and B^T [r, N]
+  const int n_wg = gridDim.x * gridDim.y;
+  const int wg = blockIdx.y * gridDim.x + blockIdx.x;
   if (a.rt) {
-    const int span = ((a.K + gridDim.x - 1) / gridDim.x + 7) & ~7;
-    const int k_beg = blockIdx.x * span, k_end = min(a.K, k_beg + span);
+    const int span = ((a.K + n_wg - 1) / n_wg + 7) & ~7;
+    const int k_beg = wg * span, k_end = min(a.K, k_beg + span);
     for (int i = threadIdx.x; i < (k_end - k_beg) * a.r; i += blockDim.x) {
       const int k = k_beg + i / a.r, c = i % a.r;
       a.rt[(int64_t)k * a.r + c] = a.R[(int64_t)c * a.K + k];
     }
   }
   if (a.bt) {
-    const int span = ((a.N + gridDim.x - 1) / gridDim.x + 7) & ~7;
-    const int n_beg = blockIdx.x * span, n_end = min(a.N, n_beg + span);
+    const int span = ((a.N + n_wg - 1) / n_wg + 7) & ~7;
+    const int n_beg = wg * span, n_end = min(a.N, n_beg + span);
     for (int i = threadIdx.x; i < (n_end - n_beg) * a.r; i += blockDim.x) {
       const int n = n_beg + i / a.r, c = i % a.r;
       a.bt[(int64_t)c * a.N + n] = a.B[(int64_t)n * a.r + c];
@@ -135,10 +142,27 @@ __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
     if (m >= a.ldt) continue;
     float sum = 0.f;
     for (int w = 0; w < nw; w++) sum += red[(w * 16 + rr) * ld + c];
+    if (gridDim.y > 1) {  // partial of this slice; k_lora_rows_finish adds the slices
+      a.ws[((int64_t)blockIdx.y * a.ldt + m) * a.r + c] = sum;
+      continue;
+    }
     const _Float16 h = m < a.M ? (_Float16)(a.s * sum) : (_Float16)0.0f;
     if (m < a.M) a.out[(int64_t)m * a.r + c] = h;
     a.outT[(int64_t)c * a.ldt + m] = h;
   }
+}
+
+// out[m][c] = fp16(s * sum of the slices' partials, in slice order) for m < M; outT [r, ldt]
+// with zeros past M.
+__global__ __launch_bounds__(256) void k_lora_rows_finish(RowsArgs a, int slices) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.ldt * a.r) return;
+  const int m = i / a.r, c = i % a.r;
+  float sum = 0.f;
+  for (int z = 0; z < slices; z++) sum += a.ws[((int64_t)z * a.ldt + m) * a.r + c];
+  const _Float16 h = m < a.M ? (_Float16)(a.s * sum) : (_Float16)0.0f;
+  if (m < a.M) a.out[(int64_t)m * a.r + c] = h;
+  a.outT[(int64_t)c * a.ldt + m] = h;
 }
 
 struct ColsProblem {
@@ -160,7 +184,10 @@ template <> struct ColsVec<8> { typedef u32x4 T; typedef u32x2 MT; };
 // workgroup: blockIdx.x < cb0 is problem p0 (dA), the rest p1 (dB).  Waves take 32-token steps
 // in turn and add their accumulators in LDS.
 template <int CPL>
-__global__ __launch_bounds__(1024) void k_lora_cols(ColsProblem p0, ColsProblem p1, int cb0, int M,
+constexpr int cols_max_waves() { return CPL >= 4 ? 8 : kMaxWaves; }
+
+template <int CPL>
+__global__ __launch_bounds__(64 * cols_max_waves<CPL>()) void k_lora_cols(ColsProblem p0, ColsProblem p1, int cb0, int M,
                                                    int ldt, int r) {
   typedef typename ColsVec<CPL>::T VT;
   typedef typename ColsVec<CPL>::MT MT;
@@ -177,46 +204,57 @@ __global__ __launch_bounds__(1024) void k_lora_cols(ColsProblem p0, ColsProblem 
   const int col = nb + CPL * ln;
   const bool col_ok = col < a.Nq;
   const int ld = WC + 1;
+  // U token blocks of 32 per batch, all loaded before any is multiplied (one memory round trip
+  // per batch instead of one per block)
+  constexpr int U = CPL == 8 ? 2 : 3;
   for (int b = 0; b < (r >> 4); b++) {  // r-blocks of 16 (the input is re-read per block)
     float4_t acc[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; c++) acc[c] = (float4_t){0.f, 0.f, 0.f, 0.f};
-    for (int t0 = wave * 32; t0 < M; t0 += nw * 32) {
-      const int mb = t0 + 8 * lg;
-      half8_t av = {};
-      if (mb < ldt) av = *reinterpret_cast<const half8_t*>(a.PT + (int64_t)(16 * b + ln) * ldt + mb);
-      VT rows[8];
+    for (int t0 = wave * 32; t0 < M; t0 += nw * 32 * U) {
+      half8_t av[U];
+      VT rows[U][8];
+      MT mks[U][8];
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        const int m = mb + e;
-        VT v = {};
-        if (m < M && col_ok) {
-          v = *reinterpret_cast<const VT*>(a.Q + (int64_t)m * a.Nq + col);
+      for (int u = 0; u < U; u++) {
+        const int mb = t0 + u * nw * 32 + 8 * lg;
+        av[u] = (half8_t){};
+        if (mb < ldt)
+          av[u] = *reinterpret_cast<const half8_t*>(a.PT + (int64_t)(16 * b + ln) * ldt + mb);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int m = mb + e;
+          rows[u][e] = VT{};
+          mks[u][e] = MT{};
+          if (m < M && col_ok) {
+            rows[u][e] = *reinterpret_cast<const VT*>(a.Q + (int64_t)m * a.Nq + col);
+            if (a.mask) mks[u][e] = *reinterpret_cast<const MT*>(a.mask + (int64_t)m * a.Nq + col);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        _Float16 hv[8][CPL];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          __builtin_memcpy(hv[e], &rows[u][e], sizeof(VT));
           if (a.mask) {
-            const MT mk = *reinterpret_cast<const MT*>(a.mask + (int64_t)m * a.Nq + col);
-            _Float16 h[CPL];
-            __builtin_memcpy(h, &v, sizeof(v));
 #pragma unroll
             for (int c = 0; c < CPL; c++) {
               uint32_t kb;
-              if constexpr (CPL == 8) kb = (mk[c >> 2] >> (8 * (c & 3))) & 0xFFu;
-              else kb = ((uint32_t)mk >> (8 * c)) & 0xFFu;
-              h[c] = kb ? (_Float16)((float)h[c] * a.mscale) : (_Float16)0.0f;
+              if constexpr (CPL == 8) kb = (mks[u][e][c >> 2] >> (8 * (c & 3))) & 0xFFu;
+              else kb = ((uint32_t)mks[u][e] >> (8 * c)) & 0xFFu;
+              hv[e][c] = kb ? (_Float16)((float)hv[e][c] * a.mscale) : (_Float16)0.0f;
             }
-            __builtin_memcpy(&v, h, sizeof(v));
           }
         }
-        rows[e] = v;
-      }
-      _Float16 hv[8][CPL];
 #pragma unroll
-      for (int e = 0; e < 8; e++) __builtin_memcpy(hv[e], &rows[e], sizeof(VT));
+        for (int c = 0; c < CPL; c++) {
+          half8_t bv;
 #pragma unroll
-      for (int c = 0; c < CPL; c++) {
-        half8_t bv;
-#pragma unroll
-        for (int e = 0; e < 8; e++) bv[e] = hv[e][c];
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc[c], 0, 0, 0);
+          for (int e = 0; e < 8; e++) bv[e] = hv[e][c];
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[u], bv, acc[c], 0, 0, 0);
+        }
       }
     }
     // acc[c][v] = C[j = 16*b + 4*lg + v][column nb + CPL*ln + c]
@@ -270,11 +308,27 @@ static int waves_for(int steps) {
   return w < 4 ? 4 : w > kMaxWaves ? kMaxWaves : w;
 }
 
-static int rows_launch(const RowsArgs& a, hipStream_t stream) {
-  int nw = waves_for(a.K / 32);
+// Reduction slices for the rows kernel: one (a single launch) unless the reduction is long
+// (>= 1024) and a workspace is given; then enough slices for about 256 workgroups, at most 4.
+static int rows_slices(int K, int ldt) {
+  if (K < 1024) return 1;
+  const int row_blocks = (ldt + 15) / 16;
+  int sl = 256 / row_blocks;
+  return sl < 1 ? 1 : sl > 4 ? 4 : sl;
+}
+
+static int rows_launch(RowsArgs a, void* workspace, hipStream_t stream) {
+  // the workspace size query assumes ldt = M rounded up to 8; any other ldt runs unsliced
+  const bool ws_ok = workspace && a.ldt == (a.M + 7) / 8 * 8;
+  const int slices = ws_ok ? rows_slices(a.K, a.ldt) : 1;
+  a.ws = static_cast<float*>(workspace);
+  int nw = waves_for(a.K / 32 / slices);
   while (nw > 1 && (size_t)nw * 16 * (a.r + 1) * sizeof(float) > (size_t)kColsLds) nw--;
   const size_t lds = (size_t)nw * 16 * (a.r + 1) * sizeof(float);
-  hipLaunchKernelGGL(k_lora_rows, dim3((a.ldt + 15) / 16), dim3(64 * nw), lds, stream, a);
+  hipLaunchKernelGGL(k_lora_rows, dim3((a.ldt + 15) / 16, slices), dim3(64 * nw), lds, stream, a);
+  if (slices > 1)
+    hipLaunchKernelGGL(k_lora_rows_finish, dim3((a.ldt * a.r + 255) / 256), dim3(256), 0, stream,
+                       a, slices);
   return check_launch();
 }
 
@@ -284,6 +338,7 @@ static int cols_launch_t(const ColsProblem& p0, const ColsProblem& p1, int nprob
   constexpr int WC = 16 * CPL;
   const int cb0 = (p0.Nq + WC - 1) / WC, cb1 = nprob > 1 ? (p1.Nq + WC - 1) / WC : 0;
   int nw = waves_for((M + 31) / 32);
+  if (nw > cols_max_waves<CPL>()) nw = cols_max_waves<CPL>();
   const int per_wave = r * (WC + 1) * (int)sizeof(float);
   while (nw > 1 && nw * per_wave > kColsLds) nw--;
   if (nw * per_wave > kColsLds) return MXS_ERR_SIZE;
@@ -309,14 +364,15 @@ using namespace mxs;
 extern "C" {
 
 int64_t mxs_lora_workspace_bytes(int M, int K, int N, int r) {
-  (void)M; (void)K; (void)N; (void)r;
-  return 0;  // every LoRA product reduces inside its workgroups
+  const int ldt = (M + 7) / 8 * 8;
+  const int sk = rows_slices(K, ldt), sn = rows_slices(N, ldt);
+  const int sl = sk > sn ? sk : sn;
+  return sl > 1 ? (int64_t)sl * ldt * r * (int64_t)sizeof(float) : 0;
 }
 
 int mxs_lora_h(const void* x, int M, int K, const void* lora_a, int r, const void* mask,
                float mask_scale, float s, void* h, void* ht, int ldt, void* at,
                const void* lora_b, int N, void* bt, void* workspace, hipStream_t stream) {
-  (void)workspace;
   if (M < 0 || K < 0 || N < 0 || r <= 0) return MXS_ERR_ARG;
   if (M == 0) return MXS_OK;
   if (!x || !lora_a || !h || !ht || (bt && !lora_b)) return MXS_ERR_ARG;
@@ -339,12 +395,11 @@ int mxs_lora_h(const void* x, int M, int K, const void* lora_a, int r, const voi
   a.B = static_cast<const _Float16*>(lora_b);
   a.N = N;
   a.bt = static_cast<_Float16*>(bt);
-  return rows_launch(a, stream);
+  return rows_launch(a, workspace, stream);
 }
 
 int mxs_lora_dh(const void* dy, int M, int N, const void* lora_bt, int r, float s, void* dh,
                 void* dht, int ldt, void* workspace, hipStream_t stream) {
-  (void)workspace;
   if (M < 0 || N < 0 || r <= 0) return MXS_ERR_ARG;
   if (M == 0) return MXS_OK;
   if (!dy || !lora_bt || !dh || !dht) return MXS_ERR_ARG;
@@ -361,7 +416,7 @@ int mxs_lora_dh(const void* dy, int M, int N, const void* lora_bt, int r, float 
   a.s = s;
   a.out = static_cast<_Float16*>(dh);
   a.outT = static_cast<_Float16*>(dht);
-  return rows_launch(a, stream);
+  return rows_launch(a, workspace, stream);
 }
 
 int mxs_lora_grads(const void* dht, const void* ht, int ldt, const void* x, const void* dy, int M,

@@ -7,8 +7,8 @@ back to another implementation: an unsupported shape raises.
 Workspaces: the split-K GEMMs write fp32 partial sums to a workspace that a second small kernel
 adds up in a fixed order; its contents need no initialisation and are dead after the call, so
 one buffer serves any number of calls issued in order on one stream.  Calls take it as `ws` or
-allocate it from torch's caching allocator.  The LoRA kernels reduce inside their workgroups
-and need none (their `ws` argument is accepted and ignored).
+allocate it from torch's caching allocator.  The LoRA H / dH kernels use one the same way for
+reductions of 1024 or more (split over workgroups); the dA / dB kernel needs none.
 """
 
 import torch
@@ -149,6 +149,7 @@ def lora_h(x2d, lora_a, s, mask=None, mask_scale=1.0, ws=None, n_out=None, want_
     dev = x2d.device
     h = torch.empty((M, r), dtype=torch.float16, device=dev)
     ht = torch.empty((r, _ldt(M)), dtype=torch.float16, device=dev)
+    ws = _workspace(lora_workspace_bytes(M, K, n_out or K, r), dev, ws)
     at = bt = None
     N = 0
     if want_at:
@@ -176,6 +177,7 @@ def lora_dh(dy2d, lora_b, s, ws=None, k_in=None, lora_bt=None):
     r = lora_bt.shape[0]
     if lora_bt.shape != (r, N):
         raise ValueError("lora_bt must be [r, N]")
+    ws = _workspace(lora_workspace_bytes(M, k_in or N, N, r), dy2d.device, ws)
     dh = torch.empty((M, r), dtype=torch.float16, device=dy2d.device)
     dht = torch.empty((r, _ldt(M)), dtype=torch.float16, device=dy2d.device)
     _lib.call("mxs_lora_dh", _lib.ptr(dy2d), M, N, _lib.ptr(lora_bt.contiguous()), r, float(s),

@@ -216,6 +216,38 @@ def test_lora_reductions_across_many_workgroups(cuda, M):
         assert torch.equal(h2, h) and torch.equal(da2, da) and torch.equal(db2, db)
 
 
+def test_lora_sliced_and_single_launch_reductions_agree(cuda):
+    """A 8960-long reduction runs over 4 slices of workgroups when given a workspace and in one
+    launch without; both match the oracle (the summation order differs, the bound does not)."""
+    from mindxsoup_amd import _lib, kernels
+
+    M, K, N = 300, 8960, 8960
+    x, a, b, dy, keep = _lora_inputs(cuda, M, K, N, 21)
+    s, p = 2.0, 0.05
+    assert kernels.lora_workspace_bytes(M, K, N, 16) > 0
+    h, ht = kernels.lora_h(x, a, s, keep, 1 / (1 - p))            # sliced (workspace allocated)
+    h1 = torch.empty_like(h)
+    ht1 = torch.empty_like(ht)
+    _lib.call("mxs_lora_h", _lib.ptr(x), M, K, _lib.ptr(a), 16, _lib.ptr(keep), 1 / (1 - p), s,
+              _lib.ptr(h1), _lib.ptr(ht1), ht1.shape[1], None, None, 0, None, None,
+              _lib.stream_of(cuda))                                  # single launch
+    bt = b.t().contiguous()
+    dh, _ = kernels.lora_dh(dy, None, s, lora_bt=bt)                  # sliced
+    dh1 = torch.empty_like(dh)
+    dht1 = torch.empty((16, (M + 7) // 8 * 8), dtype=torch.float16, device=cuda)
+    _lib.call("mxs_lora_dh", _lib.ptr(dy), M, N, _lib.ptr(bt), 16, s, _lib.ptr(dh1),
+              _lib.ptr(dht1), dht1.shape[1], None, _lib.stream_of(cuda))
+    xn, an, bn, dyn, kn = (_np(x).astype(np.float16), _np(a).astype(np.float16),
+                           _np(b).astype(np.float16), _np(dy).astype(np.float16),
+                           keep.cpu().numpy())
+    ref_h = s * O.lora_h(xn, an, kn, p)
+    ref_dh = s * (dyn.astype(np.float64) @ bn.astype(np.float64))
+    for got, ref in ((h, ref_h), (h1, ref_h), (dh, ref_dh), (dh1, ref_dh)):
+        assert O.max_rel(_np(got), ref) < TOL
+    assert torch.equal(ht[:, :M].t(), h) and torch.all(ht[:, M:] == 0)
+    assert torch.equal(ht1[:, :M].t(), h1) and torch.all(ht1[:, M:] == 0)
+
+
 def test_lora_grads_without_tokens(cuda):
     from mindxsoup_amd import kernels
 
