@@ -227,9 +227,9 @@ def shared_workspace(dev):
 def proj_fwd(p, s=ALPHA / RANK):
     from mindxsoup_amd import kernels
 
-    h, ht, at, bt = kernels.lora_h(p["x"], p["a"], s, p["keep"], 1.0 / (1.0 - P_DROP),
-                                   ws=p["ws"], n_out=p["n"], want_at=True, lora_b=p["b"])
-    y = kernels.nf4_linear_fwd(p["x"], p["packed"], p["st"], None, h, p["b"], ws=p["ws"])
+    hp, at, bt = kernels.lora_h_partials(p["x"], p["a"], s, p["keep"], 1.0 / (1.0 - P_DROP),
+                                         lora_b=p["b"])
+    y, ht = kernels.nf4_linear_fwd_hp(p["x"], p["packed"], p["st"], hp, p["b"], ws=p["ws"])
     return y, (ht, at, bt)
 
 
@@ -238,9 +238,9 @@ def proj_bwd(p, saved, s=ALPHA / RANK):
 
     ht, at, bt = saved
     ms = 1.0 / (1.0 - P_DROP)
-    dh, dht = kernels.lora_dh(p["dy"], None, s, ws=p["ws"], k_in=p["k"], lora_bt=bt)
-    dx = kernels.nf4_linear_bwd_dx(p["dy"], p["packed"], p["st"], dh, None, p["keep"], ms,
-                                   lora_at=at, ws=p["ws"])
+    dhp = kernels.lora_dh_partials(p["dy"], bt, s)
+    dx, dht = kernels.nf4_linear_bwd_dx_hp(p["dy"], p["packed"], p["st"], dhp, at, p["keep"], ms,
+                                           ws=p["ws"])
     da, db = kernels.lora_grads(dht, ht, p["x"], p["dy"], p["keep"], ms)
     return dx, da, db
 

@@ -120,6 +120,28 @@ int mxs_nf4_linear_bwd_dx(const void* dy, int M, int N, int K, const void* packe
                           const void* mask, float mask_scale, void* dx, void* workspace, int cfg,
                           int splits, hipStream_t stream);
 
+/* mxs_nf4_linear_fwd with the LoRA activations given as fp32 partial sums (from
+ * mxs_lora_h_partials) instead of lora_h: lora_hp [hp_slices][ldt][r] (1 <= hp_slices <= 4,
+ * ldt >= M, ldt % 8 == 0), already times s.  The GEMM adds the slices in order, rounds to fp16
+ * and uses that as lora_h; with lora_ht != NULL it also writes that fp16 operand transposed,
+ * [r, ldt] with zeros past M (the input of mxs_lora_grads' dB).  Saves the separate launch that
+ * would finish lora_h. */
+int mxs_nf4_linear_fwd_hp(const void* x, int M, int K, int N, const void* packed,
+                          const void* absmax8, const float* code, const float* absmax2,
+                          const float* offset, const void* bias, const float* lora_hp,
+                          int hp_slices, int ldt, const void* lora_b, int r, void* lora_ht,
+                          void* y, void* workspace, int cfg, int splits, hipStream_t stream);
+
+/* mxs_nf4_linear_bwd_dx with s * dH given as fp32 partial sums (from mxs_lora_dh_partials),
+ * [hp_slices][ldt][r]; with lora_dht != NULL it also writes fp16 s * dH transposed, [r, ldt]
+ * (the input of mxs_lora_grads' dA). */
+int mxs_nf4_linear_bwd_dx_hp(const void* dy, int M, int N, int K, const void* packed,
+                             const void* absmax8, const float* code, const float* absmax2,
+                             const float* offset, const float* lora_dhp, int hp_slices, int ldt,
+                             const void* lora_at, int r, const void* mask, float mask_scale,
+                             void* lora_dht, void* dx, void* workspace, int cfg, int splits,
+                             hipStream_t stream);
+
 /* ---- LoRA side branch (peft lora.Linear around the 4-bit base, r % 16 == 0, r <= 128) ------
  * The transposed outputs/inputs (ht, dht) are fp16 [r, ldt] with ldt >= M, ldt % 8 == 0 (columns
  * past M hold zeros).  Results are deterministic (fixed summation order).  `workspace` may be
@@ -152,6 +174,22 @@ int mxs_lora_grad_a(const void* dht, int ldt, const void* x, int M, int K, int r
 /* dB[N,r] (fp32) = dY^T . h (h = s * H): lora_B's weight gradient. */
 int mxs_lora_grad_b(const void* ht, int ldt, const void* dy, int M, int N, int r, float* db,
                     void* workspace, hipStream_t stream);
+
+/* Number of reduction slices (1..4) mxs_lora_h_partials / mxs_lora_dh_partials use for M tokens
+ * and a reduction of length Kr: their partials buffer is fp32 [slices][ldt][r]. */
+int mxs_lora_slices(int M, int Kr);
+
+/* The products of mxs_lora_h as fp32 partial sums times s, one per reduction slice, for the
+ * fused GEMM (mxs_nf4_linear_fwd_hp) to finish: partials [mxs_lora_slices(M, K)][ldt][r]
+ * (rows past M hold zeros).  One launch; at / bt side outputs as in mxs_lora_h. */
+int mxs_lora_h_partials(const void* x, int M, int K, const void* lora_a, int r, const void* mask,
+                        float mask_scale, float s, int ldt, void* at, const void* lora_b, int N,
+                        void* bt, float* partials, hipStream_t stream);
+
+/* The products of mxs_lora_dh as fp32 partial sums times s, [mxs_lora_slices(M, N)][ldt][r], for
+ * mxs_nf4_linear_bwd_dx_hp.  One launch. */
+int mxs_lora_dh_partials(const void* dy, int M, int N, const void* lora_bt, int r, float s,
+                         int ldt, float* partials, hipStream_t stream);
 
 /* mxs_lora_grad_a and mxs_lora_grad_b in one launch (either output may be NULL): the two weight
  * gradients autograd computes for peft's lora_A and lora_B (solution/attention.py:197-199 under

@@ -57,7 +57,8 @@ struct RowsArgs {
   const _Float16* B;      // optional [N, r]; with bt, bt [r, N] = B^T
   int N;
   _Float16* bt;
-  float* ws;              // with gridDim.y > 1: fp32 partials [slices][ldt][r]
+  float* ws;              // fp32 partials [slices][ldt][r], times s (sliced or partial mode)
+  int partial_out;        // write the partials even for one slice; no final fp16 outputs
 };
 
 // out[m][c] = fp16(s * sum_k drop(P)[m][k] * R[c][k]) for the 16 rows of blockIdx.x.
@@ -137,13 +138,13 @@ __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
   }
   __syncthreads();
   for (int i = threadIdx.x; i < 16 * a.r; i += blockDim.x) {
-    const int rr = i / a.r, c = i % a.r;
+    const int c = i >> 4, rr = i & 15;  // consecutive threads: consecutive m of one outT row
     const int m = m0 + rr;
     if (m >= a.ldt) continue;
     float sum = 0.f;
     for (int w = 0; w < nw; w++) sum += red[(w * 16 + rr) * ld + c];
-    if (gridDim.y > 1) {  // partial of this slice; k_lora_rows_finish adds the slices
-      a.ws[((int64_t)blockIdx.y * a.ldt + m) * a.r + c] = sum;
+    if (gridDim.y > 1 || a.partial_out) {  // this slice's partial, times s
+      a.ws[((int64_t)blockIdx.y * a.ldt + m) * a.r + c] = a.s * sum;
       continue;
     }
     const _Float16 h = m < a.M ? (_Float16)(a.s * sum) : (_Float16)0.0f;
@@ -152,17 +153,39 @@ __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
   }
 }
 
-// out[m][c] = fp16(s * sum of the slices' partials, in slice order) for m < M; outT [r, ldt]
-// with zeros past M.
-__global__ __launch_bounds__(256) void k_lora_rows_finish(RowsArgs a, int slices) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i >= a.ldt * a.r) return;
-  const int m = i / a.r, c = i % a.r;
-  float sum = 0.f;
-  for (int z = 0; z < slices; z++) sum += a.ws[((int64_t)z * a.ldt + m) * a.r + c];
-  const _Float16 h = m < a.M ? (_Float16)(a.s * sum) : (_Float16)0.0f;
-  if (m < a.M) a.out[(int64_t)m * a.r + c] = h;
-  a.outT[(int64_t)c * a.ldt + m] = h;
+// out[m][c] = fp16(sum of the slices' partials, in slice order) for m < M; outT [r, ldt]
+// with zeros past M.  One thread per row m: its partials and its out row are contiguous, and
+// consecutive threads write consecutive m of each outT row.
+__global__ __launch_bounds__(64) void k_lora_rows_finish(RowsArgs a, int slices) {
+  const int m = blockIdx.x * 64 + threadIdx.x;
+  if (m >= a.ldt) return;
+  for (int c0 = 0; c0 < a.r; c0 += 16) {
+    float4_t v[4][4];  // [slice][quad of columns]; all loads before the first add
+#pragma unroll
+    for (int z = 0; z < 4; z++)
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        v[z][q] = z < slices
+                      ? *reinterpret_cast<const float4_t*>(a.ws + ((int64_t)z * a.ldt + m) * a.r + c0 + 4 * q)
+                      : (float4_t){0.f, 0.f, 0.f, 0.f};
+    half8_t h[2];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      float4_t sum = v[0][q];
+#pragma unroll
+      for (int z = 1; z < 4; z++)
+        if (z < slices) sum += v[z][q];
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        h[q >> 1][4 * (q & 1) + e] = m < a.M ? (_Float16)sum[e] : (_Float16)0.0f;
+    }
+    if (m < a.M) {
+      *reinterpret_cast<half8_t*>(a.out + (int64_t)m * a.r + c0) = h[0];
+      *reinterpret_cast<half8_t*>(a.out + (int64_t)m * a.r + c0 + 8) = h[1];
+    }
+#pragma unroll
+    for (int c = 0; c < 16; c++) a.outT[(int64_t)(c0 + c) * a.ldt + m] = h[c >> 3][c & 7];
+  }
 }
 
 struct ColsProblem {
@@ -318,17 +341,18 @@ static int rows_slices(int K, int ldt) {
 }
 
 static int rows_launch(RowsArgs a, void* workspace, hipStream_t stream) {
-  // the workspace size query assumes ldt = M rounded up to 8; any other ldt runs unsliced
-  const bool ws_ok = workspace && a.ldt == (a.M + 7) / 8 * 8;
-  const int slices = ws_ok ? rows_slices(a.K, a.ldt) : 1;
+  // the workspace size query assumes ldt = M rounded up to 8; any other ldt runs unsliced.  In
+  // partial mode the caller sized the partials by mxs_lora_slices(M, K) for its ldt.
+  const bool ws_ok = workspace && (a.partial_out || a.ldt == (a.M + 7) / 8 * 8);
+  const int slices = ws_ok ? rows_slices(a.K, (a.M + 7) / 8 * 8) : 1;
   a.ws = static_cast<float*>(workspace);
   int nw = waves_for(a.K / 32 / slices);
   while (nw > 1 && (size_t)nw * 16 * (a.r + 1) * sizeof(float) > (size_t)kColsLds) nw--;
   const size_t lds = (size_t)nw * 16 * (a.r + 1) * sizeof(float);
   hipLaunchKernelGGL(k_lora_rows, dim3((a.ldt + 15) / 16, slices), dim3(64 * nw), lds, stream, a);
-  if (slices > 1)
-    hipLaunchKernelGGL(k_lora_rows_finish, dim3((a.ldt * a.r + 255) / 256), dim3(256), 0, stream,
-                       a, slices);
+  if (slices > 1 && !a.partial_out)
+    hipLaunchKernelGGL(k_lora_rows_finish, dim3((a.ldt + 63) / 64), dim3(64), 0, stream, a,
+                       slices);
   return check_launch();
 }
 
@@ -417,6 +441,58 @@ int mxs_lora_dh(const void* dy, int M, int N, const void* lora_bt, int r, float 
   a.out = static_cast<_Float16*>(dh);
   a.outT = static_cast<_Float16*>(dht);
   return rows_launch(a, workspace, stream);
+}
+
+int mxs_lora_slices(int M, int Kr) {
+  if (M <= 0 || Kr <= 0) return 1;
+  return rows_slices(Kr, (M + 7) / 8 * 8);
+}
+
+int mxs_lora_h_partials(const void* x, int M, int K, const void* lora_a, int r, const void* mask,
+                        float mask_scale, float s, int ldt, void* at, const void* lora_b, int N,
+                        void* bt, float* partials, hipStream_t stream) {
+  if (M < 0 || K < 0 || N < 0 || r <= 0) return MXS_ERR_ARG;
+  if (M == 0) return MXS_OK;
+  if (!x || !lora_a || !partials || (bt && !lora_b)) return MXS_ERR_ARG;
+  if (r % 16 || r > 16 * kMaxRB || K % 32 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  if (((uintptr_t)x % 16) || ((uintptr_t)lora_a % 16) || (mask && ((uintptr_t)mask % 8)))
+    return MXS_ERR_ALIGN;
+  RowsArgs a{};
+  a.P = static_cast<const _Float16*>(x);
+  a.M = M;
+  a.K = K;
+  a.mask = static_cast<const uint8_t*>(mask);
+  a.mscale = mask_scale;
+  a.R = static_cast<const _Float16*>(lora_a);
+  a.r = r;
+  a.ldt = ldt;
+  a.s = s;
+  a.rt = static_cast<_Float16*>(at);
+  a.B = static_cast<const _Float16*>(lora_b);
+  a.N = N;
+  a.bt = static_cast<_Float16*>(bt);
+  a.partial_out = 1;
+  return rows_launch(a, partials, stream);
+}
+
+int mxs_lora_dh_partials(const void* dy, int M, int N, const void* lora_bt, int r, float s,
+                         int ldt, float* partials, hipStream_t stream) {
+  if (M < 0 || N < 0 || r <= 0) return MXS_ERR_ARG;
+  if (M == 0) return MXS_OK;
+  if (!dy || !lora_bt || !partials) return MXS_ERR_ARG;
+  if (r % 16 || r > 16 * kMaxRB || N % 32 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  if (((uintptr_t)dy % 16) || ((uintptr_t)lora_bt % 16)) return MXS_ERR_ALIGN;
+  RowsArgs a{};
+  a.P = static_cast<const _Float16*>(dy);
+  a.M = M;
+  a.K = N;
+  a.mscale = 1.0f;
+  a.R = static_cast<const _Float16*>(lora_bt);
+  a.r = r;
+  a.ldt = ldt;
+  a.s = s;
+  a.partial_out = 1;
+  return rows_launch(a, partials, stream);
 }
 
 int mxs_lora_grads(const void* dht, const void* ht, int ldt, const void* x, const void* dy, int M,

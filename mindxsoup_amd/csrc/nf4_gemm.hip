@@ -41,6 +41,12 @@ struct GemmArgs {
   int r;
   const uint8_t* mask;      // backward: dropout keep mask [M, Nc] or null
   float mask_scale;         // 1 / (1 - p)
+  // LoRA activations given as fp32 partial sums instead of lora_h: [hp_slices][ldt][r], already
+  // times s; the GEMM adds them in slice order and rounds to fp16 (the same value lora_h holds)
+  const float* lora_hp;
+  int hp_slices;
+  _Float16* lora_ht;        // optional out: that fp16 operand transposed, [r, ldt], zeros past M
+  int ldt;
   _Float16* C;              // [M, ldc]
   int64_t ldc;
   float* ws;                // split-K partials [splits, M, Nc]
@@ -92,27 +98,58 @@ __device__ __forceinline__ void init_acc(const GemmArgs& a, float16_t (&acc)[TM]
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
   if (blockIdx.z != 0) return;
   const bool vec = (a.Nc % 4) == 0 && (a.ldc % 4) == 0;
-  if (a.lora_h) {
+  if (a.lora_h || a.lora_hp) {
     // lora_w is [Nc, r] in both directions (the backward pass gets lora_A transposed), so the
-    // W-side operand is one 16-byte load per tile and 16 ranks.
+    // W-side operand is one 16-byte load per tile and 16 ranks.  The accumulators are still zero
+    // here, so the LoRA products go straight into them (masked in place afterwards).
     const bool masked = BWD && a.mask;
+    // the first column tile's waves that own the first columns write the operand transposed
+    const bool write_t = a.lora_ht && blockIdx.x == 0 && nb == 0;
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       const int m = mb + i * 32 + lrow;
+      for (int r0 = 0; r0 < a.r; r0 += 16) {
+        half8_t hf = {};
+        if (a.lora_hp) {
+          if (m < a.M) {
+            float4_t p0[4], p1[4];  // all slices' loads before the first add (<= 4 slices)
+#pragma unroll
+            for (int z = 0; z < 4; z++) {
+              const float* src = a.lora_hp + ((int64_t)z * a.ldt + m) * a.r + r0 + 8 * lseg;
+              p0[z] = z < a.hp_slices ? *reinterpret_cast<const float4_t*>(src) : (float4_t){};
+              p1[z] = z < a.hp_slices ? *reinterpret_cast<const float4_t*>(src + 4) : (float4_t){};
+            }
+            float4_t s0 = p0[0], s1 = p1[0];
+#pragma unroll
+            for (int z = 1; z < 4; z++)
+              if (z < a.hp_slices) {
+                s0 += p0[z];
+                s1 += p1[z];
+              }
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+              hf[e] = (_Float16)s0[e];
+              hf[4 + e] = (_Float16)s1[e];
+            }
+          }
+          if (write_t && m < a.ldt) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) a.lora_ht[(int64_t)(r0 + 8 * lseg + e) * a.ldt + m] = hf[e];
+          }
+        } else if (m < a.M) {
+          hf = *reinterpret_cast<const half8_t*>(a.lora_h + (int64_t)m * a.r + r0 + 8 * lseg);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          const int ncol = nb + j * 32 + lrow;  // column this lane feeds as the W-side operand
+          half8_t wf = {};
+          if (ncol < a.Nc) wf = *reinterpret_cast<const half8_t*>(a.lora_w + (int64_t)ncol * a.r + r0 + 8 * lseg);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, hf, acc[i][j], 0, 0, 0);
+        }
+      }
+      if (!masked) continue;
 #pragma unroll
       for (int j = 0; j < TN; j++) {
-        const int ncol = nb + j * 32 + lrow;  // column this lane feeds as the W-side operand
-        float16_t lacc = {};
-        for (int r0 = 0; r0 < a.r; r0 += 16) {
-          half8_t hf = {}, wf = {};
-          if (m < a.M) hf = *reinterpret_cast<const half8_t*>(a.lora_h + (int64_t)m * a.r + r0 + 8 * lseg);
-          if (ncol < a.Nc) wf = *reinterpret_cast<const half8_t*>(a.lora_w + (int64_t)ncol * a.r + r0 + 8 * lseg);
-          lacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, hf, lacc, 0, 0, 0);
-        }
-        if (!masked) {
-          acc[i][j] = lacc;
-          continue;
-        }
 #pragma unroll
         for (int g = 0; g < 4; g++) {
           const int n = nb + j * 32 + 8 * g + 4 * lseg;
@@ -128,7 +165,7 @@ __device__ __forceinline__ void init_acc(const GemmArgs& a, float16_t (&acc)[TM]
           }
 #pragma unroll
           for (int e = 0; e < 4; e++)
-            acc[i][j][4 * g + e] = ((keep >> (8 * e)) & 0xffu) ? lacc[4 * g + e] * a.mask_scale : 0.0f;
+            acc[i][j][4 * g + e] = ((keep >> (8 * e)) & 0xffu) ? acc[i][j][4 * g + e] * a.mask_scale : 0.0f;
         }
       }
     }
@@ -203,8 +240,18 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
   if (e >= plane) return;
   const int m = (int)(e / Nc), n = (int)(e % Nc);
   if ((Nc % 4) == 0 && (ldc % 4) == 0) {
+    // loads of four splits at a time are issued before they are added (in split order)
     float4_t v = *reinterpret_cast<const float4_t*>(ws + e);
-    for (int z = 1; z < splits; z++) v += *reinterpret_cast<const float4_t*>(ws + z * plane + e);
+    for (int z0 = 1; z0 < splits; z0 += 4) {
+      float4_t p[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        p[u] = z0 + u < splits ? *reinterpret_cast<const float4_t*>(ws + (z0 + u) * plane + e)
+                               : (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < 4; u++)
+        if (z0 + u < splits) v += p[u];
+    }
     *reinterpret_cast<half4_t*>(C + (int64_t)m * ldc + n) = __builtin_convertvector(v, half4_t);
   } else {
     for (int q = 0; q < 4 && e + q < plane; q++) {
@@ -864,6 +911,14 @@ static int gemm_entry(bool bwd, const GemmArgs& a, int cfg, int splits, hipStrea
   if (a.lora_h && (!a.lora_w || a.r <= 0 || a.r % 16 != 0)) return MXS_ERR_SIZE;
   if (a.lora_h && (((uintptr_t)a.lora_h % 16) != 0 || ((uintptr_t)a.lora_w % 16) != 0))
     return MXS_ERR_ALIGN;
+  if (a.lora_hp) {
+    if (!a.lora_w || a.r <= 0 || a.r % 16 != 0 || a.hp_slices < 1 || a.hp_slices > 4 ||
+        a.ldt < a.M || a.ldt % 8 != 0)
+      return MXS_ERR_SIZE;
+    if (((uintptr_t)a.lora_hp % 16) != 0 || ((uintptr_t)a.lora_w % 16) != 0 ||
+        ((uintptr_t)a.lora_ht % 2) != 0)
+      return MXS_ERR_ALIGN;
+  }
   if (cfg < 0) choose(a.M, a.Nc, a.Kr, &cfg, &splits);
   if (cfg >= kNumCfg || cfg == 5) return MXS_ERR_ARG;
   return bwd ? launch_by_id<true>(cfg, a, splits, stream)
@@ -932,6 +987,70 @@ int mxs_nf4_linear_bwd_dx(const void* dy, int M, int N, int K, const void* packe
   a.Kr = N;
   a.Kw = K;
   a.lora_h = static_cast<const _Float16*>(lora_dh);
+  a.lora_w = static_cast<const _Float16*>(lora_at);
+  a.r = r;
+  a.mask = static_cast<const uint8_t*>(mask);
+  a.mask_scale = mask_scale;
+  a.C = static_cast<_Float16*>(dx);
+  a.ldc = K;
+  set_workspace(a, workspace);
+  return gemm_entry(true, a, cfg, splits, stream);
+}
+
+int mxs_nf4_linear_fwd_hp(const void* x, int M, int K, int N, const void* packed,
+                          const void* absmax8, const float* code, const float* absmax2,
+                          const float* offset, const void* bias, const float* lora_hp,
+                          int hp_slices, int ldt, const void* lora_b, int r, void* lora_ht,
+                          void* y, void* workspace, int cfg, int splits, hipStream_t stream) {
+  if (!lora_hp) return MXS_ERR_ARG;
+  GemmArgs a{};
+  a.A = static_cast<const _Float16*>(x);
+  a.lda = K;
+  a.packed = static_cast<const uint8_t*>(packed);
+  a.absmax8 = static_cast<const uint8_t*>(absmax8);
+  a.code = code;
+  a.absmax2 = absmax2;
+  a.offset = offset;
+  a.M = M;
+  a.Nc = N;
+  a.Kr = K;
+  a.Kw = K;
+  a.bias = static_cast<const _Float16*>(bias);
+  a.lora_hp = lora_hp;
+  a.hp_slices = hp_slices;
+  a.ldt = ldt;
+  a.lora_ht = static_cast<_Float16*>(lora_ht);
+  a.lora_w = static_cast<const _Float16*>(lora_b);
+  a.r = r;
+  a.C = static_cast<_Float16*>(y);
+  a.ldc = N;
+  set_workspace(a, workspace);
+  return gemm_entry(false, a, cfg, splits, stream);
+}
+
+int mxs_nf4_linear_bwd_dx_hp(const void* dy, int M, int N, int K, const void* packed,
+                             const void* absmax8, const float* code, const float* absmax2,
+                             const float* offset, const float* lora_dhp, int hp_slices, int ldt,
+                             const void* lora_at, int r, const void* mask, float mask_scale,
+                             void* lora_dht, void* dx, void* workspace, int cfg, int splits,
+                             hipStream_t stream) {
+  if (!lora_dhp) return MXS_ERR_ARG;
+  GemmArgs a{};
+  a.A = static_cast<const _Float16*>(dy);
+  a.lda = N;
+  a.packed = static_cast<const uint8_t*>(packed);
+  a.absmax8 = static_cast<const uint8_t*>(absmax8);
+  a.code = code;
+  a.absmax2 = absmax2;
+  a.offset = offset;
+  a.M = M;
+  a.Nc = K;
+  a.Kr = N;
+  a.Kw = K;
+  a.lora_hp = lora_dhp;
+  a.hp_slices = hp_slices;
+  a.ldt = ldt;
+  a.lora_ht = static_cast<_Float16*>(lora_dht);
   a.lora_w = static_cast<const _Float16*>(lora_at);
   a.r = r;
   a.mask = static_cast<const uint8_t*>(mask);

@@ -123,6 +123,97 @@ def nf4_linear_bwd_dx(dy2d, packed, state, lora_dh=None, lora_a=None, mask=None,
     return dx
 
 
+def lora_slices(M, Kr):
+    """Reduction slices the partial-sum LoRA kernels use (1..4)."""
+    return int(_lib.lib().mxs_lora_slices(M, Kr))
+
+
+def lora_h_partials(x2d, lora_a, s, mask=None, mask_scale=1.0, lora_b=None):
+    """(hp, at, bt): s * drop(x) @ A^T as fp32 partial sums [slices, ldt, r] (the fused forward
+    GEMM finishes them), lora_A^T [K, r] and, given lora_b [N, r], lora_B^T [r, N]."""
+    x2d = x2d.contiguous()
+    lora_a = lora_a.to(torch.float16).contiguous()
+    M, K = x2d.shape
+    r = lora_a.shape[0]
+    dev = x2d.device
+    hp = torch.empty((lora_slices(M, K), _ldt(M), r), dtype=torch.float32, device=dev)
+    at = torch.empty((K, r), dtype=torch.float16, device=dev)
+    bt, N = None, 0
+    if lora_b is not None:
+        lora_b = lora_b.to(torch.float16).contiguous()
+        N = lora_b.shape[0]
+        if lora_b.shape != (N, r):
+            raise ValueError("lora_b must be [N, r]")
+        bt = torch.empty((r, N), dtype=torch.float16, device=dev)
+    _lib.call("mxs_lora_h_partials", _lib.ptr(x2d), M, K, _lib.ptr(lora_a), r, _lib.ptr(_c(mask)),
+              float(mask_scale), float(s), hp.shape[1], _lib.ptr(at), _lib.ptr(lora_b), N,
+              _lib.ptr(bt), _lib.ptr(hp), _lib.stream_of(dev))
+    return hp, at, bt
+
+
+def lora_dh_partials(dy2d, lora_bt, s):
+    """s * dY @ B as fp32 partial sums [slices, ldt, r] (the fused dX GEMM finishes them);
+    lora_bt = lora_B^T [r, N]."""
+    dy2d = dy2d.contiguous()
+    M, N = dy2d.shape
+    r = lora_bt.shape[0]
+    if lora_bt.shape != (r, N):
+        raise ValueError("lora_bt must be [r, N]")
+    dhp = torch.empty((lora_slices(M, N), _ldt(M), r), dtype=torch.float32, device=dy2d.device)
+    _lib.call("mxs_lora_dh_partials", _lib.ptr(dy2d), M, N, _lib.ptr(lora_bt.contiguous()), r,
+              float(s), dhp.shape[1], _lib.ptr(dhp), _lib.stream_of(dy2d.device))
+    return dhp
+
+
+def nf4_linear_fwd_hp(x2d, packed, state, lora_hp, lora_b, bias=None, cfg=-1, splits=1, ws=None):
+    """(y, ht): Y = x2d @ W^T (+ bias) + fp16(sum of lora_hp) @ lora_b^T, and that fp16 LoRA
+    operand transposed [r, ldt] (zeros past M)."""
+    n, k = state.shape
+    if x2d.dtype != torch.float16 or x2d.dim() != 2 or x2d.shape[1] != k:
+        raise ValueError("x must be fp16 [M, in_features]")
+    x2d = x2d.contiguous()
+    M = x2d.shape[0]
+    S, ldt, r = lora_hp.shape
+    if ldt != _ldt(M) or lora_b.shape != (n, r) or lora_hp.dtype != torch.float32:
+        raise ValueError("lora_hp [slices, ldt, r] fp32 needs lora_b [N, r]")
+    lora_b = lora_b.to(torch.float16).contiguous()
+    if bias is not None:
+        bias = bias.to(torch.float16).contiguous()
+    y = torch.empty((M, n), dtype=torch.float16, device=x2d.device)
+    ht = torch.empty((r, ldt), dtype=torch.float16, device=x2d.device)
+    ws = _ws(M, n, k, x2d.device, cfg, splits, ws)
+    _lib.call("mxs_nf4_linear_fwd_hp", _lib.ptr(x2d), M, k, n, *_nf4_args(packed, state),
+              _lib.ptr(bias), _lib.ptr(lora_hp.contiguous()), S, ldt, _lib.ptr(lora_b), r,
+              _lib.ptr(ht), _lib.ptr(y), _lib.ptr(ws), cfg, splits, _lib.stream_of(x2d.device))
+    return y, ht
+
+
+def nf4_linear_bwd_dx_hp(dy2d, packed, state, lora_dhp, lora_at, mask=None, mask_scale=1.0,
+                         cfg=-1, splits=1, ws=None):
+    """(dx, dht): dX = dy2d @ W + mask * mask_scale * (fp16(sum of lora_dhp) @ lora_at^T), and
+    that fp16 operand transposed [r, ldt]."""
+    n, k = state.shape
+    if dy2d.dtype != torch.float16 or dy2d.dim() != 2 or dy2d.shape[1] != n:
+        raise ValueError("dy must be fp16 [M, out_features]")
+    dy2d = dy2d.contiguous()
+    M = dy2d.shape[0]
+    S, ldt, r = lora_dhp.shape
+    if ldt != _ldt(M) or lora_at.shape != (k, r) or lora_dhp.dtype != torch.float32:
+        raise ValueError("lora_dhp [slices, ldt, r] fp32 needs lora_at [K, r]")
+    if mask is not None:
+        if mask.dtype != torch.uint8 or mask.shape != (M, k):
+            raise ValueError("mask must be uint8 [M, K]")
+        mask = mask.contiguous()
+    dx = torch.empty((M, k), dtype=torch.float16, device=dy2d.device)
+    dht = torch.empty((r, ldt), dtype=torch.float16, device=dy2d.device)
+    ws = _ws(M, k, n, dy2d.device, cfg, splits, ws)
+    _lib.call("mxs_nf4_linear_bwd_dx_hp", _lib.ptr(dy2d), M, n, k, *_nf4_args(packed, state),
+              _lib.ptr(lora_dhp.contiguous()), S, ldt, _lib.ptr(lora_at.contiguous()), r,
+              _lib.ptr(mask), float(mask_scale), _lib.ptr(dht), _lib.ptr(dx), _lib.ptr(ws), cfg,
+              splits, _lib.stream_of(dy2d.device))
+    return dx, dht
+
+
 def transpose(t2d):
     """[rows, cols] fp16 -> [cols, rows] fp16 on the GPU (mxs_transpose_f16)."""
     t2d = t2d.contiguous()

@@ -80,9 +80,11 @@ class NF4LinearFunction(torch.autograd.Function):
 
 class NF4LoraFunction(torch.autograd.Function):
     """base(x) + s * B(A(drop(x))) for a frozen NF4 base, fused:
-    forward:  Hs = s * drop(x) A^T (mxs_lora_h), Y = x W^T + bias + Hs B^T (one fused GEMM);
-    backward: dHs = s * dY B, dX = dY W + keep/(1-p) * dHs A (one fused GEMM),
-              dA = dHs^T drop(x), dB = dY^T Hs.
+    forward:  Hs = s * drop(x) A^T as slice partials (mxs_lora_h_partials), then one fused GEMM
+              that finishes Hs and computes Y = x W^T + bias + Hs B^T (and writes Hs^T);
+    backward: dHs = s * dY B as slice partials (mxs_lora_dh_partials), then one fused GEMM
+              that finishes dHs and computes dX = dY W + keep/(1-p) * dHs A (and writes dHs^T);
+              dA = dHs^T drop(x) and dB = dY^T Hs in one launch.
     `keep` is the u8 dropout mask [M, K] (None without dropout); mask_scale = 1/(1-p)."""
 
     @staticmethod
@@ -90,9 +92,8 @@ class NF4LoraFunction(torch.autograd.Function):
         a16 = lora_a.to(torch.float16).contiguous()
         b16 = lora_b.to(torch.float16).contiguous()
         n, k = state.shape
-        h, ht, at, bt = kernels.lora_h(x2d, a16, s, keep, mask_scale, want_at=True,
-                                       lora_b=b16)
-        y = kernels.nf4_linear_fwd(x2d, packed, state, bias, h, b16)
+        hp, at, bt = kernels.lora_h_partials(x2d, a16, s, keep, mask_scale, lora_b=b16)
+        y, ht = kernels.nf4_linear_fwd_hp(x2d, packed, state, hp, b16, bias)
         ctx.save_for_backward(x2d, keep, ht, at, bt)
         ctx.packed, ctx.state, ctx.mask_scale, ctx.s = packed, state, mask_scale, s
         ctx.dtypes = (lora_a.dtype, lora_b.dtype)
@@ -102,11 +103,11 @@ class NF4LoraFunction(torch.autograd.Function):
     def backward(ctx, dy):
         x2d, keep, ht, at, bt = ctx.saved_tensors
         dy = dy.to(torch.float16).contiguous()
-        dh, dht = kernels.lora_dh(dy, None, ctx.s, lora_bt=bt)
-        dx = None
-        if ctx.needs_input_grad[0]:
-            dx = kernels.nf4_linear_bwd_dx(dy, ctx.packed, ctx.state, dh, None, keep,
-                                           ctx.mask_scale, lora_at=at)
+        dhp = kernels.lora_dh_partials(dy, bt, ctx.s)
+        dx, dht = kernels.nf4_linear_bwd_dx_hp(dy, ctx.packed, ctx.state, dhp, at, keep,
+                                               ctx.mask_scale)
+        if not ctx.needs_input_grad[0]:
+            dx = None
         da, db = kernels.lora_grads(dht, ht, x2d, dy, keep, ctx.mask_scale,
                                     want_a=ctx.needs_input_grad[1],
                                     want_b=ctx.needs_input_grad[2])

@@ -248,6 +248,33 @@ def test_lora_sliced_and_single_launch_reductions_agree(cuda):
     assert torch.equal(ht1[:, :M].t(), h1) and torch.all(ht1[:, M:] == 0)
 
 
+@pytest.mark.parametrize("n,k,M", [(1536, 1536, 300), (256, 1536, 37), (1536, 8960, 700),
+                                   (8960, 1536, 64)])
+def test_partial_sum_lora_path_equals_finished_path(cuda, n, k, M):
+    """The GEMMs that finish the LoRA partial sums themselves (and write Hs^T / dHs^T) give the
+    same bits as finishing them in a separate launch first."""
+    from mindxsoup_amd import kernels
+
+    print(f"case partials n={n} k={k} M={M}", flush=True)
+    layer = _layer(cuda, n, k, 31, bias=True)
+    st = layer.weight.quant_state
+    packed = layer.weight.data.view(-1, 1)
+    x, a, b, dy, keep = _lora_inputs(cuda, M, k, n, 32)
+    s, ms = 2.0, 1 / 0.95
+    h, ht, at, bt = kernels.lora_h(x, a, s, keep, ms, n_out=n, want_at=True, lora_b=b)
+    y = kernels.nf4_linear_fwd(x, packed, st, layer.bias, h, b)
+    hp, at2, bt2 = kernels.lora_h_partials(x, a, s, keep, ms, lora_b=b)
+    assert hp.shape[0] == kernels.lora_slices(M, k)
+    y2, ht2 = kernels.nf4_linear_fwd_hp(x, packed, st, hp, b, layer.bias)
+    assert torch.equal(y2, y) and torch.equal(ht2, ht)
+    assert torch.equal(at2, at) and torch.equal(bt2, bt)
+    dh, dht = kernels.lora_dh(dy, None, s, k_in=k, lora_bt=bt)
+    dx = kernels.nf4_linear_bwd_dx(dy, packed, st, dh, None, keep, ms, lora_at=at)
+    dhp = kernels.lora_dh_partials(dy, bt, s)
+    dx2, dht2 = kernels.nf4_linear_bwd_dx_hp(dy, packed, st, dhp, at, keep, ms)
+    assert torch.equal(dx2, dx) and torch.equal(dht2, dht)
+
+
 def test_lora_grads_without_tokens(cuda):
     from mindxsoup_amd import kernels
 
