@@ -458,7 +458,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void k_nf4_gemm(GemmArgs a)
   const float offset = a.offset[0];
 
   float16_t acc[T::TM][T::TN];
-  init_acc<T::TM, T::TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
 
   auto mma = [&](int buf, int kk) {
     const _Float16* as = As + buf * T::LDS_A;
@@ -495,6 +494,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void k_nf4_gemm(GemmArgs a)
     typename L::Stage S0, S1;
     L::issue(a, S0, t, kt0, m0, n0);
     L::issue(a, S1, t, min(kt0 + 1, kt1 - 1), m0, n0);
+    // accumulator start (bias, LoRA) while the first tiles are in flight
+    init_acc<T::TM, T::TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
     __syncthreads();  // tables
 #pragma unroll
     for (int part = 0; part < 4; part++)
@@ -507,6 +508,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void k_nf4_gemm(GemmArgs a)
       step(1, kt + 1, S0, S1);
     }
     if (kt < kt1) step(0, kt, S1, S0);
+  } else {
+    init_acc<T::TM, T::TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
   }
 
   epilogue<T::TM, T::TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
@@ -788,15 +791,18 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
     const int lrow = lane & 31;
     const int lseg = lane >> 5;
     float16_t acc[TM][TN];
-    init_acc<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
     if (kt0 < kt1) {
       lds_barrier();  // tables
+      // accumulator start (bias, LoRA) while the producers stage K-step kt0
+      init_acc<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
       lds_barrier();  // K-step kt0 ready
       for (int kt = kt0; kt < kt1; kt++) {
         const int r = kt - kt0;
         mma_kstep<TM, TN>(acc, As + (r % 3) * LDS_A, Bs + (r & 1) * LDS_B, wm0, wn0, lrow, lseg);
         lds_barrier();
       }
+    } else {
+      init_acc<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
     }
     epilogue<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
   }
