@@ -17,6 +17,8 @@
 // the input gradient masked by the dropout keep mask), computed before the main loop; the
 // epilogue stores fp16.  With split-K (gridDim.z > 1) each split writes fp32 partials and
 // k_splitk_reduce sums them (split 0 carries bias and LoRA).
+#include <type_traits>
+
 #include "common.h"
 #include "mxs_nf4.h"
 
@@ -395,17 +397,45 @@ __device__ __forceinline__ void fill_tables(const GemmArgs& a, float2_t* s_pair,
 
 // One wave's 32x32x16 MFMAs over one 64-deep K-step held in LDS (A rows wm0.., B rows wn0..),
 // with the operand fragments of sub-step kk+1 read while sub-step kk multiplies.
-template <int TM, int TN>
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// MFMA W-side fragment (32 columns n0.. x 16 reduction indices k0..) from a B tile stored with
+// the reduction index as the row: bt[k * ldb + n].  Two transposing LDS reads: in each group of
+// 16 lanes, source lane s reads row k + s/4, columns n + 4*(s%4)..+3, and lane j receives the 4
+// rows of column n + j -- 4 consecutive reduction indices of one column, as the MFMA operand
+// takes them (lanes 0-31: k0..k0+7, lanes 32-63: k0+8..k0+15; lane%32 = column).
+__device__ __forceinline__ half8_t frag_bt(const _Float16* bt, int ldb, int n0, int k0, int lane) {
+  const int g = lane >> 4, sl = lane & 15;
+  const int n = n0 + 16 * (g & 1) + 4 * (sl & 3);
+  const int k = k0 + 8 * (g >> 1) + (sl >> 2);
+  typedef __attribute__((address_space(3))) short4_t lds_short4;
+  // whole-vector casts: __builtin_bit_cast of a single vector element reads element 0 with
+  // this compiler
+  const half4_t lo = __builtin_bit_cast(
+      half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(bt + k * ldb + n)));
+  const half4_t hi = __builtin_bit_cast(
+      half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(bt + (k + 4) * ldb + n)));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// One K-step of MFMAs for a wave's TM x TN tiles.  A fragments from the swizzled [rows][64] A
+// tile; W fragments from the swizzled [cols][64] B tile, or (LDB > 0) from a B tile stored
+// [64][LDB] with the reduction index as the row (frag_bt).
+template <int TM, int TN, int LDB = 0>
 __device__ __forceinline__ void mma_kstep(float16_t (&acc)[TM][TN], const _Float16* as,
                                           const _Float16* bs, int wm0, int wn0, int lrow,
                                           int lseg) {
+  const int lane = lseg * 32 + lrow;
+  auto bfrag = [&](int j, int kk) -> half8_t {
+    if constexpr (LDB > 0) return frag_bt(bs, LDB, wn0 + j * 32, 16 * kk, lane);
+    else return *reinterpret_cast<const half8_t*>(bs + lds_off(wn0 + j * 32 + lrow, 2 * kk + lseg));
+  };
   half8_t af[2][TM], bf[2][TN];
 #pragma unroll
   for (int i = 0; i < TM; i++)
     af[0][i] = *reinterpret_cast<const half8_t*>(as + lds_off(wm0 + i * 32 + lrow, lseg));
 #pragma unroll
-  for (int j = 0; j < TN; j++)
-    bf[0][j] = *reinterpret_cast<const half8_t*>(bs + lds_off(wn0 + j * 32 + lrow, lseg));
+  for (int j = 0; j < TN; j++) bf[0][j] = bfrag(j, 0);
 #pragma unroll
   for (int kk = 0; kk < kBK / 16; kk++) {
     const int cur = kk & 1;
@@ -415,9 +445,7 @@ __device__ __forceinline__ void mma_kstep(float16_t (&acc)[TM][TN], const _Float
         af[cur ^ 1][i] = *reinterpret_cast<const half8_t*>(
             as + lds_off(wm0 + i * 32 + lrow, 2 * (kk + 1) + lseg));
 #pragma unroll
-      for (int j = 0; j < TN; j++)
-        bf[cur ^ 1][j] = *reinterpret_cast<const half8_t*>(
-            bs + lds_off(wn0 + j * 32 + lrow, 2 * (kk + 1) + lseg));
+      for (int j = 0; j < TN; j++) bf[cur ^ 1][j] = bfrag(j, kk + 1);
     }
 #pragma unroll
     for (int i = 0; i < TM; i++)
@@ -685,6 +713,96 @@ struct BLoad<BN, true> {
   }
 };
 
+// NF4 side of a backward K-step for the warp-specialized kernel, with the B tile stored as W's
+// rows: bt[k][n] = W[k0 + k][n0 + n] (k: reduction index = W row, n: output column), row
+// stride LDB halfs (BN, or BN + 32 when BN * 2 bytes is a multiple of 256, so that the four rows
+// one transposing read touches fall in different LDS banks).  Item = 16 packed bytes of one W
+// row (32 columns, one block scale: n0 is a multiple of 32, so a chunk never straddles a
+// block), 3 memory instructions; a 160-column tile adds one 4-byte item per lane for columns
+// 128-159.  The decoded values are written as 4 contiguous 16-byte stores.
+template <int BN>
+struct BLoadT {
+  static constexpr int NTP = 256;
+  static constexpr int LDB = (BN * 2) % 256 == 0 ? BN + 32 : BN;
+  static constexpr int C16 = BN >= 128 ? 128 : BN;  // columns loaded as 16-byte items
+  static constexpr int REST = BN - C16;
+  static_assert(REST == 0 || REST == 32, "B tile columns: <= 128, or 128 + 32");
+  static constexpr int CPR = C16 / 32;               // 16-byte items per row
+  static constexpr int TOTAL = kBK * CPR;
+  static constexpr int VMEM = REST ? 6 : 3;
+  static_assert(TOTAL % 64 == 0 && TOTAL <= NTP, "B items in whole waves, one round");
+
+  struct Stage {
+    u32x4 w;
+    uint32_t q8;
+    float a2;
+    uint32_t w4, q8b;
+    float a2b;
+  };
+
+  __device__ static __forceinline__ void issue(const GemmArgs& a, Stage& S, int p, int kt,
+                                               int n0) {
+    const int k0 = kt * kBK;
+    {
+      const int q = min(p, TOTAL - 1);  // lanes past TOTAL load a duplicate item
+      const int row = q / CPR, c = q % CPR;
+      const int col = min(n0 + 32 * c, a.Nc - 32);
+      const int64_t idx = (int64_t)(k0 + row) * a.Kw + col;
+      S.q8 = a.absmax8[idx >> 6];
+      S.a2 = a.absmax2[idx >> 14];
+      S.w = *reinterpret_cast<const u32x4*>(a.packed + (idx >> 1));
+    }
+    if constexpr (REST > 0) {
+      const int row = p >> 2, sub = p & 3;
+      const int col = min(n0 + C16 + 8 * sub, a.Nc - 8);
+      const int64_t idx = (int64_t)(k0 + row) * a.Kw + col;
+      S.q8b = a.absmax8[idx >> 6];
+      S.a2b = a.absmax2[idx >> 14];
+      S.w4 = *reinterpret_cast<const uint32_t*>(a.packed + (idx >> 1));
+    }
+  }
+
+  __device__ static __forceinline__ void commit(const Stage& S, _Float16* bs, int p,
+                                                const float2_t* s_pair, const float* s_code,
+                                                float offset) {
+    float2_t pr[4][4];
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
+    float2_t pb[4];
+    if constexpr (REST > 0) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) pb[j] = s_pair[(S.w4 >> (8 * j)) & 0xffu];
+    }
+    if (p < TOTAL) {
+      const int row = p / CPR, c = p % CPR;
+      const float sc = nested_scale(s_code[S.q8], S.a2, offset);
+#pragma unroll
+      for (int d = 0; d < 4; d++) {
+        u32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pr[d][j][0] * sc, pr[d][j][1] * sc);
+        *reinterpret_cast<u32x4*>(bs + row * LDB + 32 * c + 8 * d) = v;
+      }
+    }
+    if constexpr (REST > 0) {
+      const int row = p >> 2, sub = p & 3;
+      const float sc = nested_scale(s_code[S.q8b], S.a2b, offset);
+      u32x4 v;
+#pragma unroll
+      for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pb[j][0] * sc, pb[j][1] * sc);
+      *reinterpret_cast<u32x4*>(bs + row * LDB + C16 + 8 * sub) = v;
+    }
+  }
+};
+
+// LDS halfs of the warp-specialized kernel's tiles: 3-deep A ring + 2-deep B buffer.
+template <int BM, int BN, bool BWD>
+constexpr int ws_lds_halfs() {
+  return 3 * BM * kBK + 2 * (BWD ? kBK * BLoadT<BN>::LDB : BN * kBK);
+}
+
 // Direct global -> LDS copy of one K-step's A tile (BM rows x 64 fp16) by the producer waves:
 // each global_load_lds_dwordx4 writes 8 rows (64 lanes x 16 B, consecutive in LDS); lane l takes
 // the logical segment that the row's XOR swizzle places at its physical slot.
@@ -722,8 +840,9 @@ template <int BM, int BN, int CWM, int CWN, bool BWD>
 __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
   constexpr int WM = BM / CWM, WN = BN / CWN, TM = WM / 32, TN = WN / 32;
   static_assert(CWM * CWN == 4 && WM % 32 == 0 && WN % 32 == 0, "consumer wave tiles");
-  using B = BLoad<BN, BWD>;
-  constexpr int LDS_A = BM * kBK, LDS_B = BN * kBK;
+  using B = std::conditional_t<BWD, BLoadT<BN>, BLoad<BN, false>>;
+  constexpr int LDB = BWD ? BLoadT<BN>::LDB : 0;  // B tile stored [64][LDB] (backward)
+  constexpr int LDS_A = BM * kBK, LDS_B = BWD ? kBK * LDB : BN * kBK;
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
   _Float16* As = smem;                      // [3][BM][64]
   _Float16* Bs = smem + 3 * LDS_A;          // [2][BN][64]
@@ -798,7 +917,8 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
       lds_barrier();  // K-step kt0 ready
       for (int kt = kt0; kt < kt1; kt++) {
         const int r = kt - kt0;
-        mma_kstep<TM, TN>(acc, As + (r % 3) * LDS_A, Bs + (r & 1) * LDS_B, wm0, wn0, lrow, lseg);
+        mma_kstep<TM, TN, LDB>(acc, As + (r % 3) * LDS_A, Bs + (r & 1) * LDS_B, wm0, wn0, lrow,
+                               lseg);
         lds_barrier();
       }
     } else {
@@ -844,7 +964,7 @@ static int launch_ws(const GemmArgs& a0, int splits, hipStream_t stream) {
   splits = n_steps > 0 ? (n_steps + a.steps_per_split - 1) / a.steps_per_split : 1;
   const dim3 grid((a.Nc + BN - 1) / BN, (a.M + BM - 1) / BM, splits);
   if (splits > 1 && !a.ws) return MXS_ERR_ARG;
-  const size_t lds = (size_t)(3 * BM + 2 * BN) * kBK * sizeof(_Float16);
+  const size_t lds = (size_t)ws_lds_halfs<BM, BN, BWD>() * sizeof(_Float16);
   static bool lds_set = false;  // idempotent attribute; a benign race between threads
   if (!lds_set) {
     hipError_t e = hipFuncSetAttribute(
@@ -884,9 +1004,10 @@ constexpr int kNumCfg = 10;
 // MI355X at the Qwen2.5-1.5B projection shapes (M = 1024):
 //   wide outputs (Nc >= 4096): warp-specialized 256x160, one tile per CU, no split;
 //   narrow outputs with a long reduction (Kr >= 4096): warp-specialized 256x96, split-K 4;
-//   mid outputs (Nc >= 1024): 128x128 (2x4 waves), split-K 2;
-//   small outputs: 64x128, split-K 4 when the reduction is long enough.
-// Splits keep at least 8 K-steps each.
+//   mid outputs (Nc >= 1024): warp-specialized 128x128, split-K 2 (a short reduction: 64x128
+//   all-wave tiles, no split);
+//   small outputs: 64x128 all-wave tiles, split-K 4 when the reduction is long enough.
+// Splits keep at least 6 K-steps each.
 static void choose(int M, int Nc, int Kr, int* cfg, int* splits) {
   const int n_steps = Kr / kBK;
   int c, sp;
@@ -895,12 +1016,16 @@ static void choose(int M, int Nc, int Kr, int* cfg, int* splits) {
   } else if (Kr >= 4096) {
     c = 9; sp = 4;
   } else if (Nc >= 1024) {
-    c = 3; sp = 2;
+    if (Kr >= 1024) {
+      c = 8; sp = 2;
+    } else {
+      c = 4; sp = 1;
+    }
   } else {
     c = 4; sp = Kr >= 1024 ? 4 : 1;
   }
   (void)M;
-  while (sp > 1 && n_steps / sp < 8) sp >>= 1;
+  while (sp > 1 && n_steps / sp < 6) sp >>= 1;
   *cfg = c;
   *splits = sp;
 }
