@@ -234,6 +234,100 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, float16_t (&acc)[TM]
 }
 
 // Split-K: C = fp16(sum over the split planes of ws), summed in split order (deterministic).
+// Epilogue through LDS (warp-specialized kernel): a wave's accumulators leave in 32-row slices.
+// The slice is written to the wave's own LDS area in the accumulator layout (8-byte fp16 or
+// 16-byte fp32 items; row stride padded to 2 x odd (fp16) or 4 x odd (fp32) dwords, so the 32
+// rows of one write hit distinct banks), read back row-major, and stored 16 contiguous bytes
+// per lane, so every store instruction writes whole cache lines instead of 16 bytes in each of
+// 32 rows.  Only the writing wave touches its area, so no barrier is needed between slices;
+// LDS instructions of one wave complete in order.  `area` holds 32 * stride dwords.
+template <int TM, int TN>
+struct StagedStore {
+  static constexpr int WN = TN * 32;
+  static constexpr int S16 = WN / 2 + 2;  // fp16 row stride in dwords
+  static constexpr int S32 = WN + 4;      // fp32 row stride in dwords
+  static constexpr int AREA_DWORDS = 32 * S32;
+};
+
+template <int TM, int TN>
+__device__ __forceinline__ void epilogue_staged(const GemmArgs& a, float16_t (&acc)[TM][TN],
+                                                int mb, int nb, int lane, float* area) {
+  using SS = StagedStore<TM, TN>;
+  constexpr int WN = SS::WN;
+  const int lrow = lane & 31, lseg = lane >> 5;
+  const bool split = gridDim.z > 1;
+  // whole 16-byte chunks can be stored when rows keep 16-byte alignment
+  const bool vec = split ? (a.Nc % 4) == 0 : ((a.Nc % 8) == 0 && (a.ldc % 8) == 0 &&
+                                               ((uintptr_t)a.C % 16) == 0);
+#pragma unroll
+  for (int i = 0; i < TM; i++) {
+    const int row0 = mb + i * 32;
+    if (row0 >= a.M) break;
+    if (split) {
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const float4_t v = {acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                              acc[i][j][4 * g + 3]};
+          *reinterpret_cast<float4_t*>(area + lrow * SS::S32 + 32 * j + 8 * g + 4 * lseg) = v;
+        }
+    } else {
+      uint32_t* ar = reinterpret_cast<uint32_t*>(area);
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          u32x2 v;
+          v[0] = pack_f16x2(acc[i][j][4 * g], acc[i][j][4 * g + 1]);
+          v[1] = pack_f16x2(acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]);
+          *reinterpret_cast<u32x2*>(ar + lrow * SS::S16 + 16 * j + 4 * g + 2 * lseg) = v;
+        }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    if (split) {
+      constexpr int CPR = WN / 4;  // 16-byte chunks per row
+#pragma unroll
+      for (int q = 0; q < CPR / 2; q++) {
+        const int c = q * 64 + lane;
+        const int r = c / CPR, cc = c % CPR;
+        const int m = row0 + r, n = nb + 4 * cc;
+        const float4_t v = *reinterpret_cast<const float4_t*>(area + r * SS::S32 + 4 * cc);
+        if (m >= a.M || n >= a.Nc) continue;
+        float* w = a.ws + ((int64_t)blockIdx.z * a.M + m) * a.Nc + n;
+        if (vec && n + 3 < a.Nc) {
+          *reinterpret_cast<float4_t*>(w) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (n + e < a.Nc) w[e] = v[e];
+        }
+      }
+    } else {
+      constexpr int CPR = WN / 8;
+      const uint32_t* ar = reinterpret_cast<const uint32_t*>(area);
+#pragma unroll
+      for (int q = 0; q < CPR / 2; q++) {
+        const int c = q * 64 + lane;
+        const int r = c / CPR, cc = c % CPR;
+        const int m = row0 + r, n = nb + 8 * cc;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(ar + r * SS::S16 + 4 * cc);
+        if (m >= a.M || n >= a.Nc) continue;
+        _Float16* dst = a.C + (int64_t)m * a.ldc + n;
+        if (vec && n + 7 < a.Nc) {
+          *reinterpret_cast<u32x4*>(dst) = v;
+        } else {
+          const half8_t h = __builtin_bit_cast(half8_t, v);
+#pragma unroll
+          for (int e = 0; e < 8; e++)
+            if (n + e < a.Nc) dst[e] = h[e];
+        }
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // reads done before the next slice
+  }
+}
+
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int splits,
                                                       int M, int Nc, _Float16* __restrict__ C,
                                                       int64_t ldc) {
@@ -543,19 +637,16 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void k_nf4_gemm(GemmArgs a)
   epilogue<T::TM, T::TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
 }
 
-// NF4 side of a K-step for the warp-specialized kernel's 256 producer threads.
-//   forward:  item = 16 packed bytes of W row n (32 values, half of the row's block for this
-//             K-step, one block scale), 3 memory instructions each (dwordx4, absmax8 byte,
-//             absmax2 float); a 160-row tile adds one 4-byte item per lane for rows 128-159
-//   backward: item = 4 W rows x 8 output columns (4 block scales), decoded along W's rows
-template <int BN, bool BWD>
-struct BLoad;
-
+// NF4 side of a forward K-step for the warp-specialized kernel's 256 producer threads.
+// Item = 16 packed bytes of W row n (32 values, half of the row's block for this K-step, one
+// block scale), 3 memory instructions (dwordx4, absmax8 byte, absmax2 float); a 160-row tile
+// adds one 4-byte item per lane for rows 128-159, so every producer lane decodes 40 values and
+// no wave does a second 16-byte round alone.  Per-lane byte offsets are computed once (setup);
+// a K-step only moves the uniform base pointers, so the loads take the scalar-base address
+// form and cost no per-step vector address arithmetic.  Offsets are 32-bit: the launcher only
+// picks this kernel when W has fewer than 2^32 values.
 template <int BN>
-struct BLoad<BN, false> {
-  // Rows [0, R16) as 16-byte items (2 lanes per row); for BN = 160 the last 32 rows as 4-byte
-  // items (8 lanes per row), so every producer lane decodes 40 values and no wave does a
-  // second 16-byte round alone.
+struct BLoad {
   static constexpr int NTP = 256;
   static constexpr int R16 = BN >= 128 ? 128 : BN;
   static constexpr int REST = BN - R16;
@@ -571,26 +662,34 @@ struct BLoad<BN, false> {
     uint32_t w4, q8b;  // 4-byte item (REST rows)
     float a2b;
   };
+  struct Src {
+    uint32_t w, blk;    // packed byte offset of the item at K-step 0; its row's first block
+    uint32_t w4, blk4;  // the same for the 4-byte item
+  };
 
-  __device__ static __forceinline__ void issue(const GemmArgs& a, Stage& S, int p, int kt,
-                                               int n0) {
-    const int k0 = kt * kBK;
-    {
-      const int q = min(p, TOTAL - 1);  // lanes past TOTAL load a duplicate item
-      const int n = min(n0 + (q >> 1), a.Nc - 1);
-      const int64_t blk = ((int64_t)n * a.Kw + k0) >> 6;
-      S.q8 = a.absmax8[blk];
-      S.a2 = a.absmax2[blk >> 8];
-      S.w = *reinterpret_cast<const u32x4*>(a.packed + (int64_t)n * (a.Kw / 2) + k0 / 2 +
-                                             (q & 1) * 16);
-    }
+  __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0) {
+    Src r;
+    const int q = min(p, TOTAL - 1);  // lanes past TOTAL load a duplicate item
+    const uint32_t n = min(n0 + (q >> 1), a.Nc - 1);
+    r.w = n * (uint32_t)(a.Kw / 2) + (q & 1) * 16;
+    r.blk = n * (uint32_t)(a.Kw / 64);
+    const uint32_t n4 = min(n0 + R16 + (p >> 3), a.Nc - 1);
+    r.w4 = n4 * (uint32_t)(a.Kw / 2) + (p & 7) * 4;
+    r.blk4 = n4 * (uint32_t)(a.Kw / 64);
+    return r;
+  }
+
+  __device__ static __forceinline__ void issue(const GemmArgs& a, const Src& src, Stage& S,
+                                               int kt) {
+    const uint8_t* pk = a.packed + kt * (kBK / 2);  // uniform
+    const uint8_t* q8 = a.absmax8 + kt;             // block of row n at K-step kt: blk + kt
+    S.q8 = q8[src.blk];
+    S.a2 = a.absmax2[(src.blk + kt) >> 8];
+    S.w = *reinterpret_cast<const u32x4*>(pk + src.w);
     if constexpr (REST > 0) {
-      const int n = min(n0 + R16 + (p >> 3), a.Nc - 1);
-      const int64_t blk = ((int64_t)n * a.Kw + k0) >> 6;
-      S.q8b = a.absmax8[blk];
-      S.a2b = a.absmax2[blk >> 8];
-      S.w4 = *reinterpret_cast<const uint32_t*>(a.packed + (int64_t)n * (a.Kw / 2) + k0 / 2 +
-                                                 (p & 7) * 4);
+      S.q8b = q8[src.blk4];
+      S.a2b = a.absmax2[(src.blk4 + kt) >> 8];
+      S.w4 = *reinterpret_cast<const uint32_t*>(pk + src.w4);
     }
   }
 
@@ -627,92 +726,6 @@ struct BLoad<BN, false> {
   }
 };
 
-template <int BN>
-struct BLoad<BN, true> {
-  static constexpr bool BWD = true;
-  static constexpr int NTP = 256;
-  static constexpr int TOTAL = (BN / 8) * (kBK / 4);
-  static constexpr int ITEMS = (TOTAL + NTP - 1) / NTP;
-  static constexpr int NW = 4;
-  static constexpr int VMEM = 3 * NW * ITEMS;  // memory instructions one issue() makes per lane
-  static_assert(TOTAL % 64 == 0, "B items in whole waves");
-
-  struct Stage {
-    uint32_t w[ITEMS][NW];
-    uint32_t q8[ITEMS][NW];
-    float a2[ITEMS][NW];
-  };
-
-  __device__ static __forceinline__ void issue(const GemmArgs& a, Stage& S, int p, int kt,
-                                               int n0) {
-    const int k0 = kt * kBK;
-#pragma unroll
-    for (int u = 0; u < ITEMS; u++) {
-      const int q = min(p + u * NTP, TOTAL - 1);  // lanes past TOTAL load a duplicate item
-      if (!BWD) {
-        const int n = min(n0 + (q >> 3), a.Nc - 1);
-        const int64_t blk = ((int64_t)n * a.Kw + k0) >> 6;
-        S.q8[u][0] = a.absmax8[blk];
-        S.a2[u][0] = a.absmax2[blk >> 8];
-        S.w[u][0] = *reinterpret_cast<const uint32_t*>(
-            a.packed + (int64_t)n * (a.Kw / 2) + k0 / 2 + (q & 7) * 4);
-      } else {
-        const int chunk = q % (BN / 8);
-        const int rg = q / (BN / 8);
-        const int col = min(n0 + chunk * 8, a.Nc - 8);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int64_t idx = (int64_t)(k0 + rg * 4 + i) * a.Kw + col;
-          S.q8[u][i] = a.absmax8[idx >> 6];
-          S.a2[u][i] = a.absmax2[idx >> 14];
-          S.w[u][i] = *reinterpret_cast<const uint32_t*>(a.packed + (idx >> 1));
-        }
-      }
-    }
-  }
-
-  __device__ static __forceinline__ void commit(const Stage& S, _Float16* bs, int p,
-                                                const float2_t* s_pair, const float* s_code,
-                                                float offset) {
-#pragma unroll
-    for (int u = 0; u < ITEMS; u++) {
-      const int q = p + u * NTP;
-      if (q >= TOTAL) break;
-      if (!BWD) {
-        const float sc = nested_scale(s_code[S.q8[u][0]], S.a2[u][0], offset);
-        const uint32_t w = S.w[u][0];
-        u32x4 v;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const float2_t pr = s_pair[(w >> (8 * j)) & 0xffu];
-          v[j] = pack_f16x2(pr[0] * sc, pr[1] * sc);
-        }
-        *reinterpret_cast<u32x4*>(bs + lds_off(q >> 3, q & 7)) = v;
-      } else {
-        const int chunk = q % (BN / 8);
-        const int rg = q / (BN / 8);
-        float sc[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) sc[i] = nested_scale(s_code[S.q8[u][i]], S.a2[u][i], offset);
-#pragma unroll
-        for (int part = 0; part < 4; part++) {
-          float2_t pr[4];
-#pragma unroll
-          for (int i = 0; i < 4; i++) pr[i] = s_pair[(S.w[u][i] >> (8 * part)) & 0xffu];
-#pragma unroll
-          for (int cc = 0; cc < 2; cc++) {
-            u32x2 v;
-            v[0] = pack_f16x2(pr[0][cc] * sc[0], pr[1][cc] * sc[1]);
-            v[1] = pack_f16x2(pr[2][cc] * sc[2], pr[3][cc] * sc[3]);
-            const int row = chunk * 8 + part * 2 + cc;
-            *reinterpret_cast<u32x2*>(bs + lds_off(row, rg >> 1) + (rg & 1) * 4) = v;
-          }
-        }
-      }
-    }
-  }
-};
-
 // NF4 side of a backward K-step for the warp-specialized kernel, with the B tile stored as W's
 // rows: bt[k][n] = W[k0 + k][n0 + n] (k: reduction index = W row, n: output column), row
 // stride LDB halfs (BN, or BN + 32 when BN * 2 bytes is a multiple of 256, so that the four rows
@@ -739,26 +752,33 @@ struct BLoadT {
     uint32_t w4, q8b;
     float a2b;
   };
+  // value index of the item within its K-step's 64-row slab of W (row * Kw + col); the slab of
+  // K-step kt starts at value kt * 64 * Kw (32-bit: W has fewer than 2^32 values)
+  struct Src {
+    uint32_t x, x4;
+  };
 
-  __device__ static __forceinline__ void issue(const GemmArgs& a, Stage& S, int p, int kt,
-                                               int n0) {
-    const int k0 = kt * kBK;
-    {
-      const int q = min(p, TOTAL - 1);  // lanes past TOTAL load a duplicate item
-      const int row = q / CPR, c = q % CPR;
-      const int col = min(n0 + 32 * c, a.Nc - 32);
-      const int64_t idx = (int64_t)(k0 + row) * a.Kw + col;
-      S.q8 = a.absmax8[idx >> 6];
-      S.a2 = a.absmax2[idx >> 14];
-      S.w = *reinterpret_cast<const u32x4*>(a.packed + (idx >> 1));
-    }
+  __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0) {
+    Src r;
+    const int q = min(p, TOTAL - 1);  // lanes past TOTAL load a duplicate item
+    const int row = q / CPR, c = q % CPR;
+    r.x = (uint32_t)row * a.Kw + min(n0 + 32 * c, a.Nc - 32);
+    r.x4 = (uint32_t)(p >> 2) * a.Kw + min(n0 + C16 + 8 * (p & 3), a.Nc - 8);
+    return r;
+  }
+
+  __device__ static __forceinline__ void issue(const GemmArgs& a, const Src& src, Stage& S,
+                                               int kt) {
+    const uint32_t slab = (uint32_t)kt * kBK * a.Kw;   // uniform
+    const uint8_t* pk = a.packed + slab / 2;
+    const uint8_t* q8 = a.absmax8 + slab / 64;
+    S.q8 = q8[src.x >> 6];
+    S.a2 = a.absmax2[(slab + src.x) >> 14];
+    S.w = *reinterpret_cast<const u32x4*>(pk + (src.x >> 1));
     if constexpr (REST > 0) {
-      const int row = p >> 2, sub = p & 3;
-      const int col = min(n0 + C16 + 8 * sub, a.Nc - 8);
-      const int64_t idx = (int64_t)(k0 + row) * a.Kw + col;
-      S.q8b = a.absmax8[idx >> 6];
-      S.a2b = a.absmax2[idx >> 14];
-      S.w4 = *reinterpret_cast<const uint32_t*>(a.packed + (idx >> 1));
+      S.q8b = q8[src.x4 >> 6];
+      S.a2b = a.absmax2[(slab + src.x4) >> 14];
+      S.w4 = *reinterpret_cast<const uint32_t*>(pk + (src.x4 >> 1));
     }
   }
 
@@ -805,30 +825,54 @@ constexpr int ws_lds_halfs() {
 
 // Direct global -> LDS copy of one K-step's A tile (BM rows x 64 fp16) by the producer waves:
 // each global_load_lds_dwordx4 writes 8 rows (64 lanes x 16 B, consecutive in LDS); lane l takes
-// the logical segment that the row's XOR swizzle places at its physical slot.
+// the logical segment that the row's XOR swizzle places at its physical slot.  Wave pw copies
+// row groups pw, pw + 4, ...  Each lane's source byte offsets from the tile's first row are
+// computed once (32-bit: the launcher checks BM * lda * 2 < 2^32); a K-step only moves the
+// uniform source pointer and the ring slot, so a copy costs two scalar instructions and the
+// load.
+// M0 is a reserved register to the compiler; the copy below writes it on purpose (see there)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 template <int BM>
-__device__ __forceinline__ void dma_a_tile(const GemmArgs& a, _Float16* as, int pw, int lane,
-                                           int kt, int m0) {
-  const int k0 = kt * kBK;
+struct ACopy {
+  static constexpr int N = BM / 32;  // copies per producer wave per K-step
+  uint32_t off[N];
+  const char* base;  // A row m0 (uniform)
+  uint32_t lds;      // LDS byte address of this wave's first row group in ring slot 0 (uniform)
+
+  __device__ __forceinline__ void init(const GemmArgs& a, const _Float16* as, int pw, int lane,
+                                       int m0) {
 #pragma unroll
-  for (int g = pw; g < BM / 8; g += 4) {
-    const int row = g * 8 + (lane >> 3);
-    const int seg = ((lane & 7) ^ row ^ (row >> 3)) & 7;
-    const int m = min(m0 + row, a.M - 1);
-    const _Float16* src = a.A + (int64_t)m * a.lda + k0 + seg * 8;
-    // Inline asm rather than __builtin_amdgcn_global_load_lds: the compiler cannot tell these
-    // LDS writes from the producers' table reads and would drain every outstanding load before
-    // each of those reads.  Completion is awaited explicitly (wait_vmcnt) before the barrier
-    // that hands the tile over.  M0 = this wave's LDS destination (the low 32 bits of a generic
-    // pointer into LDS are the LDS address); no other code in the kernel uses M0.
-    const uint32_t dst = __builtin_amdgcn_readfirstlane(
-        static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as + g * 8 * kBK)));
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :
-                 : "s"(dst), "v"(src)
-                 : "memory", "m0");
+    for (int i = 0; i < N; i++) {
+      const int row = (pw + 4 * i) * 8 + (lane >> 3);
+      const int seg = ((lane & 7) ^ row ^ (row >> 3)) & 7;
+      const uint32_t m = min(m0 + row, a.M - 1) - m0;
+      off[i] = (m * (uint32_t)a.lda + seg * 8) * 2;
+    }
+    base = reinterpret_cast<const char*>(a.A + (int64_t)m0 * a.lda);
+    lds = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as + pw * 8 * kBK)));
   }
-}
+
+  // copy K-step kt into ring slot `slot_bytes` (byte offset of the slot from slot 0)
+  __device__ __forceinline__ void copy(uint32_t slot_bytes, int kt) const {
+    const char* src = base + (size_t)kt * kBK * sizeof(_Float16);
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+      // Inline asm rather than __builtin_amdgcn_global_load_lds: the compiler cannot tell
+      // these LDS writes from the producers' table reads and would drain every outstanding
+      // load before each of those reads.  Completion is awaited explicitly (wait_vmcnt) before
+      // the barrier that hands the tile over.  M0 = the LDS destination of this wave's 8 rows;
+      // no other code in the kernel uses M0.
+      const uint32_t dst = lds + slot_bytes + i * 4 * 8 * kBK * sizeof(_Float16);
+      asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                   :
+                   : "s"(dst), "v"(off[i]), "s"(src)
+                   : "memory", "m0");
+    }
+  }
+};
+#pragma clang diagnostic pop
 
 // Warp-specialized kernel: 4 consumer waves (one per SIMD, CWM x CWN over the BM x BN tile)
 // only read LDS fragments and issue MFMAs; 4 producer waves (the other wave of each SIMD) copy
@@ -840,7 +884,7 @@ template <int BM, int BN, int CWM, int CWN, bool BWD>
 __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
   constexpr int WM = BM / CWM, WN = BN / CWN, TM = WM / 32, TN = WN / 32;
   static_assert(CWM * CWN == 4 && WM % 32 == 0 && WN % 32 == 0, "consumer wave tiles");
-  using B = std::conditional_t<BWD, BLoadT<BN>, BLoad<BN, false>>;
+  using B = std::conditional_t<BWD, BLoadT<BN>, BLoad<BN>>;
   constexpr int LDB = BWD ? BLoadT<BN>::LDB : 0;  // B tile stored [64][LDB] (backward)
   constexpr int LDS_A = BM * kBK, LDS_B = BWD ? kBK * LDB : BN * kBK;
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
@@ -870,14 +914,18 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
       // number of memory instructions in flight is a constant and each wait names exactly the
       // group it needs.  Order within step kt: commit B(kt+1), A(kt+2), B(kt+3), wait A(kt+1).
       constexpr int LB = B::VMEM;
-      constexpr int LA = BM / 32;  // dma_a_tile instructions per producer wave
+      constexpr int LA = ACopy<BM>::N;  // A-tile copy instructions per producer wave
+      constexpr uint32_t SLOT = LDS_A * sizeof(_Float16);
       const int last = kt1 - 1;
+      ACopy<BM> ac;
+      ac.init(a, As, pw, lane, m0);
+      const typename B::Src src = B::setup(a, p, n0);
       typename B::Stage S0, S1, S2;
-      B::issue(a, S0, p, kt0, n0);
-      dma_a_tile<BM>(a, As, pw, lane, kt0, m0);
-      B::issue(a, S1, p, min(kt0 + 1, last), n0);
-      dma_a_tile<BM>(a, As + LDS_A, pw, lane, min(kt0 + 1, last), m0);
-      B::issue(a, S2, p, min(kt0 + 2, last), n0);
+      B::issue(a, src, S0, kt0);
+      ac.copy(0, kt0);
+      B::issue(a, src, S1, min(kt0 + 1, last));
+      ac.copy(SLOT, min(kt0 + 1, last));
+      B::issue(a, src, S2, min(kt0 + 2, last));
       lds_barrier();  // tables
       B::commit(S0, Bs, p, s_pair, s_code, offset);
       wait_vmcnt<2 * LB + LA>();  // A(kt0): after it only B(kt0+1), A(kt0+1), B(kt0+2)
@@ -887,8 +935,8 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
         // the compiler's own wait before this commit (B(kt+1) registers) also completes
         // A(kt+1), issued after B(kt+1); B(kt+2) stays in flight
         if (kt + 1 < kt1) B::commit(Sc, Bs + ((r + 1) & 1) * LDS_B, p, s_pair, s_code, offset);
-        dma_a_tile<BM>(a, As + ((r + 2) % 3) * LDS_A, pw, lane, min(kt + 2, last), m0);
-        B::issue(a, Si, p, min(kt + 3, last), n0);
+        ac.copy(((r + 2) % 3) * SLOT, min(kt + 2, last));
+        B::issue(a, src, Si, min(kt + 3, last));
         wait_vmcnt<2 * LB + LA>();  // A(kt+1): after it only B(kt+2), A(kt+2), B(kt+3)
         lds_barrier();
       };
@@ -900,8 +948,9 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
       }
       if (kt < kt1) step(kt, S1, S0);
       if (kt + 1 < kt1) step(kt + 1, S2, S1);
-      wait_vmem_all();  // no copy into LDS may be in flight when the workgroup ends
+      wait_vmem_all();  // no copy into the A ring may still be in flight
     }
+    lds_barrier();  // the A ring is free for the consumers' staged epilogue
   } else {
     // ---- consumers ----
     const int wave = t >> 6;
@@ -924,7 +973,11 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
     } else {
       init_acc<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
     }
-    epilogue<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
+    lds_barrier();  // the producers' last copies have landed
+    static_assert(4 * StagedStore<TM, TN>::AREA_DWORDS * 4 <= 3 * LDS_A * 2,
+                  "staged epilogue areas fit in the A ring");
+    epilogue_staged<TM, TN>(a, acc, m0 + wm0, n0 + wn0, lane,
+                            reinterpret_cast<float*>(As) + wave * StagedStore<TM, TN>::AREA_DWORDS);
   }
 }
 
@@ -956,6 +1009,10 @@ static int launch_cfg(const GemmArgs& a0, int splits, hipStream_t stream) {
 
 template <int BM, int BN, int CWM, int CWN, bool BWD>
 static int launch_ws(const GemmArgs& a0, int splits, hipStream_t stream) {
+  // the producers' 32-bit offsets: W values and one A tile's bytes below 2^32; otherwise the
+  // all-wave kernel (64-bit addressing) takes the call
+  if ((int64_t)a0.Nc * a0.Kr >= (int64_t(1) << 32) || (int64_t)BM * a0.lda * 2 >= (int64_t(1) << 32))
+    return launch_cfg<64, 128, 1, 4, BWD>(a0, splits, stream);
   GemmArgs a = a0;
   const int n_steps = a.Kr / kBK;
   if (splits < 1) splits = 1;
@@ -1004,8 +1061,7 @@ constexpr int kNumCfg = 10;
 // MI355X at the Qwen2.5-1.5B projection shapes (M = 1024):
 //   wide outputs (Nc >= 4096): warp-specialized 256x160, one tile per CU, no split;
 //   narrow outputs with a long reduction (Kr >= 4096): warp-specialized 256x96, split-K 4;
-//   mid outputs (Nc >= 1024): warp-specialized 128x128, split-K 2 (a short reduction: 64x128
-//   all-wave tiles, no split);
+//   mid outputs (Nc >= 1024): warp-specialized 128x128, no split;
 //   small outputs: 64x128 all-wave tiles, split-K 4 when the reduction is long enough.
 // Splits keep at least 6 K-steps each.
 static void choose(int M, int Nc, int Kr, int* cfg, int* splits) {
@@ -1016,11 +1072,7 @@ static void choose(int M, int Nc, int Kr, int* cfg, int* splits) {
   } else if (Kr >= 4096) {
     c = 9; sp = 4;
   } else if (Nc >= 1024) {
-    if (Kr >= 1024) {
-      c = 8; sp = 2;
-    } else {
-      c = 4; sp = 1;
-    }
+    c = 8; sp = 1;
   } else {
     c = 4; sp = Kr >= 1024 ? 4 : 1;
   }
