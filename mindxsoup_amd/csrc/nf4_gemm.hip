@@ -85,108 +85,340 @@ struct Tile {
 // keeps row m = mb + 32i + l%32 and, in register group g (4 registers), the 4 consecutive
 // columns n = nb + 32j + 8g + 4(l/32) .. +3.
 //
-// Accumulator start value: the terms that do not depend on the reduction, computed before the
-// main loop (their loads overlap the first tiles' arrival): bias, and the LoRA term as one MFMA
-// per tile per 16 ranks (masked by the dropout keep mask and scaled in the backward pass).  Only
-// the first split of a split-K launch carries them; the others start at zero.
+// Accumulator start value: the terms that do not depend on the reduction: bias, and the LoRA
+// term as one MFMA per tile per 16 ranks (masked by the dropout keep mask and scaled in the
+// backward pass).  Only the first split of a split-K launch carries them; the others start at
+// zero.  load() prefetches the bias of narrow tiles; the kernels call it before anything else so
+// that it shares the first round trip to memory with the first tiles' loads.  finish() builds
+// the accumulators.  The LoRA operands and the keep mask come either from LDS areas that the
+// warp-specialized kernel's producers staged (`ls`: [rows][16] fp16 operand of the workgroup's
+// rows then [cols][16] of lora_w, r = 16; `kls`: the workgroup's keep bytes, row stride `kst`)
+// or straight from memory.
 template <int TM, int TN, bool BWD>
-__device__ __forceinline__ void init_acc(const GemmArgs& a, float16_t (&acc)[TM][TN], int mb,
-                                         int nb, int lrow, int lseg) {
+struct AccStart {
+  // the bias is prefetched only for narrow wave tiles (register budget of the wide ones)
+  static constexpr bool kBiasPre = !BWD && TN <= 2;
+  half4_t bias[kBiasPre ? TN : 1][4];  // 4 bias values per register group
+
+  __device__ static __forceinline__ half4_t load_bias(const GemmArgs& a, int n) {
+    half4_t b;
+    if (((uintptr_t)a.bias % 8) == 0 && n + 3 < a.Nc) {
+      b = *reinterpret_cast<const half4_t*>(a.bias + n);
+    } else {
 #pragma unroll
-  for (int i = 0; i < TM; i++)
+      for (int e = 0; e < 4; e++) b[e] = n + e < a.Nc ? a.bias[n + e] : (_Float16)0.0f;
+    }
+    return b;
+  }
+
+  __device__ __forceinline__ void load(const GemmArgs& a, int nb, int lseg) {
+    if constexpr (kBiasPre) {
+      if (blockIdx.z == 0 && a.bias) {
 #pragma unroll
-    for (int j = 0; j < TN; j++)
+        for (int j = 0; j < TN; j++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
-  if (blockIdx.z != 0) return;
-  const bool vec = (a.Nc % 4) == 0 && (a.ldc % 4) == 0;
-  if (a.lora_h || a.lora_hp) {
+          for (int g = 0; g < 4; g++) bias[j][g] = load_bias(a, nb + j * 32 + 8 * g + 4 * lseg);
+      }
+    }
+  }
+
+  // start value of tile column j before the LoRA products: the bias (forward) or zero
+  __device__ __forceinline__ float16_t base(const GemmArgs& a, int j, int nb, int lseg) const {
+    float16_t c = {};
+    if constexpr (!BWD) {
+      if (blockIdx.z == 0 && a.bias) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          half4_t b;
+          if constexpr (kBiasPre) b = bias[j][g];
+          else b = load_bias(a, nb + j * 32 + 8 * g + 4 * lseg);
+#pragma unroll
+          for (int e = 0; e < 4; e++) c[4 * g + e] = (float)b[e];
+        }
+      }
+    }
+    return c;
+  }
+
+  // LoRA operand (ranks r0..r0+15) of output row m, straight from memory: the fp16 operand, or
+  // the fp32 partial sums added in slice order and rounded to fp16
+  __device__ static __forceinline__ half8_t lora_row(const GemmArgs& a, int m, int r0, int lseg) {
+    half8_t hf = {};
+    if (m >= a.M) return hf;
+    if (a.lora_hp) {
+      float4_t q0[4], q1[4];  // all slices' loads before the first add (<= 4 slices)
+#pragma unroll
+      for (int z = 0; z < 4; z++) {
+        const float* src = a.lora_hp + ((int64_t)z * a.ldt + m) * a.r + r0 + 8 * lseg;
+        q0[z] = z < a.hp_slices ? *reinterpret_cast<const float4_t*>(src) : (float4_t){};
+        q1[z] = z < a.hp_slices ? *reinterpret_cast<const float4_t*>(src + 4) : (float4_t){};
+      }
+      float4_t s0 = q0[0], s1 = q1[0];
+#pragma unroll
+      for (int z = 1; z < 4; z++)
+        if (z < a.hp_slices) {
+          s0 += q0[z];
+          s1 += q1[z];
+        }
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        hf[e] = (_Float16)s0[e];
+        hf[4 + e] = (_Float16)s1[e];
+      }
+    } else {
+      hf = *reinterpret_cast<const half8_t*>(a.lora_h + (int64_t)m * a.r + r0 + 8 * lseg);
+    }
+    return hf;
+  }
+
+  // 4 keep bytes of row m, columns n..n+3, from memory
+  __device__ static __forceinline__ uint32_t keep_mem(const GemmArgs& a, int m, int n) {
+    uint32_t k = 0;
+    if (m >= a.M) return k;
+    if ((a.Nc % 4) == 0 && (a.ldc % 4) == 0 && n + 3 < a.Nc) {
+      k = *reinterpret_cast<const uint32_t*>(a.mask + (int64_t)m * a.Nc + n);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        if (n + e < a.Nc) k |= (uint32_t)a.mask[(int64_t)m * a.Nc + n + e] << (8 * e);
+    }
+    return k;
+  }
+
+  // Each tile's accumulator is born from its first LoRA MFMA (or its base value).  The first
+  // column tile's waves that own the first columns write the fp16 LoRA operand transposed.
+  // wr0 / wc0: the wave's first row / column within the workgroup tile (for the LDS areas).
+  __device__ __forceinline__ void finish(const GemmArgs& a, float16_t (&acc)[TM][TN], int mb,
+                                         int nb, int lrow, int lseg, int wr0, int wc0,
+                                         const _Float16* ls = nullptr, int ls_cols = 0,
+                                         const uint8_t* kls = nullptr, int kst = 0) {
+    if (blockIdx.z != 0 || !(a.lora_h || a.lora_hp)) {
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = base(a, j, nb, lseg);
+      return;
+    }
     // lora_w is [Nc, r] in both directions (the backward pass gets lora_A transposed), so the
-    // W-side operand is one 16-byte load per tile and 16 ranks.  The accumulators are still zero
-    // here, so the LoRA products go straight into them (masked in place afterwards).
-    const bool masked = BWD && a.mask;
-    // the first column tile's waves that own the first columns write the operand transposed
-    const bool write_t = a.lora_ht && blockIdx.x == 0 && nb == 0;
+    // W-side operand is one 16-byte load per tile and 16 ranks
+    const bool write_t = a.lora_hp && a.lora_ht && blockIdx.x == 0 && nb == 0;
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       const int m = mb + i * 32 + lrow;
       for (int r0 = 0; r0 < a.r; r0 += 16) {
-        half8_t hf = {};
-        if (a.lora_hp) {
-          if (m < a.M) {
-            float4_t p0[4], p1[4];  // all slices' loads before the first add (<= 4 slices)
+        const half8_t hf =
+            ls ? *reinterpret_cast<const half8_t*>(ls + (wr0 + i * 32 + lrow) * 16 + 8 * lseg)
+               : lora_row(a, m, r0, lseg);
+        if (write_t && m < a.ldt) {
 #pragma unroll
-            for (int z = 0; z < 4; z++) {
-              const float* src = a.lora_hp + ((int64_t)z * a.ldt + m) * a.r + r0 + 8 * lseg;
-              p0[z] = z < a.hp_slices ? *reinterpret_cast<const float4_t*>(src) : (float4_t){};
-              p1[z] = z < a.hp_slices ? *reinterpret_cast<const float4_t*>(src + 4) : (float4_t){};
-            }
-            float4_t s0 = p0[0], s1 = p1[0];
-#pragma unroll
-            for (int z = 1; z < 4; z++)
-              if (z < a.hp_slices) {
-                s0 += p0[z];
-                s1 += p1[z];
-              }
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-              hf[e] = (_Float16)s0[e];
-              hf[4 + e] = (_Float16)s1[e];
-            }
-          }
-          if (write_t && m < a.ldt) {
-#pragma unroll
-            for (int e = 0; e < 8; e++) a.lora_ht[(int64_t)(r0 + 8 * lseg + e) * a.ldt + m] = hf[e];
-          }
-        } else if (m < a.M) {
-          hf = *reinterpret_cast<const half8_t*>(a.lora_h + (int64_t)m * a.r + r0 + 8 * lseg);
+          for (int e = 0; e < 8; e++) a.lora_ht[(int64_t)(r0 + 8 * lseg + e) * a.ldt + m] = hf[e];
         }
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-          const int ncol = nb + j * 32 + lrow;  // column this lane feeds as the W-side operand
-          half8_t wf = {};
-          if (ncol < a.Nc) wf = *reinterpret_cast<const half8_t*>(a.lora_w + (int64_t)ncol * a.r + r0 + 8 * lseg);
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, hf, acc[i][j], 0, 0, 0);
+          half8_t wf;
+          if (ls) {
+            wf = *reinterpret_cast<const half8_t*>(ls + (ls_cols + wc0 + j * 32 + lrow) * 16 +
+                                                   8 * lseg);
+          } else {
+            const int ncol = nb + j * 32 + lrow;
+            wf = ncol < a.Nc
+                ? *reinterpret_cast<const half8_t*>(a.lora_w + (int64_t)ncol * a.r + r0 + 8 * lseg)
+                : (half8_t){};
+          }
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              wf, hf, r0 == 0 ? base(a, j, nb, lseg) : acc[i][j], 0, 0, 0);
         }
       }
-      if (!masked) continue;
+      if constexpr (BWD) {
+        if (a.mask) {
 #pragma unroll
-      for (int j = 0; j < TN; j++) {
+          for (int j = 0; j < TN; j++)
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const int n = nb + j * 32 + 8 * g + 4 * lseg;
-          uint32_t keep = 0;
-          if (m < a.M) {
-            if (vec && n + 3 < a.Nc) {
-              keep = *reinterpret_cast<const uint32_t*>(a.mask + (int64_t)m * a.Nc + n);
-            } else {
+            for (int g = 0; g < 4; g++) {
+              const int c = j * 32 + 8 * g + 4 * lseg;
+              const uint32_t keep =
+                  kls ? *reinterpret_cast<const uint32_t*>(kls + (wr0 + i * 32 + lrow) * kst + wc0 + c)
+                      : keep_mem(a, m, nb + c);
 #pragma unroll
               for (int e = 0; e < 4; e++)
-                if (n + e < a.Nc) keep |= (uint32_t)a.mask[(int64_t)m * a.Nc + n + e] << (8 * e);
+                acc[i][j][4 * g + e] =
+                    ((keep >> (8 * e)) & 0xffu) ? acc[i][j][4 * g + e] * a.mask_scale : 0.0f;
             }
-          }
-#pragma unroll
-          for (int e = 0; e < 4; e++)
-            acc[i][j][4 * g + e] = ((keep >> (8 * e)) & 0xffu) ? acc[i][j][4 * g + e] * a.mask_scale : 0.0f;
         }
       }
     }
   }
-  if (a.bias) {
+
+  // finish() for operands staged in LDS (first split, r = 16): straight-line LDS reads and one
+  // MFMA per tile; `ls`: [rows][16] operand then (at row ls_cols) [cols][16] of lora_w; `kls`
+  // (backward, may be null): keep bytes, row stride kst.
+  __device__ __forceinline__ void finish_staged(const GemmArgs& a, float16_t (&acc)[TM][TN],
+                                                int mb, int nb, int lrow, int lseg, int wr0,
+                                                int wc0, const _Float16* ls, int ls_cols,
+                                                const uint8_t* kls, int kst) {
+    half8_t wf[TN];
 #pragma unroll
     for (int j = 0; j < TN; j++)
+      wf[j] = *reinterpret_cast<const half8_t*>(ls + (ls_cols + wc0 + j * 32 + lrow) * 16 + 8 * lseg);
+    const bool write_t = a.lora_hp && a.lora_ht && blockIdx.x == 0 && nb == 0;
 #pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const int n = nb + j * 32 + 8 * g + 4 * lseg;
-        float b[4];
+    for (int i = 0; i < TM; i++) {
+      const half8_t hf =
+          *reinterpret_cast<const half8_t*>(ls + (wr0 + i * 32 + lrow) * 16 + 8 * lseg);
 #pragma unroll
-        for (int e = 0; e < 4; e++) b[e] = (n + e < a.Nc) ? (float)a.bias[n + e] : 0.0f;
+      for (int j = 0; j < TN; j++)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[j], hf, base(a, j, nb, lseg), 0, 0, 0);
+      if (write_t) {
+        const int m = mb + i * 32 + lrow;
+        if (m < a.ldt) {
 #pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-          for (int e = 0; e < 4; e++) acc[i][j][4 * g + e] += b[e];
+          for (int e = 0; e < 8; e++) a.lora_ht[(int64_t)(8 * lseg + e) * a.ldt + m] = hf[e];
+        }
       }
+      if constexpr (BWD) {
+        if (kls) {
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+              const uint32_t keep = *reinterpret_cast<const uint32_t*>(
+                  kls + (wr0 + i * 32 + lrow) * kst + wc0 + j * 32 + 8 * g + 4 * lseg);
+#pragma unroll
+              for (int e = 0; e < 4; e++)
+                acc[i][j][4 * g + e] =
+                    ((keep >> (8 * e)) & 0xffu) ? acc[i][j][4 * g + e] * a.mask_scale : 0.0f;
+            }
+        }
+      }
+    }
   }
+};
+
+// The backward pass's dropout keep bytes of the warp-specialized kernel's BM x BN tile, staged
+// by its producers in LDS (row stride BN + 4 bytes: an odd number of dwords, so the consumers'
+// 4-byte reads of one column over 32 rows hit distinct banks).  Rows are loaded 16 contiguous
+// bytes per lane, instead of 4 bytes from each of 32 rows per instruction.
+template <int BM, int BN>
+struct MaskStage {
+  static constexpr int KST = BN + 4;
+  static constexpr int CH = BN / 16;                // 16-byte chunks per row
+  static constexpr int N = (BM * CH + 255) / 256;   // chunks per producer thread
+  u32x4 v[N];
+
+  __device__ __forceinline__ void issue(const GemmArgs& a, int p, int m0, int n0) {
+    const bool vec = (a.Nc % 16) == 0 && ((uintptr_t)a.mask % 16) == 0;
+#pragma unroll
+    for (int u = 0; u < N; u++) {
+      const int c = p + 256 * u;
+      const int row = c / CH, cc = c % CH;
+      const int m = m0 + row, n = n0 + 16 * cc;
+      u32x4 x = {};
+      if (c < BM * CH && m < a.M) {
+        const uint8_t* src = a.mask + (int64_t)m * a.Nc + n;
+        if (vec && n + 15 < a.Nc) {
+          x = *reinterpret_cast<const u32x4*>(src);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 16; e++)
+            if (n + e < a.Nc) x[e >> 2] |= (uint32_t)src[e] << (8 * (e & 3));
+        }
+      }
+      v[u] = x;
+    }
+  }
+
+  __device__ __forceinline__ void commit(uint8_t* kls, int p) const {
+#pragma unroll
+    for (int u = 0; u < N; u++) {
+      const int c = p + 256 * u;
+      if (c >= BM * CH) break;
+      uint32_t* dst = reinterpret_cast<uint32_t*>(kls + (c / CH) * KST + 16 * (c % CH));
+#pragma unroll
+      for (int d = 0; d < 4; d++) dst[d] = v[u][d];
+    }
+  }
+};
+
+// LoRA operands of the warp-specialized kernel staged by its producers (r = 16): the fp16
+// operand of the workgroup's BM rows (partial sums added in slice order and rounded, as
+// AccStart::lora_row does) and lora_w's BN rows, 32 bytes per row, into [BM][16] and [BN][16].
+// The source blocks are contiguous (BM rows x 16 ranks per slice), so they are read as 16-byte
+// chunks in lane order: every load instruction covers 1 KB of consecutive memory.  Thread p
+// takes chunks p, p + 256, ...; a chunk is 4 ranks of one row (fp32) or 8 ranks (fp16).  The
+// loads are issued before the first tiles' so that they share one round trip.
+template <int BM, int BN>
+struct LoraStage {
+  static constexpr int NP = BM * 4 / 256;          // fp32 chunks per slice per thread
+  static constexpr int NH = (BM * 2 + 255) / 256;  // fp16-operand chunks per thread
+  static constexpr int NW = (BN * 2 + 255) / 256;  // lora_w chunks per thread
+  static_assert(BM * 4 % 256 == 0, "whole fp32 chunk rounds");
+  float4_t q[4][NP];  // partial sums: slice z, chunk p + 256u
+  u32x4 hv[NH];       // or the fp16 operand
+  u32x4 w[NW];
+
+  __device__ __forceinline__ void issue(const GemmArgs& a, int p, int m0, int n0) {
+    if (a.lora_hp) {
+#pragma unroll
+      for (int z = 0; z < 4; z++) {
+        const float4_t* src =
+            reinterpret_cast<const float4_t*>(a.lora_hp + ((int64_t)z * a.ldt + m0) * 16);
+#pragma unroll
+        for (int u = 0; u < NP; u++) {
+          const int c = p + 256 * u;
+          const bool ok = z < a.hp_slices && m0 + c / 4 < a.M;
+          q[z][u] = ok ? src[c] : (float4_t){};
+        }
+      }
+    } else {
+      const u32x4* src = reinterpret_cast<const u32x4*>(a.lora_h + (int64_t)m0 * 16);
+#pragma unroll
+      for (int u = 0; u < NH; u++) {
+        const int c = p + 256 * u;
+        hv[u] = c < BM * 2 && m0 + c / 2 < a.M ? src[c] : (u32x4){};
+      }
+    }
+    const u32x4* wsrc = reinterpret_cast<const u32x4*>(a.lora_w + (int64_t)n0 * 16);
+#pragma unroll
+    for (int u = 0; u < NW; u++) {
+      const int c = p + 256 * u;
+      w[u] = c < BN * 2 && n0 + c / 2 < a.Nc ? wsrc[c] : (u32x4){};
+    }
+  }
+
+  // after the loads have landed: rows into the LDS area `ls`
+  __device__ __forceinline__ void commit(const GemmArgs& a, _Float16* ls, int p) const {
+    if (a.lora_hp) {
+#pragma unroll
+      for (int u = 0; u < NP; u++) {
+        const int c = p + 256 * u;
+        float4_t sum = q[0][u];  // slices added in order
+#pragma unroll
+        for (int z = 1; z < 4; z++)
+          if (z < a.hp_slices) sum += q[z][u];
+        const u32x2 h = {pack_f16x2(sum[0], sum[1]), pack_f16x2(sum[2], sum[3])};
+        *reinterpret_cast<u32x2*>(ls + 4 * c) = h;  // row c/4, ranks 4(c%4)..+3
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < NH; u++) {
+        const int c = p + 256 * u;
+        if (c < BM * 2) *reinterpret_cast<u32x4*>(ls + 8 * c) = hv[u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NW; u++) {
+      const int c = p + 256 * u;
+      if (c < BN * 2) *reinterpret_cast<u32x4*>(ls + BM * 16 + 8 * c) = w[u];
+    }
+  }
+};
+
+template <int TM, int TN, bool BWD>
+__device__ __forceinline__ void init_acc(const GemmArgs& a, float16_t (&acc)[TM][TN], int mb,
+                                         int nb, int lrow, int lseg) {
+  AccStart<TM, TN, BWD> st;
+  st.load(a, nb, lseg);
+  st.finish(a, acc, mb, nb, lrow, lseg, 0, 0);
 }
 
 // Epilogue: fp16 stores of the tiles (one 8-byte store per register group), or with split-K
@@ -817,10 +1049,11 @@ struct BLoadT {
   }
 };
 
-// LDS halfs of the warp-specialized kernel's tiles: 3-deep A ring + 2-deep B buffer.
+// LDS halfs of the warp-specialized kernel: 3-deep A ring + 2-deep B buffer + the staged LoRA
+// operands ([BM][16] and [BN][16]).
 template <int BM, int BN, bool BWD>
 constexpr int ws_lds_halfs() {
-  return 3 * BM * kBK + 2 * (BWD ? kBK * BLoadT<BN>::LDB : BN * kBK);
+  return 3 * BM * kBK + 2 * (BWD ? kBK * BLoadT<BN>::LDB : BN * kBK) + (BM + BN) * 16;
 }
 
 // Direct global -> LDS copy of one K-step's A tile (BM rows x 64 fp16) by the producer waves:
@@ -890,6 +1123,12 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
   _Float16* As = smem;                      // [3][BM][64]
   _Float16* Bs = smem + 3 * LDS_A;          // [2][BN][64]
+  _Float16* Ls = Bs + 2 * LDS_B;            // LoRA operands: [BM][16], then [BN][16]
+  // B buffer of K-step parity x: buffer 1 sits right after A-ring slot 2, so that the two
+  // (both idle until K-step kt0 multiplies) can hold the staged keep mask
+  auto bbuf = [&](int x) { return Bs + ((x & 1) ^ 1) * LDS_B; };
+  uint8_t* Ks = reinterpret_cast<uint8_t*>(As + 2 * LDS_A);
+  static_assert(BM * MaskStage<BM, BN>::KST <= (LDS_A + LDS_B) * 2, "staged keep mask fits");
   __shared__ float2_t s_pair[256];
   __shared__ float s_code[256];
 
@@ -900,41 +1139,64 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
   const int n_steps = a.Kr / kBK;
   const int kt0 = blockIdx.z * a.steps_per_split;
   const int kt1 = min(n_steps, kt0 + a.steps_per_split);
-  fill_tables(a, s_pair, s_code, t, 512);
+  // the producers stage the LoRA operands (r = 16) and the keep mask in LDS for the consumers
+  const bool lora = blockIdx.z == 0 && (a.lora_hp || a.lora_h);
+  const bool lora16 = lora && a.r == 16;
+  const bool kmask = BWD && lora && a.mask;
+  // wave index as a scalar: the producer / consumer split below is a uniform branch, so neither
+  // side's live registers are carried through the other side's code
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm0 = (wave / CWN) * WM;
+  const int wn0 = (wave % CWN) * WN;
+  const int lrow = lane & 31;
+  const int lseg = lane >> 5;
 
-  if (t >= 256) {
+  if (wave >= 4) {
     // ---- producers (they stay to the end: every wave takes part in every barrier) ----
-    if (kt0 < kt1) {
-      const int p = t - 256;
-      const int pw = p >> 6;
-      const float offset = a.offset[0];
-      // NF4 tile of K-step kt is issued three steps ahead into register stage (kt - kt0) % 3
-      // and committed to LDS one step ahead; the A tile is copied two steps ahead into the LDS
-      // ring.  Every issue is unconditional (steps past the end re-load the last one), so the
-      // number of memory instructions in flight is a constant and each wait names exactly the
-      // group it needs.  Order within step kt: commit B(kt+1), A(kt+2), B(kt+3), wait A(kt+1).
-      constexpr int LB = B::VMEM;
-      constexpr int LA = ACopy<BM>::N;  // A-tile copy instructions per producer wave
-      constexpr uint32_t SLOT = LDS_A * sizeof(_Float16);
-      const int last = kt1 - 1;
-      ACopy<BM> ac;
-      ac.init(a, As, pw, lane, m0);
-      const typename B::Src src = B::setup(a, p, n0);
-      typename B::Stage S0, S1, S2;
+    const int p = t - 256;
+    const int pw = p >> 6;
+    const bool run = kt0 < kt1;
+    LoraStage<BM, BN> lst;
+    MaskStage<BM, BN> mst;
+    if (lora16) lst.issue(a, p, m0, n0);  // before the tiles: one round trip for all
+    if (kmask) mst.issue(a, p, m0, n0);
+    const float offset = a.offset[0];
+    // NF4 tile of K-step kt is issued three steps ahead into register stage (kt - kt0) % 3 and
+    // committed to LDS one step ahead; the A tile is copied two steps ahead into the LDS ring.
+    // Every issue is unconditional (steps past the end re-load the last one), so the number of
+    // memory instructions in flight is a constant and each wait names exactly the group it
+    // needs.  Order within step kt: commit B(kt+1), A(kt+2), B(kt+3), wait A(kt+1).
+    constexpr int LB = B::VMEM;
+    constexpr int LA = ACopy<BM>::N;  // A-tile copy instructions per producer wave
+    constexpr uint32_t SLOT = LDS_A * sizeof(_Float16);
+    const int last = kt1 - 1;
+    ACopy<BM> ac;
+    ac.init(a, As, pw, lane, m0);
+    const typename B::Src src = B::setup(a, p, n0);
+    typename B::Stage S0, S1, S2;
+    if (run) {
       B::issue(a, src, S0, kt0);
       ac.copy(0, kt0);
       B::issue(a, src, S1, min(kt0 + 1, last));
       ac.copy(SLOT, min(kt0 + 1, last));
       B::issue(a, src, S2, min(kt0 + 2, last));
-      lds_barrier();  // tables
-      B::commit(S0, Bs, p, s_pair, s_code, offset);
+    }
+    if (lora16 || kmask) {
+      if (run) wait_vmcnt<3 * LB + 2 * LA>();  // the staged loads, issued before all of those
+      else wait_vmem_all();
+      if (lora16) lst.commit(a, Ls, p);
+      if (kmask) mst.commit(Ks, p);
+    }
+    lds_barrier();  // tables, LoRA operands
+    if (run) {
+      B::commit(S0, bbuf(0), p, s_pair, s_code, offset);
       wait_vmcnt<2 * LB + LA>();  // A(kt0): after it only B(kt0+1), A(kt0+1), B(kt0+2)
       lds_barrier();  // K-step kt0 ready
       auto step = [&](int kt, typename B::Stage& Sc, typename B::Stage& Si) {
         const int r = kt - kt0;
         // the compiler's own wait before this commit (B(kt+1) registers) also completes
         // A(kt+1), issued after B(kt+1); B(kt+2) stays in flight
-        if (kt + 1 < kt1) B::commit(Sc, Bs + ((r + 1) & 1) * LDS_B, p, s_pair, s_code, offset);
+        if (kt + 1 < kt1) B::commit(Sc, bbuf(r + 1), p, s_pair, s_code, offset);
         ac.copy(((r + 2) % 3) * SLOT, min(kt + 2, last));
         B::issue(a, src, Si, min(kt + 3, last));
         wait_vmcnt<2 * LB + LA>();  // A(kt+1): after it only B(kt+2), A(kt+2), B(kt+3)
@@ -953,25 +1215,25 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
     lds_barrier();  // the A ring is free for the consumers' staged epilogue
   } else {
     // ---- consumers ----
-    const int wave = t >> 6;
-    const int wm0 = (wave / CWN) * WM;
-    const int wn0 = (wave % CWN) * WN;
-    const int lrow = lane & 31;
-    const int lseg = lane >> 5;
+    AccStart<TM, TN, BWD> start;
+    start.load(a, n0 + wn0, lseg);  // before the tables' loads
+    fill_tables(a, s_pair, s_code, t, 256);
     float16_t acc[TM][TN];
+    lds_barrier();  // tables, LoRA operands
+    // accumulator start (bias, LoRA) while the producers stage K-step kt0
+    if (lora16)
+      start.finish_staged(a, acc, m0 + wm0, n0 + wn0, lrow, lseg, wm0, wn0, Ls, BM,
+                          kmask ? Ks : nullptr, MaskStage<BM, BN>::KST);
+    else
+      start.finish(a, acc, m0 + wm0, n0 + wn0, lrow, lseg, wm0, wn0, nullptr, 0,
+                   kmask ? Ks : nullptr, MaskStage<BM, BN>::KST);
     if (kt0 < kt1) {
-      lds_barrier();  // tables
-      // accumulator start (bias, LoRA) while the producers stage K-step kt0
-      init_acc<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
       lds_barrier();  // K-step kt0 ready
       for (int kt = kt0; kt < kt1; kt++) {
         const int r = kt - kt0;
-        mma_kstep<TM, TN, LDB>(acc, As + (r % 3) * LDS_A, Bs + (r & 1) * LDS_B, wm0, wn0, lrow,
-                               lseg);
+        mma_kstep<TM, TN, LDB>(acc, As + (r % 3) * LDS_A, bbuf(r), wm0, wn0, lrow, lseg);
         lds_barrier();
       }
-    } else {
-      init_acc<TM, TN, BWD>(a, acc, m0 + wm0, n0 + wn0, lrow, lseg);
     }
     lds_barrier();  // the producers' last copies have landed
     static_assert(4 * StagedStore<TM, TN>::AREA_DWORDS * 4 <= 3 * LDS_A * 2,
