@@ -87,7 +87,7 @@ int mxs_nf4_quantize(const void* w_f16, int64_t n_values, const float* code, voi
                      void* workspace, hipStream_t stream);
 
 /* ---- Fused NF4 GEMMs (forward and input gradient of the frozen Linear4bit) ---------------
- * cfg: tile configuration id (0-4: all-wave kernels, 6-9: producer/consumer kernels; 5 is
+ * cfg: tile configuration id (0-4: all-wave kernels, 6-11: producer/consumer kernels; 5 is
  * invalid) or -1 to let the library choose tiles and split-K for the shape; splits: reduction
  * splits (used with cfg >= 0).  When the plan splits the reduction, `workspace` must hold
  * mxs_nf4_gemm_workspace_bytes(M, Nc, Kr, cfg, splits) bytes of device memory (fp32 partial

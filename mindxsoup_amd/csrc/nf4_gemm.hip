@@ -298,18 +298,18 @@ struct AccStart {
 // by its producers in LDS (row stride BN + 4 bytes: an odd number of dwords, so the consumers'
 // 4-byte reads of one column over 32 rows hit distinct banks).  Rows are loaded 16 contiguous
 // bytes per lane, instead of 4 bytes from each of 32 rows per instruction.
-template <int BM, int BN>
+template <int BM, int BN, int NTP>
 struct MaskStage {
   static constexpr int KST = BN + 4;
   static constexpr int CH = BN / 16;                // 16-byte chunks per row
-  static constexpr int N = (BM * CH + 255) / 256;   // chunks per producer thread
+  static constexpr int N = (BM * CH + NTP - 1) / NTP;  // chunks per producer thread
   u32x4 v[N];
 
   __device__ __forceinline__ void issue(const GemmArgs& a, int p, int m0, int n0) {
     const bool vec = (a.Nc % 16) == 0 && ((uintptr_t)a.mask % 16) == 0;
 #pragma unroll
     for (int u = 0; u < N; u++) {
-      const int c = p + 256 * u;
+      const int c = p + NTP * u;
       const int row = c / CH, cc = c % CH;
       const int m = m0 + row, n = n0 + 16 * cc;
       u32x4 x = {};
@@ -330,7 +330,7 @@ struct MaskStage {
   __device__ __forceinline__ void commit(uint8_t* kls, int p) const {
 #pragma unroll
     for (int u = 0; u < N; u++) {
-      const int c = p + 256 * u;
+      const int c = p + NTP * u;
       if (c >= BM * CH) break;
       uint32_t* dst = reinterpret_cast<uint32_t*>(kls + (c / CH) * KST + 16 * (c % CH));
 #pragma unroll
@@ -341,18 +341,19 @@ struct MaskStage {
 
 // LoRA operands of the warp-specialized kernel staged by its producers (r = 16): the fp16
 // operand of the workgroup's BM rows (partial sums added in slice order and rounded, as
-// AccStart::lora_row does) and lora_w's BN rows, 32 bytes per row, into [BM][16] and [BN][16].
+// AccStart::lora_row does) and lora_w's BN rows, 32 bytes per row, into [BM][16] and [BN][16],
+// by the NTP producer threads.
 // The source blocks are contiguous (BM rows x 16 ranks per slice), so they are read as 16-byte
 // chunks in lane order: every load instruction covers 1 KB of consecutive memory.  Thread p
-// takes chunks p, p + 256, ...; a chunk is 4 ranks of one row (fp32) or 8 ranks (fp16).  The
+// takes chunks p, p + NTP, ...; a chunk is 4 ranks of one row (fp32) or 8 ranks (fp16).  The
 // loads are issued before the first tiles' so that they share one round trip.
-template <int BM, int BN>
+template <int BM, int BN, int NTP>
 struct LoraStage {
-  static constexpr int NP = BM * 4 / 256;          // fp32 chunks per slice per thread
-  static constexpr int NH = (BM * 2 + 255) / 256;  // fp16-operand chunks per thread
-  static constexpr int NW = (BN * 2 + 255) / 256;  // lora_w chunks per thread
-  static_assert(BM * 4 % 256 == 0, "whole fp32 chunk rounds");
-  float4_t q[4][NP];  // partial sums: slice z, chunk p + 256u
+  static constexpr int NP = BM * 4 / NTP;              // fp32 chunks per slice per thread
+  static constexpr int NH = (BM * 2 + NTP - 1) / NTP;  // fp16-operand chunks per thread
+  static constexpr int NW = (BN * 2 + NTP - 1) / NTP;  // lora_w chunks per thread
+  static_assert(BM * 4 % NTP == 0, "whole fp32 chunk rounds");
+  float4_t q[4][NP];  // partial sums: slice z, chunk p + NTP u
   u32x4 hv[NH];       // or the fp16 operand
   u32x4 w[NW];
 
@@ -364,7 +365,7 @@ struct LoraStage {
             reinterpret_cast<const float4_t*>(a.lora_hp + ((int64_t)z * a.ldt + m0) * 16);
 #pragma unroll
         for (int u = 0; u < NP; u++) {
-          const int c = p + 256 * u;
+          const int c = p + NTP * u;
           const bool ok = z < a.hp_slices && m0 + c / 4 < a.M;
           q[z][u] = ok ? src[c] : (float4_t){};
         }
@@ -373,14 +374,14 @@ struct LoraStage {
       const u32x4* src = reinterpret_cast<const u32x4*>(a.lora_h + (int64_t)m0 * 16);
 #pragma unroll
       for (int u = 0; u < NH; u++) {
-        const int c = p + 256 * u;
+        const int c = p + NTP * u;
         hv[u] = c < BM * 2 && m0 + c / 2 < a.M ? src[c] : (u32x4){};
       }
     }
     const u32x4* wsrc = reinterpret_cast<const u32x4*>(a.lora_w + (int64_t)n0 * 16);
 #pragma unroll
     for (int u = 0; u < NW; u++) {
-      const int c = p + 256 * u;
+      const int c = p + NTP * u;
       w[u] = c < BN * 2 && n0 + c / 2 < a.Nc ? wsrc[c] : (u32x4){};
     }
   }
@@ -390,7 +391,7 @@ struct LoraStage {
     if (a.lora_hp) {
 #pragma unroll
       for (int u = 0; u < NP; u++) {
-        const int c = p + 256 * u;
+        const int c = p + NTP * u;
         float4_t sum = q[0][u];  // slices added in order
 #pragma unroll
         for (int z = 1; z < 4; z++)
@@ -401,13 +402,13 @@ struct LoraStage {
     } else {
 #pragma unroll
       for (int u = 0; u < NH; u++) {
-        const int c = p + 256 * u;
+        const int c = p + NTP * u;
         if (c < BM * 2) *reinterpret_cast<u32x4*>(ls + 8 * c) = hv[u];
       }
     }
 #pragma unroll
     for (int u = 0; u < NW; u++) {
-      const int c = p + 256 * u;
+      const int c = p + NTP * u;
       if (c < BN * 2) *reinterpret_cast<u32x4*>(ls + BM * 16 + 8 * c) = w[u];
     }
   }
@@ -1049,6 +1050,121 @@ struct BLoadT {
   }
 };
 
+// NF4 side of a forward K-step for 512 producer threads (tiles up to 128 columns): item = 8
+// packed bytes of W row n (16 values, a quarter of the row's block for this K-step), 3 memory
+// instructions; same addressing scheme as BLoad.
+template <int BN>
+struct BLoad8 {
+  static constexpr int TOTAL = BN * 4;  // 8-byte items
+  static constexpr int VMEM = 3;
+  static_assert(TOTAL % 64 == 0 && TOTAL <= 512, "B items in whole waves, one round");
+
+  struct Stage {
+    u32x2 w;
+    uint32_t q8;
+    float a2;
+  };
+  struct Src {
+    uint32_t w, blk;
+  };
+
+  __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0) {
+    Src r;
+    const int q = min(p, TOTAL - 1);
+    const uint32_t n = min(n0 + (q >> 2), a.Nc - 1);
+    r.w = n * (uint32_t)(a.Kw / 2) + (q & 3) * 8;
+    r.blk = n * (uint32_t)(a.Kw / 64);
+    return r;
+  }
+
+  __device__ static __forceinline__ void issue(const GemmArgs& a, const Src& src, Stage& S,
+                                               int kt) {
+    const uint8_t* pk = a.packed + kt * (kBK / 2);
+    S.q8 = (a.absmax8 + kt)[src.blk];
+    S.a2 = a.absmax2[(src.blk + kt) >> 8];
+    S.w = *reinterpret_cast<const u32x2*>(pk + src.w);
+  }
+
+  __device__ static __forceinline__ void commit(const Stage& S, _Float16* bs, int p,
+                                                const float2_t* s_pair, const float* s_code,
+                                                float offset) {
+    float2_t pr[2][4];
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
+    if (p < TOTAL) {
+      const float sc = nested_scale(s_code[S.q8], S.a2, offset);
+#pragma unroll
+      for (int d = 0; d < 2; d++) {
+        u32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pr[d][j][0] * sc, pr[d][j][1] * sc);
+        *reinterpret_cast<u32x4*>(bs + lds_off(p >> 2, (p & 3) * 2 + d)) = v;
+      }
+    }
+  }
+};
+
+// NF4 side of a backward K-step for 512 producer threads (tiles up to 128 columns), B tile
+// stored as W's rows like BLoadT: item = 8 packed bytes of one W row (16 columns, one block
+// scale), decoded to two contiguous 16-byte stores.
+template <int BN>
+struct BLoadT8 {
+  static constexpr int LDB = BLoadT<BN>::LDB;
+  static constexpr int CPR = BN / 16;       // 8-byte items per row
+  static constexpr int TOTAL = kBK * CPR;
+  static constexpr int VMEM = 3;
+  static_assert(BN % 16 == 0 && TOTAL % 64 == 0 && TOTAL <= 512, "B items in whole waves");
+
+  struct Stage {
+    u32x2 w;
+    uint32_t q8;
+    float a2;
+  };
+  struct Src {
+    uint32_t x;  // value index of the item within its K-step's 64-row slab of W
+  };
+
+  __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0) {
+    Src r;
+    const int q = min(p, TOTAL - 1);
+    const int row = q / CPR, c = q % CPR;
+    r.x = (uint32_t)row * a.Kw + min(n0 + 16 * c, a.Nc - 16);
+    return r;
+  }
+
+  __device__ static __forceinline__ void issue(const GemmArgs& a, const Src& src, Stage& S,
+                                               int kt) {
+    const uint32_t slab = (uint32_t)kt * kBK * a.Kw;
+    const uint8_t* pk = a.packed + slab / 2;
+    S.q8 = (a.absmax8 + slab / 64)[src.x >> 6];
+    S.a2 = a.absmax2[(slab + src.x) >> 14];
+    S.w = *reinterpret_cast<const u32x2*>(pk + (src.x >> 1));
+  }
+
+  __device__ static __forceinline__ void commit(const Stage& S, _Float16* bs, int p,
+                                                const float2_t* s_pair, const float* s_code,
+                                                float offset) {
+    float2_t pr[2][4];
+#pragma unroll
+    for (int d = 0; d < 2; d++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
+    if (p < TOTAL) {
+      const int row = p / CPR, c = p % CPR;
+      const float sc = nested_scale(s_code[S.q8], S.a2, offset);
+#pragma unroll
+      for (int d = 0; d < 2; d++) {
+        u32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pr[d][j][0] * sc, pr[d][j][1] * sc);
+        *reinterpret_cast<u32x4*>(bs + row * LDB + 16 * c + 8 * d) = v;
+      }
+    }
+  }
+};
+
 // LDS halfs of the warp-specialized kernel: 3-deep A ring + 2-deep B buffer + the staged LoRA
 // operands ([BM][16] and [BN][16]).
 template <int BM, int BN, bool BWD>
@@ -1058,17 +1174,19 @@ constexpr int ws_lds_halfs() {
 
 // Direct global -> LDS copy of one K-step's A tile (BM rows x 64 fp16) by the producer waves:
 // each global_load_lds_dwordx4 writes 8 rows (64 lanes x 16 B, consecutive in LDS); lane l takes
-// the logical segment that the row's XOR swizzle places at its physical slot.  Wave pw copies
-// row groups pw, pw + 4, ...  Each lane's source byte offsets from the tile's first row are
+// the logical segment that the row's XOR swizzle places at its physical slot.  Producer wave pw
+// of PW copies row groups pw, pw + PW, ...  Each lane's source byte offsets from the tile's
+// first row are
 // computed once (32-bit: the launcher checks BM * lda * 2 < 2^32); a K-step only moves the
 // uniform source pointer and the ring slot, so a copy costs two scalar instructions and the
 // load.
 // M0 is a reserved register to the compiler; the copy below writes it on purpose (see there)
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-template <int BM>
+template <int BM, int PW>
 struct ACopy {
-  static constexpr int N = BM / 32;  // copies per producer wave per K-step
+  static constexpr int N = BM / 8 / PW;  // copies per producer wave per K-step
+  static_assert(BM % (8 * PW) == 0, "whole row groups per producer wave");
   uint32_t off[N];
   const char* base;  // A row m0 (uniform)
   uint32_t lds;      // LDS byte address of this wave's first row group in ring slot 0 (uniform)
@@ -1077,7 +1195,7 @@ struct ACopy {
                                        int m0) {
 #pragma unroll
     for (int i = 0; i < N; i++) {
-      const int row = (pw + 4 * i) * 8 + (lane >> 3);
+      const int row = (pw + PW * i) * 8 + (lane >> 3);
       const int seg = ((lane & 7) ^ row ^ (row >> 3)) & 7;
       const uint32_t m = min(m0 + row, a.M - 1) - m0;
       off[i] = (m * (uint32_t)a.lda + seg * 8) * 2;
@@ -1097,7 +1215,7 @@ struct ACopy {
       // load before each of those reads.  Completion is awaited explicitly (wait_vmcnt) before
       // the barrier that hands the tile over.  M0 = the LDS destination of this wave's 8 rows;
       // no other code in the kernel uses M0.
-      const uint32_t dst = lds + slot_bytes + i * 4 * 8 * kBK * sizeof(_Float16);
+      const uint32_t dst = lds + slot_bytes + i * PW * 8 * kBK * sizeof(_Float16);
       asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                    :
                    : "s"(dst), "v"(off[i]), "s"(src)
@@ -1113,11 +1231,15 @@ struct ACopy {
 // the other half of a 2-deep B buffer while the consumers multiply kt.  Everything a producer
 // issues in one K-step is waited for at the start of the next, and one workgroup barrier per
 // K-step hands the buffers over.
-template <int BM, int BN, int CWM, int CWN, bool BWD>
-__global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW>
+__global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
   constexpr int WM = BM / CWM, WN = BN / CWN, TM = WM / 32, TN = WN / 32;
+  constexpr int NTP = 64 * PW;  // producer threads
   static_assert(CWM * CWN == 4 && WM % 32 == 0 && WN % 32 == 0, "consumer wave tiles");
-  using B = std::conditional_t<BWD, BLoadT<BN>, BLoad<BN>>;
+  static_assert(PW == 4 || PW == 8, "4 or 8 producer waves");
+  using B = std::conditional_t<
+      BWD, std::conditional_t<PW == 8, BLoadT8<BN>, BLoadT<BN>>,
+      std::conditional_t<PW == 8, BLoad8<BN>, BLoad<BN>>>;
   constexpr int LDB = BWD ? BLoadT<BN>::LDB : 0;  // B tile stored [64][LDB] (backward)
   constexpr int LDS_A = BM * kBK, LDS_B = BWD ? kBK * LDB : BN * kBK;
   extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
@@ -1128,7 +1250,7 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
   // (both idle until K-step kt0 multiplies) can hold the staged keep mask
   auto bbuf = [&](int x) { return Bs + ((x & 1) ^ 1) * LDS_B; };
   uint8_t* Ks = reinterpret_cast<uint8_t*>(As + 2 * LDS_A);
-  static_assert(BM * MaskStage<BM, BN>::KST <= (LDS_A + LDS_B) * 2, "staged keep mask fits");
+  static_assert(BM * MaskStage<BM, BN, NTP>::KST <= (LDS_A + LDS_B) * 2, "staged keep mask fits");
   __shared__ float2_t s_pair[256];
   __shared__ float s_code[256];
 
@@ -1156,8 +1278,8 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
     const int p = t - 256;
     const int pw = p >> 6;
     const bool run = kt0 < kt1;
-    LoraStage<BM, BN> lst;
-    MaskStage<BM, BN> mst;
+    LoraStage<BM, BN, NTP> lst;
+    MaskStage<BM, BN, NTP> mst;
     if (lora16) lst.issue(a, p, m0, n0);  // before the tiles: one round trip for all
     if (kmask) mst.issue(a, p, m0, n0);
     const float offset = a.offset[0];
@@ -1167,10 +1289,10 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
     // memory instructions in flight is a constant and each wait names exactly the group it
     // needs.  Order within step kt: commit B(kt+1), A(kt+2), B(kt+3), wait A(kt+1).
     constexpr int LB = B::VMEM;
-    constexpr int LA = ACopy<BM>::N;  // A-tile copy instructions per producer wave
+    constexpr int LA = ACopy<BM, PW>::N;  // A-tile copy instructions per producer wave
     constexpr uint32_t SLOT = LDS_A * sizeof(_Float16);
     const int last = kt1 - 1;
-    ACopy<BM> ac;
+    ACopy<BM, PW> ac;
     ac.init(a, As, pw, lane, m0);
     const typename B::Src src = B::setup(a, p, n0);
     typename B::Stage S0, S1, S2;
@@ -1223,10 +1345,10 @@ __global__ __launch_bounds__(512) void k_nf4_gemm_ws(GemmArgs a) {
     // accumulator start (bias, LoRA) while the producers stage K-step kt0
     if (lora16)
       start.finish_staged(a, acc, m0 + wm0, n0 + wn0, lrow, lseg, wm0, wn0, Ls, BM,
-                          kmask ? Ks : nullptr, MaskStage<BM, BN>::KST);
+                          kmask ? Ks : nullptr, MaskStage<BM, BN, NTP>::KST);
     else
       start.finish(a, acc, m0 + wm0, n0 + wn0, lrow, lseg, wm0, wn0, nullptr, 0,
-                   kmask ? Ks : nullptr, MaskStage<BM, BN>::KST);
+                   kmask ? Ks : nullptr, MaskStage<BM, BN, NTP>::KST);
     if (kt0 < kt1) {
       lds_barrier();  // K-step kt0 ready
       for (int kt = kt0; kt < kt1; kt++) {
@@ -1269,11 +1391,13 @@ static int launch_cfg(const GemmArgs& a0, int splits, hipStream_t stream) {
   return splits > 1 ? launch_reduce(a, splits, stream) : MXS_OK;
 }
 
-template <int BM, int BN, int CWM, int CWN, bool BWD>
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW = 4>
 static int launch_ws(const GemmArgs& a0, int splits, hipStream_t stream) {
-  // the producers' 32-bit offsets: W values and one A tile's bytes below 2^32; otherwise the
-  // all-wave kernel (64-bit addressing) takes the call
-  if ((int64_t)a0.Nc * a0.Kr >= (int64_t(1) << 32) || (int64_t)BM * a0.lda * 2 >= (int64_t(1) << 32))
+  // the producers' 32-bit offsets (W values and one A tile's bytes below 2^32) and the
+  // backward loads' column clamp (at least one load item of output columns); otherwise the
+  // all-wave kernel takes the call
+  if ((int64_t)a0.Nc * a0.Kr >= (int64_t(1) << 32) || (int64_t)BM * a0.lda * 2 >= (int64_t(1) << 32) ||
+      (BWD && a0.Nc < (PW == 8 ? 16 : 32)))
     return launch_cfg<64, 128, 1, 4, BWD>(a0, splits, stream);
   GemmArgs a = a0;
   const int n_steps = a.Kr / kBK;
@@ -1287,12 +1411,13 @@ static int launch_ws(const GemmArgs& a0, int splits, hipStream_t stream) {
   static bool lds_set = false;  // idempotent attribute; a benign race between threads
   if (!lds_set) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD>),
+        reinterpret_cast<const void*>(&k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
     lds_set = true;
   }
-  hipLaunchKernelGGL((k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD>), grid, dim3(512), lds, stream, a);
+  hipLaunchKernelGGL((k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW>), grid, dim3(64 * (4 + PW)), lds,
+                     stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   return splits > 1 ? launch_reduce(a, splits, stream) : MXS_OK;
@@ -1313,17 +1438,20 @@ static int launch_by_id(int cfg, const GemmArgs& a, int splits, hipStream_t s) {
     case 7: return launch_ws<256, 160, 4, 1, BWD>(a, splits, s);
     case 8: return launch_ws<128, 128, 2, 2, BWD>(a, splits, s);
     case 9: return launch_ws<256, 96, 4, 1, BWD>(a, splits, s);
+    case 10: return launch_ws<128, 128, 2, 2, BWD, 8>(a, splits, s);
+    case 11: return launch_ws<256, 96, 4, 1, BWD, 8>(a, splits, s);
     default: return MXS_ERR_ARG;
   }
 }
 
-constexpr int kNumCfg = 10;
+constexpr int kNumCfg = 12;
 
 // Tile and split choice for one GEMM (M x Nc output, Kr reduction), from measured sweeps on
 // MI355X at the Qwen2.5-1.5B projection shapes (M = 1024):
 //   wide outputs (Nc >= 4096): warp-specialized 256x160, one tile per CU, no split;
-//   narrow outputs with a long reduction (Kr >= 4096): warp-specialized 256x96, split-K 4;
-//   mid outputs (Nc >= 1024): warp-specialized 128x128, no split;
+//   narrow outputs with a long reduction (Kr >= 4096): warp-specialized 256x96 with 8 producer
+//   waves, split-K 4;
+//   mid outputs (Nc >= 1024): warp-specialized 128x128 with 8 producer waves, no split;
 //   small outputs: 64x128 all-wave tiles, split-K 4 when the reduction is long enough.
 // Splits keep at least 6 K-steps each.
 static void choose(int M, int Nc, int Kr, int* cfg, int* splits) {
@@ -1332,9 +1460,9 @@ static void choose(int M, int Nc, int Kr, int* cfg, int* splits) {
   if (Nc >= 4096) {
     c = 7; sp = 1;
   } else if (Kr >= 4096) {
-    c = 9; sp = 4;
+    c = 11; sp = 4;
   } else if (Nc >= 1024) {
-    c = 8; sp = 1;
+    c = 10; sp = 1;
   } else {
     c = 4; sp = Kr >= 1024 ? 4 : 1;
   }

@@ -42,7 +42,7 @@ def _np(t):
 
 @pytest.mark.parametrize("n,k", [(256, 1536), (1536, 1536), (192, 128)])
 @pytest.mark.parametrize("cfg,splits", [(-1, 1), (0, 1), (1, 2), (2, 1), (4, 3), (6, 2), (7, 1),
-                                        (8, 1), (9, 1)])
+                                        (8, 1), (9, 1), (10, 1), (10, 2), (11, 1), (11, 3)])
 def test_in_gemm_decode_is_bit_exact(cuda, n, k, cfg, splits):
     """One-hot rows: X = I gives Y = W^T and dY = I gives dX = W, each output a single exact
     product, so the fused kernels must reproduce the standalone dequant bit for bit (also with
@@ -87,7 +87,8 @@ def test_linear4bit_fwd_bwd_matches_oracle(cuda, out_features, bias, tokens):
 
 
 @pytest.mark.parametrize("cfg,splits", [(0, 1), (0, 4), (1, 1), (1, 3), (2, 2), (4, 1), (6, 1),
-                                        (6, 3), (7, 2), (8, 1), (9, 4)])
+                                        (6, 3), (7, 2), (8, 1), (9, 4), (10, 1), (10, 3),
+                                        (11, 4)])
 def test_tile_configs_agree_with_oracle(cuda, cfg, splits):
     from mindxsoup_amd import kernels
 
@@ -287,7 +288,7 @@ def test_lora_grads_without_tokens(cuda):
     assert da.shape == (r, K) and db.shape == (N, r)
 
 
-@pytest.mark.parametrize("cfg,splits", [(-1, 1), (4, 4), (9, 4), (3, 2)])
+@pytest.mark.parametrize("cfg,splits", [(-1, 1), (4, 4), (9, 4), (3, 2), (10, 2), (11, 4)])
 def test_split_k_is_deterministic_on_a_reused_workspace(cuda, cfg, splits):
     """Split-K partials are summed in split order: repeated calls (and a call of another shape
     in between, on the same workspace) give identical bits."""
