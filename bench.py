@@ -234,15 +234,11 @@ def proj_fwd(p, s=ALPHA / RANK):
 
 
 def proj_bwd(p, saved, s=ALPHA / RANK):
-    from mindxsoup_amd import kernels
+    from mindxsoup_amd.linear4bit import lora_backward
 
     ht, at, bt = saved
-    ms = 1.0 / (1.0 - P_DROP)
-    dhp = kernels.lora_dh_partials(p["dy"], bt, s)
-    dx, dht = kernels.nf4_linear_bwd_dx_hp(p["dy"], p["packed"], p["st"], dhp, at, p["keep"], ms,
-                                           ws=p["ws"])
-    da, db = kernels.lora_grads(dht, ht, p["x"], p["dy"], p["keep"], ms)
-    return dx, da, db
+    return lora_backward(p["dy"], p["x"], p["keep"], ht, at, bt, p["packed"], p["st"],
+                         1.0 / (1.0 - P_DROP), s, ws=p["ws"])
 
 
 def graph_time(fn, steps, warmup):

@@ -191,6 +191,14 @@ int mxs_lora_h_partials(const void* x, int M, int K, const void* lora_a, int r, 
 int mxs_lora_dh_partials(const void* dy, int M, int N, const void* lora_bt, int r, float s,
                          int ldt, float* partials, hipStream_t stream);
 
+/* The fp16 operand from such partial sums [slices][ldt][r] (1 <= slices <= 4; added in slice
+ * order and rounded, the value the fused GEMMs compute from the same partials): out [M, r] (may
+ * be NULL) and outT [r, ldt] with zeros past M.  Finishes dh from mxs_lora_dh_partials for
+ * mxs_lora_grads while the dX GEMM runs, i.e. the tensor autograd hands to lora_B's backward
+ * (solution/attention.py:197-199).  One launch. */
+int mxs_lora_finish(const float* partials, int slices, int M, int r, int ldt, void* out,
+                    void* outT, hipStream_t stream);
+
 /* mxs_lora_grad_a and mxs_lora_grad_b in one launch (either output may be NULL): the two weight
  * gradients autograd computes for peft's lora_A and lora_B (solution/attention.py:197-199 under
  * torch.autograd).  M == 0 writes zero gradients. */

@@ -51,6 +51,7 @@ _SIGNATURES = {
     "mxs_lora_slices": [I32, I32],
     "mxs_lora_h_partials": [P, I32, I32, P, I32, P, F32, F32, I32, P, P, I32, P, P, P],
     "mxs_lora_dh_partials": [P, I32, I32, P, I32, F32, I32, P, P],
+    "mxs_lora_finish": [P, I32, I32, I32, I32, P, P, P],
     "mxs_nf4_linear_fwd_hp": [P, I32, I32, I32, P, P, P, P, P, P, P, I32, I32, P, I32, P, P, P,
                               I32, I32, P],
     "mxs_nf4_linear_bwd_dx_hp": [P, I32, I32, I32, P, P, P, P, P, P, I32, I32, P, I32, P, F32, P,

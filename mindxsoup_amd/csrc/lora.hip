@@ -179,7 +179,7 @@ __global__ __launch_bounds__(64) void k_lora_rows_finish(RowsArgs a, int slices)
       for (int e = 0; e < 4; e++)
         h[q >> 1][4 * (q & 1) + e] = m < a.M ? (_Float16)sum[e] : (_Float16)0.0f;
     }
-    if (m < a.M) {
+    if (m < a.M && a.out) {
       *reinterpret_cast<half8_t*>(a.out + (int64_t)m * a.r + c0) = h[0];
       *reinterpret_cast<half8_t*>(a.out + (int64_t)m * a.r + c0 + 8) = h[1];
     }
@@ -493,6 +493,24 @@ int mxs_lora_dh_partials(const void* dy, int M, int N, const void* lora_bt, int 
   a.s = s;
   a.partial_out = 1;
   return rows_launch(a, partials, stream);
+}
+
+int mxs_lora_finish(const float* partials, int slices, int M, int r, int ldt, void* out,
+                    void* outT, hipStream_t stream) {
+  if (M < 0 || r <= 0 || slices < 1 || slices > 4) return MXS_ERR_ARG;
+  if (M == 0) return MXS_OK;
+  if (!partials || !outT) return MXS_ERR_ARG;
+  if (r % 16 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  if (((uintptr_t)partials % 16) || (out && ((uintptr_t)out % 16))) return MXS_ERR_ALIGN;
+  RowsArgs a{};
+  a.M = M;
+  a.r = r;
+  a.ldt = ldt;
+  a.ws = const_cast<float*>(partials);
+  a.out = static_cast<_Float16*>(out);
+  a.outT = static_cast<_Float16*>(outT);
+  hipLaunchKernelGGL(k_lora_rows_finish, dim3((ldt + 63) / 64), dim3(64), 0, stream, a, slices);
+  return (int)hipGetLastError();
 }
 
 int mxs_lora_grads(const void* dht, const void* ht, int ldt, const void* x, const void* dy, int M,

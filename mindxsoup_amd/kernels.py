@@ -189,9 +189,9 @@ def nf4_linear_fwd_hp(x2d, packed, state, lora_hp, lora_b, bias=None, cfg=-1, sp
 
 
 def nf4_linear_bwd_dx_hp(dy2d, packed, state, lora_dhp, lora_at, mask=None, mask_scale=1.0,
-                         cfg=-1, splits=1, ws=None):
+                         cfg=-1, splits=1, ws=None, want_t=True):
     """(dx, dht): dX = dy2d @ W + mask * mask_scale * (fp16(sum of lora_dhp) @ lora_at^T), and
-    that fp16 operand transposed [r, ldt]."""
+    that fp16 operand transposed [r, ldt] (None unless want_t)."""
     n, k = state.shape
     if dy2d.dtype != torch.float16 or dy2d.dim() != 2 or dy2d.shape[1] != n:
         raise ValueError("dy must be fp16 [M, out_features]")
@@ -205,13 +205,27 @@ def nf4_linear_bwd_dx_hp(dy2d, packed, state, lora_dhp, lora_at, mask=None, mask
             raise ValueError("mask must be uint8 [M, K]")
         mask = mask.contiguous()
     dx = torch.empty((M, k), dtype=torch.float16, device=dy2d.device)
-    dht = torch.empty((r, ldt), dtype=torch.float16, device=dy2d.device)
+    dht = torch.empty((r, ldt), dtype=torch.float16, device=dy2d.device) if want_t else None
     ws = _ws(M, k, n, dy2d.device, cfg, splits, ws)
     _lib.call("mxs_nf4_linear_bwd_dx_hp", _lib.ptr(dy2d), M, n, k, *_nf4_args(packed, state),
               _lib.ptr(lora_dhp.contiguous()), S, ldt, _lib.ptr(lora_at.contiguous()), r,
               _lib.ptr(mask), float(mask_scale), _lib.ptr(dht), _lib.ptr(dx), _lib.ptr(ws), cfg,
               splits, _lib.stream_of(dy2d.device))
     return dx, dht
+
+
+def lora_finish(partials, M, want_out=False):
+    """(out, outT): the fp16 operand from LoRA partial sums [slices, ldt, r] fp32 (added in slice
+    order, as the fused GEMMs do): out [M, r] (None unless want_out) and outT [r, ldt]."""
+    S, ldt, r = partials.shape
+    if partials.dtype != torch.float32 or ldt != _ldt(M):
+        raise ValueError("partials must be fp32 [slices, ldt, r]")
+    dev = partials.device
+    out = torch.empty((M, r), dtype=torch.float16, device=dev) if want_out else None
+    outT = torch.empty((r, ldt), dtype=torch.float16, device=dev)
+    _lib.call("mxs_lora_finish", _lib.ptr(partials.contiguous()), S, M, r, ldt, _lib.ptr(out),
+              _lib.ptr(outT), _lib.stream_of(dev))
+    return out, outT
 
 
 def transpose(t2d):

@@ -78,6 +78,29 @@ class NF4LinearFunction(torch.autograd.Function):
         return grad_x, None, None, None
 
 
+def lora_backward(dy, x2d, keep, ht, at, bt, packed, state, mask_scale, s, want_x=True,
+                  want_a=True, want_b=True, ws=None):
+    """(dX, dA, dB) of one NF4 + LoRA projection (None where not wanted), on the current stream:
+    dHs = s * dY B as slice partials, the fused dX GEMM (which finishes dHs and writes dHs^T),
+    then dA and dB in one launch.  (A variant that ran the weight gradients on a second stream
+    beside the GEMM lost more to the cross-queue waits of the graph, 5-10 us per fork and join,
+    than it gained.)  `ws`: an optional workspace for every call of this projection
+    (kernels.projection_workspace_bytes)."""
+    dhp = kernels.lora_dh_partials(dy, bt, s)
+    want_g = want_a or want_b
+    dx = dht = None
+    if want_x or want_g:
+        dx, dht = kernels.nf4_linear_bwd_dx_hp(dy, packed, state, dhp, at, keep, mask_scale,
+                                               ws=ws, want_t=want_g)
+    if not want_x:
+        dx = None
+    da = db = None
+    if want_g:
+        da, db = kernels.lora_grads(dht, ht, x2d, dy, keep, mask_scale, want_a=want_a,
+                                    want_b=want_b, ws=ws)
+    return dx, da, db
+
+
 class NF4LoraFunction(torch.autograd.Function):
     """base(x) + s * B(A(drop(x))) for a frozen NF4 base, fused:
     forward:  Hs = s * drop(x) A^T as slice partials (mxs_lora_h_partials), then one fused GEMM
@@ -103,14 +126,10 @@ class NF4LoraFunction(torch.autograd.Function):
     def backward(ctx, dy):
         x2d, keep, ht, at, bt = ctx.saved_tensors
         dy = dy.to(torch.float16).contiguous()
-        dhp = kernels.lora_dh_partials(dy, bt, ctx.s)
-        dx, dht = kernels.nf4_linear_bwd_dx_hp(dy, ctx.packed, ctx.state, dhp, at, keep,
-                                               ctx.mask_scale)
-        if not ctx.needs_input_grad[0]:
-            dx = None
-        da, db = kernels.lora_grads(dht, ht, x2d, dy, keep, ctx.mask_scale,
-                                    want_a=ctx.needs_input_grad[1],
-                                    want_b=ctx.needs_input_grad[2])
+        dx, da, db = lora_backward(dy, x2d, keep, ht, at, bt, ctx.packed, ctx.state,
+                                   ctx.mask_scale, ctx.s, want_x=ctx.needs_input_grad[0],
+                                   want_a=ctx.needs_input_grad[1],
+                                   want_b=ctx.needs_input_grad[2])
         if da is not None:
             da = da.to(ctx.dtypes[0])
         if db is not None:

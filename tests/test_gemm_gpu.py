@@ -276,6 +276,64 @@ def test_partial_sum_lora_path_equals_finished_path(cuda, n, k, M):
     assert torch.equal(dx2, dx) and torch.equal(dht2, dht)
 
 
+@pytest.mark.parametrize("n,k,M", [(1536, 1536, 1024), (256, 1536, 1000), (8960, 1536, 700)])
+def test_lora_finish_and_backward_sequence(cuda, n, k, M):
+    """mxs_lora_finish gives the bits the fused dX GEMM writes as dHs^T from the same partials,
+    and the shared backward sequence equals its kernels called one by one."""
+    from mindxsoup_amd import kernels
+    from mindxsoup_amd.linear4bit import lora_backward
+
+    print(f"case finish/backward n={n} k={k} M={M}", flush=True)
+    layer = _layer(cuda, n, k, 37)
+    st = layer.weight.quant_state
+    packed = layer.weight.data.view(-1, 1)
+    x, a, b, dy, keep = _lora_inputs(cuda, M, k, n, 38)
+    s, ms = 2.0, 1 / 0.95
+    hp, at, bt = kernels.lora_h_partials(x, a, s, keep, ms, lora_b=b)
+    _, ht = kernels.nf4_linear_fwd_hp(x, packed, st, hp, b)
+    dhp = kernels.lora_dh_partials(dy, bt, s)
+    dx1, dht1 = kernels.nf4_linear_bwd_dx_hp(dy, packed, st, dhp, at, keep, ms)
+    out, outT = kernels.lora_finish(dhp, M, want_out=True)
+    assert torch.equal(outT, dht1)
+    assert torch.equal(out, dht1[:, :M].t().contiguous())
+    da1, db1 = kernels.lora_grads(dht1, ht, x, dy, keep, ms)
+    dx2, da2, db2 = lora_backward(dy, x, keep, ht, at, bt, packed, st, ms, s)
+    torch.cuda.synchronize()
+    assert torch.equal(dx2, dx1) and torch.equal(da2, da1) and torch.equal(db2, db1)
+
+
+def test_backward_sequence_replays_in_a_graph(cuda):
+    """The backward sequence captured in a HIP graph: every replay, with eager work and
+    synchronizations between replays, equals the eager result."""
+    from mindxsoup_amd import kernels
+    from mindxsoup_amd.linear4bit import lora_backward
+
+    n, k, M = 1536, 1536, 1024
+    print(f"case graph backward n={n} k={k} M={M}", flush=True)
+    layer = _layer(cuda, n, k, 41)
+    st = layer.weight.quant_state
+    packed = layer.weight.data.view(-1, 1)
+    x, a, b, dy, keep = _lora_inputs(cuda, M, k, n, 42)
+    s, ms = 2.0, 1 / 0.95
+    hp, at, bt = kernels.lora_h_partials(x, a, s, keep, ms, lora_b=b)
+    _, ht = kernels.nf4_linear_fwd_hp(x, packed, st, hp, b)
+    ref = lora_backward(dy, x, keep, ht, at, bt, packed, st, ms, s)
+    torch.cuda.synchronize()
+    ref = [t.clone() for t in ref]
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = lora_backward(dy, x, keep, ht, at, bt, packed, st, ms, s)
+    for rep in range(4):
+        for o in outs:
+            o.zero_()
+        _ = kernels.lora_dh_partials(dy, bt, s)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, r in zip(outs, ref):
+            assert torch.equal(o, r), f"replay {rep} differs"
+
+
 def test_lora_grads_without_tokens(cuda):
     from mindxsoup_amd import kernels
 
