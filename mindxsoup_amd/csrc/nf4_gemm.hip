@@ -1052,7 +1052,10 @@ struct BLoadT {
 
 // NF4 side of a forward K-step for 512 producer threads (tiles up to 128 columns): item = 8
 // packed bytes of W row n (16 values, a quarter of the row's block for this K-step), 3 memory
-// instructions; same addressing scheme as BLoad.
+// instructions; same addressing scheme as BLoad.  A 96-row tile leaves producer waves 6 and 7
+// without items.  Evening out the decode per SIMD (waves 4-7 on 4-byte items) was measured and
+// rejected: the 4-byte items' fixed per-item cost made those waves slower than the imbalance it
+// removed.
 template <int BN>
 struct BLoad8 {
   static constexpr int TOTAL = BN * 4;  // 8-byte items
