@@ -77,4 +77,40 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
+// Global loads issued as inline asm: uniform base in SGPRs plus a 32-bit per-lane byte offset.
+// Like the direct-to-LDS copies, the compiler neither counts them in the vmcnt waits it
+// inserts for its own loads (so none of those waits drains them) nor waits for them itself:
+// read a result only after wait_vmcnt<N>() has covered its load and vm_ready() has passed it
+// through.  vm_ready is ordered after the wait (both have side effects) and redefines the
+// value, so no use of it can be scheduled above the wait.
+__device__ __forceinline__ uint32_t gload_u8(const void* base, uint32_t off) {
+  uint32_t v;
+  asm volatile("global_load_ubyte %0, %1, %2" : "=v"(v) : "v"(off), "s"(base));
+  return v;
+}
+__device__ __forceinline__ float gload_f32(const void* base, uint32_t off) {
+  float v;
+  asm volatile("global_load_dword %0, %1, %2" : "=v"(v) : "v"(off), "s"(base));
+  return v;
+}
+__device__ __forceinline__ uint32_t gload_b32(const void* base, uint32_t off) {
+  uint32_t v;
+  asm volatile("global_load_dword %0, %1, %2" : "=v"(v) : "v"(off), "s"(base));
+  return v;
+}
+__device__ __forceinline__ u32x2 gload_b64(const void* base, uint32_t off) {
+  u32x2 v;
+  asm volatile("global_load_dwordx2 %0, %1, %2" : "=v"(v) : "v"(off), "s"(base));
+  return v;
+}
+__device__ __forceinline__ u32x4 gload_b128(const void* base, uint32_t off) {
+  u32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, %2" : "=v"(v) : "v"(off), "s"(base));
+  return v;
+}
+template <typename T>
+__device__ __forceinline__ void vm_ready(T& v) {
+  asm volatile("" : "+v"(v));
+}
+
 }  // namespace mxs

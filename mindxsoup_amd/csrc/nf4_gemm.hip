@@ -55,6 +55,7 @@ struct GemmArgs {
   int steps_per_split;
 };
 
+
 // LDS offset (in halfs) of 16-byte segment `seg` (0..7) of row `row` in a [rows][64] tile.
 __device__ __forceinline__ int lds_off(int row, int seg) {
   return row * kBK + (((seg ^ row ^ (row >> 3)) & 7) << 3);
@@ -902,7 +903,7 @@ struct BLoad {
 
   __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0) {
     Src r;
-    const int q = min(p, TOTAL - 1);  // lanes past TOTAL load a duplicate item
+    const int q = p;  // the caller runs only lanes with an item (p < TOTAL)
     const uint32_t n = min(n0 + (q >> 1), a.Nc - 1);
     r.w = n * (uint32_t)(a.Kw / 2) + (q & 1) * 16;
     r.blk = n * (uint32_t)(a.Kw / 64);
@@ -916,44 +917,67 @@ struct BLoad {
                                                int kt) {
     const uint8_t* pk = a.packed + kt * (kBK / 2);  // uniform
     const uint8_t* q8 = a.absmax8 + kt;             // block of row n at K-step kt: blk + kt
-    S.q8 = q8[src.blk];
-    S.a2 = a.absmax2[(src.blk + kt) >> 8];
-    S.w = *reinterpret_cast<const u32x4*>(pk + src.w);
+    S.q8 = gload_u8(q8, src.blk);
+    S.a2 = gload_f32(a.absmax2, ((src.blk + kt) >> 8) * 4);
+    S.w = gload_b128(pk, src.w);
     if constexpr (REST > 0) {
-      S.q8b = q8[src.blk4];
-      S.a2b = a.absmax2[(src.blk4 + kt) >> 8];
-      S.w4 = *reinterpret_cast<const uint32_t*>(pk + src.w4);
+      S.q8b = gload_u8(q8, src.blk4);
+      S.a2b = gload_f32(a.absmax2, ((src.blk4 + kt) >> 8) * 4);
+      S.w4 = gload_b32(pk, src.w4);
     }
   }
 
-  __device__ static __forceinline__ void commit(const Stage& S, _Float16* bs, int p,
-                                                const float2_t* s_pair, const float* s_code,
-                                                float offset) {
-    float2_t pr[4][4];  // all table lookups first: one LDS round trip
+  // after the wait that covers the stage's loads
+  __device__ static __forceinline__ void ready(Stage& S) {
+    vm_ready(S.w);
+    vm_ready(S.q8);
+    vm_ready(S.a2);
+    if constexpr (REST > 0) {
+      vm_ready(S.w4);
+      vm_ready(S.q8b);
+      vm_ready(S.a2b);
+    }
+  }
+
+  // table lookups of one stage (issued a K-step before finish() uses them)
+  struct Looked {
+    float2_t pr[4][4];
+    float2_t pb[4];
+    float c, cb;
+  };
+
+  __device__ static __forceinline__ void lookup(const Stage& S, Looked& L, const float2_t* s_pair,
+                                                const float* s_code) {
 #pragma unroll
     for (int d = 0; d < 4; d++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
-    float2_t pb[4];
+      for (int j = 0; j < 4; j++) L.pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
+    L.c = s_code[S.q8];
     if constexpr (REST > 0) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) pb[j] = s_pair[(S.w4 >> (8 * j)) & 0xffu];
+      for (int j = 0; j < 4; j++) L.pb[j] = s_pair[(S.w4 >> (8 * j)) & 0xffu];
+      L.cb = s_code[S.q8b];
     }
-    if (p < TOTAL) {
-      const float sc = nested_scale(s_code[S.q8], S.a2, offset);
+  }
+
+  __device__ static __forceinline__ void finish(const Stage& S, const Looked& L, _Float16* bs,
+                                                int p, float offset) {
+    {
+      const int q = p;  // < TOTAL
+      const float sc = nested_scale(L.c, S.a2, offset);
 #pragma unroll
       for (int d = 0; d < 4; d++) {
         u32x4 v;
 #pragma unroll
-        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pr[d][j][0] * sc, pr[d][j][1] * sc);
-        *reinterpret_cast<u32x4*>(bs + lds_off(p >> 1, (p & 1) * 4 + d)) = v;
+        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(L.pr[d][j][0] * sc, L.pr[d][j][1] * sc);
+        *reinterpret_cast<u32x4*>(bs + lds_off(q >> 1, (q & 1) * 4 + d)) = v;
       }
     }
     if constexpr (REST > 0) {
-      const float sc = nested_scale(s_code[S.q8b], S.a2b, offset);
+      const float sc = nested_scale(L.cb, S.a2b, offset);
       u32x4 v;
 #pragma unroll
-      for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pb[j][0] * sc, pb[j][1] * sc);
+      for (int j = 0; j < 4; j++) v[j] = pack_f16x2(L.pb[j][0] * sc, L.pb[j][1] * sc);
       *reinterpret_cast<u32x4*>(bs + lds_off(R16 + (p >> 3), p & 7)) = v;
     }
   }
@@ -993,7 +1017,7 @@ struct BLoadT {
 
   __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0) {
     Src r;
-    const int q = min(p, TOTAL - 1);  // lanes past TOTAL load a duplicate item
+    const int q = p;  // the caller runs only lanes with an item (p < TOTAL)
     const int row = q / CPR, c = q % CPR;
     r.x = (uint32_t)row * a.Kw + min(n0 + 32 * c, a.Nc - 32);
     r.x4 = (uint32_t)(p >> 2) * a.Kw + min(n0 + C16 + 8 * (p & 3), a.Nc - 8);
@@ -1005,46 +1029,67 @@ struct BLoadT {
     const uint32_t slab = (uint32_t)kt * kBK * a.Kw;   // uniform
     const uint8_t* pk = a.packed + slab / 2;
     const uint8_t* q8 = a.absmax8 + slab / 64;
-    S.q8 = q8[src.x >> 6];
-    S.a2 = a.absmax2[(slab + src.x) >> 14];
-    S.w = *reinterpret_cast<const u32x4*>(pk + (src.x >> 1));
+    S.q8 = gload_u8(q8, src.x >> 6);
+    S.a2 = gload_f32(a.absmax2, ((slab + src.x) >> 14) * 4);
+    S.w = gload_b128(pk, src.x >> 1);
     if constexpr (REST > 0) {
-      S.q8b = q8[src.x4 >> 6];
-      S.a2b = a.absmax2[(slab + src.x4) >> 14];
-      S.w4 = *reinterpret_cast<const uint32_t*>(pk + (src.x4 >> 1));
+      S.q8b = gload_u8(q8, src.x4 >> 6);
+      S.a2b = gload_f32(a.absmax2, ((slab + src.x4) >> 14) * 4);
+      S.w4 = gload_b32(pk, src.x4 >> 1);
     }
   }
 
-  __device__ static __forceinline__ void commit(const Stage& S, _Float16* bs, int p,
-                                                const float2_t* s_pair, const float* s_code,
-                                                float offset) {
+  __device__ static __forceinline__ void ready(Stage& S) {
+    vm_ready(S.w);
+    vm_ready(S.q8);
+    vm_ready(S.a2);
+    if constexpr (REST > 0) {
+      vm_ready(S.w4);
+      vm_ready(S.q8b);
+      vm_ready(S.a2b);
+    }
+  }
+
+  struct Looked {
     float2_t pr[4][4];
+    float2_t pb[4];
+    float c, cb;
+  };
+
+  __device__ static __forceinline__ void lookup(const Stage& S, Looked& L, const float2_t* s_pair,
+                                                const float* s_code) {
 #pragma unroll
     for (int d = 0; d < 4; d++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
-    float2_t pb[4];
+      for (int j = 0; j < 4; j++) L.pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
+    L.c = s_code[S.q8];
     if constexpr (REST > 0) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) pb[j] = s_pair[(S.w4 >> (8 * j)) & 0xffu];
+      for (int j = 0; j < 4; j++) L.pb[j] = s_pair[(S.w4 >> (8 * j)) & 0xffu];
+      L.cb = s_code[S.q8b];
     }
-    if (p < TOTAL) {
-      const int row = p / CPR, c = p % CPR;
-      const float sc = nested_scale(s_code[S.q8], S.a2, offset);
+  }
+
+  __device__ static __forceinline__ void finish(const Stage& S, const Looked& L, _Float16* bs,
+                                                int p, float offset) {
+    {
+      const int q = p;  // < TOTAL
+      const int row = q / CPR, c = q % CPR;
+      const float sc = nested_scale(L.c, S.a2, offset);
 #pragma unroll
       for (int d = 0; d < 4; d++) {
         u32x4 v;
 #pragma unroll
-        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pr[d][j][0] * sc, pr[d][j][1] * sc);
+        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(L.pr[d][j][0] * sc, L.pr[d][j][1] * sc);
         *reinterpret_cast<u32x4*>(bs + row * LDB + 32 * c + 8 * d) = v;
       }
     }
     if constexpr (REST > 0) {
       const int row = p >> 2, sub = p & 3;
-      const float sc = nested_scale(s_code[S.q8b], S.a2b, offset);
+      const float sc = nested_scale(L.cb, S.a2b, offset);
       u32x4 v;
 #pragma unroll
-      for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pb[j][0] * sc, pb[j][1] * sc);
+      for (int j = 0; j < 4; j++) v[j] = pack_f16x2(L.pb[j][0] * sc, L.pb[j][1] * sc);
       *reinterpret_cast<u32x4*>(bs + row * LDB + C16 + 8 * sub) = v;
     }
   }
@@ -1073,7 +1118,7 @@ struct BLoad8 {
 
   __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0) {
     Src r;
-    const int q = min(p, TOTAL - 1);
+    const int q = p;  // the caller runs only lanes with an item (p < TOTAL)
     const uint32_t n = min(n0 + (q >> 2), a.Nc - 1);
     r.w = n * (uint32_t)(a.Kw / 2) + (q & 3) * 8;
     r.blk = n * (uint32_t)(a.Kw / 64);
@@ -1083,27 +1128,42 @@ struct BLoad8 {
   __device__ static __forceinline__ void issue(const GemmArgs& a, const Src& src, Stage& S,
                                                int kt) {
     const uint8_t* pk = a.packed + kt * (kBK / 2);
-    S.q8 = (a.absmax8 + kt)[src.blk];
-    S.a2 = a.absmax2[(src.blk + kt) >> 8];
-    S.w = *reinterpret_cast<const u32x2*>(pk + src.w);
+    S.q8 = gload_u8(a.absmax8 + kt, src.blk);
+    S.a2 = gload_f32(a.absmax2, ((src.blk + kt) >> 8) * 4);
+    S.w = gload_b64(pk, src.w);
   }
 
-  __device__ static __forceinline__ void commit(const Stage& S, _Float16* bs, int p,
-                                                const float2_t* s_pair, const float* s_code,
-                                                float offset) {
+  __device__ static __forceinline__ void ready(Stage& S) {
+    vm_ready(S.w);
+    vm_ready(S.q8);
+    vm_ready(S.a2);
+  }
+
+  struct Looked {
     float2_t pr[2][4];
+    float c;
+  };
+
+  __device__ static __forceinline__ void lookup(const Stage& S, Looked& L, const float2_t* s_pair,
+                                                const float* s_code) {
 #pragma unroll
     for (int d = 0; d < 2; d++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
-    if (p < TOTAL) {
-      const float sc = nested_scale(s_code[S.q8], S.a2, offset);
+      for (int j = 0; j < 4; j++) L.pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
+    L.c = s_code[S.q8];
+  }
+
+  __device__ static __forceinline__ void finish(const Stage& S, const Looked& L, _Float16* bs,
+                                                int p, float offset) {
+    {
+      const int q = p;  // < TOTAL
+      const float sc = nested_scale(L.c, S.a2, offset);
 #pragma unroll
       for (int d = 0; d < 2; d++) {
         u32x4 v;
 #pragma unroll
-        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pr[d][j][0] * sc, pr[d][j][1] * sc);
-        *reinterpret_cast<u32x4*>(bs + lds_off(p >> 2, (p & 3) * 2 + d)) = v;
+        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(L.pr[d][j][0] * sc, L.pr[d][j][1] * sc);
+        *reinterpret_cast<u32x4*>(bs + lds_off(q >> 2, (q & 3) * 2 + d)) = v;
       }
     }
   }
@@ -1131,7 +1191,7 @@ struct BLoadT8 {
 
   __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0) {
     Src r;
-    const int q = min(p, TOTAL - 1);
+    const int q = p;  // the caller runs only lanes with an item (p < TOTAL)
     const int row = q / CPR, c = q % CPR;
     r.x = (uint32_t)row * a.Kw + min(n0 + 16 * c, a.Nc - 16);
     return r;
@@ -1141,27 +1201,42 @@ struct BLoadT8 {
                                                int kt) {
     const uint32_t slab = (uint32_t)kt * kBK * a.Kw;
     const uint8_t* pk = a.packed + slab / 2;
-    S.q8 = (a.absmax8 + slab / 64)[src.x >> 6];
-    S.a2 = a.absmax2[(slab + src.x) >> 14];
-    S.w = *reinterpret_cast<const u32x2*>(pk + (src.x >> 1));
+    S.q8 = gload_u8(a.absmax8 + slab / 64, src.x >> 6);
+    S.a2 = gload_f32(a.absmax2, ((slab + src.x) >> 14) * 4);
+    S.w = gload_b64(pk, src.x >> 1);
   }
 
-  __device__ static __forceinline__ void commit(const Stage& S, _Float16* bs, int p,
-                                                const float2_t* s_pair, const float* s_code,
-                                                float offset) {
+  __device__ static __forceinline__ void ready(Stage& S) {
+    vm_ready(S.w);
+    vm_ready(S.q8);
+    vm_ready(S.a2);
+  }
+
+  struct Looked {
     float2_t pr[2][4];
+    float c;
+  };
+
+  __device__ static __forceinline__ void lookup(const Stage& S, Looked& L, const float2_t* s_pair,
+                                                const float* s_code) {
 #pragma unroll
     for (int d = 0; d < 2; d++)
 #pragma unroll
-      for (int j = 0; j < 4; j++) pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
-    if (p < TOTAL) {
-      const int row = p / CPR, c = p % CPR;
-      const float sc = nested_scale(s_code[S.q8], S.a2, offset);
+      for (int j = 0; j < 4; j++) L.pr[d][j] = s_pair[(S.w[d] >> (8 * j)) & 0xffu];
+    L.c = s_code[S.q8];
+  }
+
+  __device__ static __forceinline__ void finish(const Stage& S, const Looked& L, _Float16* bs,
+                                                int p, float offset) {
+    {
+      const int q = p;  // < TOTAL
+      const int row = q / CPR, c = q % CPR;
+      const float sc = nested_scale(L.c, S.a2, offset);
 #pragma unroll
       for (int d = 0; d < 2; d++) {
         u32x4 v;
 #pragma unroll
-        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(pr[d][j][0] * sc, pr[d][j][1] * sc);
+        for (int j = 0; j < 4; j++) v[j] = pack_f16x2(L.pr[d][j][0] * sc, L.pr[d][j][1] * sc);
         *reinterpret_cast<u32x4*>(bs + row * LDB + 16 * c + 8 * d) = v;
       }
     }
@@ -1234,7 +1309,7 @@ struct ACopy {
 // the other half of a 2-deep B buffer while the consumers multiply kt.  Everything a producer
 // issues in one K-step is waited for at the start of the next, and one workgroup barrier per
 // K-step hands the buffers over.
-template <int BM, int BN, int CWM, int CWN, bool BWD, int PW>
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS>
 __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
   constexpr int WM = BM / CWM, WN = BN / CWN, TM = WM / 32, TN = WN / 32;
   constexpr int NTP = 64 * PW;  // producer threads
@@ -1286,56 +1361,124 @@ __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
     if (lora16) lst.issue(a, p, m0, n0);  // before the tiles: one round trip for all
     if (kmask) mst.issue(a, p, m0, n0);
     const float offset = a.offset[0];
-    // NF4 tile of K-step kt is issued three steps ahead into register stage (kt - kt0) % 3 and
-    // committed to LDS one step ahead; the A tile is copied two steps ahead into the LDS ring.
-    // Every issue is unconditional (steps past the end re-load the last one), so the number of
-    // memory instructions in flight is a constant and each wait names exactly the group it
-    // needs.  Order within step kt: commit B(kt+1), A(kt+2), B(kt+3), wait A(kt+1).
-    constexpr int LB = B::VMEM;
-    constexpr int LA = ACopy<BM, PW>::N;  // A-tile copy instructions per producer wave
+    // NF4 tile of K-step kt is issued NS steps ahead into register stage (kt - kt0) % NS; its
+    // table lookups are issued one step ahead, right after the previous tile is finished, so
+    // their LDS latency overlaps the loads and barrier of that step; it is finished (scaled,
+    // converted, written to LDS) one step ahead of its multiply.  The A tile is copied two
+    // steps ahead into the LDS ring.
+    // Every producer wave copies its share of A.  Waves with B items decode them; whole waves
+    // past the items (a 96-column tile leaves two of eight) only copy: decoding a duplicate
+    // item there would take issue slots from the multiplying wave of the same SIMD.  (Handing
+    // the whole A tile to those two waves instead measured slower: all copies then issue
+    // from two SIMDs.)
+    // Decoding wave, order within step kt: finish B(kt+1), look up B(kt+2), copy A(kt+2),
+    // issue B(kt+NS), wait A(kt+1).  So in issue order A(j) comes right before B(j+NS-2), and
+    // the prologue keeps that order: B(kt0) .. B(kt0+NS-3), A(kt0), B(kt0+NS-2), A(kt0+1),
+    // B(kt0+NS-1).  A load of B gets NS-2 steps to land.
+    // The B loads are inline asm like the copies: every wait here is counted by hand over both
+    // (vmcnt counts in issue order), and the compiler adds none of its own, which, blind to the
+    // copies, would drain the copy of A(kt+1) along with B(kt+2).  Every issue is unconditional
+    // (steps past the end re-load the last one), so the number of memory instructions in
+    // flight is a constant and each wait names exactly the group it needs.
+    using AC = ACopy<BM, PW>;
+    constexpr int LA = AC::N;  // A-tile copy instructions per producer wave and step
     constexpr uint32_t SLOT = LDS_A * sizeof(_Float16);
     const int last = kt1 - 1;
-    ACopy<BM, PW> ac;
-    ac.init(a, As, pw, lane, m0);
-    const typename B::Src src = B::setup(a, p, n0);
-    typename B::Stage S0, S1, S2;
-    if (run) {
-      B::issue(a, src, S0, kt0);
-      ac.copy(0, kt0);
-      B::issue(a, src, S1, min(kt0 + 1, last));
-      ac.copy(SLOT, min(kt0 + 1, last));
-      B::issue(a, src, S2, min(kt0 + 2, last));
-    }
-    if (lora16 || kmask) {
-      if (run) wait_vmcnt<3 * LB + 2 * LA>();  // the staged loads, issued before all of those
-      else wait_vmem_all();
-      if (lora16) lst.commit(a, Ls, p);
-      if (kmask) mst.commit(Ks, p);
-    }
-    lds_barrier();  // tables, LoRA operands
-    if (run) {
-      B::commit(S0, bbuf(0), p, s_pair, s_code, offset);
-      wait_vmcnt<2 * LB + LA>();  // A(kt0): after it only B(kt0+1), A(kt0+1), B(kt0+2)
-      lds_barrier();  // K-step kt0 ready
-      auto step = [&](int kt, typename B::Stage& Sc, typename B::Stage& Si) {
-        const int r = kt - kt0;
-        // the compiler's own wait before this commit (B(kt+1) registers) also completes
-        // A(kt+1), issued after B(kt+1); B(kt+2) stays in flight
-        if (kt + 1 < kt1) B::commit(Sc, bbuf(r + 1), p, s_pair, s_code, offset);
-        ac.copy(((r + 2) % 3) * SLOT, min(kt + 2, last));
-        B::issue(a, src, Si, min(kt + 3, last));
-        wait_vmcnt<2 * LB + LA>();  // A(kt+1): after it only B(kt+2), A(kt+2), B(kt+3)
-        lds_barrier();
-      };
-      int kt = kt0;
-      for (; kt + 3 <= kt1; kt += 3) {
-        step(kt, S1, S0);
-        step(kt + 1, S2, S1);
-        step(kt + 2, S0, S2);
+    // the branch is uniform and taken once; both paths pass the same barriers
+    if (B::TOTAL >= NTP || __builtin_amdgcn_readfirstlane(p) < B::TOTAL) {
+      constexpr int LB = B::VMEM;
+      static_assert(NS >= 4 && NS * LB + 2 * LA <= 63, "stages: at least 4; waits fit vmcnt");
+      AC ac;
+      ac.init(a, As, pw, lane, m0);
+      const typename B::Src src = B::setup(a, p, n0);
+      typename B::Stage S[NS];
+      typename B::Looked L;
+      if (run) {
+#pragma unroll
+        for (int u = 0; u < NS - 2; u++) B::issue(a, src, S[u], min(kt0 + u, last));
+        ac.copy(0, kt0);
+        B::issue(a, src, S[NS - 2], min(kt0 + NS - 2, last));
+        ac.copy(SLOT, min(kt0 + 1, last));
+        B::issue(a, src, S[NS - 1], min(kt0 + NS - 1, last));
       }
-      if (kt < kt1) step(kt, S1, S0);
-      if (kt + 1 < kt1) step(kt + 1, S2, S1);
-      wait_vmem_all();  // no copy into the A ring may still be in flight
+      if (lora16 || kmask) {
+        if (run) wait_vmcnt<NS * LB + 2 * LA>();  // the staged loads, issued before all of those
+        else wait_vmem_all();
+        if (lora16) lst.commit(a, Ls, p);
+        if (kmask) mst.commit(Ks, p);
+      }
+      lds_barrier();  // tables, LoRA operands
+      if (run) {
+        wait_vmcnt<(NS - 1) * LB + 2 * LA>();  // B(kt0)
+        B::ready(S[0]);
+        B::lookup(S[0], L, s_pair, s_code);
+        B::finish(S[0], L, bbuf(0), p, offset);
+        wait_vmcnt<2 * LB + LA>();  // A(kt0) and what precedes it (B(kt0+1) among them)
+        B::ready(S[1]);
+        B::lookup(S[1], L, s_pair, s_code);
+        lds_barrier();  // K-step kt0 ready
+        // Sc = B(kt+1) (looked up in L), Sn = B(kt+2), Si = the stage of B(kt), free for B(kt+NS)
+        auto step = [&](int kt, typename B::Stage& Sc, typename B::Stage& Sn,
+                        typename B::Stage& Si) {
+          const int r = kt - kt0;
+          // Unconditional: past the end the stages hold the last K-step again and bbuf(r + 1) is
+          // the buffer of step kt - 1, no longer read; branches here would only give the
+          // compiler paths to merge.
+          B::finish(Sc, L, bbuf(r + 1), p, offset);
+          // B(kt+2); after it A(kt+5-NS) .. A(kt+1) and B(kt+3) .. B(kt+NS-1)
+          wait_vmcnt<(NS - 3) * (LA + LB)>();
+          B::ready(Sn);
+          B::lookup(Sn, L, s_pair, s_code);
+          ac.copy(((r + 2) % 3) * SLOT, min(kt + 2, last));
+          B::issue(a, src, Si, min(kt + NS, last));
+          wait_vmcnt<2 * LB + LA>();  // A(kt+1); after it only B(kt+NS-1), A(kt+2), B(kt+NS)
+          lds_barrier();
+          // nothing of the next step moves above this point (its arithmetic on the next stage
+          // would then sit before the copies of this step in the schedule)
+          __builtin_amdgcn_sched_barrier(0);
+        };
+        int kt = kt0;
+        for (; kt + NS <= kt1; kt += NS) {
+#pragma unroll
+          for (int u = 0; u < NS; u++) step(kt + u, S[(u + 1) % NS], S[(u + 2) % NS], S[u]);
+        }
+        // no path reaches a step without the one before it (whose wait and ready() the next
+        // step's stage relies on)
+#pragma unroll
+        for (int u = 0; u < NS - 1; u++) {
+          if (kt + u >= kt1) break;
+          step(kt + u, S[(u + 1) % NS], S[(u + 2) % NS], S[u]);
+        }
+        wait_vmem_all();  // no copy into the A ring may still be in flight
+        // The stages loaded past the end are never looked up: this use keeps their registers
+        // allocated until the loads writing them have landed.
+#pragma unroll
+        for (int u = 0; u < NS; u++) B::ready(S[u]);
+      }
+    } else {
+      AC ac;
+      ac.init(a, As, pw, lane, m0);
+      if (run) {
+        ac.copy(0, kt0);
+        ac.copy(SLOT, min(kt0 + 1, last));
+      }
+      if (lora16 || kmask) {
+        wait_vmem_all();  // the staged loads (issued before the copies)
+        if (lora16) lst.commit(a, Ls, p);
+        if (kmask) mst.commit(Ks, p);
+      }
+      lds_barrier();  // tables, LoRA operands
+      if (run) {
+        wait_vmcnt<LA>();  // A(kt0); after it only A(kt0+1)
+        lds_barrier();     // K-step kt0 ready
+        for (int kt = kt0; kt < kt1; kt++) {
+          const int r = kt - kt0;
+          ac.copy(((r + 2) % 3) * SLOT, min(kt + 2, last));
+          wait_vmcnt<LA>();  // A(kt+1); after it only A(kt+2)
+          lds_barrier();
+        }
+        wait_vmem_all();  // no copy into the A ring may still be in flight
+      }
     }
     lds_barrier();  // the A ring is free for the consumers' staged epilogue
   } else {
@@ -1394,7 +1537,7 @@ static int launch_cfg(const GemmArgs& a0, int splits, hipStream_t stream) {
   return splits > 1 ? launch_reduce(a, splits, stream) : MXS_OK;
 }
 
-template <int BM, int BN, int CWM, int CWN, bool BWD, int PW = 4>
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW = 4, int NS = 4>
 static int launch_ws(const GemmArgs& a0, int splits, hipStream_t stream) {
   // the producers' 32-bit offsets (W values and one A tile's bytes below 2^32) and the
   // backward loads' column clamp (at least one load item of output columns); otherwise the
@@ -1414,12 +1557,12 @@ static int launch_ws(const GemmArgs& a0, int splits, hipStream_t stream) {
   static bool lds_set = false;  // idempotent attribute; a benign race between threads
   if (!lds_set) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW>),
+        reinterpret_cast<const void*>(&k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW, NS>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
     lds_set = true;
   }
-  hipLaunchKernelGGL((k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW>), grid, dim3(64 * (4 + PW)), lds,
+  hipLaunchKernelGGL((k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW, NS>), grid, dim3(64 * (4 + PW)), lds,
                      stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
@@ -1442,7 +1585,7 @@ static int launch_by_id(int cfg, const GemmArgs& a, int splits, hipStream_t s) {
     case 8: return launch_ws<128, 128, 2, 2, BWD>(a, splits, s);
     case 9: return launch_ws<256, 96, 4, 1, BWD>(a, splits, s);
     case 10: return launch_ws<128, 128, 2, 2, BWD, 8>(a, splits, s);
-    case 11: return launch_ws<256, 96, 4, 1, BWD, 8>(a, splits, s);
+    case 11: return launch_ws<256, 96, 4, 1, BWD, 8, 5>(a, splits, s);
     default: return MXS_ERR_ARG;
   }
 }
