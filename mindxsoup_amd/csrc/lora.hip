@@ -207,7 +207,7 @@ template <> struct ColsVec<8> { typedef u32x4 T; typedef u32x2 MT; };
 // workgroup: blockIdx.x < cb0 is problem p0 (dA), the rest p1 (dB).  Waves take 32-token steps
 // in turn and add their accumulators in LDS.
 template <int CPL>
-constexpr int cols_max_waves() { return CPL >= 4 ? 8 : kMaxWaves; }
+constexpr int cols_max_waves() { return CPL >= 8 ? 8 : CPL >= 4 ? 12 : kMaxWaves; }
 
 template <int CPL>
 __global__ __launch_bounds__(64 * cols_max_waves<CPL>()) void k_lora_cols(ColsProblem p0, ColsProblem p1, int cb0, int M,
