@@ -120,6 +120,29 @@ int mxs_nf4_linear_bwd_dx(const void* dy, int M, int N, int K, const void* packe
                           const void* mask, float mask_scale, void* dx, void* workspace, int cfg,
                           int splits, hipStream_t stream);
 
+/* mxs_nf4_linear_bwd_dx (finished lora_dh) and mxs_lora_grads (dA = dht . drop(x) [r, K],
+ * dB = dY^T . ht^T [N, r], fp32) in one launch where they fit the GPU together: the gradient
+ * workgroups need nothing the dX tiles write and run on the CUs the tiles leave idle.  This is
+ * the whole backward of a projection after dHs, i.e. NF4LinearFunction.backward
+ * (solution/linear4bit.py:51-57) plus the input and weight gradients autograd takes through
+ * peft's LoRA branch (solution/attention.py:197-199, solution/dropout.py:62-69).  Where the
+ * planned dX kernel cannot take the extra workgroups (split-K, or the GPU already full) it
+ * makes the same two launches as the separate entry points; results are the same either way.
+ * lora_dh [M, r] and dht [r, ldt] are the outputs of one mxs_lora_dh call without a workspace;
+ * ht is the forward's transposed Hs.  All outputs are required. */
+int mxs_nf4_linear_bwd_dx_grads(const void* dy, int M, int N, int K, const void* packed,
+                                const void* absmax8, const float* code, const float* absmax2,
+                                const float* offset, const void* lora_dh, const void* lora_at,
+                                int r, const void* mask, float mask_scale, const void* dht,
+                                const void* ht, int ldt, const void* x, float* da, float* db,
+                                void* dx, void* workspace, hipStream_t stream);
+
+/* 1 when mxs_nf4_linear_bwd_dx_grads makes one launch for this shape (projection in_features K,
+ * out_features N, M tokens, rank r) on the current device, else 0.  A caller picks the dHs
+ * kernel by it: one finished launch (mxs_lora_dh) for the fused path, slice partials
+ * (mxs_lora_dh_partials + mxs_nf4_linear_bwd_dx_hp) otherwise. */
+int mxs_nf4_linear_bwd_grads_fused(int M, int N, int K, int r);
+
 /* mxs_nf4_linear_fwd with the LoRA activations given as fp32 partial sums (from
  * mxs_lora_h_partials) instead of lora_h: lora_hp [hp_slices][ldt][r] (1 <= hp_slices <= 4,
  * ldt >= M, ldt % 8 == 0), already times s.  The GEMM adds the slices in order, rounds to fp16

@@ -25,14 +25,13 @@
 //   The forward rows kernel also writes lora_A^T [K, r] and lora_B^T [r, N] for the backward
 //     (the dX epilogue's operand and the dHs kernel's operand), spread over its workgroups.
 #include "common.h"
+#include "lora_cols.h"
 #include "mxs_nf4.h"
 
 namespace mxs {
 
-constexpr int kMaxWaves = 16;        // waves per workgroup (1024 threads)
 constexpr int kMaxRB = 8;            // r <= 128 (r / 16 accumulator blocks)
 constexpr int kChunksInFlight = 4;   // 32-wide reduction chunks loaded per rows-kernel iteration
-constexpr int kColsLds = 64 * 1024;  // LDS budget for the cross-wave sums (bytes)
 
 __device__ __forceinline__ half8_t drop8(half8_t x, u32x2 keep, float scale) {
 #pragma unroll
@@ -188,114 +187,14 @@ __global__ __launch_bounds__(64) void k_lora_rows_finish(RowsArgs a, int slices)
   }
 }
 
-struct ColsProblem {
-  const _Float16* PT;     // [r, ldt] (transposed LoRA activations, zeros past M)
-  const _Float16* Q;      // [M, Nq] row-major
-  const uint8_t* mask;    // [M, Nq] keep mask or null
-  float mscale;
-  int Nq;
-  float* out;             // [r, Nq] (out_rn) or [Nq, r]
-  int out_rn;
-};
 
-template <int CPL> struct ColsVec;
-template <> struct ColsVec<2> { typedef uint32_t T; typedef uint16_t MT; };
-template <> struct ColsVec<4> { typedef u32x2 T; typedef uint32_t MT; };
-template <> struct ColsVec<8> { typedef u32x4 T; typedef u32x2 MT; };
 
-// out[j][n] = sum_m PT[j][m] * Q[m][n] over all tokens, for the 16*CPL columns of this
-// workgroup: blockIdx.x < cb0 is problem p0 (dA), the rest p1 (dB).  Waves take 32-token steps
-// in turn and add their accumulators in LDS.
-template <int CPL>
-constexpr int cols_max_waves() { return CPL >= 8 ? 8 : CPL >= 4 ? 12 : kMaxWaves; }
 
 template <int CPL>
 __global__ __launch_bounds__(64 * cols_max_waves<CPL>()) void k_lora_cols(ColsProblem p0, ColsProblem p1, int cb0, int M,
                                                    int ldt, int r) {
-  typedef typename ColsVec<CPL>::T VT;
-  typedef typename ColsVec<CPL>::MT MT;
-  constexpr int WC = 16 * CPL;  // columns per workgroup
-  extern __shared__ float red[];  // [waves][r][WC + 1]
-  const bool second = (int)blockIdx.x >= cb0;
-  const ColsProblem a = second ? p1 : p0;
-  const int nb = (second ? (int)blockIdx.x - cb0 : (int)blockIdx.x) * WC;
-  const int nw = blockDim.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int ln = lane & 15;  // columns nb + CPL*ln .. +CPL
-  const int lg = lane >> 4;  // tokens t0 + 8*lg .. +8
-  const int col = nb + CPL * ln;
-  const bool col_ok = col < a.Nq;
-  const int ld = WC + 1;
-  // U token blocks of 32 per batch, all loaded before any is multiplied (one memory round trip
-  // per batch instead of one per block)
-  constexpr int U = CPL == 8 ? 2 : 3;
-  for (int b = 0; b < (r >> 4); b++) {  // r-blocks of 16 (the input is re-read per block)
-    float4_t acc[CPL];
-#pragma unroll
-    for (int c = 0; c < CPL; c++) acc[c] = (float4_t){0.f, 0.f, 0.f, 0.f};
-    for (int t0 = wave * 32; t0 < M; t0 += nw * 32 * U) {
-      half8_t av[U];
-      VT rows[U][8];
-      MT mks[U][8];
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const int mb = t0 + u * nw * 32 + 8 * lg;
-        av[u] = (half8_t){};
-        if (mb < ldt)
-          av[u] = *reinterpret_cast<const half8_t*>(a.PT + (int64_t)(16 * b + ln) * ldt + mb);
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const int m = mb + e;
-          rows[u][e] = VT{};
-          mks[u][e] = MT{};
-          if (m < M && col_ok) {
-            rows[u][e] = *reinterpret_cast<const VT*>(a.Q + (int64_t)m * a.Nq + col);
-            if (a.mask) mks[u][e] = *reinterpret_cast<const MT*>(a.mask + (int64_t)m * a.Nq + col);
-          }
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        _Float16 hv[8][CPL];
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          __builtin_memcpy(hv[e], &rows[u][e], sizeof(VT));
-          if (a.mask) {
-#pragma unroll
-            for (int c = 0; c < CPL; c++) {
-              uint32_t kb;
-              if constexpr (CPL == 8) kb = (mks[u][e][c >> 2] >> (8 * (c & 3))) & 0xFFu;
-              else kb = ((uint32_t)mks[u][e] >> (8 * c)) & 0xFFu;
-              hv[e][c] = kb ? (_Float16)((float)hv[e][c] * a.mscale) : (_Float16)0.0f;
-            }
-          }
-        }
-#pragma unroll
-        for (int c = 0; c < CPL; c++) {
-          half8_t bv;
-#pragma unroll
-          for (int e = 0; e < 8; e++) bv[e] = hv[e][c];
-          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[u], bv, acc[c], 0, 0, 0);
-        }
-      }
-    }
-    // acc[c][v] = C[j = 16*b + 4*lg + v][column nb + CPL*ln + c]
-#pragma unroll
-    for (int c = 0; c < CPL; c++)
-#pragma unroll
-      for (int v = 0; v < 4; v++)
-        red[(wave * r + 16 * b + 4 * lg + v) * ld + CPL * ln + c] = acc[c][v];
-  }
-  __syncthreads();
-  for (int i = threadIdx.x; i < r * WC; i += blockDim.x) {
-    const int j = i / WC, n = nb + i % WC;
-    if (n >= a.Nq) continue;
-    float sum = 0.f;
-    for (int w = 0; w < nw; w++) sum += red[(w * r + j) * ld + i % WC];
-    if (a.out_rn) a.out[(int64_t)j * a.Nq + n] = sum;
-    else a.out[(int64_t)n * r + j] = sum;
-  }
+  extern __shared__ float red[];  // [waves][r][16 * CPL + 1]
+  lora_cols_block<CPL>(p0, p1, cb0, M, ldt, r, (int)blockIdx.x, (int)blockDim.x >> 6, red);
 }
 
 // dst[0, n) = 0 (a kernel, not hipMemsetAsync, so that the call can be captured in a graph).
@@ -361,10 +260,8 @@ static int cols_launch_t(const ColsProblem& p0, const ColsProblem& p1, int nprob
                          int r, hipStream_t stream) {
   constexpr int WC = 16 * CPL;
   const int cb0 = (p0.Nq + WC - 1) / WC, cb1 = nprob > 1 ? (p1.Nq + WC - 1) / WC : 0;
-  int nw = waves_for((M + 31) / 32);
-  if (nw > cols_max_waves<CPL>()) nw = cols_max_waves<CPL>();
+  const int nw = cols_waves(M, r, CPL, cols_max_waves<CPL>());
   const int per_wave = r * (WC + 1) * (int)sizeof(float);
-  while (nw > 1 && nw * per_wave > kColsLds) nw--;
   if (nw * per_wave > kColsLds) return MXS_ERR_SIZE;
   hipLaunchKernelGGL(k_lora_cols<CPL>, dim3(cb0 + cb1), dim3(64 * nw), (size_t)nw * per_wave,
                      stream, p0, p1, cb0, M, ldt, r);
@@ -375,9 +272,9 @@ static int cols_launch_t(const ColsProblem& p0, const ColsProblem& p1, int nprob
 // widest that still gives the launch enough workgroups.
 static int cols_launch(const ColsProblem& p0, const ColsProblem& p1, int nprob, int M, int ldt,
                        int r, hipStream_t stream) {
-  const int n_tot = p0.Nq + (nprob > 1 ? p1.Nq : 0);
-  if (n_tot / 128 >= 160) return cols_launch_t<8>(p0, p1, nprob, M, ldt, r, stream);
-  if (n_tot / 64 >= 96) return cols_launch_t<4>(p0, p1, nprob, M, ldt, r, stream);
+  const int cpl = cols_cpl(p0.Nq + (nprob > 1 ? p1.Nq : 0));
+  if (cpl == 8) return cols_launch_t<8>(p0, p1, nprob, M, ldt, r, stream);
+  if (cpl == 4) return cols_launch_t<4>(p0, p1, nprob, M, ldt, r, stream);
   return cols_launch_t<2>(p0, p1, nprob, M, ldt, r, stream);
 }
 

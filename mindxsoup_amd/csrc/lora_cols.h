@@ -1,0 +1,140 @@
+// LoRA gradient columns (dA = dHs^T . drop(X), dB = dY^T . Hs) for one workgroup: the body of
+// the cols kernel in lora.hip, also run by extra workgroups of the backward GEMM launch
+// (nf4_gemm.hip), which then computes dX and both gradients in one launch.
+#pragma once
+
+#include "common.h"
+
+namespace mxs {
+
+constexpr int kMaxWaves = 16;        // waves per workgroup (1024 threads)
+constexpr int kColsLds = 64 * 1024;  // LDS budget for the cross-wave sums (bytes)
+
+// Columns per lane for n_tot gradient columns: the widest that still gives the launch enough
+// workgroups.
+inline int cols_cpl(int n_tot) { return n_tot / 128 >= 160 ? 8 : n_tot / 64 >= 96 ? 4 : 2; }
+
+// Most waves a gradient workgroup of CPL columns per lane uses (register budget).
+template <int CPL>
+constexpr int cols_max_waves() { return CPL >= 8 ? 8 : CPL >= 4 ? 12 : kMaxWaves; }
+
+// Waves that share a gradient workgroup's tokens: about three 32-token steps each, 4 to
+// max_waves, and their cross-wave sums within the LDS budget.  The split of the tokens over
+// waves sets the summation order, so every launch of these columns uses this rule.
+inline int cols_waves(int M, int r, int cpl, int max_waves) {
+  int w = ((M + 31) / 32 + 2) / 3;
+  w = w < 4 ? 4 : w > max_waves ? max_waves : w;
+  const int per_wave = r * (16 * cpl + 1) * (int)sizeof(float);
+  while (w > 1 && w * per_wave > kColsLds) w--;
+  return w;
+}
+
+struct ColsProblem {
+  const _Float16* PT;     // [r, ldt] (transposed LoRA activations, zeros past M)
+  const _Float16* Q;      // [M, Nq] row-major
+  const uint8_t* mask;    // [M, Nq] keep mask or null
+  float mscale;
+  int Nq;
+  float* out;             // [r, Nq] (out_rn) or [Nq, r]
+  int out_rn;
+};
+
+template <int CPL> struct ColsVec;
+template <> struct ColsVec<2> { typedef uint32_t T; typedef uint16_t MT; };
+template <> struct ColsVec<4> { typedef u32x2 T; typedef uint32_t MT; };
+template <> struct ColsVec<8> { typedef u32x4 T; typedef u32x2 MT; };
+
+// out[j][n] = sum_m PT[j][m] * Q[m][n] over all tokens, for the 16*CPL columns of workgroup
+// `block`: block < cb0 is problem p0 (dA), the rest p1 (dB).  The first nw waves (at most
+// blockDim.x / 64) take 32-token steps in turn and add their accumulators in LDS (`red`,
+// [nw][r][16*CPL + 1] floats) in wave order; further waves only help store.  Every thread of
+// the workgroup calls it (it synchronizes the workgroup once).
+template <int CPL>
+__device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const ColsProblem& p1,
+                                                int cb0, int M, int ldt, int r, int block,
+                                                int nw, float* red) {
+  typedef typename ColsVec<CPL>::T VT;
+  typedef typename ColsVec<CPL>::MT MT;
+  constexpr int WC = 16 * CPL;  // columns per workgroup
+  const bool second = block >= cb0;
+  const ColsProblem a = second ? p1 : p0;
+  const int nb = (second ? block - cb0 : block) * WC;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int ln = lane & 15;  // columns nb + CPL*ln .. +CPL
+  const int lg = lane >> 4;  // tokens t0 + 8*lg .. +8
+  const int col = nb + CPL * ln;
+  const bool col_ok = col < a.Nq;
+  const int ld = WC + 1;
+  // U token blocks of 32 per batch, all loaded before any is multiplied (one memory round trip
+  // per batch instead of one per block)
+  constexpr int U = CPL == 8 ? 2 : 3;
+  for (int b = 0; wave < nw && b < (r >> 4); b++) {  // r-blocks of 16 (input re-read per block)
+    float4_t acc[CPL];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) acc[c] = (float4_t){0.f, 0.f, 0.f, 0.f};
+    for (int t0 = wave * 32; t0 < M; t0 += nw * 32 * U) {
+      half8_t av[U];
+      VT rows[U][8];
+      MT mks[U][8];
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        const int mb = t0 + u * nw * 32 + 8 * lg;
+        av[u] = (half8_t){};
+        if (mb < ldt)
+          av[u] = *reinterpret_cast<const half8_t*>(a.PT + (int64_t)(16 * b + ln) * ldt + mb);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const int m = mb + e;
+          rows[u][e] = VT{};
+          mks[u][e] = MT{};
+          if (m < M && col_ok) {
+            rows[u][e] = *reinterpret_cast<const VT*>(a.Q + (int64_t)m * a.Nq + col);
+            if (a.mask) mks[u][e] = *reinterpret_cast<const MT*>(a.mask + (int64_t)m * a.Nq + col);
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; u++) {
+        _Float16 hv[8][CPL];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          __builtin_memcpy(hv[e], &rows[u][e], sizeof(VT));
+          if (a.mask) {
+#pragma unroll
+            for (int c = 0; c < CPL; c++) {
+              uint32_t kb;
+              if constexpr (CPL == 8) kb = (mks[u][e][c >> 2] >> (8 * (c & 3))) & 0xFFu;
+              else kb = ((uint32_t)mks[u][e] >> (8 * c)) & 0xFFu;
+              hv[e][c] = kb ? (_Float16)((float)hv[e][c] * a.mscale) : (_Float16)0.0f;
+            }
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < CPL; c++) {
+          half8_t bv;
+#pragma unroll
+          for (int e = 0; e < 8; e++) bv[e] = hv[e][c];
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[u], bv, acc[c], 0, 0, 0);
+        }
+      }
+    }
+    // acc[c][v] = C[j = 16*b + 4*lg + v][column nb + CPL*ln + c]
+#pragma unroll
+    for (int c = 0; c < CPL; c++)
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+        red[(wave * r + 16 * b + 4 * lg + v) * ld + CPL * ln + c] = acc[c][v];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < r * WC; i += blockDim.x) {
+    const int j = i / WC, n = nb + i % WC;
+    if (n >= a.Nq) continue;
+    float sum = 0.f;
+    for (int w = 0; w < nw; w++) sum += red[(w * r + j) * ld + i % WC];
+    if (a.out_rn) a.out[(int64_t)j * a.Nq + n] = sum;
+    else a.out[(int64_t)n * r + j] = sum;
+  }
+}
+
+}  // namespace mxs

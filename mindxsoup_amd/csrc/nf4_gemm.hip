@@ -20,6 +20,7 @@
 #include <type_traits>
 
 #include "common.h"
+#include "lora_cols.h"
 #include "mxs_nf4.h"
 
 namespace mxs {
@@ -53,7 +54,15 @@ struct GemmArgs {
   int64_t ldc;
   float* ws;                // split-K partials [splits, M, Nc]
   int steps_per_split;
+  // backward: the LoRA gradients dA (cp0) and dB (cp1), computed by cols_blocks extra
+  // workgroups of the same launch in grid rows past the GEMM's (0: none).  They depend on
+  // nothing the GEMM tiles write, so they run on the CUs the tiles leave idle.
+  ColsProblem cp0, cp1;
+  int cols_blocks, cols_cb0, cols_ldt, cols_nw;  // cols_nw: waves summing (cols_waves)
 };
+
+// Columns per lane of the gradient workgroups inside the backward GEMM launch.
+constexpr int kFusedColsCPL = 2;
 
 
 // LDS offset (in halfs) of 16-byte segment `seg` (0..7) of row `row` in a [rows][64] tile.
@@ -1332,6 +1341,20 @@ __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
   __shared__ float2_t s_pair[256];
   __shared__ float s_code[256];
 
+  if constexpr (BWD && BM == 128) {
+    // grid rows past the GEMM's: LoRA gradient workgroups (before any barrier of the tiles).
+    // Only the 128-row tiles take them (the plans that leave CUs idle); compiling the branch
+    // into the others would only change their register allocation.
+    const int gy = (a.M + BM - 1) / BM;
+    if ((int)blockIdx.y >= gy) {
+      const int id = ((int)blockIdx.y - gy) * (int)gridDim.x + (int)blockIdx.x;
+      if (id < a.cols_blocks)
+        lora_cols_block<kFusedColsCPL>(a.cp0, a.cp1, a.cols_cb0, a.M, a.cols_ldt, a.r, id,
+                                       a.cols_nw, reinterpret_cast<float*>(smem));
+      return;
+    }
+  }
+
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int m0 = blockIdx.y * BM;
@@ -1543,15 +1566,23 @@ static int launch_ws(const GemmArgs& a0, int splits, hipStream_t stream) {
   // backward loads' column clamp (at least one load item of output columns); otherwise the
   // all-wave kernel takes the call
   if ((int64_t)a0.Nc * a0.Kr >= (int64_t(1) << 32) || (int64_t)BM * a0.lda * 2 >= (int64_t(1) << 32) ||
-      (BWD && a0.Nc < (PW == 8 ? 16 : 32)))
+      (BWD && a0.Nc < (PW == 8 ? 16 : 32))) {
+    if (a0.cols_blocks > 0) return MXS_ERR_ARG;  // the all-wave kernel runs no gradient rows
     return launch_cfg<64, 128, 1, 4, BWD>(a0, splits, stream);
+  }
   GemmArgs a = a0;
   const int n_steps = a.Kr / kBK;
   if (splits < 1) splits = 1;
   if (splits > n_steps) splits = n_steps > 0 ? n_steps : 1;
   a.steps_per_split = (n_steps + splits - 1) / splits;
   splits = n_steps > 0 ? (n_steps + a.steps_per_split - 1) / a.steps_per_split : 1;
-  const dim3 grid((a.Nc + BN - 1) / BN, (a.M + BM - 1) / BM, splits);
+  const int gx = (a.Nc + BN - 1) / BN;
+  int gy = (a.M + BM - 1) / BM;
+  if (a.cols_blocks > 0) {  // gradient workgroups in extra rows (unsplit backward only)
+    if (!BWD || BM != 128 || splits > 1) return MXS_ERR_ARG;
+    gy += (a.cols_blocks + gx - 1) / gx;
+  }
+  const dim3 grid(gx, gy, splits);
   if (splits > 1 && !a.ws) return MXS_ERR_ARG;
   const size_t lds = (size_t)ws_lds_halfs<BM, BN, BWD>() * sizeof(_Float16);
   static bool lds_set = false;  // idempotent attribute; a benign race between threads
@@ -1644,6 +1675,53 @@ static int gemm_entry(bool bwd, const GemmArgs& a, int cfg, int splits, hipStrea
              : launch_by_id<false>(cfg, a, splits, stream);
 }
 
+// Compute units of the current device (queried once per device).
+static int cu_count() {
+  static int counts[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    counts[dev] = n > 0 ? n : -1;
+  }
+  return counts[dev] > 0 ? counts[dev] : 0;
+}
+
+// The backward GEMM of a projection [K -> N] at M tokens and its LoRA gradient workgroups fit
+// one launch: the planned kernel is an unsplit warp-specialized one that takes the problem
+// (none of its fallback conditions holds) and its tiles plus the gradient workgroups fit the
+// CUs at once, so that the gradients run beside the tiles instead of after them.
+static bool grads_fusable(int M, int N, int K, int r, int* cfg_out, int* nw_out) {
+  if (M <= 0 || N <= 0 || K <= 0 || r <= 0 || r > 32 || N % kBK != 0 || K % kBK != 0)
+    return false;
+  // the gradient workgroups sum exactly as mxs_lora_grads' launch does: same columns per lane
+  // and the same waves (which the GEMM's workgroup must have)
+  if (cols_cpl(K + N) != kFusedColsCPL) return false;
+  const int nw = cols_waves(M, r, kFusedColsCPL, cols_max_waves<kFusedColsCPL>());
+  int cfg, sp;
+  choose(M, K, N, &cfg, &sp);
+  if (cfg < 6 || cfg >= kNumCfg || sp != 1) return false;
+  static const int kBM[] = {256, 256, 128, 256, 128, 256};  // cfg 6..11
+  static const int kBN[] = {128, 160, 128, 96, 128, 96};
+  static const int kPW[] = {4, 4, 4, 4, 8, 8};
+  const int bm = kBM[cfg - 6], bn = kBN[cfg - 6], pw = kPW[cfg - 6];
+  if (bm != 128) return false;  // only those kernels carry the gradient rows
+  if (nw > 4 + pw) return false;
+  if ((int64_t)K * N >= (int64_t(1) << 32) || (int64_t)bm * N * 2 >= (int64_t(1) << 32) ||
+      K < (pw == 8 ? 16 : 32))
+    return false;
+  constexpr int WC = 16 * kFusedColsCPL;
+  const int64_t tiles = (int64_t)((K + bn - 1) / bn) * ((M + bm - 1) / bm);
+  const int64_t cols = (K + WC - 1) / WC + (N + WC - 1) / WC;
+  // the gradient workgroups' cross-wave sums fit the kernel's LDS (at least 80 KB)
+  if ((int64_t)nw * r * (WC + 1) * 4 > 80 * 1024) return false;
+  if (tiles + cols > cu_count()) return false;
+  *cfg_out = cfg;
+  *nw_out = nw;
+  return true;
+}
+
 }  // namespace mxs
 
 using namespace mxs;
@@ -1714,6 +1792,75 @@ int mxs_nf4_linear_bwd_dx(const void* dy, int M, int N, int K, const void* packe
   a.ldc = K;
   set_workspace(a, workspace);
   return gemm_entry(true, a, cfg, splits, stream);
+}
+
+int mxs_nf4_linear_bwd_grads_fused(int M, int N, int K, int r) {
+  int cfg, nw;
+  return grads_fusable(M, N, K, r, &cfg, &nw) ? 1 : 0;
+}
+
+int mxs_nf4_linear_bwd_dx_grads(const void* dy, int M, int N, int K, const void* packed,
+                                const void* absmax8, const float* code, const float* absmax2,
+                                const float* offset, const void* lora_dh, const void* lora_at,
+                                int r, const void* mask, float mask_scale, const void* dht,
+                                const void* ht, int ldt, const void* x, float* da, float* db,
+                                void* dx, void* workspace, hipStream_t stream) {
+  if (!lora_dh || !lora_at || !dht || !ht || !x || !da || !db || !dx) return MXS_ERR_ARG;
+  int cfg, nw;
+  if (!grads_fusable(M, N, K, r, &cfg, &nw)) {  // two launches, same results
+    const int e = mxs_nf4_linear_bwd_dx(dy, M, N, K, packed, absmax8, code, absmax2, offset,
+                                        lora_dh, lora_at, r, mask, mask_scale, dx, workspace,
+                                        -1, 1, stream);
+    if (e != MXS_OK) return e;
+    return mxs_lora_grads(dht, ht, ldt, x, dy, M, K, N, r, mask, mask_scale, da, db, workspace,
+                          stream);
+  }
+  // the gradients' argument checks (mxs_lora_grads); the GEMM's follow in gemm_entry
+  if (r % 16 || K % 8 || N % 8 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  if (((uintptr_t)x % 16) || ((uintptr_t)dht % 16) || ((uintptr_t)dy % 16) ||
+      ((uintptr_t)ht % 16) || (mask && ((uintptr_t)mask % 8)))
+    return MXS_ERR_ALIGN;
+  GemmArgs a{};
+  a.A = static_cast<const _Float16*>(dy);
+  a.lda = N;
+  a.packed = static_cast<const uint8_t*>(packed);
+  a.absmax8 = static_cast<const uint8_t*>(absmax8);
+  a.code = code;
+  a.absmax2 = absmax2;
+  a.offset = offset;
+  a.M = M;
+  a.Nc = K;
+  a.Kr = N;
+  a.Kw = K;
+  a.lora_h = static_cast<const _Float16*>(lora_dh);
+  a.lora_w = static_cast<const _Float16*>(lora_at);
+  a.r = r;
+  a.mask = static_cast<const uint8_t*>(mask);
+  a.mask_scale = mask_scale;
+  a.C = static_cast<_Float16*>(dx);
+  a.ldc = K;
+  set_workspace(a, workspace);
+  ColsProblem& pa = a.cp0;  // dA [r, K] = dHs^T . drop(X)
+  pa.PT = static_cast<const _Float16*>(dht);
+  pa.Q = static_cast<const _Float16*>(x);
+  pa.mask = static_cast<const uint8_t*>(mask);
+  pa.mscale = mask_scale;
+  pa.Nq = K;
+  pa.out = da;
+  pa.out_rn = 1;
+  ColsProblem& pb = a.cp1;  // dB [N, r] = dY^T . Hs
+  pb.PT = static_cast<const _Float16*>(ht);
+  pb.Q = static_cast<const _Float16*>(dy);
+  pb.mscale = 1.0f;
+  pb.Nq = N;
+  pb.out = db;
+  pb.out_rn = 0;
+  constexpr int WC = 16 * kFusedColsCPL;
+  a.cols_cb0 = (K + WC - 1) / WC;
+  a.cols_blocks = a.cols_cb0 + (N + WC - 1) / WC;
+  a.cols_ldt = ldt;
+  a.cols_nw = nw;
+  return gemm_entry(true, a, cfg, 1, stream);
 }
 
 int mxs_nf4_linear_fwd_hp(const void* x, int M, int K, int N, const void* packed,

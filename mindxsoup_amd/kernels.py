@@ -123,6 +123,45 @@ def nf4_linear_bwd_dx(dy2d, packed, state, lora_dh=None, lora_a=None, mask=None,
     return dx
 
 
+def bwd_grads_fused(M, N, K, r):
+    """True when nf4_linear_bwd_dx_grads computes dX and both LoRA gradients in one launch for a
+    projection K -> N at M tokens (decided by the library's tile plan and the device's CUs)."""
+    return bool(_lib.lib().mxs_nf4_linear_bwd_grads_fused(M, N, K, r))
+
+
+def nf4_linear_bwd_dx_grads(dy2d, packed, state, lora_dh, lora_at, dht, ht, x2d, mask=None,
+                            mask_scale=1.0, ws=None):
+    """(dx, dA, dB): dX = dy2d @ W + mask * mask_scale * (lora_dh @ lora_at^T) fp16 [M, K],
+    dA = dht @ drop(x2d) fp32 [r, K] and dB = dy2d^T @ ht^T fp32 [N, r] -- one launch where
+    bwd_grads_fused says so.  lora_dh [M, r] and dht [r, ldt] come from one lora_dh call without
+    a workspace; ht is the forward's Hs^T."""
+    n, k = state.shape
+    if dy2d.dtype != torch.float16 or dy2d.dim() != 2 or dy2d.shape[1] != n:
+        raise ValueError("dy must be fp16 [M, out_features]")
+    dy2d, x2d = dy2d.contiguous(), x2d.contiguous()
+    M = dy2d.shape[0]
+    r = lora_dh.shape[1]
+    if x2d.shape != (M, k) or lora_dh.shape[0] != M or lora_at.shape != (k, r):
+        raise ValueError("x [M, K], lora_dh [M, r] and lora_at [K, r] disagree")
+    if dht.shape[0] != r or ht.shape != dht.shape or dht.shape[1] < M:
+        raise ValueError("dht and ht must be [r, ldt] with ldt >= M")
+    if mask is not None:
+        if mask.dtype != torch.uint8 or mask.shape != (M, k):
+            raise ValueError("mask must be uint8 [M, K]")
+        mask = mask.contiguous()
+    dev = dy2d.device
+    dx = torch.empty((M, k), dtype=torch.float16, device=dev)
+    da = torch.empty((r, k), dtype=torch.float32, device=dev)
+    db = torch.empty((n, r), dtype=torch.float32, device=dev)
+    ws = _ws(M, k, n, dev, -1, 1, ws)
+    _lib.call("mxs_nf4_linear_bwd_dx_grads", _lib.ptr(dy2d), M, n, k, *_nf4_args(packed, state),
+              _lib.ptr(lora_dh.contiguous()), _lib.ptr(lora_at.contiguous()), r, _lib.ptr(mask),
+              float(mask_scale), _lib.ptr(dht.contiguous()), _lib.ptr(ht.contiguous()),
+              dht.shape[1], _lib.ptr(x2d), _lib.ptr(da), _lib.ptr(db), _lib.ptr(dx),
+              _lib.ptr(ws), _lib.stream_of(dev))
+    return dx, da, db
+
+
 def lora_slices(M, Kr):
     """Reduction slices the partial-sum LoRA kernels use (1..4)."""
     return int(_lib.lib().mxs_lora_slices(M, Kr))
@@ -272,9 +311,11 @@ def lora_h(x2d, lora_a, s, mask=None, mask_scale=1.0, ws=None, n_out=None, want_
     return (h, ht, at, bt) if want_at else (h, ht)
 
 
-def lora_dh(dy2d, lora_b, s, ws=None, k_in=None, lora_bt=None):
+def lora_dh(dy2d, lora_b, s, ws=None, k_in=None, lora_bt=None, one_launch=False):
     """(dh, dht): dh = fp16(s * dY @ B) [M, r] and its transpose [r, ldt].  The kernel takes
-    lora_B transposed ([r, N], the bt output of lora_h); given only lora_b it is transposed here."""
+    lora_B transposed ([r, N], the bt output of lora_h); given only lora_b it is transposed here.
+    one_launch: no workspace, so the whole reduction stays in one launch (long reductions are
+    otherwise split over slices of workgroups and finished by a second launch)."""
     dy2d = dy2d.contiguous()
     M, N = dy2d.shape
     if lora_bt is None:
@@ -282,7 +323,8 @@ def lora_dh(dy2d, lora_b, s, ws=None, k_in=None, lora_bt=None):
     r = lora_bt.shape[0]
     if lora_bt.shape != (r, N):
         raise ValueError("lora_bt must be [r, N]")
-    ws = _workspace(lora_workspace_bytes(M, k_in or N, N, r), dy2d.device, ws)
+    ws = None if one_launch else _workspace(lora_workspace_bytes(M, k_in or N, N, r),
+                                            dy2d.device, ws)
     dh = torch.empty((M, r), dtype=torch.float16, device=dy2d.device)
     dht = torch.empty((r, _ldt(M)), dtype=torch.float16, device=dy2d.device)
     _lib.call("mxs_lora_dh", _lib.ptr(dy2d), M, N, _lib.ptr(lora_bt.contiguous()), r, float(s),

@@ -80,12 +80,21 @@ class NF4LinearFunction(torch.autograd.Function):
 
 def lora_backward(dy, x2d, keep, ht, at, bt, packed, state, mask_scale, s, want_x=True,
                   want_a=True, want_b=True, ws=None):
-    """(dX, dA, dB) of one NF4 + LoRA projection (None where not wanted), on the current stream:
-    dHs = s * dY B as slice partials, the fused dX GEMM (which finishes dHs and writes dHs^T),
-    then dA and dB in one launch.  (A variant that ran the weight gradients on a second stream
-    beside the GEMM lost more to the cross-queue waits of the graph, 5-10 us per fork and join,
-    than it gained.)  `ws`: an optional workspace for every call of this projection
+    """(dX, dA, dB) of one NF4 + LoRA projection (None where not wanted), on the current stream.
+    Where the dX GEMM leaves CUs idle (kernels.bwd_grads_fused: 1536-wide projections at 1024
+    tokens) and all three are wanted: dHs = s * dY B finished in one launch, then one launch for
+    dX and both weight gradients (their workgroups run beside the dX tiles).  Otherwise dHs as
+    slice partials, the fused dX GEMM (which finishes dHs and writes dHs^T), then dA and dB in
+    one launch.  (A variant that ran the weight gradients on a second stream beside the GEMM
+    lost more to the cross-queue waits of the graph, 5-10 us per fork and join, than it
+    gained.)  `ws`: an optional workspace for every call of this projection
     (kernels.projection_workspace_bytes)."""
+    M, N = dy.shape
+    K, r = x2d.shape[1], bt.shape[0]
+    if want_x and want_a and want_b and kernels.bwd_grads_fused(M, N, K, r):
+        dh, dht = kernels.lora_dh(dy, None, s, lora_bt=bt, one_launch=True)
+        return kernels.nf4_linear_bwd_dx_grads(dy, packed, state, dh, at, dht, ht, x2d, keep,
+                                               mask_scale, ws=ws)
     dhp = kernels.lora_dh_partials(dy, bt, s)
     want_g = want_a or want_b
     dx = dht = None

@@ -297,9 +297,49 @@ def test_lora_finish_and_backward_sequence(cuda, n, k, M):
     assert torch.equal(outT, dht1)
     assert torch.equal(out, dht1[:, :M].t().contiguous())
     da1, db1 = kernels.lora_grads(dht1, ht, x, dy, keep, ms)
+    if kernels.bwd_grads_fused(M, n, k, 16):
+        # the one-launch backward: dHs finished in one launch, then dX and the gradients
+        dh, dht1 = kernels.lora_dh(dy, None, s, lora_bt=bt, one_launch=True)
+        dx1 = kernels.nf4_linear_bwd_dx(dy, packed, st, dh, None, keep, ms, lora_at=at)
+        da1, db1 = kernels.lora_grads(dht1, ht, x, dy, keep, ms)
     dx2, da2, db2 = lora_backward(dy, x, keep, ht, at, bt, packed, st, ms, s)
     torch.cuda.synchronize()
     assert torch.equal(dx2, dx1) and torch.equal(da2, da1) and torch.equal(db2, db1)
+
+
+@pytest.mark.parametrize("n,k,M", [(1536, 1536, 1024), (256, 1536, 1024), (1536, 1536, 300),
+                                   (256, 1536, 37), (8960, 1536, 1024), (1536, 8960, 512)])
+def test_bwd_dx_grads_one_launch(cuda, n, k, M):
+    """mxs_nf4_linear_bwd_dx_grads equals mxs_nf4_linear_bwd_dx followed by mxs_lora_grads bit
+    for bit, whether it fuses them (1536-wide projections) or not, and its gradients match the
+    float64 products."""
+    from mindxsoup_amd import kernels
+
+    print(f"case bwd_dx_grads n={n} k={k} M={M}", flush=True)
+    layer = _layer(cuda, n, k, 51)
+    st = layer.weight.quant_state
+    packed = layer.weight.data.view(-1, 1)
+    x, a, b, dy, keep = _lora_inputs(cuda, M, k, n, 52)
+    s, ms = 2.0, 1 / 0.95
+    h, ht = kernels.lora_h(x, a, s, keep, ms)
+    at = a.t().contiguous()
+    bt = b.t().contiguous()
+    dh, dht = kernels.lora_dh(dy, None, s, lora_bt=bt, one_launch=True)
+    fused = kernels.bwd_grads_fused(M, n, k, 16)
+    if (n, k, M) == (1536, 1536, 1024) or (n, k, M) == (256, 1536, 1024):
+        assert fused, "the 1536-wide projections fuse at 1024 tokens"
+    if n == 8960:
+        assert not fused, "a split-K dX plan does not take the gradient workgroups"
+    dx, da, db = kernels.nf4_linear_bwd_dx_grads(dy, packed, st, dh, at, dht, ht, x, keep, ms)
+    dx1 = kernels.nf4_linear_bwd_dx(dy, packed, st, dh, None, keep, ms, lora_at=at)
+    da1, db1 = kernels.lora_grads(dht, ht, x, dy, keep, ms)
+    torch.cuda.synchronize()
+    assert torch.equal(dx, dx1)
+    assert torch.equal(da, da1) and torch.equal(db, db1)
+    # dA = dHs^T drop(x), dB = dY^T Hs in float64 from the same fp16 operands (oracle dropout)
+    xd = O.dropout_fp16(_np(x).astype(np.float16), keep.cpu().numpy(), 0.05).astype(np.float64)
+    assert O.max_rel(_np(da), _np(dht[:, :M]).astype(np.float64) @ xd) < TOL
+    assert O.max_rel(_np(db), _np(dy).astype(np.float64).T @ _np(h).astype(np.float64)) < TOL
 
 
 def test_backward_sequence_replays_in_a_graph(cuda):
