@@ -229,6 +229,19 @@ int mxs_lora_grads(const void* dht, const void* ht, int ldt, const void* x, cons
                    int K, int N, int r, const void* mask, float mask_scale, float* da, float* db,
                    void* workspace, hipStream_t stream);
 
+/* ---- SwiGLU of the fp16 MLP (solution/mlp.py:35-44 calls it between the projections) ------
+ * fp32 arithmetic on fp16 inputs, rounded to fp16 once; sigmoid(g) = 1 / (1 + exp(-g)).
+ * n = number of elements of contiguous fp16 buffers (any n; 16-byte aligned buffers take the
+ * vector path). */
+
+/* out = silu(gate) * up: silu_mul_kernel's forward (solution/silu_mul.py:26-44, called by
+ * SiluMulInPlace.forward :56-63). */
+int mxs_silu_mul(const void* gate, const void* up, void* out, int64_t n, hipStream_t stream);
+
+/* In-place backward for the incoming gradient `grad`: gate <- d(gate), up <- d(up), as
+ * SiluMulInPlace.backward (solution/silu_mul.py:65-71) does. */
+int mxs_silu_mul_bwd(const void* grad, void* gate, void* up, int64_t n, hipStream_t stream);
+
 /* dst[cols, rows] = src[rows, cols]^T, fp16 (lora_A -> the [K, r] operand of the backward). */
 int mxs_transpose_f16(const void* src, int rows, int cols, void* dst, hipStream_t stream);
 

@@ -373,3 +373,22 @@ def lora_grad_b(ht, dy2d, ws=None):
     _lib.call("mxs_lora_grad_b", _lib.ptr(ht), ht.shape[1], _lib.ptr(dy2d), M, N, r,
               _lib.ptr(db), _lib.ptr(ws), _lib.stream_of(dy2d.device))
     return db
+
+
+def silu_mul(gate, up):
+    """fp16 silu(gate) * up (contiguous, same shape); one HIP launch."""
+    gate, up = gate.contiguous(), up.contiguous()
+    out = torch.empty_like(gate)
+    _lib.call("mxs_silu_mul", _lib.ptr(gate), _lib.ptr(up), _lib.ptr(out), gate.numel(),
+              _lib.stream_of(gate.device))
+    return out
+
+
+def silu_mul_bwd_(grad, gate, up):
+    """In place: gate <- d(gate), up <- d(up) for the incoming fp16 gradient (gate and up must
+    be contiguous)."""
+    grad = grad.contiguous()
+    if not (gate.is_contiguous() and up.is_contiguous()):
+        raise ValueError("gate and up must be contiguous (their memory takes the gradients)")
+    _lib.call("mxs_silu_mul_bwd", _lib.ptr(grad), _lib.ptr(gate), _lib.ptr(up), gate.numel(),
+              _lib.stream_of(gate.device))

@@ -22,6 +22,12 @@
  *   quantize_nf4 / quantize_absmax_256 / dynamic_map
  *                        - round-trip bounds and the nearest-code property
  *                          (brute force over every candidate code).
+ *   silu_mul / silu_mul_bwd
+ *                        - float64 evaluation of the same formulas (within one
+ *                          fp16 ulp), closed forms at gate = 0 (out = 0,
+ *                          d_up = 0, d_gate = dh * up / 2) and for large |gate|
+ *                          (silu -> gate or 0), and the differently ordered
+ *                          derivative of solution/test_silu_mul.py:13-19.
  *   The GEMM / LoRA references live in oracle/oracle.py (numpy) and are pinned
  *   against float64 torch autograd.
  */
@@ -300,4 +306,34 @@ void oracle_set_num_threads(int n) {
 #else
     (void)n;
 #endif
+}
+
+/* SwiGLU of the fp16 MLP, solution/silu_mul.py:26-44 (silu_mul_kernel): values are computed
+ * in fp32 from the fp16 inputs and rounded to fp16 once.  sigmoid(g) = 1 / (1 + exp(-g)).
+ * Forward: out = fp16(up * (g * sigmoid(g))). */
+static inline float sigmoid_f32(float g) { return 1.0f / (1.0f + expf(-g)); }
+
+void oracle_silu_mul(const uint16_t *gate, const uint16_t *up, uint16_t *out, int64_t n) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; i++) {
+        const float g = oracle_f16_to_f32(gate[i]), u = oracle_f16_to_f32(up[i]);
+        const float s = sigmoid_f32(g);
+        const float silu = g * s;
+        out[i] = oracle_f32_to_f16(u * silu);
+    }
+}
+
+/* Backward (BACKWARD=True branch, silu_mul.py:35-41), for the incoming d(out) = dh:
+ * d(gate) = fp16((dh * up) * (s + silu * (1 - s))), d(up) = fp16(dh * silu). */
+void oracle_silu_mul_bwd(const uint16_t *dh, const uint16_t *gate, const uint16_t *up,
+                         uint16_t *d_gate, uint16_t *d_up, int64_t n) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; i++) {
+        const float g = oracle_f16_to_f32(gate[i]), u = oracle_f16_to_f32(up[i]);
+        const float d = oracle_f16_to_f32(dh[i]);
+        const float s = sigmoid_f32(g);
+        const float silu = g * s;
+        d_gate[i] = oracle_f32_to_f16((d * u) * (s + silu * (1.0f - s)));
+        d_up[i] = oracle_f32_to_f16(d * silu);
+    }
 }

@@ -60,6 +60,8 @@ def lib():
         L.oracle_quantize_absmax_256.argtypes = [P, i64, ctypes.c_float, P, P, P]
         L.oracle_num_threads.restype = ctypes.c_int
         L.oracle_set_num_threads.argtypes = [ctypes.c_int]
+        L.oracle_silu_mul.argtypes = [P, P, P, i64]
+        L.oracle_silu_mul_bwd.argtypes = [P, P, P, P, P, i64]
         _lib = L
     return _lib
 
@@ -246,3 +248,22 @@ def max_rel(got, ref):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-12))
+
+
+def silu_mul(gate_f16, up_f16):
+    """fp16 silu(gate) * up with the kernel's fp32 arithmetic (solution/silu_mul.py:26-44)."""
+    g = np.ascontiguousarray(gate_f16, dtype=np.float16)
+    u = np.ascontiguousarray(up_f16, dtype=np.float16)
+    out = np.empty_like(g)
+    lib().oracle_silu_mul(_ptr(g), _ptr(u), _ptr(out), g.size)
+    return out
+
+
+def silu_mul_bwd(dh_f16, gate_f16, up_f16):
+    """(d_gate, d_up) in fp16 for the incoming fp16 gradient dh (solution/silu_mul.py:35-41)."""
+    d = np.ascontiguousarray(dh_f16, dtype=np.float16)
+    g = np.ascontiguousarray(gate_f16, dtype=np.float16)
+    u = np.ascontiguousarray(up_f16, dtype=np.float16)
+    dg, du = np.empty_like(g), np.empty_like(g)
+    lib().oracle_silu_mul_bwd(_ptr(d), _ptr(g), _ptr(u), _ptr(dg), _ptr(du), g.size)
+    return dg, du

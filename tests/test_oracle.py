@@ -269,3 +269,47 @@ def test_lora_forward_merged_weight_identity():
 
 def test_max_rel_definition():
     assert O.max_rel([1.0, 2.0], [1.0, 4.0]) == pytest.approx(0.5)
+
+
+def _ulp_diff_f16(a, b):
+    """Distance in fp16 ulps (finite values, same-sign ordering by bit pattern)."""
+    ia = a.astype(np.float16).view(np.int16).astype(np.int64)
+    ib = b.astype(np.float16).view(np.int16).astype(np.int64)
+    ia = np.where(ia < 0, -32768 - ia, ia)
+    ib = np.where(ib < 0, -32768 - ib, ib)
+    return np.abs(ia - ib)
+
+
+def test_silu_mul_oracle_against_float64_and_closed_forms():
+    rng = np.random.default_rng(11)
+    n = 50000
+    g = (rng.standard_normal(n) * 3).astype(np.float16)
+    u = (rng.standard_normal(n) * 3).astype(np.float16)
+    d = rng.standard_normal(n).astype(np.float16)
+    out = O.silu_mul(g, u)
+    dg, du = O.silu_mul_bwd(d, g, u)
+    g64, u64, d64 = g.astype(np.float64), u.astype(np.float64), d.astype(np.float64)
+    s = 1.0 / (1.0 + np.exp(-g64))
+    silu = g64 * s
+    # the kernel's fp32 arithmetic lands within one fp16 ulp of the exact value
+    assert _ulp_diff_f16(out, (u64 * silu).astype(np.float16)).max() <= 1
+    assert _ulp_diff_f16(dg, (d64 * u64 * (s + silu * (1 - s))).astype(np.float16)).max() <= 1
+    assert _ulp_diff_f16(du, (d64 * silu).astype(np.float16)).max() <= 1
+    # gate = 0: sigmoid = 1/2, silu = 0
+    z = np.zeros(8, np.float16)
+    uu = np.array([1, -2, 3.5, 0.25, 100, -7, 2048, 1e-3], np.float16)
+    dd = np.array([2, 2, -1, 4, 0.5, 1, 1, 8], np.float16)
+    assert np.all(O.silu_mul(z, uu) == 0)
+    dgz, duz = O.silu_mul_bwd(dd, z, uu)
+    assert np.all(duz == 0)
+    assert np.array_equal(dgz, (dd.astype(np.float32) * uu.astype(np.float32) * 0.5).astype(np.float16))
+    # large |gate|: silu -> gate (sigmoid -> 1) and -> 0 (sigmoid -> 0)
+    big = np.array([30, 60, 1000], np.float16)
+    one = np.ones(3, np.float16)
+    assert np.array_equal(O.silu_mul(big, one), big)
+    assert np.all(np.abs(O.silu_mul(-big, one).astype(np.float32)) < 1e-6)
+    # the derivative in the order of solution/test_silu_mul.py:13-19 (d*u*s*(1 + g*(1-s)))
+    g32, u32, d32 = g.astype(np.float32), u.astype(np.float32), d.astype(np.float32)
+    s32 = (1.0 / (1.0 + np.exp(-g32))).astype(np.float32)
+    alt_dg = (d32 * u32 * s32 * (1 + g32 * (1 - s32))).astype(np.float16).astype(np.float32)
+    assert np.allclose(dg.astype(np.float32), alt_dg, atol=1e-3, rtol=1e-3)

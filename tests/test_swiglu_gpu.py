@@ -1,0 +1,95 @@
+"""SwiGLU of the fp16 MLP (mindxsoup_amd/silu_mul.py on csrc/swiglu.hip) against the oracle's
+restatement of solution/silu_mul.py, with the reference test's shapes and tolerance
+(solution/test_silu_mul.py:22-40: atol = rtol = 1e-3, i.e. about one fp16 ulp)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def cuda():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a GPU")
+    return torch.device("cuda:0")
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def _close(got, want):
+    g = got.astype(np.float32)
+    w = want.astype(np.float32)
+    assert np.all(np.abs(g - w) <= 1e-3 + 1e-3 * np.abs(w))
+    return float(np.mean(got.view(np.uint16) == want.view(np.uint16)))
+
+
+@pytest.mark.parametrize("shape", [(1, 8960), (37, 8960), (1, 1430, 8960), (5, 1000), (3, 2049)])
+def test_silu_mul_matches_oracle(cuda, shape):
+    from mindxsoup_amd.silu_mul import silu_mul
+
+    print(f"case silu_mul shape={shape}", flush=True)
+    torch.manual_seed(0)
+    gate = (torch.randn(shape, device=cuda) * 3).half().requires_grad_(True)
+    up = (torch.randn(shape, device=cuda) * 3).half().requires_grad_(True)
+    grad = torch.randn(shape, device=cuda).half()
+    want_out = O.silu_mul(_np(gate), _np(up))
+    want_dg, want_du = O.silu_mul_bwd(_np(grad), _np(gate), _np(up))
+    g, u = gate * 1, up * 1  # not leaves, as in the MLP: their memory becomes the gradients
+    out = silu_mul(g, u)
+    assert out.dtype == torch.float16 and out.shape == gate.shape
+    exact = _close(_np(out), want_out)
+    out.backward(grad)
+    exact_g = _close(_np(gate.grad), want_dg)
+    exact_u = _close(_np(up.grad), want_du)
+    # same fp32 formula: only expf's last bit may differ from the C library's
+    assert min(exact, exact_g, exact_u) > 0.99, (exact, exact_g, exact_u)
+
+
+def test_backward_writes_over_gate_and_up(cuda):
+    """The in-place backward: the gradients autograd hands on live in gate's and up's memory."""
+    from mindxsoup_amd.silu_mul import SiluMulInPlace
+
+    torch.manual_seed(2)
+    n, inter = 300, 8960
+    gate = torch.randn(n, inter, device=cuda).half()
+    up = torch.randn(n, inter, device=cuda).half()
+    grad = torch.randn(n, inter, device=cuda).half()
+    want_dg, want_du = O.silu_mul_bwd(_np(grad), _np(gate), _np(up))
+    g = gate.clone().requires_grad_(True)
+    u = up.clone().requires_grad_(True)
+    gi, ui = g * 1, u * 1
+    ptr_g, ptr_u = gi.data_ptr(), ui.data_ptr()
+    seen = {}
+    gi.register_hook(lambda t: seen.__setitem__("g", t.data_ptr()))
+    ui.register_hook(lambda t: seen.__setitem__("u", t.data_ptr()))
+    SiluMulInPlace.apply(gi, ui).backward(grad)
+    assert seen == {"g": ptr_g, "u": ptr_u}
+    _close(_np(g.grad), want_dg)
+    _close(_np(u.grad), want_du)
+
+
+@pytest.mark.parametrize("n,offset", [(7, 0), (1001, 1), (8 * 4096 + 5, 3), (0, 0)])
+def test_silu_mul_unaligned_and_tails(cuda, n, offset):
+    from mindxsoup_amd import kernels
+
+    print(f"case silu_mul tail n={n} offset={offset}", flush=True)
+    torch.manual_seed(3)
+    buf_g = (torch.randn(n + offset, device=cuda) * 4).half()
+    buf_u = (torch.randn(n + offset, device=cuda) * 4).half()
+    buf_d = torch.randn(n + offset, device=cuda).half()
+    g, u, d = buf_g[offset:], buf_u[offset:], buf_d[offset:]
+    out = kernels.silu_mul(g, u)
+    want = O.silu_mul(_np(g), _np(u))
+    want_dg, want_du = O.silu_mul_bwd(_np(d), _np(g), _np(u))
+    kernels.silu_mul_bwd_(d, g, u)
+    torch.cuda.synchronize()
+    if n:
+        _close(_np(out), want)
+        _close(_np(g), want_dg)
+        _close(_np(u), want_du)
