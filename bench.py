@@ -264,6 +264,49 @@ def graph_time(fn, steps, warmup):
     return a.elapsed_time(b) / steps, wall
 
 
+def bench_mlp(dev, g, steps, warmup):
+    """One Qwen2 MLP block (gate, up, down with LoRA r=16, dropout 0.05; SwiGLU) forward +
+    backward through autograd at M = 1024, one HIP graph per step: the SwiGLU fused into the
+    up/down GEMM epilogues (mlp.NF4LoraMLPFunction) against the reference's composition of the
+    three projections and silu_mul (solution/mlp.py:42-44) over the same kernels."""
+    from mindxsoup_amd import mlp as mlp_mod
+    from mindxsoup_amd.linear4bit import Linear4bit, LoraLinear4bit
+
+    layers = []
+    for n, k in ((8960, 1536), (8960, 1536), (1536, 8960)):
+        w = (torch.randn((n, k), device=dev, generator=g) * 0.02).half()
+        m = LoraLinear4bit(Linear4bit.from_weight(w, None), r=RANK, lora_alpha=ALPHA,
+                           lora_dropout=P_DROP)
+        del w
+        with torch.no_grad():
+            m.lora_B["default"].weight.normal_(0.0, 0.01, generator=g)
+        layers.append(m)
+    block = mlp_mod.MLP(*layers).train()
+    x = torch.randn((M_TOKENS, 1536), device=dev, generator=g).half().requires_grad_(True)
+    dy = torch.randn((M_TOKENS, 1536), device=dev, generator=g).half()
+    if not mlp_mod.fused_ok(block, x):
+        raise RuntimeError("the fused MLP path does not take the model's shapes")
+
+    def step():
+        block(x).backward(dy)
+
+    res = {}
+    previous = mlp_mod.FUSED_SWIGLU
+    try:
+        for key, fused in (("unfused_ms", False), ("fused_ms", True)):
+            mlp_mod.FUSED_SWIGLU = fused
+            ms, _ = graph_time(step, steps, warmup)
+            res[key] = round(ms, 4)
+    finally:
+        mlp_mod.FUSED_SWIGLU = previous
+    fl = 2 * proj_flops(8960, 1536) + proj_flops(1536, 8960)
+    res["gflop"] = round(fl / 1e9, 3)
+    res["tflops"] = round(fl / res["fused_ms"] / 1e9, 1)
+    res["saved_ms"] = round(res["unfused_ms"] - res["fused_ms"], 4)
+    del block, layers, x, dy
+    return res
+
+
 def bench_fused(dev, steps, warmup):
     g = torch.Generator(device=dev)
     g.manual_seed(1)
@@ -296,6 +339,7 @@ def bench_fused(dev, steps, warmup):
     out["config4_bwd_down"] = {"ms": round(ms, 4), "gflop": round(fl / 1e9, 3),
                                "tflops": round(fl / ms / 1e9, 1)}
     del down, ht
+    out["mlp_block"] = bench_mlp(dev, g, steps, warmup)
     # config 5: forward + backward of all 28 layers x 7 projections, M = 1024
     layers = []
     for _ in range(LAYERS):

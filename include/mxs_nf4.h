@@ -242,6 +242,35 @@ int mxs_silu_mul(const void* gate, const void* up, void* out, int64_t n, hipStre
  * SiluMulInPlace.backward (solution/silu_mul.py:65-71) does. */
 int mxs_silu_mul_bwd(const void* grad, void* gate, void* up, int64_t n, hipStream_t stream);
 
+/* The up projection's forward with the SwiGLU after it (solution/mlp.py:42-43:
+ * silu_mul(gate_proj(x), up_proj(x))): mxs_nf4_linear_fwd_hp (lora_hp may be NULL: no LoRA
+ * term) writing y = up_proj(x) [M, N] and h = silu(gate) * y [M, N] from the same tile, with
+ * gate [M, N] the gate projection's output.  gate, y and h are 16-byte aligned, N % 8 == 0.
+ * Only where mxs_nf4_linear_glu_fused(M, N, K, 0) is 1 (else MXS_ERR_SIZE). */
+int mxs_nf4_linear_fwd_glu(const void* x, int M, int K, int N, const void* packed,
+                           const void* absmax8, const float* code, const float* absmax2,
+                           const float* offset, const void* bias, const float* lora_hp,
+                           int hp_slices, int ldt, const void* lora_b, int r, void* lora_ht,
+                           const void* gate, void* y, void* h, void* workspace,
+                           hipStream_t stream);
+
+/* The down projection's input gradient followed by the SwiGLU backward
+ * (SiluMulInPlace.backward, solution/silu_mul.py:65-71): mxs_nf4_linear_bwd_dx_hp whose
+ * output d(hidden) [M, K] is not stored; instead gate and up [M, K] (the forward's saved
+ * tensors) are overwritten with d(gate) and d(up), as the reference's in-place backward does.
+ * lora_dhp may be NULL (no LoRA term).  Only where mxs_nf4_linear_glu_fused(M, N, K, 1) is 1. */
+int mxs_nf4_linear_bwd_dx_glu(const void* dy, int M, int N, int K, const void* packed,
+                              const void* absmax8, const float* code, const float* absmax2,
+                              const float* offset, const float* lora_dhp, int hp_slices, int ldt,
+                              const void* lora_at, int r, const void* mask, float mask_scale,
+                              void* lora_dht, void* gate, void* up, void* workspace,
+                              hipStream_t stream);
+
+/* 1 when the projection [K -> N] at M tokens takes the SwiGLU epilogue in the forward (bwd = 0)
+ * or the backward (bwd = 1) on its planned kernel; else 0 (then run the GEMM and
+ * mxs_silu_mul / mxs_silu_mul_bwd). */
+int mxs_nf4_linear_glu_fused(int M, int N, int K, int bwd);
+
 /* dst[cols, rows] = src[rows, cols]^T, fp16 (lora_A -> the [K, r] operand of the backward). */
 int mxs_transpose_f16(const void* src, int rows, int cols, void* dst, hipStream_t stream);
 

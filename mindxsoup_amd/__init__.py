@@ -21,8 +21,10 @@ FEATURES = {
     "direct_nograd": True,   # no Function.apply wrappers when no graph is recorded (direct.py)
     "nf4_fused_gemm": True,  # dequant fused into the GEMM main loop (else HIP unpack + F.linear)
     "nf4_fused_lora": True,  # LoRA branch fused into the GEMM epilogues (LoraLinear4bit)
+    "mlp_fp16": True,        # Qwen2 MLP on fp16 activations (mlp.py; the SwiGLU of silu_mul.py)
+    "mlp_fused_swiglu": True,  # that MLP's SwiGLU in the up/down GEMM epilogues (LoRA layers)
     # --- reference switches outside the NF4 path (inert here) ------------------------------
-    "startup_cache": False, "example_swiglu": False, "mlp_fp16": False, "adam_host": False,
+    "startup_cache": False, "example_swiglu": False, "adam_host": False,
     "cublas_workspace": None, "fused_layer_input": False, "fused_head_acc": False,
     "lean_draw": False, "mlp_gateup_recompute": False, "mlp_tail": False, "rmsnorm": False,
     "fused_ce": False, "rope": False, "fp16_embedding": False, "head_stream": False,
@@ -42,7 +44,8 @@ FEATURES.update(PROFILES[PROFILE])
 
 
 def apply():
-    """Install the NF4 patches named by FEATURES (solution/__init__.py:113-171, NF4 part)."""
+    """Install the NF4 and fp16-MLP patches named by FEATURES (solution/__init__.py:113-171,
+    those parts)."""
     from . import linear4bit, nf4
 
     direct.enabled = FEATURES["direct_nograd"]
@@ -52,3 +55,8 @@ def apply():
         nf4.patch_bnb_nf4()
         if FEATURES["nf4_direct"]:
             linear4bit.patch_bnb_linear4bit(cache_weights=FEATURES["nf4_cache_fp16"])
+    if FEATURES["mlp_fp16"]:
+        from . import mlp
+
+        mlp.FUSED_SWIGLU = FEATURES["mlp_fused_swiglu"]
+        mlp.patch_qwen2_mlp_fp16()

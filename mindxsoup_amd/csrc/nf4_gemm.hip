@@ -21,6 +21,7 @@
 
 #include "common.h"
 #include "lora_cols.h"
+#include "swiglu.h"
 #include "mxs_nf4.h"
 
 namespace mxs {
@@ -59,6 +60,14 @@ struct GemmArgs {
   // nothing the GEMM tiles write, so they run on the CUs the tiles leave idle.
   ColsProblem cp0, cp1;
   int cols_blocks, cols_cb0, cols_ldt, cols_nw;  // cols_nw: waves summing (cols_waves)
+  // SwiGLU of the MLP applied to the fp16 output tile (buffers [M, ldc] like C):
+  //   glu 1 (up projection forward): C as usual, and glu_h = silu(glu_g) * C;
+  //   glu 2 (down projection backward): the output is d(hidden) and is not stored; glu_g and
+  //   glu_u (gate, up) are read and overwritten with d(gate) and d(up).
+  int glu;
+  _Float16* glu_g;
+  _Float16* glu_u;
+  _Float16* glu_h;
 };
 
 // Columns per lane of the gradient workgroups inside the backward GEMM launch.
@@ -571,9 +580,119 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, float16_t (&a
   }
 }
 
+// SwiGLU output of an unsplit warp-specialized tile (the split ones leave it to the reduce).
+// The epilogue is memory-bound: one tile moves its fp16 output plus one (forward: gate) or two
+// (backward: gate, up) tiles in and one more out, and every workgroup reaches it at about the
+// same time.  So the producer waves, idle once their last copy has landed, issue all their
+// gate/up loads right then (they land while the consumers run the last K-step); the consumers
+// stage their fp16 accumulators, the whole tile at once, in the A ring and leave; the producers
+// then combine and store.  One round trip per workgroup, and none of the consumers' registers.
+//   forward (BWD = false): C = y (the up projection) and h = silu(gate) * y;
+//   backward (BWD = true): the tile is d(hidden); gate <- d(gate), up <- d(up).
+template <int BM, int BN, int CWM, int CWN, int NTP, bool BWD>
+struct GluTail {
+  static constexpr int WM = BM / CWM, WN = BN / CWN, TM = WM / 32, TN = WN / 32;
+  using SS = StagedStore<TM, TN>;
+  static constexpr int CPR = BN / 8;       // 16-byte chunks per tile row
+  static constexpr int NCL = BM * CPR / NTP;  // chunks per producer lane
+  static constexpr int AREA = WM * SS::S16;   // dwords of one consumer wave's staged tile
+  static_assert(BM * CPR % NTP == 0, "the tile's chunks split evenly over the producers");
+  // chunks in flight per lane: all of them where registers allow, else a rolling window
+  static constexpr int AHEAD = NCL < (BWD ? 10 : 20) ? NCL : (BWD ? 10 : 20);
+  u32x4 g[NCL];
+  u32x4 u[BWD ? NCL : 1];
+
+  // chunk k of producer lane p: tile row m, 8-column group cc (a row's chunks on adjacent lanes)
+  __device__ static void chunk(int p, int k, int& m, int& cc) {
+    const int q = p + k * NTP;
+    m = q / CPR;
+    cc = q % CPR;
+  }
+
+  __device__ __forceinline__ void load(const GemmArgs& a, int p, int m0, int n0, int k) {
+    int m, cc;
+    chunk(p, k, m, cc);
+    const int gm = m0 + m, gn = n0 + 8 * cc;
+    g[k] = (u32x4){};
+    if constexpr (BWD) u[k] = (u32x4){};
+    if (gm < a.M && gn < a.Nc) {  // Nc % 8 == 0: whole chunks
+      const int64_t o = (int64_t)gm * a.ldc + gn;
+      g[k] = *reinterpret_cast<const u32x4*>(a.glu_g + o);
+      if constexpr (BWD) u[k] = *reinterpret_cast<const u32x4*>(a.glu_u + o);
+    }
+  }
+
+  // the first AHEAD chunks' gate / up loads (issued before the consumers' tile is staged)
+  __device__ __forceinline__ void prefetch(const GemmArgs& a, int p, int m0, int n0) {
+#pragma unroll
+    for (int k = 0; k < AHEAD; k++) load(a, p, m0, n0, k);
+  }
+
+  // every chunk: staged value, gate / up, SwiGLU, stores; chunk k + AHEAD is loaded once k is done
+  __device__ __forceinline__ void store(const GemmArgs& a, int p, int m0, int n0,
+                                        const uint32_t* staged) {
+#pragma unroll
+    for (int k = 0; k < NCL; k++) {
+      int m, cc;
+      chunk(p, k, m, cc);
+      const int gm = m0 + m, gn = n0 + 8 * cc;
+      if (gm < a.M && gn < a.Nc) {
+        const int w = (m / WM) * CWN + (8 * cc) / WN;  // the consumer wave that staged it
+        const u32x4 v = *reinterpret_cast<const u32x4*>(staged + w * AREA + (m % WM) * SS::S16 +
+                                                          ((8 * cc) % WN) / 2);
+        const int64_t o = (int64_t)gm * a.ldc + gn;
+        const half8_t h = __builtin_bit_cast(half8_t, v);
+        const half8_t gv = __builtin_bit_cast(half8_t, g[k]);
+        if constexpr (BWD) {
+          const half8_t uv = __builtin_bit_cast(half8_t, u[k]);
+          half8_t dg, du;
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            _Float16 x, y;
+            swiglu_bwd((float)h[e], (float)gv[e], (float)uv[e], x, y);
+            dg[e] = x;
+            du[e] = y;
+          }
+          *reinterpret_cast<half8_t*>(a.glu_g + o) = dg;
+          *reinterpret_cast<half8_t*>(a.glu_u + o) = du;
+        } else {
+          half8_t hh;
+#pragma unroll
+          for (int e = 0; e < 8; e++) hh[e] = swiglu_fwd((float)gv[e], (float)h[e]);
+          *reinterpret_cast<u32x4*>(a.C + o) = v;
+          *reinterpret_cast<half8_t*>(a.glu_h + o) = hh;
+        }
+      }
+      if (k + AHEAD < NCL) load(a, p, m0, n0, k + AHEAD);
+    }
+  }
+
+  // a consumer wave's accumulators as fp16, all TM row slices: row r of its tile at r * S16
+  __device__ __forceinline__ static void stage(const float16_t (&acc)[TM][TN], int lane,
+                                               uint32_t* area) {
+    const int lrow = lane & 31, lseg = lane >> 5;
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+      for (int j = 0; j < TN; j++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          u32x2 v;
+          v[0] = pack_f16x2(acc[i][j][4 * q], acc[i][j][4 * q + 1]);
+          v[1] = pack_f16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          *reinterpret_cast<u32x2*>(area + (i * 32 + lrow) * SS::S16 + 16 * j + 4 * q +
+                                    2 * lseg) = v;
+        }
+  }
+};
+
+template <int GLU>
 __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int splits,
                                                       int M, int Nc, _Float16* __restrict__ C,
-                                                      int64_t ldc) {
+                                                      int64_t ldc,
+                                                      _Float16* __restrict__ glu_g,
+                                                      _Float16* __restrict__ glu_u,
+                                                      _Float16* __restrict__ glu_h) {
   const int64_t plane = (int64_t)M * Nc;
   const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (e >= plane) return;
@@ -591,21 +710,63 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
       for (int u = 0; u < 4; u++)
         if (z0 + u < splits) v += p[u];
     }
-    *reinterpret_cast<half4_t*>(C + (int64_t)m * ldc + n) = __builtin_convertvector(v, half4_t);
+    const half4_t h = __builtin_convertvector(v, half4_t);
+    const int64_t o = (int64_t)m * ldc + n;
+    if constexpr (GLU == 2) {  // d(hidden) -> d(gate), d(up) over gate and up (SwiGLU backward)
+      const half4_t g = *reinterpret_cast<const half4_t*>(glu_g + o);
+      const half4_t u = *reinterpret_cast<const half4_t*>(glu_u + o);
+      half4_t dg, du;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        _Float16 x, y;
+        swiglu_bwd((float)h[q], (float)g[q], (float)u[q], x, y);
+        dg[q] = x;
+        du[q] = y;
+      }
+      *reinterpret_cast<half4_t*>(glu_g + o) = dg;
+      *reinterpret_cast<half4_t*>(glu_u + o) = du;
+      return;
+    }
+    *reinterpret_cast<half4_t*>(C + o) = h;
+    if constexpr (GLU == 1) {  // silu(gate) * up beside the up projection's output
+      const half4_t g = *reinterpret_cast<const half4_t*>(glu_g + o);
+      half4_t hh;
+#pragma unroll
+      for (int q = 0; q < 4; q++) hh[q] = swiglu_fwd((float)g[q], (float)h[q]);
+      *reinterpret_cast<half4_t*>(glu_h + o) = hh;
+    }
   } else {
     for (int q = 0; q < 4 && e + q < plane; q++) {
       const int mq = (int)((e + q) / Nc), nq = (int)((e + q) % Nc);
       float v = ws[e + q];
       for (int z = 1; z < splits; z++) v += ws[z * plane + e + q];
-      C[(int64_t)mq * ldc + nq] = (_Float16)v;
+      const _Float16 h = (_Float16)v;
+      const int64_t o = (int64_t)mq * ldc + nq;
+      if constexpr (GLU == 2) {
+        _Float16 x, y;
+        swiglu_bwd((float)h, (float)glu_g[o], (float)glu_u[o], x, y);
+        glu_g[o] = x;
+        glu_u[o] = y;
+        continue;
+      }
+      C[o] = h;
+      if constexpr (GLU == 1) glu_h[o] = swiglu_fwd((float)glu_g[o], (float)h);
     }
   }
 }
 
 static int launch_reduce(const GemmArgs& a, int splits, hipStream_t stream) {
   const int64_t quads = ((int64_t)a.M * a.Nc + 3) / 4;
-  hipLaunchKernelGGL(k_splitk_reduce, dim3((unsigned)((quads + 255) / 256)), dim3(256), 0, stream,
-                     a.ws, splits, a.M, a.Nc, a.C, (int64_t)a.ldc);
+  const dim3 grid((unsigned)((quads + 255) / 256));
+  if (a.glu == 1)
+    hipLaunchKernelGGL(k_splitk_reduce<1>, grid, dim3(256), 0, stream, a.ws, splits, a.M, a.Nc,
+                       a.C, (int64_t)a.ldc, a.glu_g, a.glu_u, a.glu_h);
+  else if (a.glu == 2)
+    hipLaunchKernelGGL(k_splitk_reduce<2>, grid, dim3(256), 0, stream, a.ws, splits, a.M, a.Nc,
+                       a.C, (int64_t)a.ldc, a.glu_g, a.glu_u, a.glu_h);
+  else
+    hipLaunchKernelGGL(k_splitk_reduce<0>, grid, dim3(256), 0, stream, a.ws, splits, a.M, a.Nc,
+                       a.C, (int64_t)a.ldc, a.glu_g, a.glu_u, a.glu_h);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MXS_OK : (int)e;
 }
@@ -1318,7 +1479,7 @@ struct ACopy {
 // the other half of a 2-deep B buffer while the consumers multiply kt.  Everything a producer
 // issues in one K-step is waited for at the start of the next, and one workgroup barrier per
 // K-step hands the buffers over.
-template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS>
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU>
 __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
   constexpr int WM = BM / CWM, WN = BN / CWN, TM = WM / 32, TN = WN / 32;
   constexpr int NTP = 64 * PW;  // producer threads
@@ -1503,6 +1664,19 @@ __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
         wait_vmem_all();  // no copy into the A ring may still be in flight
       }
     }
+    if constexpr (GLU) {
+      // Nothing is in flight here.  This wait says so to a path-insensitive reading too, which
+      // could pair the issuing prologue with a skipped main loop (the two test one `run`).
+      wait_vmem_all();
+      if (gridDim.z == 1) {
+        GluTail<BM, BN, CWM, CWN, NTP, BWD> glu;
+        glu.prefetch(a, p, m0, n0);  // in flight across both barriers
+        lds_barrier();               // the A ring is free for the consumers' staged tile
+        lds_barrier();               // the tile is staged
+        glu.store(a, p, m0, n0, reinterpret_cast<const uint32_t*>(As));
+        return;
+      }
+    }
     lds_barrier();  // the A ring is free for the consumers' staged epilogue
   } else {
     // ---- consumers ----
@@ -1529,6 +1703,15 @@ __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
     lds_barrier();  // the producers' last copies have landed
     static_assert(4 * StagedStore<TM, TN>::AREA_DWORDS * 4 <= 3 * LDS_A * 2,
                   "staged epilogue areas fit in the A ring");
+    if constexpr (GLU) {
+      using G = GluTail<BM, BN, CWM, CWN, NTP, BWD>;
+      static_assert(4 * G::AREA * 4 <= 3 * LDS_A * 2, "the staged tile fits in the A ring");
+      if (gridDim.z == 1) {
+        G::stage(acc, lane, reinterpret_cast<uint32_t*>(As) + wave * G::AREA);
+        lds_barrier();  // the tile is staged for the producers
+        return;
+      }
+    }
     epilogue_staged<TM, TN>(a, acc, m0 + wm0, n0 + wn0, lane,
                             reinterpret_cast<float*>(As) + wave * StagedStore<TM, TN>::AREA_DWORDS);
   }
@@ -1537,6 +1720,9 @@ __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool BWD>
 static int launch_cfg(const GemmArgs& a0, int splits, hipStream_t stream) {
   using T = Tile<BM, BN, WAVES_M, WAVES_N, BWD>;
+  // the all-wave kernel has neither the SwiGLU epilogue nor the gradient rows
+  if (a0.glu) return MXS_ERR_SIZE;
+  if (a0.cols_blocks > 0) return MXS_ERR_ARG;
   GemmArgs a = a0;
   const int n_steps = a.Kr / kBK;
   if (splits < 1) splits = 1;
@@ -1567,7 +1753,6 @@ static int launch_ws(const GemmArgs& a0, int splits, hipStream_t stream) {
   // all-wave kernel takes the call
   if ((int64_t)a0.Nc * a0.Kr >= (int64_t(1) << 32) || (int64_t)BM * a0.lda * 2 >= (int64_t(1) << 32) ||
       (BWD && a0.Nc < (PW == 8 ? 16 : 32))) {
-    if (a0.cols_blocks > 0) return MXS_ERR_ARG;  // the all-wave kernel runs no gradient rows
     return launch_cfg<64, 128, 1, 4, BWD>(a0, splits, stream);
   }
   GemmArgs a = a0;
@@ -1585,16 +1770,22 @@ static int launch_ws(const GemmArgs& a0, int splits, hipStream_t stream) {
   const dim3 grid(gx, gy, splits);
   if (splits > 1 && !a.ws) return MXS_ERR_ARG;
   const size_t lds = (size_t)ws_lds_halfs<BM, BN, BWD>() * sizeof(_Float16);
-  static bool lds_set = false;  // idempotent attribute; a benign race between threads
-  if (!lds_set) {
-    hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW, NS>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  // the SwiGLU output has kernels of its own, so the others keep their registers
+  const void* fn =
+      a.glu ? reinterpret_cast<const void*>(&k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW, NS, true>)
+            : reinterpret_cast<const void*>(&k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW, NS, false>);
+  static bool lds_set[2] = {false, false};  // idempotent attribute; a benign race between threads
+  if (!lds_set[a.glu ? 1 : 0]) {
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
-    lds_set = true;
+    lds_set[a.glu ? 1 : 0] = true;
   }
-  hipLaunchKernelGGL((k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW, NS>), grid, dim3(64 * (4 + PW)), lds,
-                     stream, a);
+  if (a.glu)
+    hipLaunchKernelGGL((k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW, NS, true>), grid,
+                       dim3(64 * (4 + PW)), lds, stream, a);
+  else
+    hipLaunchKernelGGL((k_nf4_gemm_ws<BM, BN, CWM, CWN, BWD, PW, NS, false>), grid,
+                       dim3(64 * (4 + PW)), lds, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   return splits > 1 ? launch_reduce(a, splits, stream) : MXS_OK;
@@ -1652,8 +1843,17 @@ static void choose(int M, int Nc, int Kr, int* cfg, int* splits) {
 static int gemm_entry(bool bwd, const GemmArgs& a, int cfg, int splits, hipStream_t stream) {
   if (a.M < 0 || a.Nc < 0 || a.Kr < 0) return MXS_ERR_ARG;
   if (a.M == 0 || a.Nc == 0) return MXS_OK;
-  if (!a.A || !a.packed || !a.absmax8 || !a.code || !a.absmax2 || !a.offset || !a.C)
+  if (!a.A || !a.packed || !a.absmax8 || !a.code || !a.absmax2 || !a.offset ||
+      (!a.C && a.glu != 2))
     return MXS_ERR_ARG;
+  if (a.glu) {  // the SwiGLU buffers: [M, ldc] fp16, 16-byte aligned rows
+    if (a.glu != (bwd ? 2 : 1)) return MXS_ERR_ARG;  // forward: silu(gate) * y; backward: adjoint
+    if (!a.glu_g || (a.glu == 1 && !a.glu_h) || (a.glu == 2 && !a.glu_u)) return MXS_ERR_ARG;
+    if (a.Nc % 8 != 0 || a.ldc % 8 != 0) return MXS_ERR_SIZE;
+    if (((uintptr_t)a.glu_g % 16) || ((uintptr_t)a.glu_u % 16) || ((uintptr_t)a.glu_h % 16) ||
+        ((uintptr_t)a.C % 16))
+      return MXS_ERR_ALIGN;
+  }
   if (a.Kr % kBK != 0 || a.Kw % kBK != 0) return MXS_ERR_SIZE;
   if (bwd && a.Nc % 8 != 0) return MXS_ERR_SIZE;
   if (a.lda % 8 != 0 || ((uintptr_t)a.A % 16) != 0 || ((uintptr_t)a.packed % 16) != 0)
@@ -1720,6 +1920,20 @@ static bool grads_fusable(int M, int N, int K, int r, int* cfg_out, int* nw_out)
   *cfg_out = cfg;
   *nw_out = nw;
   return true;
+}
+
+// The planned kernel for a GEMM [M, Nc] over Kr takes the SwiGLU output: a warp-specialized
+// configuration that none of its fallback conditions sends to the all-wave kernel.
+static bool glu_plan_ok(int M, int Nc, int Kr, bool bwd) {
+  if (M <= 0 || Nc <= 0 || Kr <= 0 || Nc % 8 != 0 || Kr % kBK != 0) return false;
+  int cfg, sp;
+  choose(M, Nc, Kr, &cfg, &sp);
+  if (cfg < 6 || cfg >= kNumCfg) return false;
+  static const int kBM[] = {256, 256, 128, 256, 128, 256};  // cfg 6..11
+  static const int kPW[] = {4, 4, 4, 4, 8, 8};
+  const int bm = kBM[cfg - 6], pw = kPW[cfg - 6];
+  return (int64_t)Nc * Kr < (int64_t(1) << 32) && (int64_t)bm * Kr * 2 < (int64_t(1) << 32) &&
+         !(bwd && Nc < (pw == 8 ? 16 : 32));
 }
 
 }  // namespace mxs
@@ -1925,6 +2139,82 @@ int mxs_nf4_linear_bwd_dx_hp(const void* dy, int M, int N, int K, const void* pa
   a.ldc = K;
   set_workspace(a, workspace);
   return gemm_entry(true, a, cfg, splits, stream);
+}
+
+int mxs_nf4_linear_glu_fused(int M, int N, int K, int bwd) {
+  return bwd ? (glu_plan_ok(M, K, N, true) ? 1 : 0) : (glu_plan_ok(M, N, K, false) ? 1 : 0);
+}
+
+int mxs_nf4_linear_fwd_glu(const void* x, int M, int K, int N, const void* packed,
+                           const void* absmax8, const float* code, const float* absmax2,
+                           const float* offset, const void* bias, const float* lora_hp,
+                           int hp_slices, int ldt, const void* lora_b, int r, void* lora_ht,
+                           const void* gate, void* y, void* h, void* workspace,
+                           hipStream_t stream) {
+  GemmArgs a{};
+  a.A = static_cast<const _Float16*>(x);
+  a.lda = K;
+  a.packed = static_cast<const uint8_t*>(packed);
+  a.absmax8 = static_cast<const uint8_t*>(absmax8);
+  a.code = code;
+  a.absmax2 = absmax2;
+  a.offset = offset;
+  a.M = M;
+  a.Nc = N;
+  a.Kr = K;
+  a.Kw = K;
+  a.bias = static_cast<const _Float16*>(bias);
+  if (lora_hp) {
+    a.lora_hp = lora_hp;
+    a.hp_slices = hp_slices;
+    a.ldt = ldt;
+    a.lora_ht = static_cast<_Float16*>(lora_ht);
+    a.lora_w = static_cast<const _Float16*>(lora_b);
+    a.r = r;
+  }
+  a.C = static_cast<_Float16*>(y);
+  a.ldc = N;
+  a.glu = 1;
+  a.glu_g = static_cast<_Float16*>(const_cast<void*>(gate));
+  a.glu_h = static_cast<_Float16*>(h);
+  set_workspace(a, workspace);
+  return gemm_entry(false, a, -1, 1, stream);
+}
+
+int mxs_nf4_linear_bwd_dx_glu(const void* dy, int M, int N, int K, const void* packed,
+                              const void* absmax8, const float* code, const float* absmax2,
+                              const float* offset, const float* lora_dhp, int hp_slices, int ldt,
+                              const void* lora_at, int r, const void* mask, float mask_scale,
+                              void* lora_dht, void* gate, void* up, void* workspace,
+                              hipStream_t stream) {
+  GemmArgs a{};
+  a.A = static_cast<const _Float16*>(dy);
+  a.lda = N;
+  a.packed = static_cast<const uint8_t*>(packed);
+  a.absmax8 = static_cast<const uint8_t*>(absmax8);
+  a.code = code;
+  a.absmax2 = absmax2;
+  a.offset = offset;
+  a.M = M;
+  a.Nc = K;
+  a.Kr = N;
+  a.Kw = K;
+  if (lora_dhp) {
+    a.lora_hp = lora_dhp;
+    a.hp_slices = hp_slices;
+    a.ldt = ldt;
+    a.lora_ht = static_cast<_Float16*>(lora_dht);
+    a.lora_w = static_cast<const _Float16*>(lora_at);
+    a.r = r;
+    a.mask = static_cast<const uint8_t*>(mask);
+    a.mask_scale = mask_scale;
+  }
+  a.ldc = K;
+  a.glu = 2;
+  a.glu_g = static_cast<_Float16*>(gate);
+  a.glu_u = static_cast<_Float16*>(up);
+  set_workspace(a, workspace);
+  return gemm_entry(true, a, -1, 1, stream);
 }
 
 }  // extern "C"

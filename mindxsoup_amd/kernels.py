@@ -253,6 +253,88 @@ def nf4_linear_bwd_dx_hp(dy2d, packed, state, lora_dhp, lora_at, mask=None, mask
     return dx, dht
 
 
+def glu_fused(M, N, K, bwd):
+    """True when the projection K -> N at M tokens takes the SwiGLU epilogue on its planned
+    kernel: nf4_linear_fwd_glu (bwd False) or nf4_linear_bwd_dx_glu (bwd True)."""
+    return bool(_lib.lib().mxs_nf4_linear_glu_fused(M, N, K, int(bool(bwd))))
+
+
+def _glu_operand(t, M, n, name):
+    if t.dtype != torch.float16 or t.shape != (M, n) or not t.is_contiguous() \
+            or t.data_ptr() % 16:
+        raise ValueError(f"{name} must be a contiguous, 16-byte aligned fp16 [M, {n}] tensor")
+    return t
+
+
+def nf4_linear_fwd_glu(x2d, packed, state, gate, lora_hp=None, lora_b=None, bias=None, ws=None):
+    """(y, h, ht): the up projection Y = x2d @ W^T (+ bias) (+ fp16(sum of lora_hp) @ lora_b^T)
+    and H = silu(gate) * Y, both fp16 [M, N], from one launch; ht is the LoRA operand transposed
+    [r, ldt] (None without LoRA).  Only where glu_fused(M, N, K, False)."""
+    n, k = state.shape
+    if x2d.dtype != torch.float16 or x2d.dim() != 2 or x2d.shape[1] != k:
+        raise ValueError("x must be fp16 [M, in_features]")
+    x2d = x2d.contiguous()
+    M = x2d.shape[0]
+    _glu_operand(gate, M, n, "gate")
+    dev = x2d.device
+    S = ldt = r = 0
+    ht = None
+    if lora_hp is not None:
+        S, ldt, r = lora_hp.shape
+        if ldt != _ldt(M) or lora_b is None or lora_b.shape != (n, r) \
+                or lora_hp.dtype != torch.float32:
+            raise ValueError("lora_hp [slices, ldt, r] fp32 needs lora_b [N, r]")
+        lora_b = lora_b.to(torch.float16).contiguous()
+        lora_hp = lora_hp.contiguous()
+        ht = torch.empty((r, ldt), dtype=torch.float16, device=dev)
+    if bias is not None:
+        bias = bias.to(torch.float16).contiguous()
+    y = torch.empty((M, n), dtype=torch.float16, device=dev)
+    h = torch.empty((M, n), dtype=torch.float16, device=dev)
+    ws = _ws(M, n, k, dev, -1, 1, ws)
+    _lib.call("mxs_nf4_linear_fwd_glu", _lib.ptr(x2d), M, k, n, *_nf4_args(packed, state),
+              _lib.ptr(bias), _lib.ptr(lora_hp), S, ldt, _lib.ptr(lora_b), r, _lib.ptr(ht),
+              _lib.ptr(gate), _lib.ptr(y), _lib.ptr(h), _lib.ptr(ws), _lib.stream_of(dev))
+    return y, h, ht
+
+
+def nf4_linear_bwd_dx_glu_(dy2d, packed, state, gate, up, lora_dhp=None, lora_at=None,
+                           mask=None, mask_scale=1.0, ws=None, want_t=True):
+    """In place: the down projection's dH = dy2d @ W (+ mask * mask_scale * (fp16(sum of
+    lora_dhp) @ lora_at^T)) goes through the SwiGLU backward in the GEMM's epilogue: gate <-
+    d(gate), up <- d(up) (fp16 [M, K]); dH itself is not stored.  Returns dht, the LoRA operand
+    transposed [r, ldt] (None without LoRA or unless want_t).  Only where
+    glu_fused(M, N, K, True)."""
+    n, k = state.shape
+    if dy2d.dtype != torch.float16 or dy2d.dim() != 2 or dy2d.shape[1] != n:
+        raise ValueError("dy must be fp16 [M, out_features]")
+    dy2d = dy2d.contiguous()
+    M = dy2d.shape[0]
+    _glu_operand(gate, M, k, "gate")
+    _glu_operand(up, M, k, "up")
+    dev = dy2d.device
+    S = ldt = r = 0
+    dht = None
+    if lora_dhp is not None:
+        S, ldt, r = lora_dhp.shape
+        if ldt != _ldt(M) or lora_at is None or lora_at.shape != (k, r) \
+                or lora_dhp.dtype != torch.float32:
+            raise ValueError("lora_dhp [slices, ldt, r] fp32 needs lora_at [K, r]")
+        lora_dhp, lora_at = lora_dhp.contiguous(), lora_at.contiguous()
+        if mask is not None:
+            if mask.dtype != torch.uint8 or mask.shape != (M, k):
+                raise ValueError("mask must be uint8 [M, K]")
+            mask = mask.contiguous()
+        if want_t:
+            dht = torch.empty((r, ldt), dtype=torch.float16, device=dev)
+    ws = _ws(M, k, n, dev, -1, 1, ws)
+    _lib.call("mxs_nf4_linear_bwd_dx_glu", _lib.ptr(dy2d), M, n, k, *_nf4_args(packed, state),
+              _lib.ptr(lora_dhp), S, ldt, _lib.ptr(lora_at), r, _lib.ptr(mask),
+              float(mask_scale), _lib.ptr(dht), _lib.ptr(gate), _lib.ptr(up), _lib.ptr(ws),
+              _lib.stream_of(dev))
+    return dht
+
+
 def lora_finish(partials, M, want_out=False):
     """(out, outT): the fp16 operand from LoRA partial sums [slices, ldt, r] fp32 (added in slice
     order, as the fused GEMMs do): out [M, r] (None unless want_out) and outT [r, ldt]."""

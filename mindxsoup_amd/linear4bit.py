@@ -299,12 +299,14 @@ class LoraLinear4bit(torch.nn.Module):
             return None
         return self.active_adapters[0]
 
-    def draw_keep(self, x2d, p):
-        """The dropout keep mask [M, K] as u8 (a fresh Bernoulli(1 - p) draw)."""
+    def draw_keep(self, x2d, p, shape=None):
+        """The dropout keep mask [M, K] (x2d's shape, or `shape`) as u8 (a fresh
+        Bernoulli(1 - p) draw)."""
         if self.next_keep is not None:
             keep, self.next_keep = self.next_keep, None
             return keep
-        return torch.empty(x2d.shape, dtype=torch.uint8, device=x2d.device).bernoulli_(1.0 - p)
+        return torch.empty(x2d.shape if shape is None else shape, dtype=torch.uint8,
+                           device=x2d.device).bernoulli_(1.0 - p)
 
     def forward(self, x):
         name = self._adapter()
