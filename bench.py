@@ -303,8 +303,52 @@ def bench_mlp(dev, g, steps, warmup):
     res["gflop"] = round(fl / 1e9, 3)
     res["tflops"] = round(fl / res["fused_ms"] / 1e9, 1)
     res["saved_ms"] = round(res["unfused_ms"] - res["fused_ms"], 4)
+    res["kernels_us"] = swiglu_kernel_times(block, x, dy, steps, warmup)
     del block, layers, x, dy
     return res
+
+
+def swiglu_kernel_times(block, x, dy, steps, warmup):
+    """The SwiGLU's kernels alone at the block's shapes (us per launch, 20 launches per graph
+    replay): up_proj's forward GEMM plain and with the SwiGLU tail, and the elementwise kernel;
+    down_proj's dX GEMM plain and with the adjoint tail, and the elementwise backward."""
+    from mindxsoup_amd import kernels
+
+    s, ms_ = ALPHA / RANK, 1.0 / (1.0 - P_DROP)
+    up, down = block.up_proj, block.down_proj
+    pu, su = up.base_layer.weight.data.view(-1, 1), up.base_layer.weight.quant_state
+    pd, sd = down.base_layer.weight.data.view(-1, 1), down.base_layer.weight.quant_state
+    a_u = up.lora_A["default"].weight.half()
+    b_u = up.lora_B["default"].weight.half()
+    b_d = down.lora_B["default"].weight.half()
+    a_d = down.lora_A["default"].weight.half()
+    xs = x.detach()
+    M = xs.shape[0]
+    gate = torch.randn((M, 8960), device=xs.device).half()
+    upv = torch.randn((M, 8960), device=xs.device).half()
+    keep = (torch.rand((M, 8960), device=xs.device) >= P_DROP).to(torch.uint8)
+    hp, _, _ = kernels.lora_h_partials(xs, a_u, s, None, 1.0, lora_b=b_u)
+    at_d, bt_d = a_d.t().contiguous(), b_d.t().contiguous()
+    dhp = kernels.lora_dh_partials(dy, bt_d, s)
+    y0, _ = kernels.nf4_linear_fwd_hp(xs, pu, su, hp, b_u)
+    dh0, _ = kernels.nf4_linear_bwd_dx_hp(dy, pd, sd, dhp, at_d, keep, ms_)
+    g2, u2 = gate.clone(), upv.clone()
+    cases = {
+        "up_fwd_gemm": lambda: kernels.nf4_linear_fwd_hp(xs, pu, su, hp, b_u),
+        "up_fwd_gemm_swiglu": lambda: kernels.nf4_linear_fwd_glu(xs, pu, su, gate, hp, b_u),
+        "silu_mul": lambda: kernels.silu_mul(gate, y0),
+        "down_dx_gemm": lambda: kernels.nf4_linear_bwd_dx_hp(dy, pd, sd, dhp, at_d, keep, ms_),
+        "down_dx_gemm_swiglu": lambda: kernels.nf4_linear_bwd_dx_glu_(dy, pd, sd, g2, u2, dhp,
+                                                                      at_d, keep, ms_),
+        "silu_mul_bwd": lambda: kernels.silu_mul_bwd_(dh0, g2, u2),
+    }
+    reps = 20
+    out = {}
+    for name, fn in cases.items():
+        ms, _ = graph_time(lambda: [fn() for _ in range(reps)], max(3, steps // 10),
+                           max(2, warmup // 5))
+        out[name] = round(ms * 1e3 / reps, 2)
+    return out
 
 
 def bench_fused(dev, steps, warmup):

@@ -94,3 +94,29 @@ def test_silu_mul_unaligned_and_tails(cuda, n, offset):
         _close(_np(out), want)
         _close(_np(g), want_dg)
         _close(_np(u), want_du)
+
+
+def test_special_values_match_oracle_exactly(cuda):
+    """Where exp over- or underflows (|gate| large, infinities) and at gate = 0, the hardware
+    exp2 and reciprocal give the oracle's values (libm expf, IEEE division).  Values are equal;
+    a zero's sign may differ where sigmoid(gate) falls into fp32's subnormal range (gate near
+    -88: the hardware reciprocal returns 0 there, so d(gate) is +0 where libm's subnormal
+    sigmoid leaves -0)."""
+    from mindxsoup_amd import kernels
+
+    gv = np.array([0.0, -0.0, 1e-7, -1e-7, 20, -20, 88, -88, 100, -100, 1000, -1000, 65504,
+                   -65504, np.inf, -np.inf], np.float16)
+    uv = np.array([1, -3, 2, 0.5, 1, 1, -2, 2, 1, 1, 0.25, 4, 1, 1, 1, 1], np.float16)
+    dv = np.array([1, 2, -1, 4, 1, -1, 0.5, 2, 1, 1, 1, 1, 0.5, 0.5, 1, 1], np.float16)
+    g = torch.from_numpy(gv).to(cuda)
+    u = torch.from_numpy(uv).to(cuda)
+    d = torch.from_numpy(dv).to(cuda)
+    out = kernels.silu_mul(g, u)
+    kernels.silu_mul_bwd_(d, g, u)
+    torch.cuda.synchronize()
+    want = O.silu_mul(gv, uv)
+    want_dg, want_du = O.silu_mul_bwd(dv, gv, uv)
+    for got, ref in ((out, want), (g, want_dg), (u, want_du)):
+        got = _np(got)
+        same = (got == ref) | (np.isnan(got) & np.isnan(ref))
+        assert same.all(), (got, ref)
