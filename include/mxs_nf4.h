@@ -266,6 +266,22 @@ int mxs_nf4_linear_bwd_dx_glu(const void* dy, int M, int N, int K, const void* p
                               void* lora_dht, void* gate, void* up, void* workspace,
                               hipStream_t stream);
 
+/* q, k, v of Qwen2 attention with the rotary position embedding (solution/attention.py:28-82,
+ * qkv_rope_kernel; with no LoRA term and no v it is solution/rope.py:41-66, rope_kernel).
+ * tensors[8] = q_a, q_b, k, v_a, v_b (inputs), q_o, k_o, v_o (outputs); each a [B, H, T, 128]
+ * view with unit stride along the head and (b, h, t) element strides in strides[3 * i ..],
+ * e.g. a projection's [B, T, H * 128] output has (T * H * 128, 128, H * 128).  Forward:
+ * x = a (+ b * scale) in fp32, q and k rotated (y1 = x1 c1 - x2 s1, y2 = x2 c2 + x1 s2 over
+ * the halves x1 = x[0:64], x2 = x[64:128] and the cos / sin row of the position), v only
+ * added; backward (backward = 1) rotates by the opposite angle (dq, dk; dv copied).  cos / sin:
+ * fp32 rows of 128 with strides (cos_stride_b, cos_stride_t); cos_stride_b may be 0.  q_b, v_b
+ * may be NULL; v_a and v_o NULL together (no v heads).  Inputs all fp16 (in_f32 = 0) or all
+ * fp32; outputs fp16 or fp32 (out_f32).  Pointers and strides multiples of 4 elements. */
+int mxs_qkv_rope(const void* const tensors[8], const int64_t strides[24], const float* cos,
+                 const float* sin, int64_t cos_stride_b, int64_t cos_stride_t, int batch,
+                 int n_tokens, int n_q, int n_kv, int in_f32, int out_f32, int backward,
+                 float q_scale, float v_scale, hipStream_t stream);
+
 /* 1 when the projection [K -> N] at M tokens takes the SwiGLU epilogue in the forward (bwd = 0)
  * or the backward (bwd = 1) on its planned kernel; else 0 (then run the GEMM and
  * mxs_silu_mul / mxs_silu_mul_bwd). */

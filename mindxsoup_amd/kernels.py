@@ -474,3 +474,46 @@ def silu_mul_bwd_(grad, gate, up):
         raise ValueError("gate and up must be contiguous (their memory takes the gradients)")
     _lib.call("mxs_silu_mul_bwd", _lib.ptr(grad), _lib.ptr(gate), _lib.ptr(up), gate.numel(),
               _lib.stream_of(gate.device))
+
+
+def qkv_rope(q_a, q_b, k, v_a, v_b, cos, sin, q_o, k_o, v_o, backward=False, q_scale=1.0,
+             v_scale=1.0):
+    """mxs_qkv_rope on [B, H, T, 128] views with unit stride along the head (any other strides):
+    q_o = rot(q_a + q_scale * q_b), k_o = rot(k), v_o = v_a + v_scale * v_b (q_b, v_a, v_b may
+    be None; v_o with v_a); rot the forward rotation, or its inverse with backward.  Inputs all
+    fp16 or all fp32, outputs all fp16 or all fp32; cos / sin fp32 [1 or B, T, 128] rows with
+    unit last stride."""
+    ins = [q_a, q_b, k, v_a, v_b]
+    outs = [q_o, k_o, v_o]
+    in_dt = {t.dtype for t in ins if t is not None}
+    out_dt = {t.dtype for t in outs if t is not None}
+    if len(in_dt) != 1 or len(out_dt) != 1 or not in_dt <= {torch.float16, torch.float32} \
+            or not out_dt <= {torch.float16, torch.float32}:
+        raise ValueError("inputs of one dtype and outputs of one dtype, each fp16 or fp32")
+    batch, n_q, n_tokens, dim = q_a.shape
+    n_kv = k.shape[1]
+    if dim != 128 or k.shape != (batch, n_kv, n_tokens, 128):
+        raise ValueError("q and k must be [B, H, T, 128]")
+    for t, n in ((q_b, n_q), (v_a, n_kv), (v_b, n_kv), (q_o, n_q), (k_o, n_kv), (v_o, n_kv)):
+        if t is not None and t.shape != (batch, n, n_tokens, 128):
+            raise ValueError("operand shapes disagree")
+    if (v_a is None) != (v_o is None) or (v_b is not None and v_a is None):
+        raise ValueError("v_o goes with v_a, v_b needs v_a")
+    for t in ins + outs:
+        if t is not None and t.stride(-1) != 1:
+            raise ValueError("unit stride along the head required")
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.shape != sin.shape \
+            or cos.stride() != sin.stride() or cos.stride(-1) != 1 \
+            or tuple(cos.shape[1:]) != (n_tokens, 128) or cos.shape[0] not in (1, batch):
+        raise ValueError("cos / sin must be fp32 [1 or B, T, 128] with one layout")
+    import ctypes
+
+    tens = (ctypes.c_void_p * 8)(*[None if t is None else t.data_ptr() for t in ins + outs])
+    strides = (ctypes.c_int64 * 24)(*[s for t in ins + outs
+                                      for s in ((0, 0, 0) if t is None else
+                                                (t.stride(0), t.stride(1), t.stride(2)))])
+    cs_b = cos.stride(0) if cos.shape[0] == batch else 0
+    _lib.call("mxs_qkv_rope", tens, strides, _lib.ptr(cos), _lib.ptr(sin), cs_b, cos.stride(1),
+              batch, n_tokens, n_q, n_kv, int(torch.float32 in in_dt),
+              int(torch.float32 in out_dt), int(bool(backward)), float(q_scale),
+              float(v_scale), _lib.stream_of(q_a.device))

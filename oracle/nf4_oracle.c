@@ -28,6 +28,14 @@
  *                          d_up = 0, d_gate = dh * up / 2) and for large |gate|
  *                          (silu -> gate or 0), and the differently ordered
  *                          derivative of solution/test_silu_mul.py:13-19.
+ *   qkv_rope             - float64 rotate-half RoPE (transformers'
+ *                          apply_rotary_pos_emb, solution/test_rope.py:19-23)
+ *                          within one fp16 ulp; forward then backward restores
+ *                          the input (a rotation and its inverse); pair norms
+ *                          preserved; closed forms (cos = 1, sin = 0 is the
+ *                          identity; cos = 0, sin = 1 maps (x1, x2) to
+ *                          (-x2, x1)); a power-of-two LoRA scale equals adding
+ *                          the pre-scaled LoRA (solution/test_attention.py:226).
  *   The GEMM / LoRA references live in oracle/oracle.py (numpy) and are pinned
  *   against float64 torch autograd.
  */
@@ -335,5 +343,64 @@ void oracle_silu_mul_bwd(const uint16_t *dh, const uint16_t *gate, const uint16_
         const float silu = g * s;
         d_gate[i] = oracle_f32_to_f16((d * u) * (s + silu * (1.0f - s)));
         d_up[i] = oracle_f32_to_f16(d * silu);
+    }
+}
+
+/* q/k/v of Qwen2 attention, solution/attention.py:28-82 (qkv_rope_kernel, _qkv_heads): per
+ * position (b, t) and head of 128 values, x = a (+ b * scale) in fp32; q and k heads rotated,
+ * v heads not; one rounding to the output type.  With x1 = x[0:64], x2 = x[64:128], the cos
+ * row c = (c1, c2) and the sin row s = (s1, s2) of the position:
+ *   forward   y1 = x1 * c1 + x2 * (-s1)    y2 = x2 * c2 + x1 * s2
+ *   backward  y1 = x1 * c1 + x2 * s2       y2 = x2 * c2 + x1 * (-s1)
+ * (attention.py:70-74, rope.py:54-66: sign +1 / -1 with the sin halves swapped).  Each product
+ * and sum is one fp32 operation (no contraction).  Layouts: inputs and outputs [B, T, H * 128]
+ * contiguous (a [B, H, T, 128] view with [B, T, H, 128] memory, as the projections write it);
+ * cos / sin fp32 [Bc, T, 128] with Bc = 1 (shared over the batch) or B.  q_b / v_b / v_a may
+ * be NULL (no LoRA term; no v).  in_f32 / out_f32 select fp32 (1) or fp16 (0) storage. */
+static inline float rope_load(const void *p, int64_t i, int f32) {
+    return f32 ? ((const float *)p)[i] : oracle_f16_to_f32(((const uint16_t *)p)[i]);
+}
+
+static inline void rope_store(void *p, int64_t i, float v, int f32) {
+    if (f32) ((float *)p)[i] = v;
+    else ((uint16_t *)p)[i] = oracle_f32_to_f16(v);
+}
+
+static void rope_heads(const void *a, const void *b, float scale, void *y, int64_t row, int heads,
+                       const float *c, const float *sn, int rotate, int backward, int in_f32,
+                       int out_f32) {
+    for (int h = 0; h < heads; h++) {
+        const int64_t base = (row * heads + h) * 128;
+        for (int j = 0; j < 64; j++) {
+            float x1 = rope_load(a, base + j, in_f32), x2 = rope_load(a, base + 64 + j, in_f32);
+            if (b) {
+                x1 = x1 + rope_load(b, base + j, in_f32) * scale;
+                x2 = x2 + rope_load(b, base + 64 + j, in_f32) * scale;
+            }
+            float y1 = x1, y2 = x2;
+            if (rotate) {
+                const float c1 = c[j], c2 = c[64 + j];
+                const float p = backward ? sn[64 + j] : -sn[j];
+                const float r = backward ? -sn[j] : sn[64 + j];
+                y1 = x1 * c1 + x2 * p;
+                y2 = x2 * c2 + x1 * r;
+            }
+            rope_store(y, base + j, y1, out_f32);
+            rope_store(y, base + 64 + j, y2, out_f32);
+        }
+    }
+}
+
+void oracle_qkv_rope(const void *q_a, const void *q_b, const void *k, const void *v_a,
+                     const void *v_b, const float *cos, const float *sin, int cos_batch,
+                     void *q_o, void *k_o, void *v_o, int batch, int n_tokens, int n_q, int n_kv,
+                     int in_f32, int out_f32, int backward, float q_scale, float v_scale) {
+#pragma omp parallel for schedule(static)
+    for (int64_t row = 0; row < (int64_t)batch * n_tokens; row++) {
+        const int64_t crow = cos_batch == 1 ? row % n_tokens : row;
+        const float *c = cos + crow * 128, *sn = sin + crow * 128;
+        rope_heads(q_a, q_b, q_scale, q_o, row, n_q, c, sn, 1, backward, in_f32, out_f32);
+        rope_heads(k, NULL, 1.0f, k_o, row, n_kv, c, sn, 1, backward, in_f32, out_f32);
+        if (v_a) rope_heads(v_a, v_b, v_scale, v_o, row, n_kv, c, sn, 0, backward, in_f32, out_f32);
     }
 }

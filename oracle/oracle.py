@@ -62,6 +62,10 @@ def lib():
         L.oracle_set_num_threads.argtypes = [ctypes.c_int]
         L.oracle_silu_mul.argtypes = [P, P, P, i64]
         L.oracle_silu_mul_bwd.argtypes = [P, P, P, P, P, i64]
+        L.oracle_qkv_rope.argtypes = [P, P, P, P, P, P, P, ctypes.c_int, P, P, P, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                      ctypes.c_float]
         _lib = L
     return _lib
 
@@ -267,3 +271,32 @@ def silu_mul_bwd(dh_f16, gate_f16, up_f16):
     dg, du = np.empty_like(g), np.empty_like(g)
     lib().oracle_silu_mul_bwd(_ptr(d), _ptr(g), _ptr(u), _ptr(dg), _ptr(du), g.size)
     return dg, du
+
+
+def qkv_rope(q_a, q_b, k, v_a, v_b, cos, sin, n_q, n_kv, q_scale=1.0, v_scale=1.0,
+             backward=False, out_dtype=np.float16):
+    """(q, k, v) of solution/attention.py:28-82 (qkv_rope_kernel) on [B, T, heads * 128] arrays
+    (fp16 or fp32, all one dtype; q_b, v_a, v_b may be None), cos / sin [1 or B, T, 128]; the
+    outputs are [B, T, heads * 128] of out_dtype (v None without v_a).  backward=True rotates
+    back (the kernel's backward launch, attention.py:156-167)."""
+    dt = np.asarray(q_a).dtype
+    if dt not in (np.float16, np.float32):
+        raise ValueError("fp16 or fp32 inputs")
+    conv = [None if t is None else np.ascontiguousarray(t, dtype=dt) for t in (q_a, q_b, k, v_a, v_b)]
+    q_a_, q_b_, k_, v_a_, v_b_ = conv
+    batch, n_tokens, _ = q_a_.shape
+    c = np.ascontiguousarray(cos, dtype=np.float32)
+    s_ = np.ascontiguousarray(sin, dtype=np.float32)
+    if c.shape != s_.shape or c.shape[1:] != (n_tokens, 128) or c.shape[0] not in (1, batch):
+        raise ValueError("cos / sin must be [1 or B, T, 128]")
+    q_o = np.empty((batch, n_tokens, n_q * 128), out_dtype)
+    k_o = np.empty((batch, n_tokens, n_kv * 128), out_dtype)
+    v_o = None if v_a_ is None else np.empty((batch, n_tokens, n_kv * 128), out_dtype)
+    lib().oracle_qkv_rope(_ptr(q_a_), _ptr(q_b_) if q_b_ is not None else None, _ptr(k_),
+                          _ptr(v_a_) if v_a_ is not None else None,
+                          _ptr(v_b_) if v_b_ is not None else None, _ptr(c), _ptr(s_),
+                          c.shape[0], _ptr(q_o), _ptr(k_o),
+                          _ptr(v_o) if v_o is not None else None, batch, n_tokens, n_q, n_kv,
+                          int(dt == np.float32), int(np.dtype(out_dtype) == np.float32),
+                          int(backward), float(q_scale), float(v_scale))
+    return q_o, k_o, v_o

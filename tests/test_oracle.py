@@ -313,3 +313,102 @@ def test_silu_mul_oracle_against_float64_and_closed_forms():
     s32 = (1.0 / (1.0 + np.exp(-g32))).astype(np.float32)
     alt_dg = (d32 * u32 * s32 * (1 + g32 * (1 - s32))).astype(np.float16).astype(np.float32)
     assert np.allclose(dg.astype(np.float32), alt_dg, atol=1e-3, rtol=1e-3)
+
+
+def _qwen_cos_sin(batch, n_tokens, offsets=True):
+    """cos / sin as Qwen2RotaryEmbedding makes them (theta 1e6, head_dim 128), fp32 [B, T, 128]."""
+    import torch
+    from transformers import Qwen2Config
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RotaryEmbedding
+
+    cfg = Qwen2Config(hidden_size=1536, num_attention_heads=12, num_key_value_heads=2,
+                      rope_theta=1e6)
+    rot = Qwen2RotaryEmbedding(cfg)
+    pos = torch.arange(n_tokens)[None, :].expand(batch, -1)
+    if offsets:  # rows differ, like left padding
+        pos = pos + torch.arange(batch)[:, None] * 3
+    cos, sin = rot(torch.zeros(1, dtype=torch.float32), pos)
+    return cos.float().numpy(), sin.float().numpy()
+
+
+def test_qkv_rope_oracle_against_transformers_and_properties():
+    """oracle qkv_rope (solution/attention.py:28-82) against float64 torch running transformers'
+    own apply_rotary_pos_emb on (base + scale * LoRA), within one fp16 ulp; v = base + LoRA
+    exactly; backward is the inverse rotation; closed forms and the power-of-two scale."""
+    torch = pytest.importorskip("torch")
+    qwen2 = pytest.importorskip("transformers.models.qwen2.modeling_qwen2")
+    rng = np.random.default_rng(21)
+    B, T, nq, nkv = 3, 37, 12, 2
+    cos, sin = _qwen_cos_sin(B, T)
+
+    def proj(h):
+        return (rng.standard_normal((B, T, h * 128)) * 2).astype(np.float16)
+
+    qa, qb, k, va, vb = proj(nq), proj(nq), proj(nkv), proj(nkv), proj(nkv)
+    q, ko, v = O.qkv_rope(qa, qb, k, va, vb, cos, sin, nq, nkv, 2.0, 2.0)
+
+    def heads(x, h):
+        return torch.from_numpy(np.asarray(x, np.float64)).view(B, T, h, 128).transpose(1, 2)
+
+    c64, s64 = torch.from_numpy(cos.astype(np.float64)), torch.from_numpy(sin.astype(np.float64))
+    xq = heads(qa.astype(np.float64) + 2.0 * qb.astype(np.float64), nq)
+    rq, rk = qwen2.apply_rotary_pos_emb(xq, heads(k, nkv), c64, s64)
+    back = lambda t, h: t.transpose(1, 2).reshape(B, T, h * 128).numpy()  # noqa: E731
+    # fp32 outputs within fp32 rounding of two products and a sum: 2^-22 (|x1 c| + |x2 s|) ...
+    q32, k32o, _ = O.qkv_rope(qa, qb, k, None, None, cos, sin, nq, nkv, 2.0, 2.0,
+                              out_dtype=np.float32)
+    for got, ref, x, h in ((q32, back(rq, nq), qa.astype(np.float64) + 2.0 * qb, nq),
+                           (k32o, back(rk, nkv), k.astype(np.float64), nkv)):
+        xh = x.reshape(B, T, h, 2, 64)
+        c_, s_ = cos.reshape(B, T, 1, 2, 64), sin.reshape(B, T, 1, 2, 64)
+        mag = np.abs(xh) * np.abs(c_) + np.abs(xh[:, :, :, ::-1]) * np.abs(s_)
+        assert np.all(np.abs(got - ref) <= 2.0 ** -22 * mag.reshape(got.shape))
+    # ... and the fp16 outputs are those values rounded once (round to nearest even)
+    assert np.array_equal(q, q32.astype(np.float16)) and np.array_equal(ko, k32o.astype(np.float16))
+    assert np.array_equal(v, (va.astype(np.float32) + 2.0 * vb.astype(np.float32)).astype(np.float16))
+    # a power-of-two scale equals adding the pre-scaled LoRA (solution/test_attention.py:226-246)
+    q2, k2, v2 = O.qkv_rope(qa, (qb.astype(np.float32) * 2).astype(np.float16), k, va,
+                            (vb.astype(np.float32) * 2).astype(np.float16), cos, sin, nq, nkv)
+    assert np.array_equal(q2, q) and np.array_equal(k2, ko) and np.array_equal(v2, v)
+    # backward rotates by the opposite angle: fp32 forward then backward restores the input
+    x32 = rng.standard_normal((B, T, nq * 128)).astype(np.float32)
+    k32 = rng.standard_normal((B, T, nkv * 128)).astype(np.float32)
+    y, yk, _ = O.qkv_rope(x32, None, k32, None, None, cos, sin, nq, nkv, out_dtype=np.float32)
+    xb, kb, _ = O.qkv_rope(y, None, yk, None, None, cos, sin, nq, nkv, backward=True,
+                           out_dtype=np.float32)
+    assert np.abs(xb - x32).max() < 1e-5 and np.abs(kb - k32).max() < 1e-5
+    # with cos / sin rows whose halves differ (Qwen's are equal, which would hide a swapped half):
+    # the forward against transformers' formula, and the backward as the forward's transpose,
+    # <R x, g> = <x, R^T g>
+    cr = rng.uniform(-1, 1, (B, T, 128)).astype(np.float32)
+    sr = rng.uniform(-1, 1, (B, T, 128)).astype(np.float32)
+    yr, _, _ = O.qkv_rope(x32, None, k32, None, None, cr, sr, nq, nkv, out_dtype=np.float32)
+    ref_r, _ = qwen2.apply_rotary_pos_emb(heads(x32, nq), heads(k32, nkv),
+                                          torch.from_numpy(cr.astype(np.float64)),
+                                          torch.from_numpy(sr.astype(np.float64)))
+    assert np.abs(yr - back(ref_r, nq)).max() < 1e-5 * np.abs(yr).max()
+    g = rng.standard_normal(y.shape).astype(np.float32)
+    rtg, _, _ = O.qkv_rope(g, None, k32, None, None, cr, sr, nq, nkv, backward=True,
+                           out_dtype=np.float32)
+    lhs = float(np.sum(yr.astype(np.float64) * g))
+    rhs = float(np.sum(x32.astype(np.float64) * rtg))
+    assert abs(lhs - rhs) < 1e-5 * float(np.sum(np.abs(yr.astype(np.float64) * g)))
+    # pair norms preserved (Qwen's cos / sin halves are equal)
+    pair = lambda t: t.reshape(B, T, nq, 2, 64)  # noqa: E731
+    n_in = (pair(x32).astype(np.float64) ** 2).sum(axis=3)
+    n_out = (pair(y).astype(np.float64) ** 2).sum(axis=3)
+    assert np.abs(n_in - n_out).max() < 1e-4 * n_in.max()
+    # closed forms: angle 0 is the identity, angle pi/2 maps (x1, x2) -> (-x2, x1)
+    one, zero = np.ones((1, T, 128), np.float32), np.zeros((1, T, 128), np.float32)
+    i_q, _, _ = O.qkv_rope(qa, None, k, None, None, one, zero, nq, nkv)
+    assert np.array_equal(i_q.astype(np.float32), qa.astype(np.float32))
+    r_q, _, _ = O.qkv_rope(qa, None, k, None, None, zero, one, nq, nkv)
+    h = qa.reshape(B, T, nq, 2, 64).astype(np.float32)
+    want = np.stack([-h[:, :, :, 1], h[:, :, :, 0]], axis=3).reshape(qa.shape)
+    assert np.array_equal(r_q.astype(np.float32), want)
+    # cos / sin shared over the batch ([1, T, 128]) equal the broadcast rows
+    c1, s1 = _qwen_cos_sin(1, T, offsets=False)
+    cb, sb = np.repeat(c1, B, axis=0), np.repeat(s1, B, axis=0)
+    a1 = O.qkv_rope(qa, qb, k, va, vb, c1, s1, nq, nkv, 2.0, 2.0)
+    a2 = O.qkv_rope(qa, qb, k, va, vb, cb, sb, nq, nkv, 2.0, 2.0)
+    assert all(np.array_equal(x_, y_) for x_, y_ in zip(a1, a2))
