@@ -351,6 +351,54 @@ def swiglu_kernel_times(block, x, dy, steps, warmup):
     return out
 
 
+def bench_qkv_rope(dev, g, steps, warmup):
+    """The q/k/v LoRA-add + RoPE + cast kernel (mxs_qkv_rope) at one layer of the model, 1024
+    tokens (12 q heads, 2 k/v heads of 128): forward with the projections' LoRA outputs added
+    (the reference's call, solution/attention.py:271-276) and without (LoRA already inside the
+    fused projections: q and k rotated, v passed through), and the backward (dq, dk rotated
+    back, dv copied).  HBM-bound: GB/s over the bytes each launch must move."""
+    from mindxsoup_amd import kernels
+
+    T, nq, nkv, D = M_TOKENS, 12, 2, 128
+
+    def t(h):
+        return torch.randn((1, T, h * D), device=dev, generator=g).half()
+
+    def heads(x, h):
+        return x.view(1, T, h, D).transpose(1, 2)
+
+    qa, qb, k, va, vb = t(nq), t(nq), t(nkv), t(nkv), t(nkv)
+    pos = torch.arange(T, device=dev, dtype=torch.float32)
+    inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, device=dev, dtype=torch.float32) / D))
+    emb = torch.cat([pos[:, None] * inv[None], pos[:, None] * inv[None]], dim=-1)[None]
+    cos, sin = emb.cos().contiguous(), emb.sin().contiguous()
+    qo, ko, vo = t(nq), t(nkv), t(nkv)
+    cs = 2 * T * D * 4  # cos + sin rows read per launch
+    cases = {
+        "fwd_lora_add": ((heads(qa, nq), heads(qb, nq), heads(k, nkv), heads(va, nkv),
+                          heads(vb, nkv)), False, T * D * 2 * (2 * nq + nkv + 2 * nkv) + cs
+                         + T * D * 2 * (nq + 2 * nkv)),
+        "fwd_fused_lora": ((heads(qa, nq), None, heads(k, nkv), None, None), False,
+                           T * D * 2 * 2 * (nq + nkv) + cs),
+        "bwd": ((heads(qa, nq), None, heads(k, nkv), heads(va, nkv), None), True,
+                T * D * 2 * 2 * (nq + 2 * nkv) + cs),
+    }
+    reps = 20
+    res = {}
+    for name, (ins, bwd, nbytes) in cases.items():
+        outs = (heads(qo, nq), heads(ko, nkv), heads(vo, nkv) if ins[3] is not None else None)
+
+        def fn():
+            for _ in range(reps):
+                kernels.qkv_rope(*ins, cos, sin, *outs, backward=bwd, q_scale=2.0, v_scale=2.0)
+
+        ms, _ = graph_time(fn, max(3, steps // 10), max(2, warmup // 5))
+        us = ms * 1e3 / reps
+        res[name] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
+                     "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 3)}
+    return res
+
+
 def bench_fused(dev, steps, warmup):
     g = torch.Generator(device=dev)
     g.manual_seed(1)
@@ -384,6 +432,7 @@ def bench_fused(dev, steps, warmup):
                                "tflops": round(fl / ms / 1e9, 1)}
     del down, ht
     out["mlp_block"] = bench_mlp(dev, g, steps, warmup)
+    out["qkv_rope"] = bench_qkv_rope(dev, g, steps, warmup)
     # config 5: forward + backward of all 28 layers x 7 projections, M = 1024
     layers = []
     for _ in range(LAYERS):

@@ -276,7 +276,8 @@ int mxs_nf4_linear_bwd_dx_glu(const void* dy, int M, int N, int K, const void* p
  * added; backward (backward = 1) rotates by the opposite angle (dq, dk; dv copied).  cos / sin:
  * fp32 rows of 128 with strides (cos_stride_b, cos_stride_t); cos_stride_b may be 0.  q_b, v_b
  * may be NULL; v_a and v_o NULL together (no v heads).  Inputs all fp16 (in_f32 = 0) or all
- * fp32; outputs fp16 or fp32 (out_f32).  Pointers and strides multiples of 4 elements. */
+ * fp32; outputs fp16 or fp32 (out_f32).  Pointers 16-byte aligned, strides multiples of
+ * 16 bytes (8 fp16 or 4 fp32 elements); cos / sin strides multiples of 4. */
 int mxs_qkv_rope(const void* const tensors[8], const int64_t strides[24], const float* cos,
                  const float* sin, int64_t cos_stride_b, int64_t cos_stride_t, int batch,
                  int n_tokens, int n_q, int n_kv, int in_f32, int out_f32, int backward,
