@@ -241,6 +241,47 @@ def proj_bwd(p, saved, s=ALPHA / RANK):
                          1.0 / (1.0 - P_DROP), s, ws=p["ws"])
 
 
+# Projections of one layer whose LoRA row products share a launch (indices into PROJ): forward,
+# those reading the same activations (q/k/v; gate/up); backward, those whose output gradients
+# the model produces together (q/k/v from attention's backward, gate/up from the SwiGLU's).
+FWD_GROUPS = [(0, 1, 2), (3,), (4, 5), (6,)]
+BWD_GROUPS = [(6,), (5, 4), (3,), (2, 1, 0)]
+
+
+def layer_fwd(projs, s=ALPHA / RANK):
+    """Forward of one layer's 7 projections: grouped LoRA row products, then each fused GEMM."""
+    from mindxsoup_amd import kernels
+
+    saved = [None] * len(projs)
+    for grp in FWD_GROUPS:
+        ps = [projs[i] for i in grp]
+        if len(ps) == 1:
+            saved[grp[0]] = proj_fwd(ps[0], s)[1]
+            continue
+        outs = kernels.lora_h_partials_group([p["x"] for p in ps], [p["a"] for p in ps], s,
+                                             [p["keep"] for p in ps], 1.0 / (1.0 - P_DROP),
+                                             [p["b"] for p in ps])
+        for i, p, (hp, at, bt) in zip(grp, ps, outs):
+            _, ht = kernels.nf4_linear_fwd_hp(p["x"], p["packed"], p["st"], hp, p["b"],
+                                              ws=p["ws"])
+            saved[i] = (ht, at, bt)
+    return saved
+
+
+def layer_bwd(projs, saved, s=ALPHA / RANK):
+    """Backward of one layer's 7 projections in reverse order, each group's dHs in one launch."""
+    from mindxsoup_amd.linear4bit import lora_backward, prepare_dh
+
+    for grp in BWD_GROUPS:
+        ps = [projs[i] for i in grp]
+        pre = prepare_dh([(p["dy"], saved[i][2], p["k"], s, (True, True, True))
+                          for i, p in zip(grp, ps)])
+        for i, p, kw in zip(grp, ps, pre):
+            ht, at, bt = saved[i]
+            lora_backward(p["dy"], p["x"], p["keep"], ht, at, bt, p["packed"], p["st"],
+                          1.0 / (1.0 - P_DROP), s, ws=p["ws"], **kw)
+
+
 def graph_time(fn, steps, warmup):
     """Capture fn() in a HIP graph, replay: mean ms per replay (events on the capture stream's
     replay stream) and the wall-clock mean."""
@@ -449,18 +490,28 @@ def bench_fused(dev, steps, warmup):
     def step():
         saved = []
         for projs in layers:
+            saved.append(layer_fwd(projs))
+        for projs, hts in zip(reversed(layers), reversed(saved)):
+            layer_bwd(projs, hts)
+
+    def step_ungrouped():  # each projection's LoRA row products in launches of their own
+        saved = []
+        for projs in layers:
             saved.append([proj_fwd(p)[1] for p in projs])
         for projs, hts in zip(reversed(layers), reversed(saved)):
             for p, ht in zip(reversed(projs), reversed(hts)):
                 proj_bwd(p, ht)
 
     ms, wall = graph_time(step, max(3, steps // 5), max(2, warmup // 5))
+    ms_u, _ = graph_time(step_ungrouped, max(3, steps // 5), max(2, warmup // 5))
     fl = LAYERS * sum(proj_flops(n, k) for _, n, k in PROJ)
     tf = fl / ms / 1e9
     out["config5_stack"] = {"ms_per_step": round(ms, 4), "wall_ms_per_step": round(wall, 4),
                             "tflop_per_step": round(fl / 1e12, 4), "tflops": round(tf, 1),
                             "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4),
-                            "launches": "one HIP graph per step"}
+                            "launches": "one HIP graph per step",
+                            "lora_rows": "q/k/v and gate/up grouped per launch",
+                            "ungrouped_ms_per_step": round(ms_u, 4)}
     del layers
     return out
 

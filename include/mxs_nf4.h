@@ -214,6 +214,31 @@ int mxs_lora_h_partials(const void* x, int M, int K, const void* lora_a, int r, 
 int mxs_lora_dh_partials(const void* dy, int M, int N, const void* lora_bt, int r, float s,
                          int ldt, float* partials, hipStream_t stream);
 
+/* mxs_lora_h_partials for n (1..4) projections over the same M tokens in ONE launch: the q, k,
+ * v (or gate, up) projections of a layer read the same activations (solution/attention.py
+ * :259-266, solution/mlp.py:42-43).  Problem i: x[i] [M, K[i]], lora_a[i] [r, K[i]], mask[i]
+ * (mask may be NULL, or any entry), the side outputs at[i], lora_b[i] / N[i] / bt[i] (each array
+ * may be NULL), partials[i] [mxs_lora_slices(M, K[i])][ldt][r].  Each problem's workgroups run
+ * as its own launch would: the partials are the same bits as n separate calls. */
+int mxs_lora_h_partials_group(int n, const void* const x[], int M, const int K[],
+                              const void* const lora_a[], int r, const void* const mask[],
+                              float mask_scale, float s, int ldt, void* const at[],
+                              const void* const lora_b[], const int N[], void* const bt[],
+                              float* const partials[], hipStream_t stream);
+
+/* mxs_lora_dh_partials for n (1..4) projections in ONE launch (their output gradients arrive
+ * together: q/k/v from attention's backward, gate/up from the SwiGLU's); same bits as n calls. */
+int mxs_lora_dh_partials_group(int n, const void* const dy[], int M, const int N[],
+                               const void* const lora_bt[], int r, float s, int ldt,
+                               float* const partials[], hipStream_t stream);
+
+/* mxs_lora_dh without a workspace (one launch per problem: finished dh [M, r] and dht [r, ldt])
+ * for n (1..4) projections in ONE launch; same bits as n such calls.  The input of
+ * mxs_nf4_linear_bwd_dx_grads for each. */
+int mxs_lora_dh_group(int n, const void* const dy[], int M, const int N[],
+                      const void* const lora_bt[], int r, float s, int ldt, void* const dh[],
+                      void* const dht[], hipStream_t stream);
+
 /* The fp16 operand from such partial sums [slices][ldt][r] (1 <= slices <= 4; added in slice
  * order and rounded, the value the fused GEMMs compute from the same partials): out [M, r] (may
  * be NULL) and outT [r, ldt] with zeros past M.  Finishes dh from mxs_lora_dh_partials for

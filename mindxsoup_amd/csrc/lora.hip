@@ -60,27 +60,29 @@ struct RowsArgs {
   int partial_out;        // write the partials even for one slice; no final fp16 outputs
 };
 
-// out[m][c] = fp16(s * sum_k drop(P)[m][k] * R[c][k]) for the 16 rows of blockIdx.x.
-__global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
-  extern __shared__ float red[];  // [waves][16][r + 1]
-  const int nw = blockDim.x >> 6;
+// out[m][c] = fp16(s * sum_k drop(P)[m][k] * R[c][k]) for the 16 rows of row block rb, over
+// reduction slice `slice` of `slices`.  Waves [0, nw) reduce; any waves past nw (a grouped
+// launch sized for another problem) only take part in the barrier and the stores, so the result
+// is the same bits as a launch of exactly nw waves.  wg of n_wg places the side outputs.
+__device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice, int slices,
+                                           int nw, int wg, int n_wg, float* red) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int m0 = blockIdx.x * 16;
+  const int m0 = rb * 16;
   const int row = m0 + (lane & 15);
   const int g = lane >> 4;
   const int rbn = a.r >> 4;
   const int chunks = a.K >> 5;
-  // reduction slice of this workgroup (blockIdx.y of gridDim.y): chunks [c_beg, c_end)
-  const int cps = (chunks + gridDim.y - 1) / gridDim.y;
-  const int c_beg = blockIdx.y * cps;
+  // reduction slice of this workgroup: chunks [c_beg, c_end)
+  const int cps = (chunks + slices - 1) / slices;
+  const int c_beg = slice * cps;
   const int c_end = min(chunks, c_beg + cps);
   const bool row_ok = row < a.M;
   const int64_t prow = (int64_t)(row_ok ? row : 0) * a.K + 8 * g;
   float4_t acc[kMaxRB];
 #pragma unroll
   for (int b = 0; b < kMaxRB; b++) acc[b] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  for (int c0 = c_beg + wave; c0 < c_end; c0 += kChunksInFlight * nw) {
+  for (int c0 = c_beg + wave; wave < nw && c0 < c_end; c0 += kChunksInFlight * nw) {
     half8_t x[kChunksInFlight];
 #pragma unroll
     for (int u = 0; u < kChunksInFlight; u++) {
@@ -111,14 +113,12 @@ __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
   const int ld = a.r + 1;
 #pragma unroll
   for (int b = 0; b < kMaxRB; b++) {
-    if (b >= rbn) break;
+    if (b >= rbn || wave >= nw) break;
 #pragma unroll
     for (int v = 0; v < 4; v++)
       red[(wave * 16 + 4 * g + v) * ld + 16 * b + (lane & 15)] = acc[b][v];
   }
   // side outputs, spread over the workgroups: R^T [K, r] and B^T [r, N]
-  const int n_wg = gridDim.x * gridDim.y;
-  const int wg = blockIdx.y * gridDim.x + blockIdx.x;
   if (a.rt) {
     const int span = ((a.K + n_wg - 1) / n_wg + 7) & ~7;
     const int k_beg = wg * span, k_end = min(a.K, k_beg + span);
@@ -142,14 +142,41 @@ __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
     if (m >= a.ldt) continue;
     float sum = 0.f;
     for (int w = 0; w < nw; w++) sum += red[(w * 16 + rr) * ld + c];
-    if (gridDim.y > 1 || a.partial_out) {  // this slice's partial, times s
-      a.ws[((int64_t)blockIdx.y * a.ldt + m) * a.r + c] = a.s * sum;
+    if (slices > 1 || a.partial_out) {  // this slice's partial, times s
+      a.ws[((int64_t)slice * a.ldt + m) * a.r + c] = a.s * sum;
       continue;
     }
     const _Float16 h = m < a.M ? (_Float16)(a.s * sum) : (_Float16)0.0f;
     if (m < a.M) a.out[(int64_t)m * a.r + c] = h;
     a.outT[(int64_t)c * a.ldt + m] = h;
   }
+}
+
+__global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
+  extern __shared__ float red[];  // [waves][16][r + 1]
+  rows_block(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y, (int)blockDim.x >> 6,
+             (int)(blockIdx.y * gridDim.x + blockIdx.x), (int)(gridDim.x * gridDim.y), red);
+}
+
+// Several rows problems over the same tokens in one launch (the q/k/v or gate/up projections
+// share their input; their output gradients arrive together): problem i owns workgroups
+// [start[i], start[i+1]), laid out as its own launch's grid, with its own slices and waves.
+constexpr int kMaxGroup = 4;
+struct RowsGroup {
+  RowsArgs p[kMaxGroup];
+  int start[kMaxGroup + 1];
+  int rbs[kMaxGroup], slices[kMaxGroup], nw[kMaxGroup];
+  int n;
+};
+
+__global__ __launch_bounds__(1024) void k_lora_rows_group(RowsGroup g) {
+  extern __shared__ float red[];  // [waves][16][r + 1]
+  const int bid = (int)blockIdx.x;
+  int i = 0;
+  while (i + 1 < g.n && bid >= g.start[i + 1]) i++;
+  const int local = bid - g.start[i];
+  rows_block(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i], g.nw[i], local,
+             g.start[i + 1] - g.start[i], red);
 }
 
 // out[m][c] = fp16(sum of the slices' partials, in slice order) for m < M; outT [r, ldt]
@@ -239,19 +266,48 @@ static int rows_slices(int K, int ldt) {
   return sl < 1 ? 1 : sl > 4 ? 4 : sl;
 }
 
+// Slices and waves of one rows problem.  The workspace size query assumes ldt = M rounded up
+// to 8; any other ldt runs unsliced.  In partial mode the caller sized the partials by
+// mxs_lora_slices(M, K) for its ldt.
+static void rows_plan(const RowsArgs& a, bool have_ws, int* slices, int* nw) {
+  const bool ws_ok = have_ws && (a.partial_out || a.ldt == (a.M + 7) / 8 * 8);
+  *slices = ws_ok ? rows_slices(a.K, (a.M + 7) / 8 * 8) : 1;
+  int w = waves_for(a.K / 32 / *slices);
+  while (w > 1 && (size_t)w * 16 * (a.r + 1) * sizeof(float) > (size_t)kColsLds) w--;
+  *nw = w;
+}
+
 static int rows_launch(RowsArgs a, void* workspace, hipStream_t stream) {
-  // the workspace size query assumes ldt = M rounded up to 8; any other ldt runs unsliced.  In
-  // partial mode the caller sized the partials by mxs_lora_slices(M, K) for its ldt.
-  const bool ws_ok = workspace && (a.partial_out || a.ldt == (a.M + 7) / 8 * 8);
-  const int slices = ws_ok ? rows_slices(a.K, (a.M + 7) / 8 * 8) : 1;
+  int slices, nw;
+  rows_plan(a, workspace != nullptr, &slices, &nw);
   a.ws = static_cast<float*>(workspace);
-  int nw = waves_for(a.K / 32 / slices);
-  while (nw > 1 && (size_t)nw * 16 * (a.r + 1) * sizeof(float) > (size_t)kColsLds) nw--;
   const size_t lds = (size_t)nw * 16 * (a.r + 1) * sizeof(float);
   hipLaunchKernelGGL(k_lora_rows, dim3((a.ldt + 15) / 16, slices), dim3(64 * nw), lds, stream, a);
   if (slices > 1 && !a.partial_out)
     hipLaunchKernelGGL(k_lora_rows_finish, dim3((a.ldt + 63) / 64), dim3(64), 0, stream, a,
                        slices);
+  return check_launch();
+}
+
+// One launch for n rows problems: partial mode (a.ws = the problem's partials, sliced as a
+// single launch with that workspace would be) or finished mode (a.ws null: one slice, fp16
+// out / outT), each as its own launch would run.
+static int rows_group_launch(const RowsArgs* probs, int n, hipStream_t stream) {
+  if (n < 1 || n > kMaxGroup) return MXS_ERR_ARG;
+  RowsGroup g{};
+  g.n = n;
+  int total = 0, nw_max = 1;
+  for (int i = 0; i < n; i++) {
+    g.p[i] = probs[i];
+    rows_plan(g.p[i], g.p[i].ws != nullptr, &g.slices[i], &g.nw[i]);
+    g.rbs[i] = (g.p[i].ldt + 15) / 16;
+    g.start[i] = total;
+    total += g.rbs[i] * g.slices[i];
+    nw_max = g.nw[i] > nw_max ? g.nw[i] : nw_max;
+  }
+  g.start[n] = total;
+  const size_t lds = (size_t)nw_max * 16 * (probs[0].r + 1) * sizeof(float);
+  hipLaunchKernelGGL(k_lora_rows_group, dim3(total), dim3(64 * nw_max), lds, stream, g);
   return check_launch();
 }
 
@@ -390,6 +446,104 @@ int mxs_lora_dh_partials(const void* dy, int M, int N, const void* lora_bt, int 
   a.s = s;
   a.partial_out = 1;
   return rows_launch(a, partials, stream);
+}
+
+int mxs_lora_h_partials_group(int n, const void* const x[], int M, const int K[],
+                              const void* const lora_a[], int r, const void* const mask[],
+                              float mask_scale, float s, int ldt, void* const at[],
+                              const void* const lora_b[], const int N[], void* const bt[],
+                              float* const partials[], hipStream_t stream) {
+  if (n < 1 || n > kMaxGroup || M < 0 || r <= 0 || !x || !K || !lora_a || !partials)
+    return MXS_ERR_ARG;
+  if (M == 0) return MXS_OK;
+  if (r % 16 || r > 16 * kMaxRB || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  RowsArgs probs[kMaxGroup];
+  for (int i = 0; i < n; i++) {
+    const void* mk = mask ? mask[i] : nullptr;
+    void* at_i = at ? at[i] : nullptr;
+    const void* b_i = lora_b ? lora_b[i] : nullptr;
+    void* bt_i = bt ? bt[i] : nullptr;
+    const int n_i = N ? N[i] : 0;
+    if (K[i] < 0 || n_i < 0) return MXS_ERR_ARG;
+    if (!x[i] || !lora_a[i] || !partials[i] || (bt_i && !b_i)) return MXS_ERR_ARG;
+    if (K[i] % 32) return MXS_ERR_SIZE;
+    if (((uintptr_t)x[i] % 16) || ((uintptr_t)lora_a[i] % 16) || (mk && ((uintptr_t)mk % 8)))
+      return MXS_ERR_ALIGN;
+    RowsArgs a{};
+    a.P = static_cast<const _Float16*>(x[i]);
+    a.M = M;
+    a.K = K[i];
+    a.mask = static_cast<const uint8_t*>(mk);
+    a.mscale = mask_scale;
+    a.R = static_cast<const _Float16*>(lora_a[i]);
+    a.r = r;
+    a.ldt = ldt;
+    a.s = s;
+    a.rt = static_cast<_Float16*>(at_i);
+    a.B = static_cast<const _Float16*>(b_i);
+    a.N = n_i;
+    a.bt = static_cast<_Float16*>(bt_i);
+    a.partial_out = 1;
+    a.ws = partials[i];
+    probs[i] = a;
+  }
+  return rows_group_launch(probs, n, stream);
+}
+
+int mxs_lora_dh_partials_group(int n, const void* const dy[], int M, const int N[],
+                               const void* const lora_bt[], int r, float s, int ldt,
+                               float* const partials[], hipStream_t stream) {
+  if (n < 1 || n > kMaxGroup || M < 0 || r <= 0 || !dy || !N || !lora_bt || !partials)
+    return MXS_ERR_ARG;
+  if (M == 0) return MXS_OK;
+  if (r % 16 || r > 16 * kMaxRB || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  RowsArgs probs[kMaxGroup];
+  for (int i = 0; i < n; i++) {
+    if (N[i] < 0 || !dy[i] || !lora_bt[i] || !partials[i]) return MXS_ERR_ARG;
+    if (N[i] % 32) return MXS_ERR_SIZE;
+    if (((uintptr_t)dy[i] % 16) || ((uintptr_t)lora_bt[i] % 16)) return MXS_ERR_ALIGN;
+    RowsArgs a{};
+    a.P = static_cast<const _Float16*>(dy[i]);
+    a.M = M;
+    a.K = N[i];
+    a.mscale = 1.0f;
+    a.R = static_cast<const _Float16*>(lora_bt[i]);
+    a.r = r;
+    a.ldt = ldt;
+    a.s = s;
+    a.partial_out = 1;
+    a.ws = partials[i];
+    probs[i] = a;
+  }
+  return rows_group_launch(probs, n, stream);
+}
+
+int mxs_lora_dh_group(int n, const void* const dy[], int M, const int N[],
+                      const void* const lora_bt[], int r, float s, int ldt, void* const dh[],
+                      void* const dht[], hipStream_t stream) {
+  if (n < 1 || n > kMaxGroup || M < 0 || r <= 0 || !dy || !N || !lora_bt || !dh || !dht)
+    return MXS_ERR_ARG;
+  if (M == 0) return MXS_OK;
+  if (r % 16 || r > 16 * kMaxRB || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  RowsArgs probs[kMaxGroup];
+  for (int i = 0; i < n; i++) {
+    if (N[i] < 0 || !dy[i] || !lora_bt[i] || !dh[i] || !dht[i]) return MXS_ERR_ARG;
+    if (N[i] % 32) return MXS_ERR_SIZE;
+    if (((uintptr_t)dy[i] % 16) || ((uintptr_t)lora_bt[i] % 16)) return MXS_ERR_ALIGN;
+    RowsArgs a{};
+    a.P = static_cast<const _Float16*>(dy[i]);
+    a.M = M;
+    a.K = N[i];
+    a.mscale = 1.0f;
+    a.R = static_cast<const _Float16*>(lora_bt[i]);
+    a.r = r;
+    a.ldt = ldt;
+    a.s = s;
+    a.out = static_cast<_Float16*>(dh[i]);
+    a.outT = static_cast<_Float16*>(dht[i]);
+    probs[i] = a;
+  }
+  return rows_group_launch(probs, n, stream);
 }
 
 int mxs_lora_finish(const float* partials, int slices, int M, int r, int ldt, void* out,

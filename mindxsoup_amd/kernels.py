@@ -204,6 +204,101 @@ def lora_dh_partials(dy2d, lora_bt, s):
     return dhp
 
 
+def _ptr_array(ts):
+    import ctypes
+
+    return (ctypes.c_void_p * len(ts))(*[None if t is None else t.data_ptr() for t in ts])
+
+
+def _int_array(vals):
+    import ctypes
+
+    return (ctypes.c_int * len(vals))(*vals)
+
+
+def lora_h_partials_group(xs, lora_as, s, masks=None, mask_scale=1.0, lora_bs=None):
+    """lora_h_partials for up to 4 projections over the same tokens in one launch: a list of
+    (hp, at, bt) as lora_h_partials returns them, the same bits.  xs may repeat one tensor (the
+    q/k/v or gate/up projections share their input)."""
+    n = len(xs)
+    masks = masks or [None] * n
+    lora_bs = lora_bs or [None] * n
+    xs = [x.contiguous() for x in xs]
+    M = xs[0].shape[0]
+    if any(x.shape[0] != M for x in xs) or not 1 <= n <= 4:
+        raise ValueError("1..4 problems over the same number of tokens")
+    a16 = [a.to(torch.float16).contiguous() for a in lora_as]
+    r = a16[0].shape[0]
+    dev = xs[0].device
+    outs, bts, b16 = [], [], []
+    for x, a, b in zip(xs, a16, lora_bs):
+        K = x.shape[1]
+        if a.shape != (r, K):
+            raise ValueError("lora_a must be [r, K] with one r")
+        hp = torch.empty((lora_slices(M, K), _ldt(M), r), dtype=torch.float32, device=dev)
+        at = torch.empty((K, r), dtype=torch.float16, device=dev)
+        bt = None
+        if b is not None:
+            b = b.to(torch.float16).contiguous()
+            if b.shape[1] != r:
+                raise ValueError("lora_b must be [N, r]")
+            bt = torch.empty((r, b.shape[0]), dtype=torch.float16, device=dev)
+        outs.append((hp, at, bt))
+        bts.append(bt)
+        b16.append(b)
+    masks = [_c(m) for m in masks]
+    _lib.call("mxs_lora_h_partials_group", n, _ptr_array(xs), M,
+              _int_array([x.shape[1] for x in xs]), _ptr_array(a16), r, _ptr_array(masks),
+              float(mask_scale), float(s), _ldt(M), _ptr_array([o[1] for o in outs]),
+              _ptr_array(b16), _int_array([0 if b is None else b.shape[0] for b in b16]),
+              _ptr_array(bts), _ptr_array([o[0] for o in outs]), _lib.stream_of(dev))
+    return outs
+
+
+def lora_dh_partials_group(dys, lora_bts, s):
+    """lora_dh_partials for up to 4 projections in one launch: a list of partials, the same bits
+    as separate calls."""
+    n = len(dys)
+    dys = [d.contiguous() for d in dys]
+    M = dys[0].shape[0]
+    if any(d.shape[0] != M for d in dys) or not 1 <= n <= 4 or len(lora_bts) != n:
+        raise ValueError("1..4 problems over the same number of tokens")
+    bts = [b.contiguous() for b in lora_bts]
+    r = bts[0].shape[0]
+    for d, b in zip(dys, bts):
+        if b.shape != (r, d.shape[1]):
+            raise ValueError("lora_bt must be [r, N] with one r")
+    dev = dys[0].device
+    outs = [torch.empty((lora_slices(M, d.shape[1]), _ldt(M), r), dtype=torch.float32,
+                        device=dev) for d in dys]
+    _lib.call("mxs_lora_dh_partials_group", n, _ptr_array(dys), M,
+              _int_array([d.shape[1] for d in dys]), _ptr_array(bts), r, float(s), _ldt(M),
+              _ptr_array(outs), _lib.stream_of(dev))
+    return outs
+
+
+def lora_dh_group(dys, lora_bts, s):
+    """lora_dh(dy, None, s, lora_bt=bt, one_launch=True) for up to 4 projections in one launch:
+    a list of (dh [M, r], dht [r, ldt]), the same bits as separate calls."""
+    n = len(dys)
+    dys = [d.contiguous() for d in dys]
+    M = dys[0].shape[0]
+    if any(d.shape[0] != M for d in dys) or not 1 <= n <= 4 or len(lora_bts) != n:
+        raise ValueError("1..4 problems over the same number of tokens")
+    bts = [b.contiguous() for b in lora_bts]
+    r = bts[0].shape[0]
+    for d, b in zip(dys, bts):
+        if b.shape != (r, d.shape[1]):
+            raise ValueError("lora_bt must be [r, N] with one r")
+    dev = dys[0].device
+    dh = [torch.empty((M, r), dtype=torch.float16, device=dev) for _ in dys]
+    dht = [torch.empty((r, _ldt(M)), dtype=torch.float16, device=dev) for _ in dys]
+    _lib.call("mxs_lora_dh_group", n, _ptr_array(dys), M, _int_array([d.shape[1] for d in dys]),
+              _ptr_array(bts), r, float(s), _ldt(M), _ptr_array(dh), _ptr_array(dht),
+              _lib.stream_of(dev))
+    return list(zip(dh, dht))
+
+
 def nf4_linear_fwd_hp(x2d, packed, state, lora_hp, lora_b, bias=None, cfg=-1, splits=1, ws=None):
     """(y, ht): Y = x2d @ W^T (+ bias) + fp16(sum of lora_hp) @ lora_b^T, and that fp16 LoRA
     operand transposed [r, ldt] (zeros past M)."""

@@ -78,8 +78,40 @@ class NF4LinearFunction(torch.autograd.Function):
         return grad_x, None, None, None
 
 
+def _dh_kind(M, N, K, r, want_x, want_a, want_b):
+    """How lora_backward takes dHs for this projection: "finished" (one launch, for the dX GEMM
+    that also computes dA and dB) or "partials" (finished by the dX GEMM)."""
+    fused = want_x and want_a and want_b and kernels.bwd_grads_fused(M, N, K, r)
+    return "finished" if fused else "partials"
+
+
+def prepare_dh(items):
+    """dHs for several projections at once, grouped into one launch per kind (and LoRA scaling):
+    items are (dy [M, N], lora_bt [r, N], K, s, (want_x, want_a, want_b)); returns for each the
+    keyword arguments (dh= or dhp=) of lora_backward.  The q/k/v projections' output gradients
+    arrive together from attention's backward, gate/up's from the SwiGLU's."""
+    out = [None] * len(items)
+    groups = {}
+    for i, (dy, bt, K, s, wants) in enumerate(items):
+        M, N = dy.shape
+        kind = _dh_kind(M, N, K, bt.shape[0], *wants)
+        groups.setdefault((kind, float(s)), []).append(i)
+    for (kind, s), idx in groups.items():
+        for j in range(0, len(idx), 4):
+            part = idx[j:j + 4]
+            dys = [items[i][0] for i in part]
+            bts = [items[i][1] for i in part]
+            if kind == "finished":
+                for i, r in zip(part, kernels.lora_dh_group(dys, bts, s)):
+                    out[i] = {"dh": r}
+            else:
+                for i, r in zip(part, kernels.lora_dh_partials_group(dys, bts, s)):
+                    out[i] = {"dhp": r}
+    return out
+
+
 def lora_backward(dy, x2d, keep, ht, at, bt, packed, state, mask_scale, s, want_x=True,
-                  want_a=True, want_b=True, ws=None):
+                  want_a=True, want_b=True, ws=None, dh=None, dhp=None):
     """(dX, dA, dB) of one NF4 + LoRA projection (None where not wanted), on the current stream.
     Where the dX GEMM leaves CUs idle (kernels.bwd_grads_fused: 1536-wide projections at 1024
     tokens) and all three are wanted: dHs = s * dY B finished in one launch, then one launch for
@@ -88,14 +120,17 @@ def lora_backward(dy, x2d, keep, ht, at, bt, packed, state, mask_scale, s, want_
     one launch.  (A variant that ran the weight gradients on a second stream beside the GEMM
     lost more to the cross-queue waits of the graph, 5-10 us per fork and join, than it
     gained.)  `ws`: an optional workspace for every call of this projection
-    (kernels.projection_workspace_bytes)."""
+    (kernels.projection_workspace_bytes).  `dh` = (dh, dht) or `dhp` (partials): dHs already
+    computed, of the kind this projection's plan takes (prepare_dh)."""
     M, N = dy.shape
     K, r = x2d.shape[1], bt.shape[0]
-    if want_x and want_a and want_b and kernels.bwd_grads_fused(M, N, K, r):
-        dh, dht = kernels.lora_dh(dy, None, s, lora_bt=bt, one_launch=True)
-        return kernels.nf4_linear_bwd_dx_grads(dy, packed, state, dh, at, dht, ht, x2d, keep,
-                                               mask_scale, ws=ws)
-    dhp = kernels.lora_dh_partials(dy, bt, s)
+    if _dh_kind(M, N, K, r, want_x, want_a, want_b) == "finished":
+        if dh is None:
+            dh = kernels.lora_dh(dy, None, s, lora_bt=bt, one_launch=True)
+        return kernels.nf4_linear_bwd_dx_grads(dy, packed, state, dh[0], at, dh[1], ht, x2d,
+                                               keep, mask_scale, ws=ws)
+    if dhp is None:
+        dhp = kernels.lora_dh_partials(dy, bt, s)
     want_g = want_a or want_b
     dx = dht = None
     if want_x or want_g:

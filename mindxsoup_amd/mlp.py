@@ -23,7 +23,7 @@ SwiGLU reads it, as the separate kernel does, and both evaluate the same fp32 fo
 import torch
 
 from . import direct, kernels, linear4bit
-from .linear4bit import LoraLinear4bit, _cast_bias_once, _direct_ok, lora_backward
+from .linear4bit import LoraLinear4bit, _cast_bias_once, _direct_ok, lora_backward, prepare_dh
 from .silu_mul import silu_mul
 
 FUSED_SWIGLU = True  # FEATURES["mlp_fused_swiglu"]
@@ -56,11 +56,17 @@ class NF4LoraMLPFunction(torch.autograd.Function):
         inter, hidden = pu.state.shape
         g_a, g_b, u_a, u_b, d_a, d_b = (t.to(torch.float16).contiguous()
                                         for t in (ga, gb, ua, ub, da, db))
-        hp, at_g, bt_g = kernels.lora_h_partials(x2d, g_a, pg.s, pg.keep, pg.mask_scale,
-                                                 lora_b=g_b)
-        gate, ht_g = kernels.nf4_linear_fwd_hp(x2d, pg.packed, pg.state, hp, g_b, pg.bias)
-        hp, at_u, bt_u = kernels.lora_h_partials(x2d, u_a, pu.s, pu.keep, pu.mask_scale,
-                                                 lora_b=u_b)
+        # gate's and up's LoRA row products read the same x: one launch when they can share it
+        if pg.s == pu.s and pg.mask_scale == pu.mask_scale:
+            (hp_g, at_g, bt_g), (hp, at_u, bt_u) = kernels.lora_h_partials_group(
+                [x2d, x2d], [g_a, u_a], pg.s, [pg.keep, pu.keep], pg.mask_scale, [g_b, u_b])
+        else:
+            hp_g, at_g, bt_g = kernels.lora_h_partials(x2d, g_a, pg.s, pg.keep, pg.mask_scale,
+                                                       lora_b=g_b)
+            hp, at_u, bt_u = kernels.lora_h_partials(x2d, u_a, pu.s, pu.keep, pu.mask_scale,
+                                                     lora_b=u_b)
+        gate, ht_g = kernels.nf4_linear_fwd_hp(x2d, pg.packed, pg.state, hp_g, g_b, pg.bias)
+        del hp_g
         if kernels.glu_fused(M, inter, hidden, False):
             up, h, ht_u = kernels.nf4_linear_fwd_glu(x2d, pu.packed, pu.state, gate, hp, u_b,
                                                      pu.bias)
@@ -103,13 +109,16 @@ class NF4LoraMLPFunction(torch.autograd.Function):
             grads_d = kernels.lora_grads(dht_d, ht_d, h, dy, pd.keep, pd.mask_scale,
                                          want_a=need[5], want_b=need[6])
         del h
-        # up_proj and gate_proj with d(up) and d(gate) as their incoming gradients
+        # up_proj and gate_proj with d(up) and d(gate) as their incoming gradients; their dHs
+        # in one launch
+        wants_u, wants_g = (need[0], need[3], need[4]), (need[0], need[1], need[2])
+        pre_u, pre_g = prepare_dh([(up, bt_u, x2d.shape[1], pu.s, wants_u),
+                                   (gate, bt_g, x2d.shape[1], pg.s, wants_g)])
         dx, dua, dub = lora_backward(up, x2d, pu.keep, ht_u, at_u, bt_u, pu.packed, pu.state,
-                                     pu.mask_scale, pu.s, want_x=need[0], want_a=need[3],
-                                     want_b=need[4])
+                                     pu.mask_scale, pu.s, *wants_u, **pre_u)
+        del pre_u
         dxg, dga, dgb = lora_backward(gate, x2d, pg.keep, ht_g, at_g, bt_g, pg.packed, pg.state,
-                                      pg.mask_scale, pg.s, want_x=need[0], want_a=need[1],
-                                      want_b=need[2])
+                                      pg.mask_scale, pg.s, *wants_g, **pre_g)
         if dx is not None:
             dx += dxg
         grads = [dga, dgb, dua, dub, grads_d[0], grads_d[1]]
