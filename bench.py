@@ -261,6 +261,13 @@ def layer_fwd(projs, s=ALPHA / RANK):
         outs = kernels.lora_h_partials_group([p["x"] for p in ps], [p["a"] for p in ps], s,
                                              [p["keep"] for p in ps], 1.0 / (1.0 - P_DROP),
                                              [p["b"] for p in ps])
+        if grp == (0, 1, 2):  # q, k, v: one GEMM launch (k and v alone would plan split-K)
+            ys = kernels.nf4_linear_fwd_hp_group([p["x"] for p in ps], [p["packed"] for p in ps],
+                                                 [p["st"] for p in ps], [o[0] for o in outs],
+                                                 [p["b"] for p in ps])
+            for i, (_, at, bt), (_, ht) in zip(grp, outs, ys):
+                saved[i] = (ht, at, bt)
+            continue
         for i, p, (hp, at, bt) in zip(grp, ps, outs):
             _, ht = kernels.nf4_linear_fwd_hp(p["x"], p["packed"], p["st"], hp, p["b"],
                                               ws=p["ws"])

@@ -267,6 +267,22 @@ int mxs_silu_mul(const void* gate, const void* up, void* out, int64_t n, hipStre
  * SiluMulInPlace.backward (solution/silu_mul.py:65-71) does. */
 int mxs_silu_mul_bwd(const void* grad, void* gate, void* up, int64_t n, hipStream_t stream);
 
+/* mxs_nf4_linear_fwd_hp for n (1..4) projections of one input width K over the same M tokens in
+ * ONE launch (the q, k and v projections of a layer read the same activations,
+ * solution/attention.py:259-266): problem i has x[i] [M, K], out_features N[i], its NF4 weight
+ * (packed[i] .. offset[i]), bias[i], LoRA partials lora_hp[i] (hp_slices, ldt, r shared),
+ * lora_b[i] [N[i], r], lora_ht[i], output y[i] [M, N[i]]; the bias, lora_hp, lora_b and lora_ht
+ * arrays may be NULL (or any entry: no bias / no LoRA term).  Every problem runs on 128x128
+ * tiles with 8 producer waves, unsplit: the same bits as mxs_nf4_linear_fwd_hp with cfg 10 and
+ * one split for each (the N = 256 projections alone would plan split-K tiles and a reduce). */
+int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, const int N[],
+                                const void* const packed[], const void* const absmax8[],
+                                const float* const code[], const float* const absmax2[],
+                                const float* const offset[], const void* const bias[],
+                                const float* const lora_hp[], int hp_slices, int ldt,
+                                const void* const lora_b[], int r, void* const lora_ht[],
+                                void* const y[], hipStream_t stream);
+
 /* The up projection's forward with the SwiGLU after it (solution/mlp.py:42-43:
  * silu_mul(gate_proj(x), up_proj(x))): mxs_nf4_linear_fwd_hp (lora_hp may be NULL: no LoRA
  * term) writing y = up_proj(x) [M, N] and h = silu(gate) * y [M, N] from the same tile, with

@@ -220,7 +220,7 @@ struct AccStart {
     }
     // lora_w is [Nc, r] in both directions (the backward pass gets lora_A transposed), so the
     // W-side operand is one 16-byte load per tile and 16 ranks
-    const bool write_t = a.lora_hp && a.lora_ht && blockIdx.x == 0 && nb == 0;
+    const bool write_t = a.lora_hp && a.lora_ht && nb == 0;  // first column tile
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       const int m = mb + i * 32 + lrow;
@@ -279,7 +279,7 @@ struct AccStart {
 #pragma unroll
     for (int j = 0; j < TN; j++)
       wf[j] = *reinterpret_cast<const half8_t*>(ls + (ls_cols + wc0 + j * 32 + lrow) * 16 + 8 * lseg);
-    const bool write_t = a.lora_hp && a.lora_ht && blockIdx.x == 0 && nb == 0;
+    const bool write_t = a.lora_hp && a.lora_ht && nb == 0;  // first column tile
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       const half8_t hf =
@@ -1479,8 +1479,9 @@ struct ACopy {
 // the other half of a 2-deep B buffer while the consumers multiply kt.  Everything a producer
 // issues in one K-step is waited for at the start of the next, and one workgroup barrier per
 // K-step hands the buffers over.
+// One output tile (bx, by) of the warp-specialized GEMM; split index blockIdx.z.
 template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU>
-__global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
+__device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
   constexpr int WM = BM / CWM, WN = BN / CWN, TM = WM / 32, TN = WN / 32;
   constexpr int NTP = 64 * PW;  // producer threads
   static_assert(CWM * CWN == 4 && WM % 32 == 0 && WN % 32 == 0, "consumer wave tiles");
@@ -1502,24 +1503,10 @@ __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
   __shared__ float2_t s_pair[256];
   __shared__ float s_code[256];
 
-  if constexpr (BWD && BM == 128) {
-    // grid rows past the GEMM's: LoRA gradient workgroups (before any barrier of the tiles).
-    // Only the 128-row tiles take them (the plans that leave CUs idle); compiling the branch
-    // into the others would only change their register allocation.
-    const int gy = (a.M + BM - 1) / BM;
-    if ((int)blockIdx.y >= gy) {
-      const int id = ((int)blockIdx.y - gy) * (int)gridDim.x + (int)blockIdx.x;
-      if (id < a.cols_blocks)
-        lora_cols_block<kFusedColsCPL>(a.cp0, a.cp1, a.cols_cb0, a.M, a.cols_ldt, a.r, id,
-                                       a.cols_nw, reinterpret_cast<float*>(smem));
-      return;
-    }
-  }
-
   const int t = threadIdx.x;
   const int lane = t & 63;
-  const int m0 = blockIdx.y * BM;
-  const int n0 = blockIdx.x * BN;
+  const int m0 = by * BM;
+  const int n0 = bx * BN;
   const int n_steps = a.Kr / kBK;
   const int kt0 = blockIdx.z * a.steps_per_split;
   const int kt1 = min(n_steps, kt0 + a.steps_per_split);
@@ -1717,6 +1704,47 @@ __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
   }
 }
 
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU>
+__global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws(GemmArgs a) {
+  if constexpr (BWD && BM == 128) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
+    // grid rows past the GEMM's: LoRA gradient workgroups (before any barrier of the tiles).
+    // Only the 128-row tiles take them (the plans that leave CUs idle); compiling the branch
+    // into the others would only change their register allocation.
+    const int gy = (a.M + BM - 1) / BM;
+    if ((int)blockIdx.y >= gy) {
+      const int id = ((int)blockIdx.y - gy) * (int)gridDim.x + (int)blockIdx.x;
+      if (id < a.cols_blocks)
+        lora_cols_block<kFusedColsCPL>(a.cp0, a.cp1, a.cols_cb0, a.M, a.cols_ldt, a.r, id,
+                                       a.cols_nw, reinterpret_cast<float*>(smem));
+      return;
+    }
+  }
+
+  ws_tile<BM, BN, CWM, CWN, BWD, PW, NS, GLU>(a, (int)blockIdx.x, (int)blockIdx.y);
+}
+
+// Several forward GEMMs in one launch (the q/k/v projections of a layer read the same x):
+// problem i owns workgroups [start[i], start[i+1]), its tiles in row-major order over its
+// gx[i] column tiles.  Unsplit; each tile computes what the problem's own launch of this
+// configuration computes.
+constexpr int kMaxGemmGroup = 4;
+struct GemmGroup {
+  GemmArgs p[kMaxGemmGroup];
+  int start[kMaxGemmGroup + 1];
+  int gx[kMaxGemmGroup];
+  int n;
+};
+
+template <int BM, int BN, int CWM, int CWN, int PW, int NS>
+__global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws_group(GemmGroup g) {
+  const int bid = (int)blockIdx.x;
+  int i = 0;
+  while (i + 1 < g.n && bid >= g.start[i + 1]) i++;
+  const int local = bid - g.start[i];
+  ws_tile<BM, BN, CWM, CWN, false, PW, NS, false>(g.p[i], local % g.gx[i], local / g.gx[i]);
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool BWD>
 static int launch_cfg(const GemmArgs& a0, int splits, hipStream_t stream) {
   using T = Tile<BM, BN, WAVES_M, WAVES_N, BWD>;
@@ -1840,9 +1868,11 @@ static void choose(int M, int Nc, int Kr, int* cfg, int* splits) {
   *splits = sp;
 }
 
-static int gemm_entry(bool bwd, const GemmArgs& a, int cfg, int splits, hipStream_t stream) {
+// Argument checks of one GEMM problem: MXS_OK, an MXS_ERR_* code, or 1 when there is nothing
+// to compute (no tokens or no output columns).
+static int check_gemm(bool bwd, const GemmArgs& a) {
   if (a.M < 0 || a.Nc < 0 || a.Kr < 0) return MXS_ERR_ARG;
-  if (a.M == 0 || a.Nc == 0) return MXS_OK;
+  if (a.M == 0 || a.Nc == 0) return 1;
   if (!a.A || !a.packed || !a.absmax8 || !a.code || !a.absmax2 || !a.offset ||
       (!a.C && a.glu != 2))
     return MXS_ERR_ARG;
@@ -1869,6 +1899,12 @@ static int gemm_entry(bool bwd, const GemmArgs& a, int cfg, int splits, hipStrea
         ((uintptr_t)a.lora_ht % 2) != 0)
       return MXS_ERR_ALIGN;
   }
+  return MXS_OK;
+}
+
+static int gemm_entry(bool bwd, const GemmArgs& a, int cfg, int splits, hipStream_t stream) {
+  const int c = check_gemm(bwd, a);
+  if (c != MXS_OK) return c == 1 ? MXS_OK : c;
   if (cfg < 0) choose(a.M, a.Nc, a.Kr, &cfg, &splits);
   if (cfg >= kNumCfg || cfg == 5) return MXS_ERR_ARG;
   return bwd ? launch_by_id<true>(cfg, a, splits, stream)
@@ -1934,6 +1970,41 @@ static bool glu_plan_ok(int M, int Nc, int Kr, bool bwd) {
   const int bm = kBM[cfg - 6], pw = kPW[cfg - 6];
   return (int64_t)Nc * Kr < (int64_t(1) << 32) && (int64_t)bm * Kr * 2 < (int64_t(1) << 32) &&
          !(bwd && Nc < (pw == 8 ? 16 : 32));
+}
+
+// The forward GEMMs of several problems in one launch of 128x128 tiles with 8 producer waves,
+// unsplit (k_nf4_gemm_ws_group).  Every problem must take that kernel (its 32-bit offsets).
+static int launch_ws_group(const GemmArgs* probs, int n, hipStream_t stream) {
+  constexpr int BM = 128, BN = 128, PW = 8, NS = 4;
+  if (n < 1 || n > kMaxGemmGroup) return MXS_ERR_ARG;
+  GemmGroup g{};
+  g.n = n;
+  int total = 0;
+  for (int i = 0; i < n; i++) {
+    GemmArgs a = probs[i];
+    if ((int64_t)a.Nc * a.Kr >= (int64_t(1) << 32) || (int64_t)BM * a.lda * 2 >= (int64_t(1) << 32))
+      return MXS_ERR_SIZE;
+    a.steps_per_split = a.Kr / kBK;
+    g.p[i] = a;
+    g.gx[i] = (a.Nc + BN - 1) / BN;
+    g.start[i] = total;
+    total += g.gx[i] * ((a.M + BM - 1) / BM);
+  }
+  g.start[n] = total;
+  if (total == 0) return MXS_OK;
+  const size_t lds = (size_t)ws_lds_halfs<BM, BN, false>() * sizeof(_Float16);
+  static bool lds_set = false;  // idempotent attribute; a benign race between threads
+  if (!lds_set) {
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&k_nf4_gemm_ws_group<BM, BN, 2, 2, PW, NS>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+    lds_set = true;
+  }
+  hipLaunchKernelGGL((k_nf4_gemm_ws_group<BM, BN, 2, 2, PW, NS>), dim3(total), dim3(64 * (4 + PW)),
+                     lds, stream, g);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MXS_OK : (int)e;
 }
 
 }  // namespace mxs
@@ -2139,6 +2210,52 @@ int mxs_nf4_linear_bwd_dx_hp(const void* dy, int M, int N, int K, const void* pa
   a.ldc = K;
   set_workspace(a, workspace);
   return gemm_entry(true, a, cfg, splits, stream);
+}
+
+int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, const int N[],
+                                const void* const packed[], const void* const absmax8[],
+                                const float* const code[], const float* const absmax2[],
+                                const float* const offset[], const void* const bias[],
+                                const float* const lora_hp[], int hp_slices, int ldt,
+                                const void* const lora_b[], int r, void* const lora_ht[],
+                                void* const y[], hipStream_t stream) {
+  if (n < 1 || n > kMaxGemmGroup || !x || !N || !packed || !absmax8 || !code || !absmax2 ||
+      !offset || !y)
+    return MXS_ERR_ARG;
+  GemmArgs probs[kMaxGemmGroup];
+  int live = 0;
+  for (int i = 0; i < n; i++) {
+    GemmArgs a{};
+    a.A = static_cast<const _Float16*>(x[i]);
+    a.lda = K;
+    a.packed = static_cast<const uint8_t*>(packed[i]);
+    a.absmax8 = static_cast<const uint8_t*>(absmax8[i]);
+    a.code = code[i];
+    a.absmax2 = absmax2[i];
+    a.offset = offset[i];
+    a.M = M;
+    a.Nc = N[i];
+    a.Kr = K;
+    a.Kw = K;
+    a.bias = bias ? static_cast<const _Float16*>(bias[i]) : nullptr;
+    const float* hp = lora_hp ? lora_hp[i] : nullptr;
+    if (hp) {
+      a.lora_hp = hp;
+      a.hp_slices = hp_slices;
+      a.ldt = ldt;
+      a.lora_ht = lora_ht ? static_cast<_Float16*>(lora_ht[i]) : nullptr;
+      a.lora_w = lora_b ? static_cast<const _Float16*>(lora_b[i]) : nullptr;
+      a.r = r;
+    }
+    a.C = static_cast<_Float16*>(y[i]);
+    a.ldc = N[i];
+    const int c = check_gemm(false, a);
+    if (c == 1) continue;  // nothing to compute for this one
+    if (c != MXS_OK) return c;
+    probs[live++] = a;
+  }
+  if (live == 0) return MXS_OK;
+  return launch_ws_group(probs, live, stream);
 }
 
 int mxs_nf4_linear_glu_fused(int M, int N, int K, int bwd) {

@@ -322,6 +322,49 @@ def nf4_linear_fwd_hp(x2d, packed, state, lora_hp, lora_b, bias=None, cfg=-1, sp
     return y, ht
 
 
+def nf4_linear_fwd_hp_group(x2ds, packeds, states, lora_hps=None, lora_bs=None, biases=None):
+    """nf4_linear_fwd_hp for up to 4 projections of one input width over the same tokens in one
+    launch (128x128 tiles, unsplit): a list of (y, ht) (ht None without LoRA), the bits of
+    nf4_linear_fwd_hp(..., cfg=10, splits=1) for each."""
+    n = len(x2ds)
+    lora_hps = lora_hps or [None] * n
+    lora_bs = lora_bs or [None] * n
+    biases = biases or [None] * n
+    x2ds = [x.contiguous() for x in x2ds]
+    M, K = x2ds[0].shape
+    if not 1 <= n <= 4 or any(x.shape != (M, K) or x.dtype != torch.float16 for x in x2ds):
+        raise ValueError("1..4 fp16 inputs [M, K] of one shape")
+    dev = x2ds[0].device
+    S = ldt = r = 0
+    ys, hts, b16, bias16 = [], [], [], []
+    for st, hp, b, bias in zip(states, lora_hps, lora_bs, biases):
+        nn_, k = st.shape
+        if k != K:
+            raise ValueError("every weight must take K inputs")
+        ys.append(torch.empty((M, nn_), dtype=torch.float16, device=dev))
+        ht = None
+        if hp is not None:
+            S, ldt, r = hp.shape
+            if ldt != _ldt(M) or b is None or b.shape != (nn_, r) or hp.dtype != torch.float32:
+                raise ValueError("lora_hp [slices, ldt, r] fp32 needs lora_b [N, r]")
+            b = b.to(torch.float16).contiguous()
+            ht = torch.empty((r, ldt), dtype=torch.float16, device=dev)
+        hts.append(ht)
+        b16.append(b)
+        bias16.append(None if bias is None else bias.to(torch.float16).contiguous())
+    hps = [None if hp is None else hp.contiguous() for hp in lora_hps]
+    if any(hp is not None and hp.shape != (S, ldt, r) for hp in hps):
+        raise ValueError("LoRA partials of one shape")
+    _lib.call("mxs_nf4_linear_fwd_hp_group", n, _ptr_array(x2ds), M, K,
+              _int_array([st.shape[0] for st in states]), _ptr_array(packeds),
+              _ptr_array([st.absmax for st in states]),
+              _ptr_array([st.state2.code for st in states]),
+              _ptr_array([st.state2.absmax for st in states]),
+              _ptr_array([st.offset for st in states]), _ptr_array(bias16), _ptr_array(hps), S,
+              ldt, _ptr_array(b16), r, _ptr_array(hts), _ptr_array(ys), _lib.stream_of(dev))
+    return list(zip(ys, hts))
+
+
 def nf4_linear_bwd_dx_hp(dy2d, packed, state, lora_dhp, lora_at, mask=None, mask_scale=1.0,
                          cfg=-1, splits=1, ws=None, want_t=True):
     """(dx, dht): dX = dy2d @ W + mask * mask_scale * (fp16(sum of lora_dhp) @ lora_at^T), and

@@ -81,3 +81,53 @@ def test_grouped_finished_dh_equals_one_launch_dh(cuda, M):
     torch.cuda.synchronize()
     for (d1, t1), (d2, t2) in zip(sep, grp):
         assert torch.equal(d1, d2) and torch.equal(t1, t2)
+
+
+def _nf4(dev, n, k, seed, bias=False):
+    from mindxsoup_amd.linear4bit import Linear4bit
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    w = (torch.randn((n, k), device=dev, generator=g) * 0.02).half()
+    b = (torch.randn((n,), device=dev, generator=g) * 0.1).half() if bias else None
+    return Linear4bit.from_weight(w, b)
+
+
+@pytest.mark.parametrize("M", [1024, 300, 37])
+@pytest.mark.parametrize("lora", [True, False])
+def test_grouped_qkv_gemm_equals_separate(cuda, M, lora):
+    """mxs_nf4_linear_fwd_hp_group over q [1536], k [256], v [256] (K = 1536, one x) against
+    each projection's own launch of the same tile configuration, bit for bit; and within 1e-2 of
+    the planned single launches (k and v alone plan split-K tiles and a reduce)."""
+    from mindxsoup_amd import kernels
+
+    print(f"case qkv gemm group M={M} lora={lora}", flush=True)
+    K = 1536
+    layers = [_nf4(cuda, n, K, 300 + i, bias=(i == 0)) for i, n in enumerate((1536, 256, 256))]
+    probs = [_inputs(cuda, M, K, L.out_features, 310 + i) for i, L in enumerate(layers)]
+    x = probs[0][0]
+    packeds = [L.weight.data.view(-1, 1) for L in layers]
+    states = [L.weight.quant_state for L in layers]
+    biases = [L.bias for L in layers]
+    hps = bs = None
+    if lora:
+        outs = kernels.lora_h_partials_group([x] * 3, [p[1] for p in probs], 2.0,
+                                             [p[4] for p in probs], 1 / 0.95,
+                                             [p[2] for p in probs])
+        hps, bs = [o[0] for o in outs], [p[2] for p in probs]
+    grp = kernels.nf4_linear_fwd_hp_group([x] * 3, packeds, states, hps, bs, biases)
+    for i in range(3):
+        if lora:
+            y1, ht1 = kernels.nf4_linear_fwd_hp(x, packeds[i], states[i], hps[i], bs[i],
+                                                biases[i], cfg=10, splits=1)
+            y0, _ = kernels.nf4_linear_fwd_hp(x, packeds[i], states[i], hps[i], bs[i],
+                                              biases[i])
+        else:
+            y1 = kernels.nf4_linear_fwd(x, packeds[i], states[i], biases[i], cfg=10, splits=1)
+            y0, ht1 = kernels.nf4_linear_fwd(x, packeds[i], states[i], biases[i]), None
+        torch.cuda.synchronize()
+        y2, ht2 = grp[i]
+        assert torch.equal(y2, y1), i
+        assert (ht2 is None) == (ht1 is None) and (ht1 is None or torch.equal(ht2, ht1))
+        err = (y2.float() - y0.float()).abs().max() / y0.float().abs().max()
+        assert err < 1e-2, (i, float(err))
