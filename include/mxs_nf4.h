@@ -283,6 +283,26 @@ int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, cons
                                 const void* const lora_b[], int r, void* const lora_ht[],
                                 void* const y[], hipStream_t stream);
 
+/* 1 when mxs_nf4_linear_bwd_dx_grads_group takes these n (1..4) projections [K -> N[i]] at M
+ * tokens: each one mxs_nf4_linear_bwd_grads_fused(M, N[i], K, r) would run as one launch on
+ * 128x128 tiles. */
+int mxs_nf4_linear_bwd_dx_grads_group_ok(int n, int M, const int N[], int K, int r);
+
+/* mxs_nf4_linear_bwd_dx_grads for n (1..4) projections of one input width K in ONE launch (the
+ * q, k and v projections' output gradients arrive together from attention's backward): each
+ * problem's dX tiles, then its dA / dB workgroups; the same bits as the n calls.  Arrays hold
+ * the per-projection pointers (mask may be NULL, or any entry); only where
+ * mxs_nf4_linear_bwd_dx_grads_group_ok says so (else MXS_ERR_SIZE). */
+int mxs_nf4_linear_bwd_dx_grads_group(int n, const void* const dy[], int M, const int N[], int K,
+                                      const void* const packed[], const void* const absmax8[],
+                                      const float* const code[], const float* const absmax2[],
+                                      const float* const offset[], const void* const lora_dh[],
+                                      const void* const lora_at[], int r,
+                                      const void* const mask[], float mask_scale,
+                                      const void* const dht[], const void* const ht[], int ldt,
+                                      const void* const x[], float* const da[],
+                                      float* const db[], void* const dx[], hipStream_t stream);
+
 /* The up projection's forward with the SwiGLU after it (solution/mlp.py:42-43:
  * silu_mul(gate_proj(x), up_proj(x))): mxs_nf4_linear_fwd_hp (lora_hp may be NULL: no LoRA
  * term) writing y = up_proj(x) [M, N] and h = silu(gate) * y [M, N] from the same tile, with

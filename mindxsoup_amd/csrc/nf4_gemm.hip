@@ -1733,16 +1733,29 @@ struct GemmGroup {
   GemmArgs p[kMaxGemmGroup];
   int start[kMaxGemmGroup + 1];
   int gx[kMaxGemmGroup];
+  int tiles[kMaxGemmGroup];  // the problem's tiles; in the backward its LoRA gradient
+                             // workgroups (cols_blocks) follow them
   int n;
 };
 
-template <int BM, int BN, int CWM, int CWN, int PW, int NS>
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS>
 __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws_group(GemmGroup g) {
   const int bid = (int)blockIdx.x;
   int i = 0;
   while (i + 1 < g.n && bid >= g.start[i + 1]) i++;
   const int local = bid - g.start[i];
-  ws_tile<BM, BN, CWM, CWN, false, PW, NS, false>(g.p[i], local % g.gx[i], local / g.gx[i]);
+  if constexpr (BWD) {
+    if (local >= g.tiles[i]) {  // before any barrier of the tiles, as in k_nf4_gemm_ws
+      extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
+      const GemmArgs& a = g.p[i];
+      const int id = local - g.tiles[i];
+      if (id < a.cols_blocks)
+        lora_cols_block<kFusedColsCPL>(a.cp0, a.cp1, a.cols_cb0, a.M, a.cols_ldt, a.r, id,
+                                       a.cols_nw, reinterpret_cast<float*>(smem));
+      return;
+    }
+  }
+  ws_tile<BM, BN, CWM, CWN, BWD, PW, NS, false>(g.p[i], local % g.gx[i], local / g.gx[i]);
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool BWD>
@@ -1972,8 +1985,10 @@ static bool glu_plan_ok(int M, int Nc, int Kr, bool bwd) {
          !(bwd && Nc < (pw == 8 ? 16 : 32));
 }
 
-// The forward GEMMs of several problems in one launch of 128x128 tiles with 8 producer waves,
-// unsplit (k_nf4_gemm_ws_group).  Every problem must take that kernel (its 32-bit offsets).
+// The GEMMs of several problems in one launch of 128x128 tiles with 8 producer waves, unsplit
+// (k_nf4_gemm_ws_group); in the backward each problem's LoRA gradient workgroups follow its
+// tiles.  Every problem must take that kernel (its 32-bit offsets, the backward's column clamp).
+template <bool BWD>
 static int launch_ws_group(const GemmArgs* probs, int n, hipStream_t stream) {
   constexpr int BM = 128, BN = 128, PW = 8, NS = 4;
   if (n < 1 || n > kMaxGemmGroup) return MXS_ERR_ARG;
@@ -1982,29 +1997,96 @@ static int launch_ws_group(const GemmArgs* probs, int n, hipStream_t stream) {
   int total = 0;
   for (int i = 0; i < n; i++) {
     GemmArgs a = probs[i];
-    if ((int64_t)a.Nc * a.Kr >= (int64_t(1) << 32) || (int64_t)BM * a.lda * 2 >= (int64_t(1) << 32))
+    if ((int64_t)a.Nc * a.Kr >= (int64_t(1) << 32) ||
+        (int64_t)BM * a.lda * 2 >= (int64_t(1) << 32) || (BWD && a.Nc < 16) ||
+        (!BWD && a.cols_blocks > 0))
       return MXS_ERR_SIZE;
     a.steps_per_split = a.Kr / kBK;
     g.p[i] = a;
     g.gx[i] = (a.Nc + BN - 1) / BN;
+    g.tiles[i] = g.gx[i] * ((a.M + BM - 1) / BM);
     g.start[i] = total;
-    total += g.gx[i] * ((a.M + BM - 1) / BM);
+    total += g.tiles[i] + (BWD ? a.cols_blocks : 0);
   }
   g.start[n] = total;
   if (total == 0) return MXS_OK;
-  const size_t lds = (size_t)ws_lds_halfs<BM, BN, false>() * sizeof(_Float16);
+  const size_t lds = (size_t)ws_lds_halfs<BM, BN, BWD>() * sizeof(_Float16);
   static bool lds_set = false;  // idempotent attribute; a benign race between threads
   if (!lds_set) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&k_nf4_gemm_ws_group<BM, BN, 2, 2, PW, NS>),
+        reinterpret_cast<const void*>(&k_nf4_gemm_ws_group<BM, BN, 2, 2, BWD, PW, NS>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
     lds_set = true;
   }
-  hipLaunchKernelGGL((k_nf4_gemm_ws_group<BM, BN, 2, 2, PW, NS>), dim3(total), dim3(64 * (4 + PW)),
-                     lds, stream, g);
+  hipLaunchKernelGGL((k_nf4_gemm_ws_group<BM, BN, 2, 2, BWD, PW, NS>), dim3(total),
+                     dim3(64 * (4 + PW)), lds, stream, g);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MXS_OK : (int)e;
+}
+
+// The arguments of a dX GEMM whose launch also computes the LoRA gradients (its workgroups past
+// the tiles): the gradients' checks (mxs_lora_grads); the GEMM's follow in check_gemm.
+static int dx_grads_args(const void* dy, int M, int N, int K, const void* packed,
+                         const void* absmax8, const float* code, const float* absmax2,
+                         const float* offset, const void* lora_dh, const void* lora_at, int r,
+                         const void* mask, float mask_scale, const void* dht, const void* ht,
+                         int ldt, const void* x, float* da, float* db, void* dx, int nw,
+                         GemmArgs& a) {
+  if (r % 16 || K % 8 || N % 8 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  if (((uintptr_t)x % 16) || ((uintptr_t)dht % 16) || ((uintptr_t)dy % 16) ||
+      ((uintptr_t)ht % 16) || (mask && ((uintptr_t)mask % 8)))
+    return MXS_ERR_ALIGN;
+  a = GemmArgs{};
+  a.A = static_cast<const _Float16*>(dy);
+  a.lda = N;
+  a.packed = static_cast<const uint8_t*>(packed);
+  a.absmax8 = static_cast<const uint8_t*>(absmax8);
+  a.code = code;
+  a.absmax2 = absmax2;
+  a.offset = offset;
+  a.M = M;
+  a.Nc = K;
+  a.Kr = N;
+  a.Kw = K;
+  a.lora_h = static_cast<const _Float16*>(lora_dh);
+  a.lora_w = static_cast<const _Float16*>(lora_at);
+  a.r = r;
+  a.mask = static_cast<const uint8_t*>(mask);
+  a.mask_scale = mask_scale;
+  a.C = static_cast<_Float16*>(dx);
+  a.ldc = K;
+  ColsProblem& pa = a.cp0;  // dA [r, K] = dHs^T . drop(X)
+  pa.PT = static_cast<const _Float16*>(dht);
+  pa.Q = static_cast<const _Float16*>(x);
+  pa.mask = static_cast<const uint8_t*>(mask);
+  pa.mscale = mask_scale;
+  pa.Nq = K;
+  pa.out = da;
+  pa.out_rn = 1;
+  ColsProblem& pb = a.cp1;  // dB [N, r] = dY^T . Hs
+  pb.PT = static_cast<const _Float16*>(ht);
+  pb.Q = static_cast<const _Float16*>(dy);
+  pb.mscale = 1.0f;
+  pb.Nq = N;
+  pb.out = db;
+  pb.out_rn = 0;
+  constexpr int WC = 16 * kFusedColsCPL;
+  a.cols_cb0 = (K + WC - 1) / WC;
+  a.cols_blocks = a.cols_cb0 + (N + WC - 1) / WC;
+  a.cols_ldt = ldt;
+  a.cols_nw = nw;
+  return MXS_OK;
+}
+
+// Problems the grouped dX + LoRA-gradient launch takes: each fusable on the 128x128 tiles.
+static bool dx_grads_group_ok(int n, int M, const int* N, int K, int r, int* nw) {
+  if (n < 1 || n > kMaxGemmGroup) return false;
+  for (int i = 0; i < n; i++) {
+    int cfg;
+    if (!grads_fusable(M, N[i], K, r, &cfg, &nw[i]) || cfg != 10) return false;
+  }
+  return true;
 }
 
 }  // namespace mxs
@@ -2100,52 +2182,47 @@ int mxs_nf4_linear_bwd_dx_grads(const void* dy, int M, int N, int K, const void*
     return mxs_lora_grads(dht, ht, ldt, x, dy, M, K, N, r, mask, mask_scale, da, db, workspace,
                           stream);
   }
-  // the gradients' argument checks (mxs_lora_grads); the GEMM's follow in gemm_entry
-  if (r % 16 || K % 8 || N % 8 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
-  if (((uintptr_t)x % 16) || ((uintptr_t)dht % 16) || ((uintptr_t)dy % 16) ||
-      ((uintptr_t)ht % 16) || (mask && ((uintptr_t)mask % 8)))
-    return MXS_ERR_ALIGN;
   GemmArgs a{};
-  a.A = static_cast<const _Float16*>(dy);
-  a.lda = N;
-  a.packed = static_cast<const uint8_t*>(packed);
-  a.absmax8 = static_cast<const uint8_t*>(absmax8);
-  a.code = code;
-  a.absmax2 = absmax2;
-  a.offset = offset;
-  a.M = M;
-  a.Nc = K;
-  a.Kr = N;
-  a.Kw = K;
-  a.lora_h = static_cast<const _Float16*>(lora_dh);
-  a.lora_w = static_cast<const _Float16*>(lora_at);
-  a.r = r;
-  a.mask = static_cast<const uint8_t*>(mask);
-  a.mask_scale = mask_scale;
-  a.C = static_cast<_Float16*>(dx);
-  a.ldc = K;
+  const int e = dx_grads_args(dy, M, N, K, packed, absmax8, code, absmax2, offset, lora_dh, lora_at,
+                              r, mask, mask_scale, dht, ht, ldt, x, da, db, dx, nw, a);
+  if (e != MXS_OK) return e;
   set_workspace(a, workspace);
-  ColsProblem& pa = a.cp0;  // dA [r, K] = dHs^T . drop(X)
-  pa.PT = static_cast<const _Float16*>(dht);
-  pa.Q = static_cast<const _Float16*>(x);
-  pa.mask = static_cast<const uint8_t*>(mask);
-  pa.mscale = mask_scale;
-  pa.Nq = K;
-  pa.out = da;
-  pa.out_rn = 1;
-  ColsProblem& pb = a.cp1;  // dB [N, r] = dY^T . Hs
-  pb.PT = static_cast<const _Float16*>(ht);
-  pb.Q = static_cast<const _Float16*>(dy);
-  pb.mscale = 1.0f;
-  pb.Nq = N;
-  pb.out = db;
-  pb.out_rn = 0;
-  constexpr int WC = 16 * kFusedColsCPL;
-  a.cols_cb0 = (K + WC - 1) / WC;
-  a.cols_blocks = a.cols_cb0 + (N + WC - 1) / WC;
-  a.cols_ldt = ldt;
-  a.cols_nw = nw;
   return gemm_entry(true, a, cfg, 1, stream);
+}
+
+
+int mxs_nf4_linear_bwd_dx_grads_group_ok(int n, int M, const int N[], int K, int r) {
+  int nw[kMaxGemmGroup];
+  return N && dx_grads_group_ok(n, M, N, K, r, nw) ? 1 : 0;
+}
+
+int mxs_nf4_linear_bwd_dx_grads_group(int n, const void* const dy[], int M, const int N[], int K,
+                                      const void* const packed[], const void* const absmax8[],
+                                      const float* const code[], const float* const absmax2[],
+                                      const float* const offset[], const void* const lora_dh[],
+                                      const void* const lora_at[], int r,
+                                      const void* const mask[], float mask_scale,
+                                      const void* const dht[], const void* const ht[], int ldt,
+                                      const void* const x[], float* const da[],
+                                      float* const db[], void* const dx[], hipStream_t stream) {
+  if (n < 1 || n > kMaxGemmGroup || !dy || !N || !packed || !absmax8 || !code || !absmax2 ||
+      !offset || !lora_dh || !lora_at || !dht || !ht || !x || !da || !db || !dx)
+    return MXS_ERR_ARG;
+  int nw[kMaxGemmGroup];
+  if (!dx_grads_group_ok(n, M, N, K, r, nw)) return MXS_ERR_SIZE;
+  GemmArgs probs[kMaxGemmGroup];
+  for (int i = 0; i < n; i++) {
+    if (!lora_dh[i] || !lora_at[i] || !dht[i] || !ht[i] || !x[i] || !da[i] || !db[i] || !dx[i])
+      return MXS_ERR_ARG;
+    const void* mk = mask ? mask[i] : nullptr;
+    int e = dx_grads_args(dy[i], M, N[i], K, packed[i], absmax8[i], code[i], absmax2[i],
+                          offset[i], lora_dh[i], lora_at[i], r, mk, mask_scale, dht[i], ht[i], ldt,
+                          x[i], da[i], db[i], dx[i], nw[i], probs[i]);
+    if (e != MXS_OK) return e;
+    e = check_gemm(true, probs[i]);
+    if (e != MXS_OK) return e == 1 ? MXS_ERR_SIZE : e;  // grads_fusable admits no empty problem
+  }
+  return launch_ws_group<true>(probs, n, stream);
 }
 
 int mxs_nf4_linear_fwd_hp(const void* x, int M, int K, int N, const void* packed,
@@ -2255,7 +2332,7 @@ int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, cons
     probs[live++] = a;
   }
   if (live == 0) return MXS_OK;
-  return launch_ws_group(probs, live, stream);
+  return launch_ws_group<false>(probs, live, stream);
 }
 
 int mxs_nf4_linear_glu_fused(int M, int N, int K, int bwd) {

@@ -162,6 +162,45 @@ def nf4_linear_bwd_dx_grads(dy2d, packed, state, lora_dh, lora_at, dht, ht, x2d,
     return dx, da, db
 
 
+def bwd_grads_group_ok(M, Ns, K, r):
+    """True when nf4_linear_bwd_dx_grads_group takes projections [K -> N] for N in Ns."""
+    return bool(_lib.lib().mxs_nf4_linear_bwd_dx_grads_group_ok(len(Ns), M, _int_array(Ns), K,
+                                                               r))
+
+
+def nf4_linear_bwd_dx_grads_group(dys, packeds, states, dhs, ats, dhts, hts, x2ds, masks=None,
+                                  mask_scale=1.0):
+    """nf4_linear_bwd_dx_grads for up to 4 projections of one input width in one launch: a list
+    of (dx, dA, dB), the bits of the separate calls.  Only where bwd_grads_group_ok."""
+    n = len(dys)
+    masks = masks or [None] * n
+    dys = [d.contiguous() for d in dys]
+    x2ds = [x.contiguous() for x in x2ds]
+    M, K = x2ds[0].shape
+    r = dhs[0].shape[1]
+    Ns = [st.shape[0] for st in states]
+    for d, x, st, dh, at, dht, ht in zip(dys, x2ds, states, dhs, ats, dhts, hts):
+        if d.shape != (M, st.shape[0]) or x.shape != (M, K) or st.shape[1] != K:
+            raise ValueError("dy [M, N], x [M, K] and the weight [N, K] disagree")
+        if dh.shape != (M, r) or at.shape != (K, r) or dht.shape[0] != r or ht.shape != dht.shape:
+            raise ValueError("LoRA operands disagree")
+    dev = dys[0].device
+    dx = [torch.empty((M, K), dtype=torch.float16, device=dev) for _ in dys]
+    da = [torch.empty((r, K), dtype=torch.float32, device=dev) for _ in dys]
+    db = [torch.empty((nn_, r), dtype=torch.float32, device=dev) for nn_ in Ns]
+    masks = [_c(m) for m in masks]
+    _lib.call("mxs_nf4_linear_bwd_dx_grads_group", n, _ptr_array(dys), M, _int_array(Ns), K,
+              _ptr_array(packeds), _ptr_array([st.absmax for st in states]),
+              _ptr_array([st.state2.code for st in states]),
+              _ptr_array([st.state2.absmax for st in states]),
+              _ptr_array([st.offset for st in states]), _ptr_array([_c(t) for t in dhs]),
+              _ptr_array([_c(t) for t in ats]), r, _ptr_array(masks), float(mask_scale),
+              _ptr_array([_c(t) for t in dhts]), _ptr_array([_c(t) for t in hts]),
+              dhts[0].shape[1], _ptr_array(x2ds), _ptr_array(da), _ptr_array(db),
+              _ptr_array(dx), _lib.stream_of(dev))
+    return list(zip(dx, da, db))
+
+
 def lora_slices(M, Kr):
     """Reduction slices the partial-sum LoRA kernels use (1..4)."""
     return int(_lib.lib().mxs_lora_slices(M, Kr))

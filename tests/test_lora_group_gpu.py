@@ -131,3 +131,34 @@ def test_grouped_qkv_gemm_equals_separate(cuda, M, lora):
         assert (ht2 is None) == (ht1 is None) and (ht1 is None or torch.equal(ht2, ht1))
         err = (y2.float() - y0.float()).abs().max() / y0.float().abs().max()
         assert err < 1e-2, (i, float(err))
+
+
+@pytest.mark.parametrize("M", [1024, 300])
+def test_grouped_qkv_backward_equals_separate(cuda, M):
+    """mxs_nf4_linear_bwd_dx_grads_group over v, k, q (K = 1536) against each projection's
+    mxs_nf4_linear_bwd_dx_grads: dX, dA and dB bit for bit."""
+    from mindxsoup_amd import kernels
+
+    print(f"case qkv backward group M={M}", flush=True)
+    K = 1536
+    layers = [_nf4(cuda, n, K, 400 + i) for i, n in enumerate((256, 256, 1536))]
+    Ns = [L.out_features for L in layers]
+    assert kernels.bwd_grads_group_ok(M, Ns, K, 16)
+    probs = [_inputs(cuda, M, K, n, 410 + i) for i, n in enumerate(Ns)]
+    x = probs[0][0]
+    s, ms = 2.0, 1 / 0.95
+    packeds = [L.weight.data.view(-1, 1) for L in layers]
+    states = [L.weight.quant_state for L in layers]
+    saved = []
+    for (_, a, b, _, keep), P, st in zip(probs, packeds, states):
+        h, ht = kernels.lora_h(x, a, s, keep, ms)
+        saved.append((ht, a.t().contiguous(), b.t().contiguous()))
+    dhs = kernels.lora_dh_group([p[3] for p in probs], [sv[2] for sv in saved], s)
+    sep = [kernels.nf4_linear_bwd_dx_grads(p[3], P, st, dh, sv[1], dht, sv[0], x, p[4], ms)
+           for p, P, st, (dh, dht), sv in zip(probs, packeds, states, dhs, saved)]
+    grp = kernels.nf4_linear_bwd_dx_grads_group(
+        [p[3] for p in probs], packeds, states, [d[0] for d in dhs], [sv[1] for sv in saved],
+        [d[1] for d in dhs], [sv[0] for sv in saved], [x] * 3, [p[4] for p in probs], ms)
+    torch.cuda.synchronize()
+    for (dx1, da1, db1), (dx2, da2, db2) in zip(sep, grp):
+        assert torch.equal(dx1, dx2) and torch.equal(da1, da2) and torch.equal(db1, db2)
