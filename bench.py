@@ -276,28 +276,16 @@ def layer_fwd(projs, s=ALPHA / RANK):
 
 
 def layer_bwd(projs, saved, s=ALPHA / RANK):
-    """Backward of one layer's 7 projections in reverse order, each group's dHs in one launch."""
-    from mindxsoup_amd import kernels
-    from mindxsoup_amd.linear4bit import lora_backward, prepare_dh
+    """Backward of one layer's 7 projections in reverse order; each group's small launches
+    (dHs, dA / dB) and the v/k/q dX GEMMs shared (linear4bit.lora_backward_group)."""
+    from mindxsoup_amd.linear4bit import lora_backward_group
 
     for grp in BWD_GROUPS:
-        ps = [projs[i] for i in grp]
-        pre = prepare_dh([(p["dy"], saved[i][2], p["k"], s, (True, True, True))
-                          for i, p in zip(grp, ps)])
-        K = ps[0]["k"]
-        if (len(ps) > 1 and all("dh" in kw for kw in pre) and all(p["k"] == K for p in ps)
-                and kernels.bwd_grads_group_ok(M_TOKENS, [p["n"] for p in ps], K, RANK)):
-            # v, k, q: one launch for the three dX GEMMs and their weight gradients
-            kernels.nf4_linear_bwd_dx_grads_group(
-                [p["dy"] for p in ps], [p["packed"] for p in ps], [p["st"] for p in ps],
-                [kw["dh"][0] for kw in pre], [saved[i][1] for i in grp],
-                [kw["dh"][1] for kw in pre], [saved[i][0] for i in grp], [p["x"] for p in ps],
-                [p["keep"] for p in ps], 1.0 / (1.0 - P_DROP))
-            continue
-        for i, p, kw in zip(grp, ps, pre):
-            ht, at, bt = saved[i]
-            lora_backward(p["dy"], p["x"], p["keep"], ht, at, bt, p["packed"], p["st"],
-                          1.0 / (1.0 - P_DROP), s, ws=p["ws"], **kw)
+        lora_backward_group([dict(dy=projs[i]["dy"], x2d=projs[i]["x"], keep=projs[i]["keep"],
+                                  ht=saved[i][0], at=saved[i][1], bt=saved[i][2],
+                                  packed=projs[i]["packed"], state=projs[i]["st"],
+                                  mask_scale=1.0 / (1.0 - P_DROP), s=s,
+                                  wants=(True, True, True)) for i in grp], ws=projs[grp[0]]["ws"])
 
 
 def graph_time(fn, steps, warmup):

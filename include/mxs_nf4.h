@@ -239,6 +239,16 @@ int mxs_lora_dh_group(int n, const void* const dy[], int M, const int N[],
                       const void* const lora_bt[], int r, float s, int ldt, void* const dh[],
                       void* const dht[], hipStream_t stream);
 
+/* mxs_lora_grads (both dA and dB) for n (1..4) projections over the same M tokens in ONE launch
+ * (gate's and up's arrive together in the MLP's backward): arrays of the per-projection
+ * pointers and sizes, mask may be NULL (or any entry).  The projections must share the
+ * columns-per-lane choice of their own launches (cols(K + N) equal, e.g. equal shapes; else
+ * MXS_ERR_SIZE); then the results are the bits of n calls. */
+int mxs_lora_grads_group(int n, const void* const dht[], const void* const ht[], int ldt,
+                         const void* const x[], const void* const dy[], int M, const int K[],
+                         const int N[], int r, const void* const mask[], float mask_scale,
+                         float* const da[], float* const db[], hipStream_t stream);
+
 /* The fp16 operand from such partial sums [slices][ldt][r] (1 <= slices <= 4; added in slice
  * order and rounded, the value the fused GEMMs compute from the same partials): out [M, r] (may
  * be NULL) and outT [r, ldt] with zeros past M.  Finishes dh from mxs_lora_dh_partials for

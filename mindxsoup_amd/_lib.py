@@ -70,6 +70,7 @@ _SIGNATURES = {
     "mxs_lora_h_partials_group": [I32, P, I32, P, P, I32, P, F32, F32, I32, P, P, P, P, P, P],
     "mxs_lora_dh_partials_group": [I32, P, I32, P, P, I32, F32, I32, P, P],
     "mxs_lora_dh_group": [I32, P, I32, P, P, I32, F32, I32, P, P, P],
+    "mxs_lora_grads_group": [I32, P, P, I32, P, P, I32, P, P, I32, P, F32, P, P, P],
     "mxs_lora_finish": [P, I32, I32, I32, I32, P, P, P],
     "mxs_nf4_linear_fwd_hp": [P, I32, I32, I32, P, P, P, P, P, P, P, I32, I32, P, I32, P, P, P,
                               I32, I32, P],

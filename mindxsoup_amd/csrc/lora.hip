@@ -224,6 +224,28 @@ __global__ __launch_bounds__(64 * cols_max_waves<CPL>()) void k_lora_cols(ColsPr
   lora_cols_block<CPL>(p0, p1, cb0, M, ldt, r, (int)blockIdx.x, (int)blockDim.x >> 6, red);
 }
 
+// dA / dB of several projections in one launch (gate's and up's arrive together): pair i owns
+// workgroups [start[i], start[i+1]), laid out as its own launch's grid (dA blocks, then dB).
+// All pairs share the columns per lane and the waves, which is what their own launches would
+// use when their shapes agree.
+struct ColsGroup {
+  ColsProblem pa[kMaxGroup], pb[kMaxGroup];
+  int start[kMaxGroup + 1];
+  int cb0[kMaxGroup];
+  int n;
+};
+
+template <int CPL>
+__global__ __launch_bounds__(64 * cols_max_waves<CPL>()) void k_lora_cols_group(ColsGroup g, int M,
+                                                                               int ldt, int r) {
+  extern __shared__ float red[];  // [waves][r][16 * CPL + 1]
+  const int bid = (int)blockIdx.x;
+  int i = 0;
+  while (i + 1 < g.n && bid >= g.start[i + 1]) i++;
+  lora_cols_block<CPL>(g.pa[i], g.pb[i], g.cb0[i], M, ldt, r, bid - g.start[i],
+                       (int)blockDim.x >> 6, red);
+}
+
 // dst[0, n) = 0 (a kernel, not hipMemsetAsync, so that the call can be captured in a graph).
 __global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ dst, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -321,6 +343,24 @@ static int cols_launch_t(const ColsProblem& p0, const ColsProblem& p1, int nprob
   if (nw * per_wave > kColsLds) return MXS_ERR_SIZE;
   hipLaunchKernelGGL(k_lora_cols<CPL>, dim3(cb0 + cb1), dim3(64 * nw), (size_t)nw * per_wave,
                      stream, p0, p1, cb0, M, ldt, r);
+  return check_launch();
+}
+
+template <int CPL>
+static int cols_group_launch_t(ColsGroup g, int M, int ldt, int r, hipStream_t stream) {
+  constexpr int WC = 16 * CPL;
+  int total = 0;
+  for (int i = 0; i < g.n; i++) {
+    g.cb0[i] = (g.pa[i].Nq + WC - 1) / WC;
+    g.start[i] = total;
+    total += g.cb0[i] + (g.pb[i].Nq + WC - 1) / WC;
+  }
+  g.start[g.n] = total;
+  const int nw = cols_waves(M, r, CPL, cols_max_waves<CPL>());
+  const int per_wave = r * (WC + 1) * (int)sizeof(float);
+  if (nw * per_wave > kColsLds) return MXS_ERR_SIZE;
+  hipLaunchKernelGGL(k_lora_cols_group<CPL>, dim3(total), dim3(64 * nw), (size_t)nw * per_wave,
+                     stream, g, M, ldt, r);
   return check_launch();
 }
 
@@ -600,6 +640,55 @@ int mxs_lora_grads(const void* dht, const void* ht, int ldt, const void* x, cons
   if (a_on) return cols_launch(pa, pa, 1, M, ldt, r, stream);
   if (b_on) return cols_launch(pb, pb, 1, M, ldt, r, stream);
   return MXS_OK;
+}
+
+int mxs_lora_grads_group(int n, const void* const dht[], const void* const ht[], int ldt,
+                         const void* const x[], const void* const dy[], int M, const int K[],
+                         const int N[], int r, const void* const mask[], float mask_scale,
+                         float* const da[], float* const db[], hipStream_t stream) {
+  if (n < 1 || n > kMaxGroup || M < 0 || r <= 0 || !dht || !ht || !x || !dy || !K || !N || !da ||
+      !db)
+    return MXS_ERR_ARG;
+  if (r % 16 || r > 16 * kMaxRB) return MXS_ERR_SIZE;
+  if (M == 0) {  // empty reductions: zero gradients
+    for (int i = 0; i < n; i++) {
+      const int e = mxs_lora_grads(nullptr, nullptr, ldt, nullptr, nullptr, 0, K[i], N[i], r,
+                                   nullptr, mask_scale, da[i], db[i], nullptr, stream);
+      if (e != MXS_OK) return e;
+    }
+    return MXS_OK;
+  }
+  ColsGroup g{};
+  g.n = n;
+  const int cpl = cols_cpl(K[0] + N[0]);
+  for (int i = 0; i < n; i++) {
+    const void* mk = mask ? mask[i] : nullptr;
+    if (K[i] <= 0 || N[i] <= 0 || !dht[i] || !ht[i] || !x[i] || !dy[i] || !da[i] || !db[i])
+      return MXS_ERR_ARG;
+    if (K[i] % 8 || N[i] % 8 || ldt < M || ldt % 8 || cols_cpl(K[i] + N[i]) != cpl)
+      return MXS_ERR_SIZE;
+    if ((uintptr_t)x[i] % 16 || (uintptr_t)dht[i] % 16 || (uintptr_t)dy[i] % 16 ||
+        (uintptr_t)ht[i] % 16 || (mk && ((uintptr_t)mk % 8)))
+      return MXS_ERR_ALIGN;
+    ColsProblem& pa = g.pa[i];  // dA [r, K] = dHs^T . drop(X)
+    pa.PT = static_cast<const _Float16*>(dht[i]);
+    pa.Q = static_cast<const _Float16*>(x[i]);
+    pa.mask = static_cast<const uint8_t*>(mk);
+    pa.mscale = mask_scale;
+    pa.Nq = K[i];
+    pa.out = da[i];
+    pa.out_rn = 1;
+    ColsProblem& pb = g.pb[i];  // dB [N, r] = dY^T . Hs
+    pb.PT = static_cast<const _Float16*>(ht[i]);
+    pb.Q = static_cast<const _Float16*>(dy[i]);
+    pb.mscale = 1.0f;
+    pb.Nq = N[i];
+    pb.out = db[i];
+    pb.out_rn = 0;
+  }
+  if (cpl == 8) return cols_group_launch_t<8>(g, M, ldt, r, stream);
+  if (cpl == 4) return cols_group_launch_t<4>(g, M, ldt, r, stream);
+  return cols_group_launch_t<2>(g, M, ldt, r, stream);
 }
 
 int mxs_lora_grad_a(const void* dht, int ldt, const void* x, int M, int K, int r,

@@ -611,6 +611,29 @@ def lora_grads(dht, ht, x2d, dy2d, mask=None, mask_scale=1.0, want_a=True, want_
     return da, db
 
 
+def lora_grads_group(dhts, hts, x2ds, dy2ds, masks=None, mask_scale=1.0):
+    """lora_grads (dA and dB) for up to 4 projections of equal shapes in one launch: a list of
+    (dA [r, K] fp32, dB [N, r] fp32), the bits of separate calls."""
+    n = len(dhts)
+    masks = masks or [None] * n
+    x2ds = [x.contiguous() for x in x2ds]
+    dy2ds = [d.contiguous() for d in dy2ds]
+    M = x2ds[0].shape[0]
+    r, ldt = dhts[0].shape
+    dev = x2ds[0].device
+    for dht, ht, x, dy in zip(dhts, hts, x2ds, dy2ds):
+        if dht.shape != (r, ldt) or ht.shape != (r, ldt) or x.shape[0] != M or dy.shape[0] != M:
+            raise ValueError("dht / ht [r, ldt], x [M, K], dy [M, N] disagree")
+    da = [torch.empty((r, x.shape[1]), dtype=torch.float32, device=dev) for x in x2ds]
+    db = [torch.empty((d.shape[1], r), dtype=torch.float32, device=dev) for d in dy2ds]
+    _lib.call("mxs_lora_grads_group", n, _ptr_array([_c(t) for t in dhts]),
+              _ptr_array([_c(t) for t in hts]), ldt, _ptr_array(x2ds), _ptr_array(dy2ds), M,
+              _int_array([x.shape[1] for x in x2ds]), _int_array([d.shape[1] for d in dy2ds]), r,
+              _ptr_array([_c(m) for m in masks]), float(mask_scale), _ptr_array(da),
+              _ptr_array(db), _lib.stream_of(dev))
+    return list(zip(da, db))
+
+
 def lora_grad_a(dht, x2d, mask=None, mask_scale=1.0, ws=None):
     """dA = dh^T @ drop(x), fp32 [r, K]."""
     x2d = x2d.contiguous()

@@ -145,6 +145,76 @@ def lora_backward(dy, x2d, keep, ht, at, bt, packed, state, mask_scale, s, want_
     return dx, da, db
 
 
+def lora_backward_group(items, ws=None):
+    """lora_backward for up to 4 projections over the same tokens whose output gradients arrive
+    together (q/k/v from attention's backward, gate/up from the SwiGLU's), with their small
+    launches shared: dHs in one launch per kind (prepare_dh); the dX GEMMs that carry the weight
+    gradients in one launch where kernels.bwd_grads_group_ok allows; otherwise each dX GEMM,
+    then dA and dB of all of them in one launch (equal shapes).  items: dicts with dy, x2d,
+    keep, ht, at, bt, packed, state, mask_scale, s and wants = (want_x, want_a, want_b).
+    Returns [(dx, dA, dB)], the bits of lora_backward on each."""
+    n = len(items)
+    pre = prepare_dh([(it["dy"], it["bt"], it["x2d"].shape[1], it["s"], it["wants"])
+                      for it in items])
+    out = [None] * n
+    M = items[0]["dy"].shape[0]
+    fused = [i for i in range(n) if "dh" in pre[i]]
+    if len(fused) > 1:
+        its = [items[i] for i in fused]
+        K, r = its[0]["x2d"].shape[1], its[0]["bt"].shape[0]
+        if (all(it["x2d"].shape[1] == K and it["mask_scale"] == its[0]["mask_scale"]
+                for it in its)
+                and kernels.bwd_grads_group_ok(M, [it["state"].shape[0] for it in its], K, r)):
+            res = kernels.nf4_linear_bwd_dx_grads_group(
+                [it["dy"] for it in its], [it["packed"] for it in its],
+                [it["state"] for it in its], [pre[i]["dh"][0] for i in fused],
+                [it["at"] for it in its], [pre[i]["dh"][1] for i in fused],
+                [it["ht"] for it in its], [it["x2d"] for it in its],
+                [it["keep"] for it in its], its[0]["mask_scale"])
+            for i, r_ in zip(fused, res):
+                out[i] = r_
+    for i in fused:
+        if out[i] is None:
+            it = items[i]
+            out[i] = lora_backward(it["dy"], it["x2d"], it["keep"], it["ht"], it["at"], it["bt"],
+                                   it["packed"], it["state"], it["mask_scale"], it["s"],
+                                   *it["wants"], ws=ws, **pre[i])
+    pending = []
+    for i in range(n):
+        if out[i] is not None:
+            continue
+        it = items[i]
+        want_x, want_a, want_b = it["wants"]
+        want_g = want_a or want_b
+        dx, dht = None, None
+        if want_x or want_g:
+            dx, dht = kernels.nf4_linear_bwd_dx_hp(it["dy"], it["packed"], it["state"],
+                                                   pre[i]["dhp"], it["at"], it["keep"],
+                                                   it["mask_scale"], ws=ws, want_t=want_g)
+        out[i] = [dx if want_x else None, None, None]
+        if want_g:
+            pending.append((i, dht))
+    both = [(i, d) for i, d in pending if items[i]["wants"][1] and items[i]["wants"][2]]
+    shapes = {(items[i]["x2d"].shape[1], items[i]["dy"].shape[1], items[i]["mask_scale"])
+              for i, _ in both}
+    if len(both) > 1 and len(shapes) == 1:
+        res = kernels.lora_grads_group([d for _, d in both], [items[i]["ht"] for i, _ in both],
+                                       [items[i]["x2d"] for i, _ in both],
+                                       [items[i]["dy"] for i, _ in both],
+                                       [items[i]["keep"] for i, _ in both],
+                                       items[both[0][0]]["mask_scale"])
+        for (i, _), (da, db) in zip(both, res):
+            out[i][1], out[i][2] = da, db
+        pending = [(i, d) for i, d in pending if (i, d) not in both]
+    for i, dht in pending:
+        it = items[i]
+        da, db = kernels.lora_grads(dht, it["ht"], it["x2d"], it["dy"], it["keep"],
+                                    it["mask_scale"], want_a=it["wants"][1],
+                                    want_b=it["wants"][2], ws=ws)
+        out[i][1], out[i][2] = da, db
+    return [tuple(o) for o in out]
+
+
 class NF4LoraFunction(torch.autograd.Function):
     """base(x) + s * B(A(drop(x))) for a frozen NF4 base, fused:
     forward:  Hs = s * drop(x) A^T as slice partials (mxs_lora_h_partials), then one fused GEMM

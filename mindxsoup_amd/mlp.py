@@ -23,7 +23,7 @@ SwiGLU reads it, as the separate kernel does, and both evaluate the same fp32 fo
 import torch
 
 from . import direct, kernels, linear4bit
-from .linear4bit import LoraLinear4bit, _cast_bias_once, _direct_ok, lora_backward, prepare_dh
+from .linear4bit import LoraLinear4bit, _cast_bias_once, _direct_ok, lora_backward_group
 from .silu_mul import silu_mul
 
 FUSED_SWIGLU = True  # FEATURES["mlp_fused_swiglu"]
@@ -109,16 +109,15 @@ class NF4LoraMLPFunction(torch.autograd.Function):
             grads_d = kernels.lora_grads(dht_d, ht_d, h, dy, pd.keep, pd.mask_scale,
                                          want_a=need[5], want_b=need[6])
         del h
-        # up_proj and gate_proj with d(up) and d(gate) as their incoming gradients; their dHs
-        # in one launch
-        wants_u, wants_g = (need[0], need[3], need[4]), (need[0], need[1], need[2])
-        pre_u, pre_g = prepare_dh([(up, bt_u, x2d.shape[1], pu.s, wants_u),
-                                   (gate, bt_g, x2d.shape[1], pg.s, wants_g)])
-        dx, dua, dub = lora_backward(up, x2d, pu.keep, ht_u, at_u, bt_u, pu.packed, pu.state,
-                                     pu.mask_scale, pu.s, *wants_u, **pre_u)
-        del pre_u
-        dxg, dga, dgb = lora_backward(gate, x2d, pg.keep, ht_g, at_g, bt_g, pg.packed, pg.state,
-                                      pg.mask_scale, pg.s, *wants_g, **pre_g)
+        # up_proj and gate_proj with d(up) and d(gate) as their incoming gradients; their small
+        # launches (dHs, dA / dB) shared
+        (dx, dua, dub), (dxg, dga, dgb) = lora_backward_group([
+            dict(dy=up, x2d=x2d, keep=pu.keep, ht=ht_u, at=at_u, bt=bt_u, packed=pu.packed,
+                 state=pu.state, mask_scale=pu.mask_scale, s=pu.s,
+                 wants=(need[0], need[3], need[4])),
+            dict(dy=gate, x2d=x2d, keep=pg.keep, ht=ht_g, at=at_g, bt=bt_g, packed=pg.packed,
+                 state=pg.state, mask_scale=pg.mask_scale, s=pg.s,
+                 wants=(need[0], need[1], need[2]))])
         if dx is not None:
             dx += dxg
         grads = [dga, dgb, dua, dub, grads_d[0], grads_d[1]]

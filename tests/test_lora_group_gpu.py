@@ -162,3 +162,53 @@ def test_grouped_qkv_backward_equals_separate(cuda, M):
     torch.cuda.synchronize()
     for (dx1, da1, db1), (dx2, da2, db2) in zip(sep, grp):
         assert torch.equal(dx1, dx2) and torch.equal(da1, da2) and torch.equal(db1, db2)
+
+
+@pytest.mark.parametrize("M", [1024, 37])
+def test_backward_group_equals_lora_backward(cuda, M):
+    """linear4bit.lora_backward_group over gate and up (dX split-K GEMMs, dA / dB in one launch)
+    and over v, k, q (the grouped dX + gradients launch) against lora_backward on each: dX, dA,
+    dB bit for bit."""
+    from mindxsoup_amd import kernels
+    from mindxsoup_amd.linear4bit import lora_backward, lora_backward_group
+
+    print(f"case backward group M={M}", flush=True)
+    s, ms = 2.0, 1 / 0.95
+    for shapes in ([(8960, 1536), (8960, 1536)], [(256, 1536), (256, 1536), (1536, 1536)]):
+        layers = [_nf4(cuda, n, k, 500 + i) for i, (n, k) in enumerate(shapes)]
+        probs = [_inputs(cuda, M, k, n, 510 + i) for i, (n, k) in enumerate(shapes)]
+        x = probs[0][0]
+        items = []
+        for (n, k), L, (_, a, b, dy, keep) in zip(shapes, layers, probs):
+            hp, at, bt = kernels.lora_h_partials(x, a, s, keep, ms, lora_b=b)
+            _, ht = kernels.nf4_linear_fwd_hp(x, L.weight.data.view(-1, 1),
+                                              L.weight.quant_state, hp, b)
+            items.append(dict(dy=dy, x2d=x, keep=keep, ht=ht, at=at, bt=bt,
+                              packed=L.weight.data.view(-1, 1), state=L.weight.quant_state,
+                              mask_scale=ms, s=s, wants=(True, True, True)))
+        want = [lora_backward(it["dy"], it["x2d"], it["keep"], it["ht"], it["at"], it["bt"],
+                              it["packed"], it["state"], ms, s) for it in items]
+        got = lora_backward_group(items)
+        torch.cuda.synchronize()
+        for w, g in zip(want, got):
+            assert all(torch.equal(a_, b_) for a_, b_ in zip(w, g))
+
+
+def test_grads_group_equals_separate(cuda):
+    from mindxsoup_amd import kernels
+
+    M, K, N = 700, 1536, 8960
+    probs = [_inputs(cuda, M, K, N, 600 + i) for i in range(2)]
+    dhts, hts = [], []
+    for x, a, b, dy, keep in probs:
+        _, ht = kernels.lora_h(x, a, 2.0, keep, 1 / 0.95)
+        _, dht = kernels.lora_dh(dy, b, 2.0)
+        dhts.append(dht)
+        hts.append(ht)
+    sep = [kernels.lora_grads(dht, ht, p[0], p[3], p[4], 1 / 0.95)
+           for dht, ht, p in zip(dhts, hts, probs)]
+    grp = kernels.lora_grads_group(dhts, hts, [p[0] for p in probs], [p[3] for p in probs],
+                                   [p[4] for p in probs], 1 / 0.95)
+    torch.cuda.synchronize()
+    for (a1, b1), (a2, b2) in zip(sep, grp):
+        assert torch.equal(a1, a2) and torch.equal(b1, b2)
