@@ -20,7 +20,7 @@ import torch
 
 from . import direct, kernels
 from .nf4 import _supported, unpack_nf4
-from .quant import quantize_4bit
+from .quant import QuantState, quantize_4bit
 
 _enabled = True
 cache_fp16 = False   # set by patch_bnb_linear4bit(cache_weights=...)
@@ -353,6 +353,48 @@ class Linear4bit(torch.nn.Module):
         w = torch.nn.Parameter(packed.view(-1, 1), requires_grad=False)
         w.quant_state = state
         self.weight = w
+
+    def _apply(self, fn, recurse=True):
+        """Module.to / .cuda move the packed bytes; the quant state (an attribute of the weight
+        parameter) follows them."""
+        super()._apply(fn, recurse)
+        state = getattr(self.weight, "quant_state", None)
+        if state is not None and state.absmax.device != self.weight.device:
+            self.weight.quant_state = state.to(self.weight.device)
+        return self
+
+    # bitsandbytes' state-dict form (nn/modules.py Linear4bit._save_to_state_dict): the packed
+    # bytes under "weight", the quant state's as_dict(packed=True) under "weight.<key>", bias.
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+        state = getattr(self.weight, "quant_state", None)
+        if state is not None:
+            for k, v in state.as_dict(packed=True).items():
+                destination[prefix + "weight." + k] = v if keep_vars else v.detach()
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        key = prefix + "weight"
+        qs = {k: v for k, v in state_dict.items() if k.startswith(key + ".")}
+        if key not in state_dict:
+            if strict:
+                missing_keys.append(key)
+            return
+        dev = self.weight.device if self.weight is not None else state_dict[key].device
+        try:
+            state = QuantState.from_dict({k[len(key) + 1:]: v for k, v in qs.items()}, dev)
+        except (ValueError, NotImplementedError, KeyError) as e:
+            error_msgs.append(f"{key}: {e}")
+            return
+        self.set_quantized(state_dict[key].to(dev).view(-1, 1), state)
+        b = prefix + "bias"
+        if self.bias is not None:
+            if b in state_dict:
+                self.bias.data = state_dict[b].to(device=dev, dtype=self.bias.dtype).clone()
+            elif strict:
+                missing_keys.append(b)
+        elif b in state_dict and strict:
+            unexpected_keys.append(b)
 
     def forward(self, x):
         if _direct_ok(self, x):

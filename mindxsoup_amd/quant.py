@@ -8,12 +8,34 @@ quantize_4bit(..., compress_statistics=True) that the reference calls
 (solution/test_nf4.py:33).
 """
 
+import json
 from dataclasses import dataclass, field
 
 import numpy as np
 import torch
 
 from . import _lib
+
+# bitsandbytes' serialized QuantState (bitsandbytes 0.43-0.45, functional.py: QuantState.as_dict,
+# from_dict, pack_dict_to_tensor; not part of the reference tree, which calls it through
+# bitsandbytes): tensor fields under their own keys, the rest as the UTF-8 bytes of a JSON
+# object in one u8 tensor under "quant_state.bitsandbytes__<quant_type>".
+_QS_KEYS = ("absmax", "quant_map", "nested_absmax", "nested_quant_map", "quant_state",
+            "quant_type", "blocksize", "dtype", "shape", "nested_blocksize", "nested_dtype",
+            "nested_offset")
+
+
+def pack_dict_to_tensor(d):
+    """A JSON-serializable dict as a u8 tensor of its UTF-8 JSON text."""
+    return torch.tensor(list(json.dumps(d).encode("utf-8")), dtype=torch.uint8)
+
+
+def unpack_tensor_to_dict(t):
+    return json.loads(bytes(t.cpu().numpy().tolist()).decode("utf-8"))
+
+
+def _dtype_name(dt):
+    return str(dt).replace("torch.", "")
 
 
 @dataclass
@@ -35,6 +57,65 @@ class QuantState:
     nested: bool = True
     packing_format_for_cpu: bool = False
     absmax_f32: torch.Tensor = field(default=None, repr=False)  # first level, before nesting
+
+    def as_dict(self, packed=False):
+        """bitsandbytes' QuantState.as_dict: absmax, quant_map (the 16 NF4 values), and for the
+        nested form nested_absmax, nested_quant_map, nested_blocksize, nested_dtype,
+        nested_offset; with packed=True the non-tensor fields go into one u8 tensor under
+        "quant_state.bitsandbytes__nf4" (the form Linear4bit writes into a state dict)."""
+        from .nf4 import NF4_VALUES
+
+        d = {"quant_type": self.quant_type, "absmax": self.absmax, "blocksize": self.blocksize,
+             "quant_map": torch.from_numpy(NF4_VALUES.copy()).to(self.absmax.device),
+             "dtype": _dtype_name(self.dtype), "shape": tuple(int(v) for v in self.shape)}
+        if self.nested:
+            d.update({"nested_absmax": self.state2.absmax,
+                      "nested_blocksize": self.state2.blocksize,
+                      "nested_quant_map": self.state2.code.clone(),
+                      "nested_dtype": _dtype_name(self.state2.absmax.dtype),
+                      "nested_offset": float(self.offset.item())})
+        if not packed:
+            return d
+        out = {k: v for k, v in d.items() if isinstance(v, torch.Tensor)}
+        out["quant_state.bitsandbytes__" + self.quant_type] = pack_dict_to_tensor(
+            {k: v for k, v in d.items() if not isinstance(v, torch.Tensor)})
+        return out
+
+    @classmethod
+    def from_dict(cls, qs_dict, device):
+        """bitsandbytes' QuantState.from_dict over keys with any prefix (packed or unpacked).
+        Only NF4 with a nested absmax at blocksizes 64 / 256 is built here."""
+        qs_dict = dict(qs_dict)
+        packed_keys = [k for k, v in qs_dict.items()
+                       if "quant_state" in k and isinstance(v, torch.Tensor)]
+        if not packed_keys and "quant_type" not in qs_dict:
+            raise ValueError("expected packed or unpacked quant_state items, found neither")
+        if len(packed_keys) > 1 or (packed_keys and
+                                    packed_keys[0].split(".")[-1] != "bitsandbytes__nf4"):
+            raise ValueError(f"unsupported quant_state items {packed_keys}")
+        if packed_keys:
+            qs_dict.update(unpack_tensor_to_dict(qs_dict.pop(packed_keys[0])))
+        qs_dict = {k.split(".")[-1]: v for k, v in qs_dict.items()}
+        unknown = set(qs_dict) - set(_QS_KEYS)
+        if unknown:
+            raise ValueError(f"unexpected quant_state keys {sorted(unknown)}")
+        from .nf4 import NF4_VALUES
+
+        qmap = qs_dict["quant_map"].detach().float().cpu().numpy()
+        if (qs_dict["quant_type"] != "nf4" or "nested_absmax" not in qs_dict
+                or int(qs_dict["blocksize"]) != 64 or int(qs_dict["nested_blocksize"]) != 256
+                or not np.array_equal(qmap, NF4_VALUES.astype(np.float32))):
+            raise NotImplementedError("the HIP path takes NF4, blocksize 64, nested absmax "
+                                      "(blocksize 256)")
+        state2 = QuantState2(qs_dict["nested_absmax"].to(device=device, dtype=torch.float32),
+                             qs_dict["nested_quant_map"].to(device=device, dtype=torch.float32),
+                             int(qs_dict["nested_blocksize"]))
+        return cls(shape=tuple(int(v) for v in qs_dict["shape"]),
+                   absmax=qs_dict["absmax"].to(device), blocksize=int(qs_dict["blocksize"]),
+                   quant_type="nf4", dtype=getattr(torch, qs_dict["dtype"]),
+                   offset=torch.tensor(float(qs_dict["nested_offset"]), dtype=torch.float32,
+                                       device=device),
+                   state2=state2, nested=True)
 
     def to(self, device):
         mv = lambda t: None if t is None else t.to(device)  # noqa: E731

@@ -47,3 +47,69 @@ def test_apply_patches_qwen2_mlp(monkeypatch):
     assert torch.equal(block(x), before)
     with pytest.raises(ValueError):
         mlp.fp16_forward(block, x)  # no previous forward to hand it to
+
+
+def _cpu_state(N=64, K=128, seed=0):
+    import numpy as np
+
+    from mindxsoup_amd.quant import QuantState, QuantState2, dynamic_map
+
+    rng = np.random.default_rng(seed)
+    nb = N * K // 64
+    packed = torch.from_numpy(rng.integers(0, 256, N * K // 2, dtype=np.uint8)).view(-1, 1)
+    state = QuantState(shape=(N, K),
+                       absmax=torch.from_numpy(rng.integers(0, 256, nb, dtype=np.uint8)),
+                       offset=torch.tensor(0.0123, dtype=torch.float32),
+                       state2=QuantState2(torch.rand((nb + 255) // 256),
+                                          torch.from_numpy(dynamic_map())))
+    return packed, state
+
+
+def test_quant_state_serialized_form():
+    """QuantState.as_dict / from_dict in bitsandbytes' serialized form: the tensor keys, the
+    packed JSON of the others, and a round trip (prefixes stripped, as from a state dict)."""
+    from mindxsoup_amd.nf4 import NF4_VALUES
+    from mindxsoup_amd.quant import QuantState, unpack_tensor_to_dict
+
+    _, st = _cpu_state()
+    d = st.as_dict(packed=True)
+    assert sorted(d) == sorted(["absmax", "quant_map", "nested_absmax", "nested_quant_map",
+                                "quant_state.bitsandbytes__nf4"])
+    meta = unpack_tensor_to_dict(d["quant_state.bitsandbytes__nf4"])
+    assert d["quant_state.bitsandbytes__nf4"].dtype == torch.uint8
+    assert meta == {"quant_type": "nf4", "blocksize": 64, "dtype": "float16", "shape": [64, 128],
+                    "nested_blocksize": 256, "nested_dtype": "float32",
+                    "nested_offset": float(st.offset.item())}
+    assert torch.equal(d["quant_map"], torch.from_numpy(NF4_VALUES.copy()))
+    back = QuantState.from_dict({"weight." + k: v for k, v in d.items()}, "cpu")
+    assert back.shape == st.shape and back.blocksize == 64 and back.nested
+    assert torch.equal(back.absmax, st.absmax) and back.offset.item() == st.offset.item()
+    assert torch.equal(back.state2.absmax, st.state2.absmax)
+    assert torch.equal(back.state2.code, st.state2.code)
+    assert torch.equal(QuantState.from_dict(st.as_dict(packed=False), "cpu").absmax, st.absmax)
+    bad = dict(d)
+    bad["quant_map"] = d["quant_map"] * 2
+    with pytest.raises(NotImplementedError):
+        QuantState.from_dict(bad, "cpu")
+
+
+def test_linear4bit_state_dict_round_trip():
+    """Linear4bit.state_dict writes bitsandbytes' keys; load_state_dict into a fresh layer
+    restores the packed bytes, the quant state and the bias."""
+    from mindxsoup_amd.linear4bit import Linear4bit
+
+    packed, st = _cpu_state(seed=3)
+    a = Linear4bit(128, 64, bias=True)
+    a.set_quantized(packed, st)
+    a.bias.data = torch.arange(64, dtype=torch.float16)
+    sd = a.state_dict()
+    assert sorted(sd) == sorted(["weight", "bias", "weight.absmax", "weight.quant_map",
+                                 "weight.nested_absmax", "weight.nested_quant_map",
+                                 "weight.quant_state.bitsandbytes__nf4"])
+    b = Linear4bit(128, 64, bias=True)
+    b.load_state_dict(sd)
+    assert torch.equal(b.weight.data, a.weight.data) and torch.equal(b.bias, a.bias)
+    qa, qb = a.weight.quant_state, b.weight.quant_state
+    assert qb.shape == qa.shape and torch.equal(qb.absmax, qa.absmax)
+    assert torch.equal(qb.state2.absmax, qa.state2.absmax)
+    assert qb.offset.item() == qa.offset.item()
