@@ -586,8 +586,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the hot path is "
-              "data-parallel with no exchange in forward/dX; see DESIGN.md). Run with --gpus 1.",
-              file=sys.stderr)
+              "data-parallel: forward and dX need no exchange, the LoRA gradients one "
+              "all-reduce per layer). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
