@@ -324,3 +324,22 @@ def test_mlp_block_replays_in_a_graph(cuda):
         assert torch.equal(yg, y0), rep
         assert len(got) == len(want) and all(torch.equal(a, b) for a, b in zip(got, want)), rep
         del junk
+
+
+def test_direct_nograd_gives_the_same_output(cuda):
+    """solution/test_row_groups.py:57-71 on this build's functions: under no_grad, direct.run
+    calls the forward without Function.apply and gives the same bits, keeping nothing alive."""
+    from mindxsoup_amd import direct
+
+    mlp = _mlp(cuda, 1536, 8960, 170)
+    mlp.eval()
+    x = torch.randn((1, 96, 1536), device=cuda)
+    with torch.no_grad():
+        ref = mlp(x)
+        direct.enabled = True
+        try:
+            got = mlp(x)
+        finally:
+            direct.enabled = False
+    assert torch.equal(ref, got)
+    assert not vars(direct._context)

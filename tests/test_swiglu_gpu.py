@@ -120,3 +120,27 @@ def test_special_values_match_oracle_exactly(cuda):
         got = _np(got)
         same = (got == ref) | (np.isnan(got) & np.isnan(ref))
         assert same.all(), (got, ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("shape", [(4, 512, 8960), (3, 77, 1001)])
+def test_swiglu_matches_pytorch(cuda, dtype, shape):
+    """solution/test_kernels.py:14-35 on silu_mul: forward and backward against fp32 PyTorch
+    (2e-3 for fp16, 1e-4 for fp32; fp32 inputs take the plain expression, as the reference's
+    guard sends them)."""
+    from mindxsoup_amd.silu_mul import silu_mul
+
+    tol = {torch.float16: 2e-3, torch.float32: 1e-4}[dtype]
+    torch.manual_seed(0)
+    gate = torch.randn(shape, device=cuda, dtype=dtype, requires_grad=True)
+    up = torch.randn(shape, device=cuda, dtype=dtype, requires_grad=True)
+    grad = torch.randn(shape, device=cuda, dtype=dtype)
+    ref = torch.nn.functional.silu(gate.float()) * up.float()
+    ref.backward(grad.float())
+    ref_dgate, ref_dup = gate.grad.float(), up.grad.float()
+    gate.grad = up.grad = None
+    out = silu_mul(gate * 1, up * 1)  # not leaves: their memory takes the gradients
+    out.backward(grad)
+    torch.testing.assert_close(out.float(), ref, rtol=tol, atol=tol)
+    torch.testing.assert_close(gate.grad.float(), ref_dgate, rtol=tol, atol=tol)
+    torch.testing.assert_close(up.grad.float(), ref_dup, rtol=tol, atol=tol)
