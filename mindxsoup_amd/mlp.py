@@ -6,9 +6,9 @@ keeps fp16 gate/up for the SwiGLU backward and casts only the MLP output back
 (solution/mlp.py:1-12, 33-44).  `fp16_forward` keeps that contract.  Where every projection is
 a `LoraLinear4bit` that the fused kernels take, `NF4LoraMLPFunction` runs the block as:
 
-  forward:  gate = gate_proj(x16) (one fused GEMM, LoRA included);
-            up_proj's GEMM writes up and hidden = silu(gate) * up from the same output tile
-            (mxs_nf4_linear_fwd_glu), so hidden needs no separate pass over gate and up;
+  forward:  gate = gate_proj(x16) and up = up_proj(x16) (fused GEMMs, LoRA included, their
+            LoRA row products in one launch); hidden = silu(gate) * up, by the elementwise
+            kernel or, with GLU_FORWARD_TAIL, from up's GEMM tile (mxs_nf4_linear_fwd_glu);
             out = down_proj(hidden).
   backward: down_proj's dX GEMM applies the SwiGLU adjoint in its epilogue and writes d(gate)
             and d(up) over gate's and up's memory (mxs_nf4_linear_bwd_dx_glu): d(hidden) is
@@ -27,6 +27,11 @@ from .linear4bit import LoraLinear4bit, _cast_bias_once, _direct_ok, lora_backwa
 from .silu_mul import silu_mul
 
 FUSED_SWIGLU = True  # FEATURES["mlp_fused_swiglu"]
+# The up projection's forward with the SwiGLU tail (mxs_nf4_linear_fwd_glu) measures break-even
+# to 2 us slower than the GEMM followed by silu_mul at 1024 tokens on MI355X (its tail moves
+# three tiles while the chip idles), so the block's forward composes them; the backward tail
+# saves about 7 us and is used.  Both give the same bits.
+GLU_FORWARD_TAIL = False
 
 _NAMES = ("gate_proj", "up_proj", "down_proj")
 
@@ -67,7 +72,7 @@ class NF4LoraMLPFunction(torch.autograd.Function):
                                                      lora_b=u_b)
         gate, ht_g = kernels.nf4_linear_fwd_hp(x2d, pg.packed, pg.state, hp_g, g_b, pg.bias)
         del hp_g
-        if kernels.glu_fused(M, inter, hidden, False):
+        if GLU_FORWARD_TAIL and kernels.glu_fused(M, inter, hidden, False):
             up, h, ht_u = kernels.nf4_linear_fwd_glu(x2d, pu.packed, pu.state, gate, hp, u_b,
                                                      pu.bias)
         else:

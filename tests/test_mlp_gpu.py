@@ -182,13 +182,15 @@ def _run(mlp, x, dy, fused, seed):
 
 
 @pytest.mark.parametrize("M", [1024, 300])
-def test_mlp_fused_equals_projections_and_silu_mul(cuda, M):
+@pytest.mark.parametrize("fwd_tail", [False, True])
+def test_mlp_fused_equals_projections_and_silu_mul(cuda, M, fwd_tail, monkeypatch):
     """NF4LoraMLPFunction against the reference's composition through the same modules
     (solution/mlp.py:42-44: down_proj(silu_mul(gate_proj(x16), up_proj(x16)))): output, input
     gradient and all six LoRA gradients bit for bit, fp32 residual input as in the reference."""
     from mindxsoup_amd import mlp as mlp_mod
 
-    print(f"case mlp fused/unfused M={M}", flush=True)
+    print(f"case mlp fused/unfused M={M} fwd_tail={fwd_tail}", flush=True)
+    monkeypatch.setattr(mlp_mod, "GLU_FORWARD_TAIL", fwd_tail)
     hidden, inter = 1536, 8960
     mlp = _mlp(cuda, hidden, inter, 90)
     mlp.train()
