@@ -23,12 +23,14 @@ FEATURES = {
     "nf4_fused_lora": True,  # LoRA branch fused into the GEMM epilogues (LoraLinear4bit)
     "mlp_fp16": True,        # Qwen2 MLP on fp16 activations (mlp.py; the SwiGLU of silu_mul.py)
     "mlp_fused_swiglu": True,  # that MLP's SwiGLU in the up/down GEMM epilogues (LoRA layers)
+    "rope": True,            # RoPE of q and k in one launch each way (rope.py)
+    "attention_fp16": True,  # fp16 q/k/v, one launch for LoRA sum + RoPE + cast (attention.py)
     # --- reference switches outside the NF4 path (inert here) ------------------------------
     "startup_cache": False, "example_swiglu": False, "adam_host": False,
     "cublas_workspace": None, "fused_layer_input": False, "fused_head_acc": False,
     "lean_draw": False, "mlp_gateup_recompute": False, "mlp_tail": False, "rmsnorm": False,
-    "fused_ce": False, "rope": False, "fp16_embedding": False, "head_stream": False,
-    "head_slice": 4096, "attention_fp16": False, "unpad": False, "recompute": False,
+    "fused_ce": False, "fp16_embedding": False, "head_stream": False,
+    "head_slice": 4096, "unpad": False, "recompute": False,
     "recompute_fp16_inputs": False, "recompute_host_inputs": False,
     "recompute_group_tokens": 0, "recompute_no_rerun": False, "offload_activations": False,
     "stream_weights": False, "warmup": False,
@@ -60,3 +62,11 @@ def apply():
 
         mlp.FUSED_SWIGLU = FEATURES["mlp_fused_swiglu"]
         mlp.patch_qwen2_mlp_fp16()
+    if FEATURES["rope"]:
+        from . import rope
+
+        rope.patch_rope()
+    if FEATURES["attention_fp16"]:
+        from . import attention
+
+        attention.patch_qwen2_attention_fp16()

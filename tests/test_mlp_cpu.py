@@ -113,3 +113,37 @@ def test_linear4bit_state_dict_round_trip():
     assert qb.shape == qa.shape and torch.equal(qb.absmax, qa.absmax)
     assert torch.equal(qb.state2.absmax, qa.state2.absmax)
     assert qb.offset.item() == qa.offset.item()
+
+
+def test_apply_patches_qwen2_attention_and_rope(monkeypatch):
+    modeling_qwen2 = pytest.importorskip("transformers.models.qwen2.modeling_qwen2")
+
+    import mindxsoup_amd
+    from mindxsoup_amd import attention, direct, linear4bit, mlp, rope
+
+    cls = modeling_qwen2.Qwen2Attention
+    monkeypatch.setattr(cls, "forward", cls.forward)
+    monkeypatch.setattr(cls, "_mindx_fp16", False, raising=False)
+    monkeypatch.setattr(modeling_qwen2, "apply_rotary_pos_emb", modeling_qwen2.apply_rotary_pos_emb)
+    monkeypatch.setattr(modeling_qwen2.Qwen2MLP, "forward", modeling_qwen2.Qwen2MLP.forward)
+    monkeypatch.setattr(modeling_qwen2.Qwen2MLP, "_mindx_fp16", False, raising=False)
+    for mod, name in ((direct, "enabled"), (linear4bit, "FUSED_GEMM"),
+                      (linear4bit, "FUSED_LORA"), (mlp, "FUSED_SWIGLU")):
+        monkeypatch.setattr(mod, name, getattr(mod, name))
+    original = cls.forward
+    mindxsoup_amd.apply()
+    assert cls._mindx_fp16 and cls.forward._mindx_original is original
+    assert getattr(modeling_qwen2.apply_rotary_pos_emb, "_mindx_patched", False)
+    # CPU inputs: the patched RoPE and attention hand the call to the originals
+    from transformers import Qwen2Config
+
+    cfg = Qwen2Config(hidden_size=256, num_attention_heads=2, num_key_value_heads=1)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    attn = cls(cfg, layer_idx=0)
+    x = torch.randn(1, 8, 256)
+    cos, sin = torch.ones(1, 8, 128), torch.zeros(1, 8, 128)
+    a, _ = cls.forward(attn, x, (cos, sin), None)
+    b, _ = original(attn, x, (cos, sin), None)
+    assert torch.equal(a, b)
+    assert attention._split_projection(torch.nn.Linear(4, 4)) is None
