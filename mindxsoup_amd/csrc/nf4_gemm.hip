@@ -2174,6 +2174,10 @@ int mxs_nf4_linear_bwd_dx_grads(const void* dy, int M, int N, int K, const void*
                                 int r, const void* mask, float mask_scale, const void* dht,
                                 const void* ht, int ldt, const void* x, float* da, float* db,
                                 void* dx, void* workspace, hipStream_t stream) {
+  if (M < 0) return MXS_ERR_ARG;
+  if (M == 0)  // no tokens: dX is empty, dA and dB are empty reductions (zeros)
+    return mxs_lora_grads(nullptr, nullptr, ldt, nullptr, nullptr, 0, K, N, r, nullptr,
+                          mask_scale, da, db, workspace, stream);
   if (!lora_dh || !lora_at || !dht || !ht || !x || !da || !db || !dx) return MXS_ERR_ARG;
   int cfg, nw;
   if (!grads_fusable(M, N, K, r, &cfg, &nw)) {  // two launches, same results
@@ -2232,6 +2236,8 @@ int mxs_nf4_linear_fwd_hp(const void* x, int M, int K, int N, const void* packed
                           const float* offset, const void* bias, const float* lora_hp,
                           int hp_slices, int ldt, const void* lora_b, int r, void* lora_ht,
                           void* y, void* workspace, int cfg, int splits, hipStream_t stream) {
+  if (M < 0) return MXS_ERR_ARG;
+  if (M == 0) return MXS_OK;  // no tokens: nothing to compute (empty partials may be NULL)
   if (!lora_hp) return MXS_ERR_ARG;
   GemmArgs a{};
   a.A = static_cast<const _Float16*>(x);
@@ -2264,6 +2270,8 @@ int mxs_nf4_linear_bwd_dx_hp(const void* dy, int M, int N, int K, const void* pa
                              const void* lora_at, int r, const void* mask, float mask_scale,
                              void* lora_dht, void* dx, void* workspace, int cfg, int splits,
                              hipStream_t stream) {
+  if (M < 0) return MXS_ERR_ARG;
+  if (M == 0) return MXS_OK;  // no tokens: nothing to compute (empty partials may be NULL)
   if (!lora_dhp) return MXS_ERR_ARG;
   GemmArgs a{};
   a.A = static_cast<const _Float16*>(dy);

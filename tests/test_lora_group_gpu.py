@@ -212,3 +212,44 @@ def test_grads_group_equals_separate(cuda):
     torch.cuda.synchronize()
     for (a1, b1), (a2, b2) in zip(sep, grp):
         assert torch.equal(a1, a2) and torch.equal(b1, b2)
+
+
+def test_grouped_paths_without_tokens(cuda):
+    """Zero tokens through every grouped entry: nothing computed, empty outputs, zero LoRA
+    gradients (an empty reduction), as the single-projection entries give."""
+    from mindxsoup_amd import kernels
+    from mindxsoup_amd.linear4bit import lora_backward_group
+
+    K = 1536
+    layers = [_nf4(cuda, n, K, 700 + i) for i, n in enumerate((8960, 8960))]
+    x = torch.empty((0, K), device=cuda, dtype=torch.float16)
+    a = [(torch.rand((16, K), device=cuda) * 0.05).half() for _ in layers]
+    b = [(torch.randn((L.out_features, 16), device=cuda) * 0.01).half() for L in layers]
+    outs = kernels.lora_h_partials_group([x, x], a, 2.0, None, 1.0, b)
+    ys = kernels.nf4_linear_fwd_hp_group([x, x], [L.weight.data.view(-1, 1) for L in layers],
+                                         [L.weight.quant_state for L in layers],
+                                         [o[0] for o in outs], b)
+    assert all(y.shape == (0, L.out_features) for (y, _), L in zip(ys, layers))
+    items = [dict(dy=torch.empty((0, L.out_features), device=cuda, dtype=torch.float16), x2d=x,
+                  keep=None, ht=ht, at=o[1], bt=o[2], packed=L.weight.data.view(-1, 1),
+                  state=L.weight.quant_state, mask_scale=1.0, s=2.0, wants=(True, True, True))
+             for L, o, (_, ht) in zip(layers, outs, ys)]
+    res = lora_backward_group(items)
+    torch.cuda.synchronize()
+    for (dx, da, db), L in zip(res, layers):
+        assert dx.shape == (0, K)
+        assert da.shape == (16, K) and not da.any()
+        assert db.shape == (L.out_features, 16) and not db.any()
+
+
+def test_dx_grads_without_tokens(cuda):
+    """mxs_nf4_linear_bwd_dx_grads with zero tokens: empty dX, zero dA and dB."""
+    from mindxsoup_amd import kernels
+
+    L = _nf4(cuda, 1536, 1536, 720)
+    e = lambda *shape: torch.empty(shape, device=cuda, dtype=torch.float16)  # noqa: E731
+    dx, da, db = kernels.nf4_linear_bwd_dx_grads(e(0, 1536), L.weight.data.view(-1, 1),
+                                                 L.weight.quant_state, e(0, 16), e(1536, 16),
+                                                 e(16, 0), e(16, 0), e(0, 1536))
+    torch.cuda.synchronize()
+    assert dx.shape == (0, 1536) and not da.any() and not db.any()
