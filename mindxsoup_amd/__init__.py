@@ -17,7 +17,7 @@ FEATURES = {
     "nf4": True,             # HIP NF4 unpack with fused double-dequant of absmax
     "nf4_direct": True,      # Linear4bit: HIP path directly, no bitsandbytes dispatch layers
     "nf4_cache_fp16": False,  # each NF4 weight unpacked once and kept in fp16
-    "layer_unpack": False,   # all weights of a layer unpacked by one launch
+    "layer_unpack": False,   # with stream_weights: the running layer decoded by one launch
     "direct_nograd": True,   # no Function.apply wrappers when no graph is recorded (direct.py)
     "nf4_fused_gemm": True,  # dequant fused into the GEMM main loop (else HIP unpack + F.linear)
     "nf4_fused_lora": True,  # LoRA branch fused into the GEMM epilogues (LoraLinear4bit)
@@ -25,6 +25,7 @@ FEATURES = {
     "mlp_fused_swiglu": True,  # that MLP's SwiGLU in the up/down GEMM epilogues (LoRA layers)
     "rope": True,            # RoPE of q and k in one launch each way (rope.py)
     "attention_fp16": True,  # fp16 q/k/v, one launch for LoRA sum + RoPE + cast (attention.py)
+    "stream_weights": False,  # decoder NF4 weights in pinned host memory, a layer at a time
     # --- reference switches outside the NF4 path (inert here) ------------------------------
     "startup_cache": False, "example_swiglu": False, "adam_host": False,
     "cublas_workspace": None, "fused_layer_input": False, "fused_head_acc": False,
@@ -33,7 +34,7 @@ FEATURES = {
     "head_slice": 4096, "unpad": False, "recompute": False,
     "recompute_fp16_inputs": False, "recompute_host_inputs": False,
     "recompute_group_tokens": 0, "recompute_no_rerun": False, "offload_activations": False,
-    "stream_weights": False, "warmup": False,
+    "warmup": False,
 }
 
 PROFILE = "rules_fast"
@@ -48,9 +49,12 @@ FEATURES.update(PROFILES[PROFILE])
 def apply():
     """Install the NF4 and fp16-MLP patches named by FEATURES (solution/__init__.py:113-171,
     those parts)."""
-    from . import linear4bit, nf4
+    from . import linear4bit, nf4, stream
 
     direct.enabled = FEATURES["direct_nograd"]
+    stream.LAYER_UNPACK = FEATURES["layer_unpack"]
+    if FEATURES["stream_weights"]:
+        stream.patch_stream_layers()  # stream.setup(model) then moves the weights
     linear4bit.FUSED_GEMM = FEATURES["nf4_fused_gemm"]
     linear4bit.FUSED_LORA = FEATURES["nf4_fused_lora"]
     if FEATURES["nf4"]:

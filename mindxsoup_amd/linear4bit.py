@@ -18,7 +18,7 @@ import math
 
 import torch
 
-from . import direct, kernels
+from . import direct, kernels, stream
 from .nf4 import _supported, unpack_nf4
 from .quant import QuantState, quantize_4bit
 
@@ -76,6 +76,56 @@ class NF4LinearFunction(torch.autograd.Function):
                 grad_x = torch.matmul(grad, _unpack(ctx.packed, state, state.dtype)
                                       .to(grad.dtype))
         return grad_x, None, None, None
+
+
+def _stream_product(module, state, x, bias, backward):
+    """x @ W^T + bias (forward) or x @ W (backward) for a module whose bytes live in host
+    memory: the decoded layer buffer when its layer is decoded, else the fused GEMM (or the
+    dequant and torch) on the slot's bytes, asked for right before this use."""
+    w16 = stream.weight_for(module)
+    if w16 is None:
+        packed, absmax = stream.bytes_for(module)
+        packed = packed.view(-1, 1)
+        if _fused(state, x):
+            st = stream.state_with(state, absmax)
+            lead = x.shape[:-1]
+            x2d = x.reshape(-1, x.shape[-1])
+            y = (kernels.nf4_linear_bwd_dx(x2d, packed, st) if backward
+                 else kernels.nf4_linear_fwd(x2d, packed, st, bias))
+            return y.view(*lead, y.shape[-1])
+        w16 = _unpack(packed, state, state.dtype, absmax)
+    w = w16.to(x.dtype)
+    return torch.matmul(x, w) if backward else torch.nn.functional.linear(x, w, bias)
+
+
+class NF4StreamFunction(torch.autograd.Function):
+    """NF4LinearFunction for a module whose bytes live in host memory (stream.py): the bytes are
+    asked for right before each use, in forward and again in backward
+    (solution/linear4bit.py:68-84)."""
+
+    @staticmethod
+    def forward(ctx, x, module, state, bias):
+        ctx.module, ctx.state = module, state
+        return _stream_product(module, state, x, bias, backward=False)
+
+    @staticmethod
+    def backward(ctx, grad):
+        grad_x = None
+        if ctx.needs_input_grad[0]:
+            grad_x = _stream_product(ctx.module, ctx.state, grad, None, backward=True)
+        return grad_x, None, None, None
+
+
+def _streamed_forward(layer, x):
+    """Linear4bit.forward's own steps (input to the compute dtype, bias cast, output back to the
+    input dtype) around the streamed product (solution/linear4bit.py:87-97)."""
+    inp_dtype = x.dtype
+    if layer.compute_dtype is not None:
+        x = x.to(layer.compute_dtype)
+    bias = _cast_bias_once(layer, x)
+    if bias is not None:
+        bias = bias.to(layer.compute_dtype)
+    return direct.run(NF4StreamFunction, x, layer, layer.weight.quant_state, bias).to(inp_dtype)
 
 
 def _dh_kind(M, N, K, r, want_x, want_a, want_b):
@@ -261,6 +311,8 @@ def _direct_ok(layer, x):
     if not _enabled:
         return False
     weight = layer.weight
+    if hasattr(weight, "_mindx_host"):
+        return False  # bytes in host memory: the streamed branch
     state = getattr(weight, "quant_state", None)
     return (isinstance(x, torch.Tensor) and x.is_cuda and x.dtype == torch.float16
             and getattr(layer, "compute_type_is_set", False)
@@ -302,11 +354,13 @@ def _cast_bias_once(layer, x):
 
 def hip_forward(layer, x, original=None):
     """The patched Linear4bit.forward (solution/linear4bit.py:161-179): fp16 cache, then the
-    direct HIP path, else `original` (bitsandbytes' forward when patched onto it)."""
+    streamed branch for offloaded weights, then the direct HIP path, else `original` (bitsandbytes' forward when patched onto it)."""
     if cache_fp16:
         weight16 = _cached_weight(layer, x)
         if weight16 is not None:
             return torch.nn.functional.linear(x, weight16, _cast_bias_once(layer, x))
+    if isinstance(x, torch.Tensor) and x.is_cuda and stream.offloaded(layer):
+        return _streamed_forward(layer, x)
     if not _direct_ok(layer, x):
         if original is None:
             raise ValueError("input not supported by the HIP NF4 path")
@@ -397,6 +451,8 @@ class Linear4bit(torch.nn.Module):
             unexpected_keys.append(b)
 
     def forward(self, x):
+        if isinstance(x, torch.Tensor) and x.is_cuda and stream.offloaded(self):
+            return _streamed_forward(self, x)
         if _direct_ok(self, x):
             return hip_forward(self, x)
         return _generic_forward(self, x)

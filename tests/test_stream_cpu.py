@@ -1,0 +1,31 @@
+"""Host bookkeeping of the layer streamer (mindxsoup_amd/stream.py): which slot a layer goes
+to (free first, then the least recently used outside the layers kept; solution/stream.py:137-160)."""
+
+from mindxsoup_amd.stream import SlotTable, _round_up
+
+
+def test_free_slots_first_then_lru():
+    t = SlotTable(3)
+    for layer in range(3):
+        s = t.victim({layer})
+        assert s == layer
+        t.assign(s, layer)
+        t.touch(s)
+    assert t.slot_of == {0: 0, 1: 1, 2: 2}
+    t.touch(0)                      # layer 0 used last: layer 1's slot is the oldest
+    assert t.victim({3}) == 1
+    assert t.victim({3, 1}) == 2    # kept layers are never chosen
+    assert t.victim({0, 1, 2}) is None
+    t.assign(1, 3)
+    assert t.slot_of == {0: 0, 3: 1, 2: 2} and t.layer == [0, 3, 2]
+
+
+def test_one_slot():
+    t = SlotTable(1)
+    assert t.victim({0}) == 0
+    t.assign(0, 0)
+    assert t.victim({0}) is None and t.victim({1}) == 0
+
+
+def test_span_alignment():
+    assert [_round_up(n) for n in (0, 1, 256, 257, 196608)] == [0, 256, 256, 512, 196608]
