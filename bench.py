@@ -446,6 +446,97 @@ def bench_qkv_rope(dev, g, steps, warmup):
     return res
 
 
+PCIE_PEAK_GBS = 63.0  # PCIe Gen5 x16, one direction, after 128b/130b encoding
+
+
+def bench_stream(dev, g, steps, warmup, n_layers=4):
+    """Host-streamed decoder weights (mindxsoup_amd/stream.py): a stack of n_layers decoder
+    layers of the model's seven NF4 projections, X [1024, 1536] fp16, forward + backward
+    (input gradients), with the weights resident in HBM, streamed through 2 device slots (the
+    fused GEMMs read the slot), and streamed with the running layer decoded by one launch.
+    Wall clock per step (the streamer's host logic and copies included), and one layer's
+    pinned host -> device copy on the copy stream against PCIe's peak."""
+    from mindxsoup_amd import stream
+    from mindxsoup_amd.linear4bit import Linear4bit
+
+    shapes = {"q_proj": (1536, 1536), "k_proj": (256, 1536), "v_proj": (256, 1536),
+              "o_proj": (1536, 1536), "gate_proj": (8960, 1536), "up_proj": (8960, 1536),
+              "down_proj": (1536, 8960)}
+
+    class Layer(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            for name, (n, k) in shapes.items():
+                w = torch.randn(n, k, device=dev, generator=g) * k ** -0.5
+                setattr(self, name, Linear4bit.from_weight(w.half()))
+
+        def forward(self, x):
+            kv = (self.k_proj(x) + self.v_proj(x)).repeat(1, 6)
+            mlp = self.down_proj(torch.nn.functional.silu(self.gate_proj(x)) * self.up_proj(x))
+            return x + self.o_proj(self.q_proj(x)) + kv + mlp
+
+    class Stack(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.model = torch.nn.Module()
+            self.model.layers = torch.nn.ModuleList([Layer() for _ in range(n_layers)])
+
+        def forward(self, x):
+            for layer in self.model.layers:
+                x = layer(x)
+            return x
+
+    x0 = (torch.randn(M_TOKENS, 1536, device=dev, generator=g) * 0.5).half()
+    dy = (torch.randn(M_TOKENS, 1536, device=dev, generator=g) * 0.01).half()
+
+    def timed(model):
+        def step():
+            x = x0.detach().requires_grad_(True)
+            model(x).backward(dy)
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
+
+    out = {"layers": n_layers, "tokens": M_TOKENS}
+    out["resident_ms_per_step"] = round(timed(Stack()), 3)
+    was = stream.enabled
+    stream.enabled = True
+    try:
+        for key, unpack, slots in (("streamed", False, 2), ("streamed_3_slots", False, 3),
+                                   ("streamed_layer_unpack", True, 2)):
+            stream.reset()
+            model = Stack()
+            assert stream.setup(model, slots=slots, layer_unpack=unpack)
+            s = stream.streamer()
+            ms = timed(model)
+            out[key + "_ms_per_step"] = round(ms, 3)
+            out[key + "_copies_per_step"] = round(s.loads / (steps + warmup), 2)
+        host = s.host_layers[0]
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        reps = 20
+        with torch.cuda.stream(s.copy_stream):
+            s.slots[0][:host.numel()].copy_(host, non_blocking=True)
+            start.record()
+            for _ in range(reps):
+                s.slots[0][:host.numel()].copy_(host, non_blocking=True)
+            end.record()
+        end.synchronize()
+        ms = start.elapsed_time(end) / reps
+        gbs = host.numel() / ms / 1e6
+        out["layer_copy"] = {"bytes": host.numel(), "ms": round(ms, 4), "GBps": round(gbs, 1),
+                             "pcie_frac": round(gbs / PCIE_PEAK_GBS, 3)}
+    finally:
+        stream.reset()
+        stream.enabled = was
+    return out
+
+
 def bench_fused(dev, steps, warmup):
     g = torch.Generator(device=dev)
     g.manual_seed(1)
@@ -480,6 +571,7 @@ def bench_fused(dev, steps, warmup):
     del down, ht
     out["mlp_block"] = bench_mlp(dev, g, steps, warmup)
     out["qkv_rope"] = bench_qkv_rope(dev, g, steps, warmup)
+    out["stream_weights"] = bench_stream(dev, g, max(5, steps // 4), max(2, warmup // 4))
     # config 5: forward + backward of all 28 layers x 7 projections, M = 1024
     layers = []
     for _ in range(LAYERS):
@@ -581,6 +673,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-gemm", action="store_true", help="dequant only")
+    ap.add_argument("--stream", action="store_true",
+                    help="only the host-streamed weights section (its JSON on stdout)")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run a 1 GiB device copy (reference for the PMC byte counters)")
     args = ap.parse_args()
@@ -593,6 +687,11 @@ def main():
     torch.cuda.set_device(dev)
     if args.calibrate:
         calibrate(dev)
+        return
+    if args.stream:
+        g = torch.Generator(device=dev)
+        g.manual_seed(1)
+        print(json.dumps(bench_stream(dev, g, args.steps, args.warmup)), flush=True)
         return
     m = model_weights(dev)
     torch.cuda.synchronize()
