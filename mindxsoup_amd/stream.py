@@ -4,10 +4,10 @@ time (mirror of solution/stream.py).
 Each layer's packed NF4 bytes, then its 8-bit block scales, sit back to back in one pinned host
 block (one host-to-device copy per layer); each module keeps a 1-byte device placeholder of the
 same shape, so the module still looks like a GPU Linear4bit.  A ring of device slots holds the
-layers in use.  While layer i runs, a second HIP stream (default priority) copies layer i +- 1
-ahead in the order the layers run (forward, or backward).  A slot is overwritten only after all
-work enqueued on the compute stream so far has finished, and the compute stream waits for a
-slot's copy before reading it.
+layers in use.  While layer i runs, a second HIP stream (default priority) copies the next
+layers (up to SLOTS - 1) in the order the layers run (forward, or backward).  A slot is
+overwritten only after all work enqueued on the compute stream so far has finished, and the
+compute stream waits for a slot's copy before reading it.
 
 Correctness never depends on the prefetching.  Every NF4 product asks for its module's bytes
 right before use (`bytes_for`), in forward and again in backward, and a layer that is not
@@ -24,7 +24,8 @@ import torch
 
 from . import nf4
 
-SLOTS = 2          # device slots (layers resident at once)
+SLOTS = 3          # device slots (layers resident at once): 24 MB each at Qwen2.5-1.5B's
+                   # shapes, and with 3 a step copies ~2 of 4 layers instead of ~4
 PREFETCH = 2       # layers copied ahead of the running one (at most SLOTS - 1)
 LAYER_UNPACK = False  # FEATURES["layer_unpack"]: the running layer decoded to fp16 in one launch
 _ALIGN = 256       # byte alignment of every module's span inside a slot
