@@ -22,7 +22,8 @@ class Block(torch.nn.Module):
             w = torch.randn(n, k, generator=gen, device=device) * k ** -0.5
             return Linear4bit.from_weight(w.half())
 
-        self.q_proj, self.k_proj, self.v_proj = lin(HIDDEN, HIDDEN), lin(HIDDEN, KV), lin(HIDDEN, KV)
+        self.q_proj = lin(HIDDEN, HIDDEN)
+        self.k_proj, self.v_proj = lin(HIDDEN, KV), lin(HIDDEN, KV)
         self.o_proj = lin(HIDDEN, HIDDEN)
         self.gate_proj, self.up_proj = lin(HIDDEN, INTER), lin(HIDDEN, INTER)
         self.down_proj = lin(INTER, HIDDEN)
