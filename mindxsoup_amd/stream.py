@@ -132,6 +132,7 @@ class LayerStreamer:
         self.loads = 0          # layer copies issued
         self.unpacked = None    # the layer whose fp16 weights the buffer holds
         self.weights = {}       # id(module) -> [N, K] fp16 view of the buffer
+        self.hooks = []         # handles of the layer hooks installed by setup()
         unpack = LAYER_UNPACK if layer_unpack is None else layer_unpack
         self.layer_tables = self._layer_tables() if unpack else None
 
@@ -285,8 +286,12 @@ def streamer():
 
 
 def reset():
-    """Forget the streamer (its modules stay offloaded and use one-off copies)."""
+    """Forget the streamer and remove its layer hooks (its modules stay offloaded and use
+    one-off copies)."""
     global _streamer
+    if _streamer is not None:
+        for h in _streamer.hooks:
+            h.remove()
     _streamer = None
 
 
@@ -339,15 +344,14 @@ def setup(causal_lm, slots=None, prefetch=None, layer_unpack=None, hints=True):
             m.compute_type_is_set = True
     _streamer = LayerStreamer(groups, slots, prefetch, layer_unpack)
     if hints:
-        for index, layer in enumerate(layers):
-            layer.register_forward_pre_hook(_hint_hook(index))
+        _streamer.hooks = [layer.register_forward_pre_hook(_hint_hook(index, _streamer))
+                           for index, layer in enumerate(layers)]
     return True
 
 
-def _hint_hook(index):
+def _hint_hook(index, s):
     def hook(module, args):
-        s = _streamer
-        if s is None:
+        if _streamer is not s:  # the streamer this hook was installed for is gone
             return None
         s.layer_begins(index, forward=True)
         x = args[0] if args else None

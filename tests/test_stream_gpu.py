@@ -133,6 +133,17 @@ def test_offloaded_without_streamer(cuda, streaming):
         assert torch.equal(b(x.float()), a(x.float()))  # the compute-dtype round trip
 
 
+def test_reset_removes_hints(cuda, streaming):
+    first, second = Toy(2, 6, cuda), Toy(3, 6, cuda)
+    assert streaming.setup(first, slots=1)
+    streaming.reset()
+    assert all(not layer._forward_pre_hooks for layer in first.model.layers)
+    assert streaming.setup(second, slots=1)
+    x, dy = _inputs(cuda, m=64)
+    _step(first, x, dy)  # one-off copies; no hint reaches the second model's streamer
+    assert streaming.streamer().loads == 0
+
+
 def test_setup_declines(cuda, streaming, monkeypatch):
     toy = Toy(2, 4, cuda)
     monkeypatch.setattr(streaming, "enabled", False)
