@@ -419,12 +419,19 @@ class Linear4bit(torch.nn.Module):
 
     # bitsandbytes' state-dict form (nn/modules.py Linear4bit._save_to_state_dict): the packed
     # bytes under "weight", the quant state's as_dict(packed=True) under "weight.<key>", bias.
+    # An offloaded weight (stream.offload) writes its host copies, not the device placeholders.
     def _save_to_state_dict(self, destination, prefix, keep_vars):
         super()._save_to_state_dict(destination, prefix, keep_vars)
-        state = getattr(self.weight, "quant_state", None)
-        if state is not None:
-            for k, v in state.as_dict(packed=True).items():
-                destination[prefix + "weight." + k] = v if keep_vars else v.detach()
+        w = self.weight
+        state = getattr(w, "quant_state", None)
+        if state is None:
+            return
+        qs = state.as_dict(packed=True)
+        if hasattr(w, "_mindx_host"):
+            destination[prefix + "weight"] = w._mindx_host.view(w._mindx_shape)
+            qs["absmax"] = w._mindx_absmax.view(state.absmax.shape)
+        for k, v in qs.items():
+            destination[prefix + "weight." + k] = v if keep_vars else v.detach()
 
     def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
                               unexpected_keys, error_msgs):

@@ -179,3 +179,13 @@ def test_loader_offload_and_stream_qwen2(cuda, streaming):
     # the LoRA layers start with B = 0, so the fused resident and the unfused streamed LoRA
     # add the same zero
     assert bool((got == want).all())
+    # a checkpoint of the streamed model holds the weights, not the device placeholders
+    sd_r, sd_s = resident.state_dict(), streamed.state_dict()
+    assert sd_r.keys() == sd_s.keys()
+    for key, v in sd_r.items():
+        assert torch.equal(v.cpu(), sd_s[key].cpu()), key
+    fresh = transformers.Qwen2ForCausalLM(cfg).half().cuda().eval()
+    replace_with_nf4(fresh, lora_targets=("q_proj", "v_proj"))
+    fresh.load_state_dict(sd_s, strict=True)
+    with torch.no_grad():
+        assert torch.equal(fresh(input_ids=ids).logits, want)
