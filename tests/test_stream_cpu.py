@@ -29,3 +29,29 @@ def test_one_slot():
 
 def test_span_alignment():
     assert [_round_up(n) for n in (0, 1, 256, 257, 196608)] == [0, 256, 256, 512, 196608]
+
+
+def test_apply_wires_the_stream_switches(monkeypatch):
+    """FEATURES["stream_weights"] allows stream.setup and FEATURES["layer_unpack"] picks the
+    layer decode (solution/__init__.py:113-171, those switches); setup declines without a GPU."""
+    import torch
+
+    import mindxsoup_amd
+    from mindxsoup_amd import direct, linear4bit, stream
+
+    for key, value in (("nf4", False), ("mlp_fp16", False), ("rope", False),
+                       ("attention_fp16", False), ("stream_weights", True),
+                       ("layer_unpack", True)):
+        monkeypatch.setitem(mindxsoup_amd.FEATURES, key, value)
+    for mod, name in ((direct, "enabled"), (linear4bit, "FUSED_GEMM"),
+                      (linear4bit, "FUSED_LORA"), (stream, "enabled"),
+                      (stream, "LAYER_UNPACK")):
+        monkeypatch.setattr(mod, name, getattr(mod, name))
+    monkeypatch.setattr(stream, "enabled", False)
+    mindxsoup_amd.apply()
+    assert stream.enabled and stream.LAYER_UNPACK
+    model = torch.nn.Module()
+    model.model = torch.nn.Module()
+    model.model.layers = torch.nn.ModuleList([torch.nn.Linear(4, 4)])
+    if not torch.cuda.is_available():
+        assert not stream.setup(model) and not stream.active()
