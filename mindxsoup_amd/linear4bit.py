@@ -301,18 +301,41 @@ class NF4LoraFunction(torch.autograd.Function):
         return dx, da, db, None, None, None, None, None, None
 
 
+class NF4LoraStreamFunction(NF4LoraFunction):
+    """NF4LoraFunction for a base whose bytes live in host memory (stream.py): the slot's bytes
+    are asked for right before the forward GEMM and again before the backward one, so the same
+    kernels run on the same bytes as for a resident base."""
+
+    @staticmethod
+    def forward(ctx, x2d, lora_a, lora_b, module, state, bias, keep, mask_scale, s):
+        packed, absmax = stream.bytes_for(module)
+        y = NF4LoraFunction.forward(ctx, x2d, lora_a, lora_b, packed.view(-1, 1),
+                                    stream.state_with(state, absmax), bias, keep, mask_scale, s)
+        ctx.module, ctx.base_state = module, state
+        ctx.packed = ctx.state = None  # the slot may hold another layer by the backward
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        packed, absmax = stream.bytes_for(ctx.module)
+        ctx.packed, ctx.state = packed.view(-1, 1), stream.state_with(ctx.base_state, absmax)
+        return NF4LoraFunction.backward(ctx, dy)
+
+
 # ---------------------------------------------------------------------------------------------
 # Modules
 # ---------------------------------------------------------------------------------------------
 
-def _direct_ok(layer, x):
+def _direct_ok(layer, x, streamed=False):
     """When the HIP path takes a call (solution/linear4bit.py:112-129, without bitsandbytes'
-    small-M kernel heuristic: the HIP path takes every token count)."""
+    small-M kernel heuristic: the HIP path takes every token count).  With `streamed`, the same
+    test for a weight whose bytes live in host memory (stream.offload), its size checked on the
+    host copy; without it such a weight is refused (it takes the streamed branch)."""
     if not _enabled:
         return False
     weight = layer.weight
-    if hasattr(weight, "_mindx_host"):
-        return False  # bytes in host memory: the streamed branch
+    if hasattr(weight, "_mindx_host") != streamed:
+        return False
     state = getattr(weight, "quant_state", None)
     return (isinstance(x, torch.Tensor) and x.is_cuda and x.dtype == torch.float16
             and getattr(layer, "compute_type_is_set", False)
@@ -324,8 +347,15 @@ def _direct_ok(layer, x):
             and len(state.shape) == 2 and x.shape[-1] == state.shape[1] and x.numel() > 0
             and not weight.requires_grad
             and (layer.bias is None or not layer.bias.requires_grad)
-            and _supported(weight.data, state.shape, state.blocksize, state.quant_type,
-                           x.dtype, state.state2.blocksize))
+            and (_host_size_ok(weight, state) if streamed else
+                 _supported(weight.data, state.shape, state.blocksize, state.quant_type,
+                            x.dtype, state.state2.blocksize)))
+
+
+def _host_size_ok(weight, state):
+    n, k = state.shape
+    return (state.quant_type == "nf4" and state.blocksize == 64
+            and weight._mindx_host.numel() * 2 == n * k)
 
 
 def _cached_weight(layer, x):
@@ -529,7 +559,8 @@ class LoraLinear4bit(torch.nn.Module):
         p = drop.p if isinstance(drop, torch.nn.Dropout) else 0.0
         state = base.weight.quant_state
         r = a.shape[0]
-        if not (FUSED_LORA and _direct_ok(base, x) and kernels.fused_shape_ok(state)
+        streamed = stream.offloaded(base)
+        if not (FUSED_LORA and _direct_ok(base, x, streamed) and kernels.fused_shape_ok(state)
                 and r % 16 == 0 and not getattr(self, "_force_unfused", False)):
             h = drop(x).to(x.dtype) if p > 0 else x
             return base(x) + (h @ a.to(x.dtype).t() @ b.to(x.dtype).t()) * self.scaling[name]
@@ -541,8 +572,12 @@ class LoraLinear4bit(torch.nn.Module):
             keep = self.draw_keep(x2d, p)
             mask_scale = 1.0 / (1.0 - p)
         bias = _cast_bias_once(base, x)
-        y = NF4LoraFunction.apply(x2d, a, b, base.weight.data.view(-1, 1), state, bias, keep,
-                                  mask_scale, float(self.scaling[name]))
+        if streamed:
+            y = NF4LoraStreamFunction.apply(x2d, a, b, base, state, bias, keep, mask_scale,
+                                            float(self.scaling[name]))
+        else:
+            y = NF4LoraFunction.apply(x2d, a, b, base.weight.data.view(-1, 1), state, bias,
+                                      keep, mask_scale, float(self.scaling[name]))
         return y.view(*lead, y.shape[-1])
 
 

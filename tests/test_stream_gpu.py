@@ -91,6 +91,48 @@ def test_streamed_equals_resident(cuda, streaming, slots):
     assert s.loads >= 4
 
 
+def _lora_toy(cuda, seed):
+    from mindxsoup_amd.linear4bit import LoraLinear4bit
+
+    toy = Toy(3, seed, cuda)
+    torch.manual_seed(seed)
+    for layer in toy.model.layers:
+        for name in ("q_proj", "gate_proj", "down_proj"):
+            lora = LoraLinear4bit(getattr(layer, name), r=16, lora_alpha=32, lora_dropout=0.05)
+            torch.nn.init.normal_(lora.lora_B["default"].weight, std=0.05)
+            setattr(layer, name, lora)
+    return toy.train()
+
+
+def test_fused_lora_streamed_equals_resident(cuda, streaming):
+    """peft-layout LoRA over offloaded bases keeps the fused kernels (NF4LoraStreamFunction):
+    output, input gradient and the LoRA gradients equal the resident model's bit for bit."""
+    from mindxsoup_amd import linear4bit
+
+    resident, streamed = _lora_toy(cuda, 9), _lora_toy(cuda, 9)
+    assert streaming.setup(streamed, slots=2)
+    x, dy = _inputs(cuda, m=256)
+    calls = []
+    original = linear4bit.NF4LoraStreamFunction.apply
+
+    def spy(*args):
+        calls.append(1)
+        return original(*args)
+
+    linear4bit.NF4LoraStreamFunction.apply = spy
+    try:
+        for model in (resident, streamed):
+            torch.manual_seed(21)  # the same dropout masks for both
+            model.y, model.g = _step(model, x, dy)
+    finally:
+        linear4bit.NF4LoraStreamFunction.apply = original
+    assert len(calls) == 9  # three LoRA projections in each of three layers, all fused
+    assert torch.equal(streamed.y, resident.y) and torch.equal(streamed.g, resident.g)
+    for (name, pr), (_, ps) in zip(resident.named_parameters(), streamed.named_parameters()):
+        if pr.requires_grad:
+            assert torch.equal(pr.grad, ps.grad), name
+
+
 def test_prefetch_copies_ahead(cuda, streaming):
     streamed = Toy(4, 1, cuda)
     assert streaming.setup(streamed, slots=3, prefetch=2, hints=False)
@@ -176,8 +218,7 @@ def test_loader_offload_and_stream_qwen2(cuda, streaming):
     with torch.no_grad():
         want = resident(input_ids=ids).logits
         got = streamed(input_ids=ids).logits
-    # the LoRA layers start with B = 0, so the fused resident and the unfused streamed LoRA
-    # add the same zero
+    # both LoRA paths are fused (the streamed one on the slot's bytes)
     assert bool((got == want).all())
     # a checkpoint of the streamed model holds the weights, not the device placeholders
     sd_r, sd_s = resident.state_dict(), streamed.state_dict()
