@@ -103,13 +103,14 @@ def dequant_bytes(m):
 
 
 def bench_dequant(m, steps, warmup):
-    from mindxsoup_amd.nf4 import launch_layer
+    from mindxsoup_amd.nf4 import launch_layer, layer_plan
 
     out = torch.empty(m["packed"].numel() * 2, dtype=torch.float16, device=m["packed"].device)
+    plan = layer_plan(m["block0"])  # once, outside the timed steps
 
     def step():
         launch_layer(m["packed"], out, m["absmax8"], m["code"], m["absmax2"], m["offset"], None,
-                     m["block0"], m["scale0"])
+                     m["block0"], m["scale0"], plan)
 
     for _ in range(warmup):
         step()
@@ -249,43 +250,52 @@ BWD_GROUPS = [(6,), (5, 4), (3,), (2, 1, 0)]
 
 
 def layer_fwd(projs, s=ALPHA / RANK):
-    """Forward of one layer's 7 projections: grouped LoRA row products, then each fused GEMM."""
+    """Forward of one layer's 7 projections: grouped LoRA row products, then each fused GEMM.
+    Returns (ys, saved): each projection's output and what its backward needs."""
     from mindxsoup_amd import kernels
 
+    ys = [None] * len(projs)
     saved = [None] * len(projs)
     for grp in FWD_GROUPS:
         ps = [projs[i] for i in grp]
         if len(ps) == 1:
-            saved[grp[0]] = proj_fwd(ps[0], s)[1]
+            ys[grp[0]], saved[grp[0]] = proj_fwd(ps[0], s)
             continue
         outs = kernels.lora_h_partials_group([p["x"] for p in ps], [p["a"] for p in ps], s,
                                              [p["keep"] for p in ps], 1.0 / (1.0 - P_DROP),
                                              [p["b"] for p in ps])
         if grp == (0, 1, 2):  # q, k, v: one GEMM launch (k and v alone would plan split-K)
-            ys = kernels.nf4_linear_fwd_hp_group([p["x"] for p in ps], [p["packed"] for p in ps],
-                                                 [p["st"] for p in ps], [o[0] for o in outs],
-                                                 [p["b"] for p in ps])
-            for i, (_, at, bt), (_, ht) in zip(grp, outs, ys):
-                saved[i] = (ht, at, bt)
+            res = kernels.nf4_linear_fwd_hp_group([p["x"] for p in ps],
+                                                  [p["packed"] for p in ps],
+                                                  [p["st"] for p in ps], [o[0] for o in outs],
+                                                  [p["b"] for p in ps])
+            for i, (_, at, bt), (y, ht) in zip(grp, outs, res):
+                ys[i], saved[i] = y, (ht, at, bt)
             continue
         for i, p, (hp, at, bt) in zip(grp, ps, outs):
-            _, ht = kernels.nf4_linear_fwd_hp(p["x"], p["packed"], p["st"], hp, p["b"],
-                                              ws=p["ws"])
+            ys[i], ht = kernels.nf4_linear_fwd_hp(p["x"], p["packed"], p["st"], hp, p["b"],
+                                                  ws=p["ws"])
             saved[i] = (ht, at, bt)
-    return saved
+    return ys, saved
 
 
 def layer_bwd(projs, saved, s=ALPHA / RANK):
     """Backward of one layer's 7 projections in reverse order; each group's small launches
-    (dHs, dA / dB) and the v/k/q dX GEMMs shared (linear4bit.lora_backward_group)."""
+    (dHs, dA / dB) and the v/k/q dX GEMMs shared (linear4bit.lora_backward_group).  Returns
+    each projection's (dX, dA, dB)."""
     from mindxsoup_amd.linear4bit import lora_backward_group
 
+    grads = [None] * len(projs)
     for grp in BWD_GROUPS:
-        lora_backward_group([dict(dy=projs[i]["dy"], x2d=projs[i]["x"], keep=projs[i]["keep"],
-                                  ht=saved[i][0], at=saved[i][1], bt=saved[i][2],
-                                  packed=projs[i]["packed"], state=projs[i]["st"],
-                                  mask_scale=1.0 / (1.0 - P_DROP), s=s,
-                                  wants=(True, True, True)) for i in grp], ws=projs[grp[0]]["ws"])
+        res = lora_backward_group([dict(dy=projs[i]["dy"], x2d=projs[i]["x"],
+                                        keep=projs[i]["keep"], ht=saved[i][0], at=saved[i][1],
+                                        bt=saved[i][2], packed=projs[i]["packed"],
+                                        state=projs[i]["st"], mask_scale=1.0 / (1.0 - P_DROP),
+                                        s=s, wants=(True, True, True)) for i in grp],
+                                  ws=projs[grp[0]]["ws"])
+        for i, r in zip(grp, res):
+            grads[i] = r
+    return grads
 
 
 def graph_time(fn, steps, warmup):
@@ -588,7 +598,7 @@ def bench_fused(dev, steps, warmup):
     def step():
         saved = []
         for projs in layers:
-            saved.append(layer_fwd(projs))
+            saved.append(layer_fwd(projs)[1])
         for projs, hts in zip(reversed(layers), reversed(saved)):
             layer_bwd(projs, hts)
 

@@ -58,12 +58,14 @@ int mxs_nf4_dequant_bytewise(const void* packed, int64_t n_bytes, const void* ab
  * block0: device int64 [n_modules + 1] ascending, block0[0] = 0, block0[n_modules] = n_blocks;
  * scale0: device int64 [n_modules].  packed and out must be 16-byte aligned.
  * wg_module: device int16 map from mxs_nf4_dequant_layer_plan (the counterpart of the
- * reference's per-program `module_of`, solution/stream.py:125-133), or NULL to look each
- * block's module up in the kernel (slower). */
+ * reference's per-program `module_of`, solution/stream.py:125-133) with its n_plan entries
+ * (one per workgroup: ceil(n_blocks / 128), else MXS_ERR_SIZE), or NULL to look each block's
+ * module up in the kernel (slower). */
 int mxs_nf4_dequant_layer(const void* packed, int64_t n_blocks, const void* absmax8,
                           const float* code, const float* absmax2, const float* offset,
                           const int64_t* block0, const int64_t* scale0, int n_modules,
-                          const int16_t* wg_module, void* out, hipStream_t stream);
+                          const int16_t* wg_module, int64_t n_plan, void* out,
+                          hipStream_t stream);
 
 /* Host-side plan for mxs_nf4_dequant_layer: from HOST block0 [n_modules + 1], writes the module
  * of each of the kernel's workgroups (-1 where one straddles two modules) into HOST wg_module

@@ -20,16 +20,16 @@ FEATURES = {
     "layer_unpack": False,   # with stream_weights: the running layer decoded by one launch
     "direct_nograd": True,   # no Function.apply wrappers when no graph is recorded (direct.py)
     "nf4_fused_gemm": True,  # dequant fused into the GEMM main loop (else HIP unpack + F.linear)
-    "nf4_fused_lora": True,  # LoRA branch fused into the GEMM epilogues (LoraLinear4bit)
+    "nf4_fused_lora": True,  # LoRA branch fused into the GEMMs (peft's LoRA layers included)
     "mlp_fp16": True,        # Qwen2 MLP on fp16 activations (mlp.py; the SwiGLU of silu_mul.py)
     "mlp_fused_swiglu": True,  # that MLP's SwiGLU in the up/down GEMM epilogues (LoRA layers)
-    "rope": True,            # RoPE of q and k in one launch each way (rope.py)
-    "attention_fp16": True,  # fp16 q/k/v, one launch for LoRA sum + RoPE + cast (attention.py)
+    "attention_fp16": True,  # fp16 q/k/v from grouped NF4 + LoRA launches, one RoPE launch
     "stream_weights": False,  # decoder NF4 weights in pinned host memory, a layer at a time
     # --- reference switches outside the NF4 path (inert here) ------------------------------
     "startup_cache": False, "example_swiglu": False, "adam_host": False,
     "cublas_workspace": None, "fused_layer_input": False, "fused_head_acc": False,
     "lean_draw": False, "mlp_gateup_recompute": False, "mlp_tail": False, "rmsnorm": False,
+    "rope": False,  # the RoPE-only patch of apply_rotary_pos_emb; attention_fp16 rotates instead
     "fused_ce": False, "fp16_embedding": False, "head_stream": False,
     "head_slice": 4096, "unpad": False, "recompute": False,
     "recompute_fp16_inputs": False, "recompute_host_inputs": False,
@@ -38,8 +38,11 @@ FEATURES = {
 }
 
 PROFILE = "rules_fast"
+# The reference's rules_fast also sets layer_unpack; here the fused GEMM on the streamed slot
+# measured faster than the whole-layer decode (3 slots, 4 layers: 2.6-3.3 ms against 3.0-4.0 ms
+# per step at 1024 tokens), so streamed weights keep the fused GEMM unless layer_unpack is set.
 PROFILES = {
-    "rules_fast": {"layer_unpack": True},
+    "rules_fast": {},
     "rules_time": {"nf4_cache_fp16": True},
     "rules_memory": {},
 }
@@ -47,9 +50,10 @@ FEATURES.update(PROFILES[PROFILE])
 
 
 def apply():
-    """Install the NF4 and fp16-MLP patches named by FEATURES (solution/__init__.py:113-171,
-    those parts)."""
-    from . import linear4bit, nf4, stream
+    """Install the patches FEATURES names (the NF4 part of solution/__init__.py:113-171): the
+    bitsandbytes dequant hooks and Linear4bit forward, peft's 4-bit LoRA layer on the fused
+    kernels, the fp16 MLP and attention paths."""
+    from . import linear4bit, nf4, peft_lora, stream
 
     direct.enabled = FEATURES["direct_nograd"]
     stream.LAYER_UNPACK = FEATURES["layer_unpack"]
@@ -61,15 +65,13 @@ def apply():
         nf4.patch_bnb_nf4()
         if FEATURES["nf4_direct"]:
             linear4bit.patch_bnb_linear4bit(cache_weights=FEATURES["nf4_cache_fp16"])
+    if FEATURES["nf4_fused_lora"]:
+        peft_lora.patch_peft_lora()
     if FEATURES["mlp_fp16"]:
         from . import mlp
 
         mlp.FUSED_SWIGLU = FEATURES["mlp_fused_swiglu"]
         mlp.patch_qwen2_mlp_fp16()
-    if FEATURES["rope"]:
-        from . import rope
-
-        rope.patch_rope()
     if FEATURES["attention_fp16"]:
         from . import attention
 

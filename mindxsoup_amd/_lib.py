@@ -34,7 +34,7 @@ F32 = ctypes.c_float
 _SIGNATURES = {
     "mxs_nf4_dequant": [P, I64, P, P, P, P, P, P, I32, P],
     "mxs_nf4_dequant_bytewise": [P, I64, P, P, P, P, P, P, I32, P],
-    "mxs_nf4_dequant_layer": [P, I64, P, P, P, P, P, P, I32, P, P, P],
+    "mxs_nf4_dequant_layer": [P, I64, P, P, P, P, P, P, I32, P, I64, P, P],
     "mxs_nf4_dequant_layer_plan": [P, I32, P, I64],
     "mxs_nf4_quantize_workspace_bytes": [I64],
     "mxs_nf4_quantize": [P, I64, P, P, P, P, P, P, P, P],

@@ -1,83 +1,109 @@
-"""Qwen2 attention with fp16 q/k/v (mirror of solution/attention.py:174-290): the input is cast to
-fp16 once, the three projections run on the NF4 path and return fp16, and one launch
-(rope.qkv_rope on csrc/rope.hip) adds any separate LoRA outputs, rotates q and k and writes the
-fp16 q/k/v that SDPA reads.  With this package's LoraLinear4bit the LoRA term is already inside
-each projection's GEMM, so qkv_rope only rotates.  Anything the fast path does not take (CPU, a
-KV cache, another attention backend, no fp16 autocast, projections that are not fp16 4-bit
-layers) goes to transformers' own forward.
-"""
+"""Qwen2 attention's q/k/v on the fused NF4 + LoRA kernels (the fp16 attention path of
+solution/attention.py, rebuilt around this package's grouped launches).
 
-import math
+The patched Qwen2Attention.forward keeps transformers' contract (same arguments, same
+(output, weights) result, transformers' attention interface for the attention itself) and
+changes how q, k and v are made:
+
+  1. the input is cast to fp16 once;
+  2. when q, k and v are LoRA layers of one rank, scaling and dropout over NF4 bases (peft's
+     layout; peft_lora.adapter_of), all three run as one NF4LoraSiblingsFunction: one launch
+     of LoRA row products and one launch of fused GEMMs forward, shared launches backward; any
+     other mix of fp16 NF4 projections (bare or LoRA) runs projection by projection, each on
+     the fused kernels;
+  3. one launch rotates q and k (rope.qkv_rope); v goes to attention as a view, uncopied.
+
+The call takes the original forward when the path cannot serve it (a reason from
+`_refusal`): no GPU tensor, a KV cache or attention weights requested, no fp16 autocast (the
+original then runs SDPA in fp32), another attention backend or head size, unusual cos / sin, or
+a projection that is not an fp16 NF4 layer the fused kernels take.
+"""
 
 import torch
 
-from .linear4bit import LoraLinear4bit
+from . import linear4bit, peft_lora
 from .rope import HEAD_DIM, qkv_rope
 
 
-def _is_fp16_4bit(linear):
-    base = getattr(linear, "base_layer", linear)
-    return getattr(getattr(base, "weight", None), "quant_state", None) is not None and \
-        getattr(base, "compute_dtype", None) == torch.float16
-
-
-def _split_projection(proj):
-    """(layer to call on the fp16 input, separate LoRA function or None, its scale), or None when
-    the fast path does not take the projection (solution/attention.py:174-202).  This package's
-    LoraLinear4bit and a bare fp16 4-bit layer are called whole; peft's LoRA wrapper around a
-    4-bit layer gives its base and its LoRA branch, whose power-of-two scaling the kernel
-    applies (exact in fp16 and fp32)."""
-    if isinstance(proj, LoraLinear4bit) or getattr(proj, "lora_A", None) is None:
-        return (proj, None, 1.0) if _is_fp16_4bit(proj) else None
-    base = getattr(proj, "base_layer", None)
-    if not _is_fp16_4bit(base):
-        return None
-    if getattr(proj, "disable_adapters", True) or getattr(proj, "merged", True):
-        return None
-    lora_a = proj.lora_A
-    active = list(getattr(proj, "active_adapters", []))
-    if len(active) != 1 or active[0] not in lora_a.keys() \
-            or active[0] in getattr(proj, "lora_variant", {}):
-        return None
-    name = active[0]
-    scaling = proj.scaling[name]
-    exact = isinstance(scaling, (int, float)) and scaling > 0 and \
-        math.frexp(scaling)[0] == 0.5 and 2.0 ** -8 <= scaling <= 2.0 ** 8
-
-    def lora(x):  # peft's LoRA branch under autocast
-        out = proj.lora_B[name](proj.lora_A[name](proj.lora_dropout[name](x)))
-        return out if exact else out * scaling
-
-    return base, lora, (float(scaling) if exact else 1.0)
-
-
-def _fast_path_ok(module, hidden_states, position_embeddings, past_key_values, kwargs):
-    """solution/attention.py:205-227."""
-    if (not isinstance(hidden_states, torch.Tensor) or not hidden_states.is_cuda
-            or hidden_states.dtype not in (torch.float32, torch.float16)
-            or hidden_states.dim() != 3 or past_key_values is not None
-            or kwargs.get("output_attentions", False)):
-        return False
-    if not (torch.is_autocast_enabled("cuda")
-            and torch.get_autocast_dtype("cuda") == torch.float16):
-        return False  # without fp16 autocast transformers runs SDPA in fp32: keep it
-    config = getattr(module, "config", None)
-    if getattr(config, "_attn_implementation", None) != "sdpa" or \
-            getattr(module, "head_dim", None) != HEAD_DIM:
-        return False
+def _refusal(module, hidden, position_embeddings, past_key_values, kwargs):
+    """Why the fp16 path does not take this call, or None when it does."""
+    if not isinstance(hidden, torch.Tensor) or not hidden.is_cuda or hidden.dim() != 3:
+        return "input is not a [B, T, hidden] GPU tensor"
+    if hidden.dtype not in (torch.float16, torch.float32):
+        return f"input dtype {hidden.dtype}"
+    if past_key_values is not None or kwargs.get("output_attentions", False):
+        return "KV cache or attention weights requested"
+    if not torch.is_autocast_enabled("cuda") or torch.get_autocast_dtype("cuda") != torch.float16:
+        return "no fp16 autocast"
+    if getattr(getattr(module, "config", None), "_attn_implementation", None) != "sdpa":
+        return "attention backend is not sdpa"
+    if getattr(module, "head_dim", None) != HEAD_DIM:
+        return "head size is not 128"
     if not isinstance(position_embeddings, (tuple, list)) or len(position_embeddings) != 2:
-        return False
-    cos, sin = position_embeddings
-    batch, n_tokens, _ = hidden_states.shape
-    return all(isinstance(x, torch.Tensor) and x.is_cuda and x.dim() == 3
-               and x.dtype in (torch.float32, torch.float16) and not x.requires_grad
-               and x.shape[0] in (1, batch) and tuple(x.shape[1:]) == (n_tokens, HEAD_DIM)
-               for x in (cos, sin))
+        return "no (cos, sin) pair"
+    b, t, _ = hidden.shape
+    for x in position_embeddings:
+        if not (isinstance(x, torch.Tensor) and x.is_cuda and x.dim() == 3
+                and x.dtype in (torch.float16, torch.float32) and not x.requires_grad
+                and x.shape[0] in (1, b) and tuple(x.shape[1:]) == (t, HEAD_DIM)):
+            return "cos / sin shape or dtype"
+    return None
+
+
+def _route(proj, x16):
+    """How one projection runs on x16: ("lora", Adapter) for a LoRA layer the fused kernels
+    take, ("base", layer) for a bare fp16 NF4 layer on the HIP path, or None."""
+    ad = peft_lora.adapter_of(proj)
+    if ad is not None:
+        return ("lora", ad) if peft_lora.takes(ad, x16) else None
+    if getattr(proj, "lora_A", None) is not None:  # a LoRA layer this path does not take
+        return None
+    if getattr(getattr(proj, "weight", None), "quant_state", None) is None or \
+            getattr(proj, "compute_dtype", None) != torch.float16:
+        return None
+    return ("base", proj) if linear4bit._direct_ok(proj, x16) else None
+
+
+def _siblings(ads, x2d):
+    """Proj records for NF4LoraSiblingsFunction, or None when the three adapters differ in
+    rank, scaling or dropout (their row products could not share a launch)."""
+    if len({(ad.rank, ad.s, ad.p, ad.dropping()) for ad in ads}) != 1:
+        return None
+    projs = []
+    for ad in ads:
+        keep, mask_scale = None, 1.0
+        if ad.dropping():
+            keep = ad.keep_mask(x2d)
+            mask_scale = 1.0 / (1.0 - ad.p)
+        base = ad.base
+        projs.append(linear4bit.Proj(base.weight.data.view(-1, 1), base.weight.quant_state,
+                                     linear4bit._cast_bias_once(base, x2d), keep, mask_scale,
+                                     ad.s))
+    projs = tuple(projs)
+    return projs if linear4bit.siblings_ok(projs, x2d.shape[1]) else None
+
+
+def project_qkv(attn, x16):
+    """q, k, v fp16 [B, T, heads * 128] of the attention's projections on x16 [B, T, hidden],
+    or None when one of them is not an fp16 NF4 projection the fused kernels take."""
+    routes = [_route(getattr(attn, n, None), x16) for n in ("q_proj", "k_proj", "v_proj")]
+    if any(r is None for r in routes):
+        return None
+    if all(kind == "lora" for kind, _ in routes) and \
+            not any(linear4bit.stream.offloaded(ad.base) for _, ad in routes):
+        x2d = x16.reshape(-1, x16.shape[-1]).contiguous()
+        projs = _siblings([ad for _, ad in routes], x2d)
+        if projs is not None:
+            ab = [t for _, ad in routes for t in (ad.a, ad.b)]
+            outs = linear4bit.NF4LoraSiblingsFunction.apply(x2d, projs, *ab)
+            return [y.view(*x16.shape[:-1], y.shape[-1]) for y in outs]
+    return [peft_lora.fused_project(obj, x16) if kind == "lora" else obj(x16)
+            for kind, obj in routes]
 
 
 def patch_qwen2_attention_fp16():
-    """Send Qwen2Attention.forward through the fp16 path (solution/attention.py:230-290); returns
-    whether transformers' Qwen2 model is importable."""
+    """Install the fp16 q/k/v path on transformers' Qwen2Attention; returns whether
+    transformers' Qwen2 model is importable."""
     try:
         from transformers.models.qwen2 import modeling_qwen2
     except Exception:
@@ -89,36 +115,27 @@ def patch_qwen2_attention_fp16():
 
     def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values=None,
                 **kwargs):
-        parts = None
-        if _fast_path_ok(self, hidden_states, position_embeddings, past_key_values, kwargs):
-            parts = [_split_projection(getattr(self, name, None))
-                     for name in ("q_proj", "k_proj", "v_proj")]
-        if parts is None or any(p is None for p in parts) or parts[1][1] is not None:
+        qkv = None
+        if _refusal(self, hidden_states, position_embeddings, past_key_values, kwargs) is None:
+            qkv = project_qkv(self, hidden_states.to(torch.float16))
+        if qkv is None:
             return original(self, hidden_states, position_embeddings, attention_mask,
                             past_key_values, **kwargs)
-        (q_layer, q_lora, q_scale), (k_layer, _, _), (v_layer, v_lora, v_scale) = parts
-        input_shape = hidden_states.shape[:-1]
-        x16 = hidden_states.to(torch.float16)
-        # the order of the original forward: q (base, LoRA), k, v (base, LoRA)
-        q_base = q_layer(x16)
-        q_add = None if q_lora is None else q_lora(hidden_states)
-        k = k_layer(x16)
-        v_base = v_layer(x16)
-        v_add = None if v_lora is None else v_lora(hidden_states)
-        n_q, n_kv = q_base.shape[-1] // self.head_dim, k.shape[-1] // self.head_dim
+        q, k, v = qkv
         cos, sin = position_embeddings
-        query, key, value = qkv_rope(q_base, q_add, k, v_base, v_add, cos, sin, n_q, n_kv,
-                                     q_scale, v_scale)
-        attention_interface = modeling_qwen2.ALL_ATTENTION_FUNCTIONS.get_interface(
+        query, key, value = qkv_rope(q, None, k, v, None, cos, sin, q.shape[-1] // HEAD_DIM,
+                                     k.shape[-1] // HEAD_DIM)
+        attend = modeling_qwen2.ALL_ATTENTION_FUNCTIONS.get_interface(
             self.config._attn_implementation, modeling_qwen2.eager_attention_forward)
-        attn_output, attn_weights = attention_interface(
-            self, query, key, value, attention_mask,
-            dropout=0.0 if not self.training else self.attention_dropout,
-            scaling=self.scaling, sliding_window=self.sliding_window, **kwargs)
-        attn_output = attn_output.reshape(*input_shape, -1).contiguous()
-        return self.o_proj(attn_output), attn_weights
+        out, weights = attend(self, query, key, value, attention_mask,
+                              dropout=self.attention_dropout if self.training else 0.0,
+                              scaling=self.scaling, sliding_window=self.sliding_window, **kwargs)
+        # SDPA hands back [B, T, heads, D]; o_proj reads [B, T, heads * D] rows
+        out = out.reshape(*hidden_states.shape[:-1], -1).contiguous()
+        return self.o_proj(out), weights
 
     forward._mindx_original = original
     cls.forward = forward
     cls._mindx_fp16 = True
     return True
+

@@ -250,11 +250,14 @@ int64_t mxs_nf4_dequant_layer_plan(const int64_t* block0, int n_modules, int16_t
 int mxs_nf4_dequant_layer(const void* packed, int64_t n_blocks, const void* absmax8,
                           const float* code, const float* absmax2, const float* offset,
                           const int64_t* block0, const int64_t* scale0, int n_modules,
-                          const int16_t* wg_module, void* out, hipStream_t stream) {
+                          const int16_t* wg_module, int64_t n_plan, void* out,
+                          hipStream_t stream) {
   if (n_blocks == 0 && n_modules >= 1) return MXS_OK;
   if (n_blocks < 0 || n_modules < 1 || !packed || !out || !absmax8 || !code || !absmax2 ||
       !offset || !block0 || !scale0)
     return MXS_ERR_ARG;
+  // every workgroup reads its entry of the plan: one of another length belongs to another layout
+  if (wg_module && n_plan != (n_blocks + kDqBlocks - 1) / kDqBlocks) return MXS_ERR_SIZE;
   if (((uintptr_t)packed % 16) != 0 || ((uintptr_t)out % 16) != 0) return MXS_ERR_ALIGN;
   DequantArgs a{};
   a.packed = static_cast<const uint32_t*>(packed);

@@ -1,33 +1,40 @@
-"""Autograd functions called directly when no gradient is recorded (solution/direct.py:15-36).
+"""Autograd Functions without the autograd wrapper when no graph is being recorded.
 
-Under no_grad, `Function.apply` only adds Python around `Function.forward`; `run` calls the
-forward with a context object that drops whatever backward would have needed.
+The reference calls each of its Functions through a helper that skips `Function.apply` under
+no_grad (solution/direct.py:15-36): in a forward that records nothing, `apply` only adds Python
+around `forward`, once per projection per layer.  `run(function, *args)` does the same here.
+Its context stand-in is built fresh for each call and dropped when the call returns, so whatever
+a forward stores on it (saved tensors, shapes) dies with the call instead of outliving it.
 """
 
 import torch
 
-enabled = False  # set by apply()
+enabled = False  # set by apply() from FEATURES["direct_nograd"]
 
 
-class _NoBackward:
-    """The context a Function's forward sees when there will be no backward."""
+class _Unrecorded:
+    """What a Function's forward gets for `ctx` when nothing is recorded: attribute writes land
+    on this throwaway object; saving and marking are no-ops."""
 
     needs_input_grad = ()
+    materialize_grads = True
 
-    def __setattr__(self, _name, _value):
-        pass  # one shared instance: it must not keep anything alive
+    def save_for_backward(self, *tensors):
+        del tensors
 
-    def save_for_backward(self, *_tensors):
-        pass
+    def mark_non_differentiable(self, *tensors):
+        del tensors
 
-    def mark_non_differentiable(self, *_tensors):
-        pass
+    def mark_dirty(self, *tensors):
+        del tensors
 
-
-_context = _NoBackward()
+    def set_materialize_grads(self, value):
+        self.materialize_grads = value
 
 
 def run(function, *args):
+    """function.apply(*args), or function.forward on a throwaway context when grad mode is off
+    (and the switch is on): same outputs, no autograd node."""
     if enabled and not torch.is_grad_enabled():
-        return function.forward(_context, *args)
+        return function.forward(_Unrecorded(), *args)
     return function.apply(*args)

@@ -36,7 +36,39 @@ def _c(t):
     return None if t is None else t.contiguous()
 
 
-def _nf4_args(packed, state):
+def check_nf4_operands(packed, state, device=None):
+    """Raise ValueError unless the NF4 operands the kernels read through raw pointers hold what
+    state.shape [N, K] says: packed contiguous uint8 with N*K/2 bytes, absmax contiguous uint8
+    with N*K/64 entries, state2.absmax contiguous fp32 with ceil(N*K/64/256) entries, the code
+    book fp32 [256], offset fp32, all on `device` (default: packed's).  An offloaded weight's
+    placeholder (a stride-0 expand of one byte, stream.offload) fails the contiguity test."""
+    n, k = (int(d) for d in state.shape)
+    blocks = n * k // 64
+    device = packed.device if device is None else device
+    if packed.dtype != torch.uint8 or not packed.is_contiguous() or 2 * packed.numel() != n * k:
+        raise ValueError(f"packed must be contiguous uint8 with {n * k // 2} bytes for "
+                         f"[{n}, {k}]")
+    absmax = state.absmax
+    if absmax.dtype != torch.uint8 or not absmax.is_contiguous() or absmax.numel() != blocks:
+        raise ValueError(f"quant_state.absmax must be contiguous uint8 [{blocks}]")
+    s2 = state.state2
+    if s2 is None:
+        raise ValueError("the fused kernels need a nested (double-quantized) absmax")
+    a2, code, off = s2.absmax, s2.code, state.offset
+    if a2.dtype != torch.float32 or not a2.is_contiguous() or \
+            a2.numel() != (blocks + 255) // 256:
+        raise ValueError(f"state2.absmax must be contiguous fp32 [{(blocks + 255) // 256}]")
+    if code.dtype != torch.float32 or not code.is_contiguous() or code.numel() != 256:
+        raise ValueError("state2.code must be contiguous fp32 [256]")
+    if off is None or off.dtype != torch.float32 or off.numel() < 1:
+        raise ValueError("quant_state.offset must be an fp32 tensor")
+    for t in (packed, absmax, a2, code, off):
+        if t.device != device:
+            raise ValueError(f"NF4 operands must be on {device}, found {t.device}")
+
+
+def _nf4_args(packed, state, device=None):
+    check_nf4_operands(packed, state, device)
     return (_lib.ptr(packed), _lib.ptr(state.absmax), _lib.ptr(state.state2.code),
             _lib.ptr(state.state2.absmax), _lib.ptr(state.offset))
 
@@ -185,6 +217,8 @@ def nf4_linear_bwd_dx_grads_group(dys, packeds, states, dhs, ats, dhts, hts, x2d
         if dh.shape != (M, r) or at.shape != (K, r) or dht.shape[0] != r or ht.shape != dht.shape:
             raise ValueError("LoRA operands disagree")
     dev = dys[0].device
+    for pk, st in zip(packeds, states):
+        check_nf4_operands(pk, st, dev)
     dx = [torch.empty((M, K), dtype=torch.float16, device=dev) for _ in dys]
     da = [torch.empty((r, K), dtype=torch.float32, device=dev) for _ in dys]
     db = [torch.empty((nn_, r), dtype=torch.float32, device=dev) for nn_ in Ns]
@@ -376,10 +410,11 @@ def nf4_linear_fwd_hp_group(x2ds, packeds, states, lora_hps=None, lora_bs=None, 
     dev = x2ds[0].device
     S = ldt = r = 0
     ys, hts, b16, bias16 = [], [], [], []
-    for st, hp, b, bias in zip(states, lora_hps, lora_bs, biases):
+    for pk, st, hp, b, bias in zip(packeds, states, lora_hps, lora_bs, biases):
         nn_, k = st.shape
         if k != K:
             raise ValueError("every weight must take K inputs")
+        check_nf4_operands(pk, st, dev)
         ys.append(torch.empty((M, nn_), dtype=torch.float16, device=dev))
         ht = None
         if hp is not None:

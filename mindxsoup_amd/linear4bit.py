@@ -301,6 +301,87 @@ class NF4LoraFunction(torch.autograd.Function):
         return dx, da, db, None, None, None, None, None, None
 
 
+class Proj:
+    """What one projection's kernels need besides its LoRA tensors: the packed NF4 weight and its
+    state, the fp16 bias, the u8 dropout keep mask (None without dropout), 1/(1-p) and the LoRA
+    scaling."""
+
+    __slots__ = ("packed", "state", "bias", "keep", "mask_scale", "s")
+
+    def __init__(self, packed, state, bias, keep, mask_scale, s):
+        self.packed, self.state, self.bias = packed, state, bias
+        self.keep, self.mask_scale, self.s = keep, mask_scale, s
+
+
+def siblings_ok(projs, K):
+    """Whether NF4LoraSiblingsFunction takes these projections of one input width K: 2 to 4 of
+    them, one LoRA scaling and one dropout rate (their row products share one launch), every
+    weight within the grouped GEMM's 32-bit offsets."""
+    return (2 <= len(projs) <= 4
+            and len({(p.s, p.mask_scale) for p in projs}) == 1
+            and all(p.state.shape[1] == K and p.state.shape[0] * K < 2 ** 32 for p in projs)
+            and 128 * K * 2 < 2 ** 32)
+
+
+class NF4LoraSiblingsFunction(torch.autograd.Function):
+    """NF4 + LoRA projections that read the same input (a layer's q, k and v), computed with
+    their launches shared: forward, one launch of LoRA row products (s * drop(x) A^T for each)
+    and one launch of the fused GEMMs; backward, lora_backward_group (the dHs launches, the dX
+    GEMMs with their dA / dB, shared where the plans allow) and dx = the sum of the projections'
+    input gradients.  Each output equals NF4LoraFunction on its projection to within the GEMM
+    tolerance (the grouped GEMM runs every problem on one tile plan).
+    Inputs: x2d fp16 [M, K], `projs` (a tuple of Proj that siblings_ok accepts), then each
+    projection's lora_A [r, K] and lora_B [N, r] (their gradients come back in their dtypes).
+    Outputs: one fp16 [M, N_i] per projection."""
+
+    @staticmethod
+    def forward(ctx, x2d, projs, *ab):
+        n = len(projs)
+        a16 = [t.to(torch.float16).contiguous() for t in ab[0::2]]
+        b16 = [t.to(torch.float16).contiguous() for t in ab[1::2]]
+        s, mask_scale = projs[0].s, projs[0].mask_scale
+        rows = kernels.lora_h_partials_group([x2d] * n, a16, s, [p.keep for p in projs],
+                                             mask_scale, b16)
+        outs = kernels.nf4_linear_fwd_hp_group([x2d] * n, [p.packed for p in projs],
+                                               [p.state for p in projs], [r[0] for r in rows],
+                                               b16, [p.bias for p in projs])
+        ctx.save_for_backward(x2d, *[p.keep for p in projs], *[o[1] for o in outs],
+                              *[r[1] for r in rows], *[r[2] for r in rows])
+        ctx.projs = projs
+        ctx.dtypes = [t.dtype for t in ab]
+        return tuple(o[0] for o in outs)
+
+    @staticmethod
+    def backward(ctx, *dys):
+        projs = ctx.projs
+        n = len(projs)
+        saved = ctx.saved_tensors
+        x2d = saved[0]
+        keeps, hts, ats, bts = (saved[1 + i * n:1 + (i + 1) * n] for i in range(4))
+        need = ctx.needs_input_grad
+        items = []
+        for i, p in enumerate(projs):
+            dy = dys[i]
+            if dy is None:
+                dy = torch.zeros((x2d.shape[0], p.state.shape[0]), dtype=torch.float16,
+                                 device=x2d.device)
+            items.append(dict(dy=dy.to(torch.float16).contiguous(), x2d=x2d, keep=keeps[i],
+                              ht=hts[i], at=ats[i], bt=bts[i], packed=p.packed, state=p.state,
+                              mask_scale=p.mask_scale, s=p.s,
+                              wants=(need[0], need[2 + 2 * i], need[3 + 2 * i])))
+        res = lora_backward_group(items)
+        dx = None
+        if need[0]:
+            dx = res[0][0]
+            for r in res[1:]:
+                dx = dx + r[0]
+        grads = []
+        for i, (_, da, db) in enumerate(res):
+            grads += [None if da is None else da.to(ctx.dtypes[2 * i]),
+                      None if db is None else db.to(ctx.dtypes[2 * i + 1])]
+        return (dx, None, *grads)
+
+
 class NF4LoraStreamFunction(NF4LoraFunction):
     """NF4LoraFunction for a base whose bytes live in host memory (stream.py): the slot's bytes
     are asked for right before the forward GEMM and again before the backward one, so the same
@@ -539,46 +620,23 @@ class LoraLinear4bit(torch.nn.Module):
             return None
         return self.active_adapters[0]
 
-    def draw_keep(self, x2d, p, shape=None):
-        """The dropout keep mask [M, K] (x2d's shape, or `shape`) as u8 (a fresh
-        Bernoulli(1 - p) draw)."""
-        if self.next_keep is not None:
-            keep, self.next_keep = self.next_keep, None
-            return keep
-        return torch.empty(x2d.shape if shape is None else shape, dtype=torch.uint8,
-                           device=x2d.device).bernoulli_(1.0 - p)
-
     def forward(self, x):
-        name = self._adapter()
-        base = self.base_layer
-        if name is None:
-            return base(x)
-        a = self.lora_A[name].weight
-        b = self.lora_B[name].weight
-        drop = self.lora_dropout[name]
-        p = drop.p if isinstance(drop, torch.nn.Dropout) else 0.0
-        state = base.weight.quant_state
-        r = a.shape[0]
-        streamed = stream.offloaded(base)
-        if not (FUSED_LORA and _direct_ok(base, x, streamed) and kernels.fused_shape_ok(state)
-                and r % 16 == 0 and not getattr(self, "_force_unfused", False)):
-            h = drop(x).to(x.dtype) if p > 0 else x
-            return base(x) + (h @ a.to(x.dtype).t() @ b.to(x.dtype).t()) * self.scaling[name]
-        lead = x.shape[:-1]
-        x2d = x.reshape(-1, x.shape[-1]).contiguous()
-        keep = None
-        mask_scale = 1.0
-        if self.training and p > 0:
-            keep = self.draw_keep(x2d, p)
-            mask_scale = 1.0 / (1.0 - p)
-        bias = _cast_bias_once(base, x)
-        if streamed:
-            y = NF4LoraStreamFunction.apply(x2d, a, b, base, state, bias, keep, mask_scale,
-                                            float(self.scaling[name]))
-        else:
-            y = NF4LoraFunction.apply(x2d, a, b, base.weight.data.view(-1, 1), state, bias,
-                                      keep, mask_scale, float(self.scaling[name]))
-        return y.view(*lead, y.shape[-1])
+        from . import peft_lora
+
+        return peft_lora.lora_forward(self, x, _composed_lora)
+
+
+def _composed_lora(layer, x):
+    """base(x) + s * B(A(drop(x))) as separate torch operations (peft's own composition), for
+    inputs or layers the fused path does not take."""
+    name = layer._adapter()
+    base = layer.base_layer
+    if name is None:
+        return base(x)
+    a = layer.lora_A[name].weight.to(x.dtype)
+    b = layer.lora_B[name].weight.to(x.dtype)
+    h = layer.lora_dropout[name](x)
+    return base(x) + (h @ a.t() @ b.t()) * layer.scaling[name]
 
 
 def patch_bnb_linear4bit(cache_weights=False):

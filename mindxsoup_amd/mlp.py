@@ -4,7 +4,8 @@ GEMMs' epilogues when all three projections are LoRA-wrapped NF4 layers.
 The reference casts the fp32 residual input to fp16 once, runs gate_proj and up_proj in fp16,
 keeps fp16 gate/up for the SwiGLU backward and casts only the MLP output back
 (solution/mlp.py:1-12, 33-44).  `fp16_forward` keeps that contract.  Where every projection is
-a `LoraLinear4bit` that the fused kernels take, `NF4LoraMLPFunction` runs the block as:
+a LoRA layer with peft's layout (this package's `LoraLinear4bit` or peft's own) that the fused
+kernels take, `NF4LoraMLPFunction` runs the block as:
 
   forward:  gate = gate_proj(x16) and up = up_proj(x16) (fused GEMMs, LoRA included, their
             LoRA row products in one launch); hidden = silu(gate) * up, by the elementwise
@@ -22,8 +23,8 @@ SwiGLU reads it, as the separate kernel does, and both evaluate the same fp32 fo
 
 import torch
 
-from . import direct, kernels, linear4bit
-from .linear4bit import LoraLinear4bit, _cast_bias_once, _direct_ok, lora_backward_group
+from . import direct, kernels, linear4bit, peft_lora, stream
+from .linear4bit import Proj as _Proj, _cast_bias_once, lora_backward_group
 from .silu_mul import silu_mul
 
 FUSED_SWIGLU = True  # FEATURES["mlp_fused_swiglu"]
@@ -34,18 +35,6 @@ FUSED_SWIGLU = True  # FEATURES["mlp_fused_swiglu"]
 GLU_FORWARD_TAIL = False
 
 _NAMES = ("gate_proj", "up_proj", "down_proj")
-
-
-class _Proj:
-    """What one projection's kernels need besides its LoRA tensors: the packed NF4 weight and its
-    state, the fp16 bias, the u8 dropout keep mask (None without dropout), 1/(1-p) and the LoRA
-    scaling."""
-
-    __slots__ = ("packed", "state", "bias", "keep", "mask_scale", "s")
-
-    def __init__(self, packed, state, bias, keep, mask_scale, s):
-        self.packed, self.state, self.bias = packed, state, bias
-        self.keep, self.mask_scale, self.s = keep, mask_scale, s
 
 
 class NF4LoraMLPFunction(torch.autograd.Function):
@@ -139,55 +128,42 @@ def _is_fp16_4bit(linear):
         getattr(base, "compute_dtype", None) == torch.float16
 
 
-def _lora_parts(layer):
-    """(a, b, p, s) of a LoRA layer's single active adapter."""
-    name = layer._adapter()
-    drop = layer.lora_dropout[name]
-    p = drop.p if isinstance(drop, torch.nn.Dropout) else 0.0
-    return (layer.lora_A[name].weight, layer.lora_B[name].weight, p,
-            float(layer.scaling[name]))
-
-
 def fused_ok(mlp, x16):
-    """Whether NF4LoraMLPFunction takes this MLP and fp16 input: every projection a LoRA-wrapped
-    NF4 layer with one active adapter of rank 16k whose fused kernels take it, shaped
-    hidden -> inter -> hidden."""
+    """Whether NF4LoraMLPFunction takes this MLP and fp16 input: every projection a LoRA layer
+    with peft's layout (peft_lora.adapter_of) over an NF4 base that the fused kernels take,
+    shaped hidden -> inter -> hidden."""
     if not (FUSED_SWIGLU and linear4bit.FUSED_LORA and x16.dim() >= 2):
         return False
-    layers = [getattr(mlp, n, None) for n in _NAMES]
-    if not all(isinstance(m, LoraLinear4bit) and m._adapter() is not None
-               and not getattr(m, "_force_unfused", False) for m in layers):
+    ads = [peft_lora.adapter_of(getattr(mlp, n, None)) for n in _NAMES]
+    if any(ad is None for ad in ads):
         return False
-    states = [m.base_layer.weight.quant_state for m in layers]
+    states = [ad.base.weight.quant_state for ad in ads]
     inter, hidden = states[0].shape
     if tuple(states[1].shape) != (inter, hidden) or tuple(states[2].shape) != (hidden, inter):
         return False
+    if any(stream.offloaded(ad.base) for ad in ads):
+        return False  # offloaded bases take each projection's streamed path
     h_probe = x16.new_empty((1, inter))  # down_proj's input: fp16 on the same device
-    for m, st, probe in zip(layers, states, (x16, x16, h_probe)):
-        if not (_direct_ok(m.base_layer, probe) and kernels.fused_shape_ok(st)
-                and m.lora_A[m._adapter()].weight.shape[0] % 16 == 0):
-            return False
-    return True
+    return all(peft_lora.takes(ad, probe) for ad, probe in zip(ads, (x16, x16, h_probe)))
 
 
 def fused_forward(mlp, x16):
     """NF4LoraMLPFunction on an MLP that fused_ok accepts (same dropout draws, in the same
     order, as calling the three projections)."""
-    layers = [getattr(mlp, n) for n in _NAMES]
+    ads = [peft_lora.adapter_of(getattr(mlp, n)) for n in _NAMES]
     lead = x16.shape[:-1]
     x2d = x16.reshape(-1, x16.shape[-1]).contiguous()
     projs, tensors = [], []
-    for m in layers:
-        a, b, p, s = _lora_parts(m)
-        base = m.base_layer
+    for ad in ads:
+        base = ad.base
         keep, mask_scale = None, 1.0
-        if m.training and p > 0:
+        if ad.dropping():
             # gate and up read x; down reads hidden, [M, inter]
-            keep = m.draw_keep(x2d, p, (x2d.shape[0], base.in_features))
-            mask_scale = 1.0 / (1.0 - p)
+            keep = ad.keep_mask(x2d, (x2d.shape[0], base.in_features))
+            mask_scale = 1.0 / (1.0 - ad.p)
         projs.append(_Proj(base.weight.data.view(-1, 1), base.weight.quant_state,
-                           _cast_bias_once(base, x16), keep, mask_scale, s))
-        tensors += [a, b]
+                           _cast_bias_once(base, x16), keep, mask_scale, ad.s))
+        tensors += [ad.a, ad.b]
     y = direct.run(NF4LoraMLPFunction, x2d, *tensors, tuple(projs))
     return y.view(*lead, y.shape[-1])
 

@@ -97,12 +97,15 @@ def unpack_nf4_bytewise(packed, shape, absmax, blocksize, dtype, absmax_8bit=Non
     return out
 
 
-def launch_layer(packed, out, absmax_8bit, code, absmax2, offset, module_of, block0, scale0):
+def launch_layer(packed, out, absmax_8bit, code, absmax2, offset, module_of, block0, scale0,
+                 plan=None):
     """One launch: `out` (fp16) gets the values of all the weights packed one after the other
     (solution/nf4.py:158-162).  block0: int64 [n_modules + 1] (first block of each weight, then
     the total); scale0: int64 [n_modules] (first absmax2 index of each weight); code
     [n_modules * 256]; offset [n_modules].  `module_of` is accepted for the reference's signature
-    and unused: the kernel finds each block's weight from block0."""
+    and unused.  `plan`: the device workgroup -> weight map of layer_plan for this block0; without
+    it, it is built here from block0's values (a host read of block0: callers in a loop build
+    it once and pass it)."""
     del module_of
     dev = _check_device(packed, out, absmax_8bit, code, absmax2, offset, block0, scale0)
     n_modules = scale0.numel()
@@ -113,24 +116,36 @@ def launch_layer(packed, out, absmax_8bit, code, absmax2, offset, module_of, blo
     if packed.numel() != 32 * n_blocks or out.numel() != 64 * n_blocks or \
             out.dtype != torch.float16:
         raise ValueError("packed/out sizes do not match the block count")
-    plan = layer_plan(block0)
+    if plan is None:
+        plan = layer_plan(block0)
+    elif plan.dtype != torch.int16 or plan.device != dev:
+        raise ValueError("plan must be the int16 device map of layer_plan")
     _lib.call("mxs_nf4_dequant_layer", _lib.ptr(packed), n_blocks, _lib.ptr(absmax_8bit),
               _lib.ptr(code), _lib.ptr(absmax2), _lib.ptr(offset), _lib.ptr(block0),
-              _lib.ptr(scale0), n_modules, _lib.ptr(plan), _lib.ptr(out), _lib.stream_of(dev))
+              _lib.ptr(scale0), n_modules, _lib.ptr(plan), plan.numel(), _lib.ptr(out),
+              _lib.stream_of(dev))
     return out
 
 
 _PLANS = {}
 
 
-def layer_plan(block0):
+def layer_plan(block0, device=None):
     """Device int16 map workgroup -> weight for the layer launch (the counterpart of the
-    reference's per-program `module_of`, solution/stream.py:125-133), built on the host once per
-    layout and cached by the block0 tensor's identity and version."""
-    key = (block0.data_ptr(), block0._version, block0.numel(), block0.device)
+    reference's per-program `module_of`, solution/stream.py:125-133), built on the host from
+    block0's values (host or device tensor, or a sequence) and cached by those values: a
+    different layout never gets another layout's plan."""
+    if isinstance(block0, torch.Tensor):
+        device = block0.device if device is None else device
+        values = block0.detach().to("cpu", torch.int64).numpy()
+    else:
+        values = np.asarray(block0, np.int64)
+    if device is None:
+        raise ValueError("layer_plan needs a device for a host block0")
+    b0 = np.ascontiguousarray(values, np.int64)
+    key = (b0.tobytes(), str(torch.device(device)))
     plan = _PLANS.get(key)
     if plan is None:
-        b0 = np.ascontiguousarray(block0.cpu().numpy(), np.int64)
         L = _lib.lib()
         n = L.mxs_nf4_dequant_layer_plan(b0.ctypes.data, b0.size - 1, None, 0)
         _lib.check(int(min(n, 0)), "mxs_nf4_dequant_layer_plan")
@@ -138,7 +153,7 @@ def layer_plan(block0):
         _lib.check(int(min(L.mxs_nf4_dequant_layer_plan(b0.ctypes.data, b0.size - 1,
                                                          host.ctypes.data, n), 0)),
                    "mxs_nf4_dequant_layer_plan")
-        plan = torch.from_numpy(host).to(block0.device)
+        plan = torch.from_numpy(host[:max(n, 0)].copy()).to(device)
         if len(_PLANS) > 64:
             _PLANS.clear()
         _PLANS[key] = plan

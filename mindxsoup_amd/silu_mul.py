@@ -1,10 +1,11 @@
-"""silu(gate) * up for the fp16 MLP, with a backward that writes its gradients over gate and up
-(the interface of solution/silu_mul.py, on the HIP kernels of csrc/swiglu.hip).
+"""SwiGLU of the fp16 MLP on the HIP kernels of csrc/swiglu.hip: h = silu(gate) * up, whose
+backward writes d(gate) and d(up) into gate's and up's own memory.
 
-gate and up are read only by this backward and are dead right after it, so the backward stores
-d(gate) into gate's memory and d(up) into up's (solution/silu_mul.py:1-13): no [N, 8960]
-gradient buffers are allocated.  Values are computed in fp32 from the fp16 inputs and rounded to
-fp16 once.
+The MLP's gate and up outputs are read by nothing but this product's backward, so their buffers
+can take their gradients (the memory argument of solution/silu_mul.py:1-13): the backward
+allocates no [tokens, intermediate] buffers.  Arithmetic is fp32 on the fp16 inputs with one
+rounding per output.  The interface (SiluMulInPlace, silu_mul and its guard) is the
+reference's, so its callers and tests apply unchanged.
 """
 
 import torch
@@ -12,30 +13,33 @@ import torch
 from . import direct, kernels
 
 
+def _kernel_takes(gate, up):
+    """fp16 GPU tensors of one non-empty shape (solution/silu_mul.py:74-78's guard)."""
+    return (isinstance(gate, torch.Tensor) and gate.is_cuda and gate.dtype == torch.float16
+            and gate.shape == up.shape and gate.numel() > 0)
+
+
 class SiluMulInPlace(torch.autograd.Function):
-    """silu(gate) * up in fp16; backward returns gate's and up's own memory holding their
-    gradients (solution/silu_mul.py:52-71).  Only for gate/up that nothing else reads after this
-    backward (the MLP's projections, whose 4-bit weights are frozen and keep no input)."""
+    """silu(gate) * up in fp16.  The saved gate and up are overwritten by the backward with
+    d(gate) and d(up) and handed back as the gradients, so nothing else may read them after the
+    backward (true of the MLP's projections, which keep no inputs of their own)."""
 
     @staticmethod
     def forward(ctx, gate, up):
-        gate = gate.contiguous()
-        up = up.to(gate.dtype).contiguous()
-        out = kernels.silu_mul(gate, up)
-        ctx.save_for_backward(gate, up)
-        return out
+        operands = (gate.contiguous(), up.to(torch.float16).contiguous())
+        ctx.save_for_backward(*operands)
+        return kernels.silu_mul(*operands)
 
     @staticmethod
-    def backward(ctx, grad):
+    def backward(ctx, dh):
         gate, up = ctx.saved_tensors
-        kernels.silu_mul_bwd_(grad.to(gate.dtype), gate, up)
+        kernels.silu_mul_bwd_(dh.to(torch.float16), gate, up)  # gate <- d(gate), up <- d(up)
         return gate, up
 
 
 def silu_mul(gate, up):
-    """The reference's guard (solution/silu_mul.py:74-78): fp16 CUDA tensors of one shape take
-    the kernel; anything else is the plain expression, as in the reference."""
-    if gate.dtype != torch.float16 or not gate.is_cuda or gate.shape != up.shape \
-            or gate.numel() == 0:
+    """h = silu(gate) * up: the kernel for fp16 GPU tensors of one shape, else torch's own
+    expression."""
+    if not _kernel_takes(gate, up):
         return torch.nn.functional.silu(gate) * up
     return direct.run(SiluMulInPlace, gate, up)

@@ -167,6 +167,7 @@ class LayerStreamer:
                            torch.cat([s.offset.reshape(-1).float() for s in sts]).to(dev)))
         self.block0 = torch.tensor(block0, dtype=torch.int64, device=dev)
         self.scale0 = torch.tensor(scale0, dtype=torch.int64, device=dev)
+        self.plan = nf4.layer_plan(block0, dev)  # built once, from the host values
         self.packed_bytes, self.absmax_start = blocks * 32, abs_start
         self.buffer = torch.empty(blocks * 64, dtype=torch.float16, device=dev)
         for g in self.groups:
@@ -189,6 +190,9 @@ class LayerStreamer:
             host = self.host_layers[layer]
             self.slots[slot][:host.numel()].copy_(host, non_blocking=True)
             self.ready[slot] = self.copy_stream.record_event()
+        # the allocator must not hand the slot's memory to anything else while this copy can
+        # still be writing it (a streamer dropped by reset() with a prefetch in flight)
+        self.slots[slot].record_stream(self.copy_stream)
         if self.unpacked == self.table.layer[slot]:
             self.unpacked = None
         self.table.assign(slot, layer)
@@ -210,7 +214,7 @@ class LayerStreamer:
         code, absmax2, offset = self.layer_tables[layer]
         nf4.launch_layer(data[:self.packed_bytes], self.buffer,
                          data[self.absmax_start:self.absmax_start + self.packed_bytes // 32],
-                         code, absmax2, offset, None, self.block0, self.scale0)
+                         code, absmax2, offset, None, self.block0, self.scale0, self.plan)
         self.unpacked = layer
 
     def bytes_for(self, module):
@@ -357,9 +361,16 @@ def _hint_hook(index, s):
         x = args[0] if args else None
         if isinstance(x, torch.Tensor) and x.requires_grad and torch.is_grad_enabled():
             # fires when this layer's backward has produced its input gradient
-            x.register_hook(lambda g: s.layer_begins(index - 1, forward=False))
+            x.register_hook(lambda g: _backward_hint(s, index - 1))
         return None
     return hook
+
+
+def _backward_hint(s, index):
+    """The input-gradient hook's hint, dropped when reset() has retired its streamer between a
+    forward and its backward."""
+    if _streamer is s:
+        s.layer_begins(index, forward=False)
 
 
 def patch_stream_layers():

@@ -11,7 +11,7 @@ pytestmark = pytest.mark.gpu
 HIDDEN, Q_HEADS, KV_HEADS = 1536, 12, 2
 
 
-def _attention(seed=0):
+def _attention(seed=0, targets=("q_proj", "v_proj")):
     transformers = pytest.importorskip("transformers")
     from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention
 
@@ -22,10 +22,10 @@ def _attention(seed=0):
     cfg._attn_implementation = "sdpa"
     torch.manual_seed(seed)
     attn = Qwen2Attention(cfg, layer_idx=0).cuda()
-    replace_with_nf4(attn, lora_targets=("q_proj", "v_proj"))
+    replace_with_nf4(attn, lora_targets=targets)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed + 1)
-    for m in (attn.q_proj, attn.v_proj):  # random B so the branch matters
+    for m in (getattr(attn, t) for t in targets):  # random B so the branch matters
         with torch.no_grad():
             w = m.lora_B["default"].weight
             w.copy_(torch.randn(w.shape, device="cuda", generator=g) * 0.02)
@@ -62,13 +62,19 @@ def _max_rel(a, b):
     return ((a.float() - b.float()).abs().max() / b.float().abs().max().clamp_min(1e-12)).item()
 
 
-@pytest.mark.parametrize("batch,n_tokens,masked", [(2, 64, False), (2, 77, True), (4, 512, True)])
-def test_matches_original_without_dropout(cuda, monkeypatch, batch, n_tokens, masked):
+@pytest.mark.parametrize("batch,n_tokens,masked,targets", [
+    (2, 64, False, ("q_proj", "v_proj")), (2, 77, True, ("q_proj", "v_proj")),
+    (4, 512, True, ("q_proj", "v_proj")), (2, 77, True, ("q_proj", "k_proj", "v_proj")),
+    (4, 512, True, ("q_proj", "k_proj", "v_proj"))])
+def test_matches_original_without_dropout(cuda, monkeypatch, batch, n_tokens, masked, targets):
+    """LoRA on q and v: each projection on its own fused kernels; on q, k and v: the three in
+    shared launches (NF4LoraSiblingsFunction)."""
     from transformers.models.qwen2 import modeling_qwen2
 
-    from mindxsoup_amd import attention
+    from mindxsoup_amd import attention, linear4bit
 
-    print(f"case attention batch={batch} tokens={n_tokens} masked={masked}", flush=True)
+    print(f"case attention batch={batch} tokens={n_tokens} masked={masked} lora={targets}",
+          flush=True)
     cls = modeling_qwen2.Qwen2Attention
     original = getattr(cls.forward, "_mindx_original", cls.forward)
     monkeypatch.setattr(cls, "forward", original)
@@ -77,7 +83,11 @@ def test_matches_original_without_dropout(cuda, monkeypatch, batch, n_tokens, ma
     calls = []
     real = attention.qkv_rope
     monkeypatch.setattr(attention, "qkv_rope", lambda *a: calls.append(1) or real(*a))
-    attn = _attention().eval()  # LoRA dropout off
+    attn = _attention(targets=targets).eval()  # LoRA dropout off
+    sib = []
+    real_sib = linear4bit.NF4LoraSiblingsFunction.apply
+    monkeypatch.setattr(linear4bit.NF4LoraSiblingsFunction, "apply",
+                        lambda *a: sib.append(1) or real_sib(*a))
     torch.manual_seed(3)
     hidden = torch.randn(batch, n_tokens, HIDDEN, device="cuda")
     cos, sin = _cos_sin(n_tokens)
@@ -86,8 +96,9 @@ def test_matches_original_without_dropout(cuda, monkeypatch, batch, n_tokens, ma
     ref = _run(attn, original, hidden, cos, sin, mask)
     ours = _run(attn, cls.forward, hidden, cos, sin, mask)
     assert calls, "the fp16 path was not taken"
+    assert bool(sib) == (len(targets) == 3), "q/k/v in shared launches exactly when all have LoRA"
     names = ["output", "grad input"] + [n for n, _ in attn.named_parameters() if "lora_" in n]
-    assert len(ours) == len(ref) == 6
+    assert len(ours) == len(ref) == 2 + 2 * len(targets)
     for name, a, b in zip(names, ours, ref):
         assert a.shape == b.shape and _max_rel(a, b) < 1e-2, f"{name}: {_max_rel(a, b):.2e}"
 

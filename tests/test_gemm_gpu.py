@@ -65,7 +65,7 @@ def test_in_gemm_decode_is_bit_exact(cuda, n, k, cfg, splits):
 
 @pytest.mark.parametrize("out_features,bias", [(1536, True), (256, True), (8960, False),
                                                (1536, False)])
-@pytest.mark.parametrize("tokens", [37, 300, 700, 1203, 2048])
+@pytest.mark.parametrize("tokens", [37, 300, 512, 700, 1203, 2048])
 def test_linear4bit_fwd_bwd_matches_oracle(cuda, out_features, bias, tokens):
     """solution/test_linear4bit.py:37-59 shapes: Y = x W^T + b and grad_x = grad W through the
     module and autograd, against float64 dequant-then-matmul."""
@@ -435,10 +435,21 @@ def test_lora_module_forward_backward(cuda):
     mod.next_keep = keep
     xg = x.clone().requires_grad_(True)
     y = mod(xg)
-    y.sum().backward()
-    assert mod.lora_A["default"].weight.grad is not None
-    assert mod.lora_B["default"].weight.grad.shape == (1536, 16)
-    assert xg.grad.shape == x.shape
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    ga, gb = mod.lora_A["default"].weight.grad, mod.lora_B["default"].weight.grad
+    assert ga.shape == (16, 1536) and gb.shape == (1536, 16) and xg.grad.shape == x.shape
+    # training values against the oracle: y, dX, dA, dB of base + s * B(A(drop(x)))
+    x2 = _np(x).reshape(-1, 1536).astype(np.float16)
+    a16, b16 = a.astype(np.float16), b.astype(np.float16)
+    w16, kp = _w_oracle(base), keep.cpu().numpy()
+    ref_y = O.lora_fwd(x2, w16, a16, b16, 2.0, kp, 0.05, bias=_np(base.bias))
+    ref_dx, ref_da, ref_db = O.lora_bwd(_np(dy).reshape(-1, 1536).astype(np.float16), x2, w16,
+                                        a16, b16, 2.0, kp, 0.05)
+    errs = [O.max_rel(_np(y).reshape(-1, 1536), ref_y),
+            O.max_rel(_np(xg.grad).reshape(-1, 1536), ref_dx),
+            O.max_rel(_np(ga), ref_da), O.max_rel(_np(gb), ref_db)]
+    assert max(errs) < TOL, errs
 
 
 def test_empty_tokens(cuda):

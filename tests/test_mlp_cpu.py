@@ -119,7 +119,7 @@ def test_apply_patches_qwen2_attention_and_rope(monkeypatch):
     modeling_qwen2 = pytest.importorskip("transformers.models.qwen2.modeling_qwen2")
 
     import mindxsoup_amd
-    from mindxsoup_amd import attention, direct, linear4bit, mlp, rope
+    from mindxsoup_amd import attention, direct, linear4bit, mlp
 
     cls = modeling_qwen2.Qwen2Attention
     monkeypatch.setattr(cls, "forward", cls.forward)
@@ -133,8 +133,9 @@ def test_apply_patches_qwen2_attention_and_rope(monkeypatch):
     original = cls.forward
     mindxsoup_amd.apply()
     assert cls._mindx_fp16 and cls.forward._mindx_original is original
-    assert getattr(modeling_qwen2.apply_rotary_pos_emb, "_mindx_patched", False)
-    # CPU inputs: the patched RoPE and attention hand the call to the originals
+    # the RoPE-only patch is not part of this build: apply_rotary_pos_emb stays transformers'
+    assert not getattr(modeling_qwen2.apply_rotary_pos_emb, "_mindx_patched", False)
+    # CPU inputs: the patched attention hands the call to the original
     from transformers import Qwen2Config
 
     cfg = Qwen2Config(hidden_size=256, num_attention_heads=2, num_key_value_heads=1)
@@ -146,4 +147,5 @@ def test_apply_patches_qwen2_attention_and_rope(monkeypatch):
     a, _ = cls.forward(attn, x, (cos, sin), None)
     b, _ = original(attn, x, (cos, sin), None)
     assert torch.equal(a, b)
-    assert attention._split_projection(torch.nn.Linear(4, 4)) is None
+    assert attention._refusal(attn, x, (cos, sin), None, {}) is not None
+    assert attention._route(torch.nn.Linear(4, 4), x) is None

@@ -1,9 +1,10 @@
-"""RoPE and the fused q/k/v LoRA-add + RoPE + cast (mindxsoup_amd/rope.py on csrc/rope.hip).
+"""The q/k rotation and q/k/v LoRA-add + RoPE + cast of the fp16 attention path
+(mindxsoup_amd/rope.py on csrc/rope.hip).
 
 Bars: bit-exact against the oracle's restatement (oracle_qkv_rope) on the same inputs, forward
-and backward, fp16 and fp32; and the reference's own tests' comparisons against fp32 PyTorch
-math with transformers' formula (solution/test_rope.py:48-150: 1e-5 for fp32, 2e-3 for fp16;
-solution/test_attention.py:190-246: 2e-3, and a power-of-two LoRA scale bit-exact).
+and backward, fp16 and fp32 in and out; and the reference's own comparisons against fp32 PyTorch
+math with transformers' formula (solution/test_rope.py:48-62 and solution/test_attention.py
+:190-246: 2e-3 for fp16 outputs, and a power-of-two LoRA scale bit-exact).
 """
 
 import numpy as np
@@ -31,16 +32,6 @@ def reference(q, k, cos, sin, unsqueeze_dim=1):
     return (q * cos) + (rotate_half(q) * sin), (k * cos) + (rotate_half(k) * sin)
 
 
-def model_like_qk(dev, batch, n_q, n_k, n_tokens, dtype):
-    """q and k as Qwen2Attention makes them: a [B, T, heads, D] buffer seen as [B, heads, T, D]."""
-    q = torch.randn(batch, n_tokens, n_q * HEAD_DIM, device=dev).to(dtype)
-    k = torch.randn(batch, n_tokens, n_k * HEAD_DIM, device=dev).to(dtype)
-    q = q.view(batch, n_tokens, n_q, HEAD_DIM).transpose(1, 2).detach().requires_grad_(True)
-    k = k.view(batch, n_tokens, n_k, HEAD_DIM).transpose(1, 2).detach().requires_grad_(True)
-    assert not q.is_contiguous() and not k.is_contiguous()
-    return q, k
-
-
 def model_like_cos_sin(dev, batch, n_tokens, dtype, theta=1e6):
     """Qwen2RotaryEmbedding: freqs = pos * inv_freq, emb = cat(freqs, freqs)."""
     inv_freq = 1.0 / (theta ** (torch.arange(0, HEAD_DIM, 2, device=dev).float() / HEAD_DIM))
@@ -51,105 +42,66 @@ def model_like_cos_sin(dev, batch, n_tokens, dtype, theta=1e6):
     return emb.cos().to(dtype), emb.sin().to(dtype)
 
 
-def run_both(q, k, cos, sin):
-    from mindxsoup_amd.rope import apply_rope
-
-    ref_q, ref_k = reference(q, k, cos, sin)
-    grad_q, grad_k = torch.randn_like(ref_q), torch.randn_like(ref_k)
-    ref_dq, ref_dk = torch.autograd.grad((ref_q, ref_k), (q, k), (grad_q, grad_k))
-    out_q, out_k = apply_rope(q, k, cos, sin)
-    dq, dk = torch.autograd.grad((out_q, out_k), (q, k), (grad_q, grad_k))
-    return (out_q, out_k, dq, dk), (ref_q, ref_k, ref_dq, ref_dk)
-
-
 def _flat(x):
     """[B, heads, T, D] -> numpy [B, T, heads * D]."""
     b, h, t, d = x.shape
     return x.detach().transpose(1, 2).reshape(b, t, h * d).cpu().numpy()
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
-@pytest.mark.parametrize("shape", [(4, 12, 2, 512), (3, 12, 2, 77)])
-def test_rope_matches_reference(cuda, dtype, shape):
-    """solution/test_rope.py:48-62."""
-    print(f"case rope {dtype} {shape}", flush=True)
+def _rows(dev, batch, n_tokens, heads, dtype=torch.float16):
+    """A projection's output as Qwen2Attention gets it: [B, T, heads * D]."""
+    return torch.randn(batch, n_tokens, heads * HEAD_DIM, device=dev).to(dtype) \
+        .requires_grad_(True)
+
+
+def _heads(x, n):
+    b, t, _ = x.shape
+    return x.view(b, t, n, HEAD_DIM).transpose(1, 2)
+
+
+def _rotate_both(q, k, v, cos, sin):
+    """qkv_rope without LoRA terms and transformers' formula in fp32 (rounded to fp16), with
+    gradients of both for the same incoming gradients."""
+    from mindxsoup_amd.rope import qkv_rope
+
+    ref_q, ref_k = reference(_heads(q.float(), Q_HEADS), _heads(k.float(), KV_HEADS), cos.float(),
+                             sin.float())
+    ref = (ref_q.half(), ref_k.half(), _heads(v, KV_HEADS))
+    grads = [torch.randn_like(r) for r in ref]
+    ref_grads = torch.autograd.grad(ref, (q, k, v), grads)
+    ours = qkv_rope(q, None, k, v, None, cos, sin, Q_HEADS, KV_HEADS)
+    our_grads = torch.autograd.grad(ours, (q, k, v), grads)
+    return ours, ref, our_grads, ref_grads
+
+
+@pytest.mark.parametrize("shape", [(4, 512), (3, 77)])
+@pytest.mark.parametrize("cos_dtype", [torch.float32, torch.float16])
+def test_rotation_matches_transformers_math(cuda, shape, cos_dtype):
+    """The rotation of the attention path on model-like q/k (solution/test_rope.py:48-62's
+    comparison, fp16 tolerance 2e-3): values, input gradients, and the layout promises (q', k'
+    in the projections' [B, T, heads, D] memory; v' is v itself, no copy)."""
+    print(f"case rope {shape} cos {cos_dtype}", flush=True)
     torch.manual_seed(0)
-    batch, n_q, n_k, n_tokens = shape
-    q, k = model_like_qk(cuda, batch, n_q, n_k, n_tokens, dtype)
-    cos, sin = model_like_cos_sin(cuda, batch, n_tokens, dtype)
-    ours, ref = run_both(q, k, cos, sin)
-    tol = TOLERANCE[dtype]
-    for name, a, b in zip(("q", "k", "dq", "dk"), ours, ref):
+    batch, n_tokens = shape
+    q, k, v = (_rows(cuda, batch, n_tokens, h) for h in (Q_HEADS, KV_HEADS, KV_HEADS))
+    cos, sin = model_like_cos_sin(cuda, batch, n_tokens, cos_dtype)
+    ours, ref, our_grads, ref_grads = _rotate_both(q, k, v, cos, sin)
+    for name, a, b in zip(("q", "k", "v", "dq", "dk", "dv"), ours + our_grads, ref + ref_grads):
         assert a.dtype == b.dtype and a.shape == b.shape, name
-        torch.testing.assert_close(a.float(), b.float(), rtol=tol, atol=tol, msg=name)
-    # no hidden copies: outputs keep the [B, T, heads, D] layout of q and k
-    assert ours[0].stride() == q.stride() and ours[1].stride() == k.stride()
+        torch.testing.assert_close(a.float(), b.float(), rtol=2e-3, atol=2e-3, msg=name)
+    assert ours[0].stride() == _heads(q, Q_HEADS).stride()
+    assert ours[1].stride() == _heads(k, KV_HEADS).stride()
+    assert ours[2].data_ptr() == v.data_ptr()
 
 
 def test_cos_sin_with_batch_one(cuda):
     """position_ids of shape [1, T] give cos/sin [1, T, D], broadcast over the batch."""
     torch.manual_seed(0)
-    q, k = model_like_qk(cuda, 4, 12, 2, 100, torch.float32)
+    q, k, v = (_rows(cuda, 4, 100, h) for h in (Q_HEADS, KV_HEADS, KV_HEADS))
     cos, sin = model_like_cos_sin(cuda, 1, 100, torch.float32)
-    ours, ref = run_both(q, k, cos, sin)
-    for a, b in zip(ours, ref):
-        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
-
-
-def test_mixed_dtypes_promote_like_pytorch(cuda):
-    """fp16 q/k with fp32 cos/sin: outputs fp32 as in the original, grads in the input dtype."""
-    torch.manual_seed(0)
-    q, k = model_like_qk(cuda, 2, 12, 2, 33, torch.float16)
-    cos, sin = model_like_cos_sin(cuda, 2, 33, torch.float32)
-    ours, ref = run_both(q, k, cos, sin)
-    for a, b in zip(ours, ref):
-        assert a.dtype == b.dtype
+    ours, ref, our_grads, ref_grads = _rotate_both(q, k, v, cos, sin)
+    for a, b in zip(ours + our_grads, ref + ref_grads):
         torch.testing.assert_close(a.float(), b.float(), rtol=2e-3, atol=2e-3)
-
-
-def test_contiguous_inputs_and_out_dtype(cuda):
-    from mindxsoup_amd.rope import apply_rope
-
-    torch.manual_seed(0)
-    q = torch.randn(2, 12, 50, HEAD_DIM, device=cuda, requires_grad=True)
-    k = torch.randn(2, 2, 50, HEAD_DIM, device=cuda, requires_grad=True)
-    cos, sin = model_like_cos_sin(cuda, 2, 50, torch.float32)
-    ours, ref = run_both(q, k, cos, sin)
-    for a, b in zip(ours, ref):
-        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
-    # fp32 q/k with out_dtype=fp16: the fp32 rotation rounded once; grads come back in fp32
-    ref_q, ref_k = (x.half() for x in reference(q, k, cos, sin))
-    grads = (torch.randn_like(ref_q), torch.randn_like(ref_k))
-    ref_dq, ref_dk = torch.autograd.grad((ref_q, ref_k), (q, k), grads)
-    out_q, out_k = apply_rope(q, k, cos, sin, out_dtype=torch.float16)
-    dq, dk = torch.autograd.grad((out_q, out_k), (q, k), grads)
-    for a, b in ((out_q, ref_q), (out_k, ref_k), (dq, ref_dq), (dk, ref_dk)):
-        assert a.dtype == b.dtype
-        torch.testing.assert_close(a.float(), b.float(), rtol=2e-3, atol=2e-3)
-
-
-def test_patch_routes_cuda_and_falls_back(cuda, monkeypatch):
-    modeling_qwen2 = pytest.importorskip("transformers.models.qwen2.modeling_qwen2")
-    from mindxsoup_amd.rope import patch_rope
-
-    monkeypatch.setattr(modeling_qwen2, "apply_rotary_pos_emb",
-                        modeling_qwen2.apply_rotary_pos_emb)  # restored after the test
-    assert patch_rope() and patch_rope()  # idempotent
-    patched = modeling_qwen2.apply_rotary_pos_emb
-    assert getattr(patched, "_mindx_patched", False)
-    torch.manual_seed(0)
-    q, k = model_like_qk(cuda, 2, 12, 2, 40, torch.float32)
-    cos, sin = model_like_cos_sin(cuda, 2, 40, torch.float32)
-    out_q, out_k = patched(q, k, cos, sin)
-    assert out_q.grad_fn is not None and "RoPEFunction" in type(out_q.grad_fn).__name__
-    ref_q, ref_k = reference(q, k, cos, sin)
-    torch.testing.assert_close(out_q, ref_q, rtol=1e-5, atol=1e-5)
-    torch.testing.assert_close(out_k, ref_k, rtol=1e-5, atol=1e-5)
-    cpu = [x.detach().cpu() for x in (q, k, cos, sin)]  # CPU tensors take the original code
-    cpu_q, cpu_k = patched(*cpu)
-    ref_q, ref_k = reference(*cpu)
-    torch.testing.assert_close(cpu_q, ref_q)
-    torch.testing.assert_close(cpu_k, ref_k)
 
 
 def _proj(dev, batch, n_tokens, heads):

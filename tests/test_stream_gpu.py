@@ -186,6 +186,25 @@ def test_reset_removes_hints(cuda, streaming):
     assert streaming.streamer().loads == 0
 
 
+def test_reset_between_forward_and_backward(cuda, streaming):
+    """A streamer retired by reset() after a forward gets no hints from that forward's backward
+    (the input-gradient hooks check which streamer is current); the backward still runs on
+    one-off copies and gives the resident gradients."""
+    resident, streamed = Toy(3, 8, cuda), Toy(3, 8, cuda)
+    x, dy = _inputs(cuda, m=64)
+    _, want_g = _step(resident, x, dy)
+    assert streaming.setup(streamed, slots=2)
+    old = streaming.streamer()
+    xg = x.detach().clone().requires_grad_(True)
+    y = streamed(xg)
+    loads = old.loads
+    streaming.reset()
+    y.backward(dy)
+    torch.cuda.synchronize()
+    assert old.loads == loads
+    assert torch.equal(xg.grad, want_g)
+
+
 def test_setup_declines(cuda, streaming, monkeypatch):
     toy = Toy(2, 4, cuda)
     monkeypatch.setattr(streaming, "enabled", False)
