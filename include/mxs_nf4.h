@@ -109,6 +109,24 @@ int mxs_nf4_linear_fwd(const void* x, int M, int K, int N, const void* packed,
                        const void* lora_b, int r, void* y, void* workspace, int cfg, int splits,
                        hipStream_t stream);
 
+/* Upper bound on the split-K partial sums mxs_nf4_linear_fwd_noalloc keeps in the library's own
+ * device memory (32 MiB per GPU, held from library load to process exit). */
+#define MXS_NF4_SCRATCH_BYTES (32u << 20)
+
+/* mxs_nf4_linear_fwd without the workspace argument, for callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * No counterpart in the reference (its forward allocates through torch).  Nothing is allocated:
+ * split-K partials go to a file-scope device array of MXS_NF4_SCRATCH_BYTES, whose address is
+ * looked up once per device on the first call made with that device current.  A plan needing
+ * more (splits * M * N * 4 bytes) returns MXS_ERR_SIZE with nothing launched.  Every call on
+ * one GPU shares that array: calls that overlap in time on one GPU (other streams or threads)
+ * race and must be serialized by the caller.  Same results as mxs_nf4_linear_fwd. */
+int mxs_nf4_linear_fwd_noalloc(const void* x, int M, int K, int N, const void* packed,
+                               const void* absmax8, const float* code, const float* absmax2,
+                               const float* offset, const void* bias, const void* lora_h,
+                               const void* lora_b, int r, void* y, int cfg, int splits,
+                               hipStream_t stream);
+
 /* dX[M,K] = dY[M,N] . W[N,K] (+ mask[M,K] * mask_scale * (lora_dh[M,r] . lora_at[K,r]^T)), with
  * W decoded from NF4 inside the GEMM.  Replaces NF4LinearFunction.backward
  * (solution/linear4bit.py:51-57: unpack again, then grad @ W) plus the LoRA branch's input

@@ -40,6 +40,7 @@ _SIGNATURES = {
     "mxs_nf4_quantize": [P, I64, P, P, P, P, P, P, P, P],
     "mxs_nf4_gemm_workspace_bytes": [I32, I32, I32, I32, I32],
     "mxs_nf4_linear_fwd": [P, I32, I32, I32, P, P, P, P, P, P, P, P, I32, P, P, I32, I32, P],
+    "mxs_nf4_linear_fwd_noalloc": [P, I32, I32, I32, P, P, P, P, P, P, P, P, I32, P, I32, I32, P],
     "mxs_nf4_linear_bwd_dx": [P, I32, I32, I32, P, P, P, P, P, P, P, I32, P, F32, P, P, I32, I32,
                               P],
     "mxs_lora_workspace_bytes": [I32, I32, I32, I32],

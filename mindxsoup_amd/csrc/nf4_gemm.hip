@@ -17,6 +17,8 @@
 // the input gradient masked by the dropout keep mask), computed before the main loop; the
 // epilogue stores fp16.  With split-K (gridDim.z > 1) each split writes fp32 partials and
 // k_splitk_reduce sums them (split 0 carries bias and LoRA).
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -2106,6 +2108,40 @@ static void set_workspace(GemmArgs& a, void* workspace) {
   a.ws = static_cast<float*>(workspace);
 }
 
+// ---- Split-K partials for callers that cannot allocate (mxs_nf4_linear_fwd_noalloc) --------
+// A file-scope device array: every GPU the library runs on holds its own copy, at its own
+// address, from module load to the end of the process.  Its host-side name is only a handle:
+// kernels get the device address that hipGetSymbolAddress returns for the current device,
+// looked up once per device and kept.  All calls on one GPU share the array, so calls that
+// overlap in time on one GPU (two streams, two threads) race on it.  Nothing needs clearing:
+// each split writes its whole partial plane before the reduce reads it.
+static __device__ __align__(256) unsigned char scratch[MXS_NF4_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (first call per device looks it up).
+static int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return MXS_ERR_ARG;
+  void* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return (int)e;
+      if (!p) return (int)hipErrorInvalidSymbol;
+      g_scratch[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return MXS_OK;
+}
+
 extern "C" {
 
 int mxs_nf4_linear_fwd(const void* x, int M, int K, int N, const void* packed,
@@ -2422,3 +2458,31 @@ int mxs_nf4_linear_bwd_dx_glu(const void* dy, int M, int N, int K, const void* p
 }
 
 }  // extern "C"
+
+// mxs_nf4_linear_fwd with the split-K partial sums in the library's own device array instead of
+// a caller workspace: no allocation of any kind.  Bytes the plan needs above
+// MXS_NF4_SCRATCH_BYTES are refused with MXS_ERR_SIZE before anything is launched.
+extern "C" int mxs_nf4_linear_fwd_noalloc(const void* x, int M, int K, int N, const void* packed,
+                                          const void* absmax8, const float* code,
+                                          const float* absmax2, const float* offset,
+                                          const void* bias, const void* lora_h,
+                                          const void* lora_b, int r, void* y, int cfg,
+                                          int splits, hipStream_t stream) {
+  if (M < 0 || K < 0 || N < 0) return MXS_ERR_ARG;
+  if (cfg < 0) choose(M, N, K, false, &cfg, &splits);
+  // the split count the launch will use (launch_cfg / launch_ws clamp it the same way)
+  const int n_steps = K / kBK;
+  int sp = splits < 1 ? 1 : splits;
+  if (sp > n_steps) sp = n_steps > 0 ? n_steps : 1;
+  const int per = (n_steps + sp - 1) / sp;
+  sp = n_steps > 0 ? (n_steps + per - 1) / per : 1;
+  void* ws = nullptr;
+  if (sp > 1 && M > 0 && N > 0) {
+    const double need = (double)sp * (double)M * (double)N * sizeof(float);
+    if (need > (double)MXS_NF4_SCRATCH_BYTES) return MXS_ERR_SIZE;
+    const int rc = scratch_address(&ws);
+    if (rc != MXS_OK) return rc;
+  }
+  return mxs_nf4_linear_fwd(x, M, K, N, packed, absmax8, code, absmax2, offset, bias, lora_h,
+                            lora_b, r, y, ws, cfg, sp, stream);
+}

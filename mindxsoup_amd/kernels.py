@@ -124,6 +124,33 @@ def nf4_linear_fwd(x2d, packed, state, bias=None, lora_h=None, lora_b=None, cfg=
     return y
 
 
+def nf4_linear_fwd_noalloc(x2d, packed, state, y, bias=None, lora_h=None, lora_b=None, cfg=-1,
+                           splits=1):
+    """nf4_linear_fwd into the caller's y [M, N] fp16 through mxs_nf4_linear_fwd_noalloc: the
+    split-K partials live in the library's own device array (MXS_NF4_SCRATCH_BYTES), so the call
+    allocates nothing.  Calls overlapping in time on one GPU share that array and race."""
+    n, k = state.shape
+    if x2d.dtype != torch.float16 or x2d.dim() != 2 or x2d.shape[1] != k or \
+            not x2d.is_contiguous():
+        raise ValueError("x must be contiguous fp16 [M, in_features]")
+    M = x2d.shape[0]
+    if y.dtype != torch.float16 or tuple(y.shape) != (M, n) or not y.is_contiguous() or \
+            y.device != x2d.device:
+        raise ValueError("y must be contiguous fp16 [M, out_features] on x's device")
+    r = 0
+    if lora_h is not None:
+        r = lora_h.shape[1]
+        if lora_b is None or tuple(lora_b.shape) != (n, r) or lora_h.shape[0] != M or \
+                not (lora_h.is_contiguous() and lora_b.is_contiguous()):
+            raise ValueError("lora_h [M, r] needs lora_b [N, r], both contiguous fp16")
+    if bias is not None and (bias.dtype != torch.float16 or not bias.is_contiguous()):
+        raise ValueError("bias must be contiguous fp16")
+    _lib.call("mxs_nf4_linear_fwd_noalloc", _lib.ptr(x2d), M, k, n,
+              *_nf4_args(packed, state, x2d.device), _lib.ptr(bias), _lib.ptr(lora_h),
+              _lib.ptr(lora_b), r, _lib.ptr(y), cfg, splits, _lib.stream_of(x2d.device))
+    return y
+
+
 def nf4_linear_bwd_dx(dy2d, packed, state, lora_dh=None, lora_a=None, mask=None,
                       mask_scale=1.0, cfg=-1, splits=1, lora_at=None, ws=None):
     """dX = dy2d @ W (+ mask * mask_scale * (lora_dh @ lora_a)), fp16 [M, K].  The kernel takes
