@@ -129,12 +129,23 @@ def bench_dequant(m, steps, warmup):
     return wall / steps * 1e3, float(np.mean(per_launch)), out
 
 
+# The GPU box gives one GPU's job a share of 16 host cores (its OMP_NUM_THREADS), whatever its
+# affinity set shows; more threads would only oversubscribe that share.
+CPU_SHARE = 16
+
+
+def host_cores():
+    """Threads for the CPU baselines: the cores this process may run on, at most the job's
+    share (both counts are reported with the baseline)."""
+    return min(len(os.sched_getaffinity(0)), CPU_SHARE)
+
+
 def cpu_baseline_dequant(m, budget_s=20.0):
     """The oracle's C decode (OpenMP) over the same packed weights, on this host: whole-model
     passes, repeated within the time budget; median."""
     from oracle import oracle as O
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = host_cores()
     O.set_num_threads(cores)
     packed = m["packed"].cpu().numpy()
     absmax8 = m["absmax8"].cpu().numpy()
@@ -162,6 +173,7 @@ def cpu_baseline_dequant(m, budget_s=20.0):
             break
     sec = float(np.median(times))
     return dict(value=round(dequant_bytes(m) / sec / 1e9, 3), unit="GB/s", cores=cores,
+                cores_available=len(os.sched_getaffinity(0)), cpu_count=os.cpu_count(),
                 kind="port",
                 sample=f"whole model (196 weights) decoded by oracle/nf4_oracle.c, "
                        f"median of {len(times)} passes, {sec:.3f} s/pass, "
@@ -319,6 +331,25 @@ def graph_time(fn, steps, warmup):
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) / steps * 1e3
     return a.elapsed_time(b) / steps, wall
+
+
+def eager_time(fn, steps, warmup):
+    """fn() launched eagerly (no graph): mean ms per call between HIP events on the current
+    stream, and the host's own ms per call (wall time of the Python calls alone, before the
+    final synchronize: the cost of argument checks, allocations and launches)."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    host = (time.perf_counter() - t0) / steps * 1e3
+    b.record(stream)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps, host
 
 
 def bench_mlp(dev, g, steps, warmup):
@@ -612,6 +643,7 @@ def bench_fused(dev, steps, warmup):
 
     ms, wall = graph_time(step, max(3, steps // 5), max(2, warmup // 5))
     ms_u, _ = graph_time(step_ungrouped, max(3, steps // 5), max(2, warmup // 5))
+    eager, host = eager_time(step, max(3, steps // 5), max(2, warmup // 5))
     fl = LAYERS * sum(proj_flops(n, k) for _, n, k in PROJ)
     tf = fl / ms / 1e9
     out["config5_stack"] = {"ms_per_step": round(ms, 4), "wall_ms_per_step": round(wall, 4),
@@ -619,7 +651,11 @@ def bench_fused(dev, steps, warmup):
                             "mfma_frac": round(tf / MFMA_PEAK_TFLOPS, 4),
                             "launches": "one HIP graph per step",
                             "lora_rows": "q/k/v and gate/up grouped per launch",
-                            "ungrouped_ms_per_step": round(ms_u, 4)}
+                            "ungrouped_ms_per_step": round(ms_u, 4),
+                            "eager_ms_per_step": round(eager, 4),
+                            "eager_host_ms_per_step": round(host, 4),
+                            "eager_host_us_per_projection_direction": round(
+                                host * 1e3 / (2 * LAYERS * len(PROJ)), 2)}
     del layers
     return out
 
@@ -629,7 +665,7 @@ def cpu_baseline_layer(dev):
     then torch CPU fp32 GEMMs (x28 extrapolated to the step, labelled as such)."""
     from oracle import oracle as O
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = host_cores()
     torch.set_num_threads(cores)
     O.set_num_threads(cores)
     g = torch.Generator(device=dev)
@@ -670,10 +706,70 @@ def cpu_baseline_layer(dev):
     sec = float(np.median(times))
     fl = sum(proj_flops(n, k) for _, n, k in PROJ)
     return {"value": round(fl / sec / 1e12, 4), "unit": "TFLOP/s", "cores": cores,
+            "cores_available": len(os.sched_getaffinity(0)), "cpu_count": os.cpu_count(),
             "kind": "port",
             "sample": f"one layer (7 projections) fwd+bwd, M=1024: oracle decode + torch CPU fp32 "
                       f"GEMMs, median {sec * 1e3:.1f} ms/layer; x28 extrapolated step "
                       f"{sec * LAYERS * 1e3:.0f} ms"}
+
+
+# One GEMM of the stack alone (for rocprofv3 counter passes and tile-plan sweeps):
+# name -> (out_features N, in_features K, direction)
+KERNELS = {"gate_fwd": (8960, 1536, "fwd"), "gateup_dx": (8960, 1536, "bwd"),
+           "down_fwd": (1536, 8960, "fwd"), "down_dx": (1536, 8960, "bwd"),
+           "qo_fwd": (1536, 1536, "fwd"), "qo_dx": (1536, 1536, "bwd")}
+
+
+def bench_kernel(dev, name, tokens, steps, warmup, cfg=-1, splits=1):
+    """One projection GEMM with its LoRA term (the partial sums of the row product already
+    made), launched `steps` times after `warmup`, eagerly on the current stream: mean us per
+    launch from HIP events on that stream, TFLOP/s over 2*M*N*K + 2*M*r*(output columns)."""
+    from mindxsoup_amd import kernels
+
+    n, k, direction = KERNELS[name]
+    g = torch.Generator(device=dev)
+    g.manual_seed(4)
+    p = make_proj(dev, g, n, k)
+    x = torch.randn((tokens, k), device=dev, generator=g).half()
+    dy = torch.randn((tokens, n), device=dev, generator=g).half()
+    keep = (torch.rand((tokens, k), device=dev, generator=g) >= P_DROP).to(torch.uint8)
+    s, ms_ = ALPHA / RANK, 1.0 / (1.0 - P_DROP)
+    nc, kr = (n, k) if direction == "fwd" else (k, n)
+    ws = kernels.new_workspace(max(kernels.projection_workspace_bytes(tokens, k, n, RANK),
+                                   kernels.gemm_workspace_bytes(tokens, nc, kr, cfg, splits)), dev)
+    if direction == "fwd":
+        hp, at, bt = kernels.lora_h_partials(x, p["a"], s, keep, ms_, lora_b=p["b"])
+
+        def launch():
+            kernels.nf4_linear_fwd_hp(x, p["packed"], p["st"], hp, p["b"], cfg=cfg,
+                                      splits=splits, ws=ws)
+        cols = n
+    else:
+        bt = p["b"].t().contiguous()
+        at = p["a"].t().contiguous()
+        dhp = kernels.lora_dh_partials(dy, bt, s)
+
+        def launch():
+            kernels.nf4_linear_bwd_dx_hp(dy, p["packed"], p["st"], dhp, at, keep, ms_, cfg=cfg,
+                                         splits=splits, ws=ws)
+        cols = k
+    for _ in range(warmup):
+        launch()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(stream)
+    for _ in range(steps):
+        launch()
+    b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) / steps * 1e3
+    fl = 2 * tokens * n * k + 2 * tokens * RANK * cols
+    return {"kernel": name, "tokens": tokens, "N": n, "K": k, "direction": direction,
+            "cfg": cfg, "splits": splits, "us_per_launch": round(us, 2),
+            "tflops": round(fl / us / 1e6, 1),
+            "mfma_frac": round(fl / us / 1e6 / MFMA_PEAK_TFLOPS, 4),
+            "timing": "HIP events around the launches (GEMM + its split-K reduce, if any)"}
 
 
 def main():
@@ -687,6 +783,11 @@ def main():
                     help="only the host-streamed weights section (its JSON on stdout)")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run a 1 GiB device copy (reference for the PMC byte counters)")
+    ap.add_argument("--kernel", choices=sorted(KERNELS),
+                    help="only one projection GEMM, launched --steps times (its JSON on stdout)")
+    ap.add_argument("--tokens", type=int, default=M_TOKENS, help="M for --kernel")
+    ap.add_argument("--cfg", type=int, default=-1, help="tile configuration for --kernel")
+    ap.add_argument("--splits", type=int, default=1, help="split-K for --kernel with --cfg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the hot path is "
@@ -697,6 +798,10 @@ def main():
     torch.cuda.set_device(dev)
     if args.calibrate:
         calibrate(dev)
+        return
+    if args.kernel:
+        print(json.dumps(bench_kernel(dev, args.kernel, args.tokens, args.steps, args.warmup,
+                                      args.cfg, args.splits)), flush=True)
         return
     if args.stream:
         g = torch.Generator(device=dev)

@@ -10,7 +10,9 @@ import os
 
 import torch
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmxs_nf4.so")
+# MXS_NF4_LIB names another build of the same library (A/B timing of kernel variants).
+LIB_PATH = os.environ.get("MXS_NF4_LIB") or \
+    os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmxs_nf4.so")
 
 MXS_DTYPE_F16 = 0
 MXS_DTYPE_F32 = 1

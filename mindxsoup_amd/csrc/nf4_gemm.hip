@@ -77,8 +77,13 @@ constexpr int kFusedColsCPL = 2;
 
 
 // LDS offset (in halfs) of 16-byte segment `seg` (0..7) of row `row` in a [rows][64] tile.
+// Physical segment = seg ^ ((row >> 1) & 7).  A 128-byte row is half of the 64 four-byte banks,
+// so rows of one parity share banks: the MFMA operand reads (16 lanes = 16 consecutive rows, one
+// segment) see 8 rows of each parity on 8 different segments, and the decoded-tile stores (16
+// lanes = 8 consecutive rows, segments 4h + d or 2h + d) see each parity's rows on distinct
+// segments too, so neither conflicts.
 __device__ __forceinline__ int lds_off(int row, int seg) {
-  return row * kBK + (((seg ^ row ^ (row >> 3)) & 7) << 3);
+  return row * kBK + (((seg ^ (row >> 1)) & 7) << 3);
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N_, bool BWD>
@@ -773,6 +778,17 @@ static int launch_reduce(const GemmArgs& a, int splits, hipStream_t stream) {
   return e == hipSuccess ? MXS_OK : (int)e;
 }
 
+// LDS tables both kernels use: the byte -> (NF4[hi], NF4[lo]) pair table and the code book.
+// (A 16-entry table read once per nibble has no bank conflicts, but its extra address math and
+// twice the LDS instructions lengthened the producers' per-step chain: slower, measured.)
+__device__ __forceinline__ void fill_tables(const GemmArgs& a, float2_t* s_pair, float* s_code,
+                                            int t, int nthreads) {
+  for (int i = t; i < 256; i += nthreads) {
+    s_code[i] = a.code[i];
+    s_pair[i] = (float2_t){kNF4[i >> 4], kNF4[i & 15]};
+  }
+}
+
 // Global -> register staging and register -> LDS commit of one K-step's tiles, for NTP
 // loading threads (thread index p in [0, NTP)).
 //   A: BM rows x 64 fp16 (16-byte segments; rows past M clamped to the last row).
@@ -886,76 +902,17 @@ struct Loader {
   }
 };
 
-// LDS tables both kernels use: the byte -> (NF4[hi], NF4[lo]) pair table and the code book.
-__device__ __forceinline__ void fill_tables(const GemmArgs& a, float2_t* s_pair, float* s_code,
-                                            int t, int nthreads) {
-  for (int i = t; i < 256; i += nthreads) {
-    s_code[i] = a.code[i];
-    s_pair[i] = (float2_t){kNF4[i >> 4], kNF4[i & 15]};
-  }
-}
-
-// One wave's 32x32x16 MFMAs over one 64-deep K-step held in LDS (A rows wm0.., B rows wn0..),
-// with the operand fragments of sub-step kk+1 read while sub-step kk multiplies.
 typedef short short4_t __attribute__((ext_vector_type(4)));
 
-// MFMA W-side fragment (32 columns n0.. x 16 reduction indices k0..) from a B tile stored with
-// the reduction index as the row: bt[k * ldb + n].  Two transposing LDS reads: in each group of
-// 16 lanes, source lane s reads row k + s/4, columns n + 4*(s%4)..+3, and lane j receives the 4
-// rows of column n + j -- 4 consecutive reduction indices of one column, as the MFMA operand
-// takes them (lanes 0-31: k0..k0+7, lanes 32-63: k0+8..k0+15; lane%32 = column).
-__device__ __forceinline__ half8_t frag_bt(const _Float16* bt, int ldb, int n0, int k0, int lane) {
-  const int g = lane >> 4, sl = lane & 15;
-  const int n = n0 + 16 * (g & 1) + 4 * (sl & 3);
-  const int k = k0 + 8 * (g >> 1) + (sl >> 2);
-  typedef __attribute__((address_space(3))) short4_t lds_short4;
-  // whole-vector casts: __builtin_bit_cast of a single vector element reads element 0 with
-  // this compiler
-  const half4_t lo = __builtin_bit_cast(
-      half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(bt + k * ldb + n)));
-  const half4_t hi = __builtin_bit_cast(
-      half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(bt + (k + 4) * ldb + n)));
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+// Backward B tile [64][ldb]: element (k, n) in halfs.  The 16-byte unit n / 8 of row k is stored
+// at unit (n / 8) ^ x(k), a permutation inside each aligned group of 4 units, so the transposing
+// operand reads (4 rows x 4 units per cycle) keep their banks; x(k) = k & 3 for 20-unit rows
+// (ldb 160), (k >> 2) & 3 for 12-unit rows (ldb 96).  It spreads the producers' 16-byte stores
+// of one cycle over all 64 banks (without it 4 of them land on each bank).
+__device__ __forceinline__ int bt_off(int k, int n, int ldb) {
+  const int x = (ldb == 96 ? (k >> 2) : k) & 3;
+  return k * ldb + ((((n >> 3) ^ x)) << 3) + (n & 7);
 }
-
-// One K-step of MFMAs for a wave's TM x TN tiles.  A fragments from the swizzled [rows][64] A
-// tile; W fragments from the swizzled [cols][64] B tile, or (LDB > 0) from a B tile stored
-// [64][LDB] with the reduction index as the row (frag_bt).
-template <int TM, int TN, int LDB = 0>
-__device__ __forceinline__ void mma_kstep(float16_t (&acc)[TM][TN], const _Float16* as,
-                                          const _Float16* bs, int wm0, int wn0, int lrow,
-                                          int lseg) {
-  const int lane = lseg * 32 + lrow;
-  auto bfrag = [&](int j, int kk) -> half8_t {
-    if constexpr (LDB > 0) return frag_bt(bs, LDB, wn0 + j * 32, 16 * kk, lane);
-    else return *reinterpret_cast<const half8_t*>(bs + lds_off(wn0 + j * 32 + lrow, 2 * kk + lseg));
-  };
-  half8_t af[2][TM], bf[2][TN];
-#pragma unroll
-  for (int i = 0; i < TM; i++)
-    af[0][i] = *reinterpret_cast<const half8_t*>(as + lds_off(wm0 + i * 32 + lrow, lseg));
-#pragma unroll
-  for (int j = 0; j < TN; j++) bf[0][j] = bfrag(j, 0);
-#pragma unroll
-  for (int kk = 0; kk < kBK / 16; kk++) {
-    const int cur = kk & 1;
-    if (kk + 1 < kBK / 16) {
-#pragma unroll
-      for (int i = 0; i < TM; i++)
-        af[cur ^ 1][i] = *reinterpret_cast<const half8_t*>(
-            as + lds_off(wm0 + i * 32 + lrow, 2 * (kk + 1) + lseg));
-#pragma unroll
-      for (int j = 0; j < TN; j++) bf[cur ^ 1][j] = bfrag(j, kk + 1);
-    }
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-      for (int j = 0; j < TN; j++)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[cur][j], af[cur][i], acc[i][j], 0,
-                                                           0, 0);
-  }
-}
-
 
 // All waves load, decode and multiply: K-step kt+2 is loaded while kt multiplies and kt+1 is
 // committed to the other LDS buffer in four parts between the MFMA sub-steps.
@@ -1173,6 +1130,15 @@ struct BLoadT {
   static constexpr int TOTAL = kBK * CPR;
   static constexpr int VMEM = REST ? 6 : 3;
   static_assert(TOTAL % 64 == 0 && TOTAL <= NTP, "B items in whole waves, one round");
+  // item q -> (row, 32-column chunk): consecutive items along the row, except with 12-unit
+  // rows (BN 96), where 16 consecutive items take one chunk of 16 consecutive rows (the layout
+  // under which bt_off's swizzle spreads a store cycle over all banks)
+  __device__ static __forceinline__ int item_row(int q) {
+    return LDB == 96 ? 16 * (q / (16 * CPR)) + (q & 15) : q / CPR;
+  }
+  __device__ static __forceinline__ int item_chunk(int q) {
+    return LDB == 96 ? (q >> 4) % CPR : q % CPR;
+  }
 
   struct Stage {
     u32x4 w;
@@ -1190,7 +1156,7 @@ struct BLoadT {
   __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0) {
     Src r;
     const int q = p;  // the caller runs only lanes with an item (p < TOTAL)
-    const int row = q / CPR, c = q % CPR;
+    const int row = item_row(q), c = item_chunk(q);
     r.x = (uint32_t)row * a.Kw + min(n0 + 32 * c, a.Nc - 32);
     r.x4 = (uint32_t)(p >> 2) * a.Kw + min(n0 + C16 + 8 * (p & 3), a.Nc - 8);
     return r;
@@ -1246,14 +1212,14 @@ struct BLoadT {
                                                 int p, float offset) {
     {
       const int q = p;  // < TOTAL
-      const int row = q / CPR, c = q % CPR;
+      const int row = item_row(q), c = item_chunk(q);
       const float sc = nested_scale(L.c, S.a2, offset);
 #pragma unroll
       for (int d = 0; d < 4; d++) {
         u32x4 v;
 #pragma unroll
         for (int j = 0; j < 4; j++) v[j] = pack_f16x2(L.pr[d][j][0] * sc, L.pr[d][j][1] * sc);
-        *reinterpret_cast<u32x4*>(bs + row * LDB + 32 * c + 8 * d) = v;
+        *reinterpret_cast<u32x4*>(bs + bt_off(row, 32 * c + 8 * d, LDB)) = v;
       }
     }
     if constexpr (REST > 0) {
@@ -1262,7 +1228,7 @@ struct BLoadT {
       u32x4 v;
 #pragma unroll
       for (int j = 0; j < 4; j++) v[j] = pack_f16x2(L.pb[j][0] * sc, L.pb[j][1] * sc);
-      *reinterpret_cast<u32x4*>(bs + row * LDB + C16 + 8 * sub) = v;
+      *reinterpret_cast<u32x4*>(bs + bt_off(row, C16 + 8 * sub, LDB)) = v;
     }
   }
 };
@@ -1351,6 +1317,13 @@ struct BLoadT8 {
   static constexpr int TOTAL = kBK * CPR;
   static constexpr int VMEM = 3;
   static_assert(BN % 16 == 0 && TOTAL % 64 == 0 && TOTAL <= 512, "B items in whole waves");
+  // item -> (row, 16-column chunk), as BLoadT maps its items
+  __device__ static __forceinline__ int item_row(int q) {
+    return LDB == 96 ? 16 * (q / (16 * CPR)) + (q & 15) : q / CPR;
+  }
+  __device__ static __forceinline__ int item_chunk(int q) {
+    return LDB == 96 ? (q >> 4) % CPR : q % CPR;
+  }
 
   struct Stage {
     u32x2 w;
@@ -1364,7 +1337,7 @@ struct BLoadT8 {
   __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0) {
     Src r;
     const int q = p;  // the caller runs only lanes with an item (p < TOTAL)
-    const int row = q / CPR, c = q % CPR;
+    const int row = item_row(q), c = item_chunk(q);
     r.x = (uint32_t)row * a.Kw + min(n0 + 16 * c, a.Nc - 16);
     return r;
   }
@@ -1402,14 +1375,14 @@ struct BLoadT8 {
                                                 int p, float offset) {
     {
       const int q = p;  // < TOTAL
-      const int row = q / CPR, c = q % CPR;
+      const int row = item_row(q), c = item_chunk(q);
       const float sc = nested_scale(L.c, S.a2, offset);
 #pragma unroll
       for (int d = 0; d < 2; d++) {
         u32x4 v;
 #pragma unroll
         for (int j = 0; j < 4; j++) v[j] = pack_f16x2(L.pr[d][j][0] * sc, L.pr[d][j][1] * sc);
-        *reinterpret_cast<u32x4*>(bs + row * LDB + 16 * c + 8 * d) = v;
+        *reinterpret_cast<u32x4*>(bs + bt_off(row, 16 * c + 8 * d, LDB)) = v;
       }
     }
   }
@@ -1446,7 +1419,7 @@ struct ACopy {
 #pragma unroll
     for (int i = 0; i < N; i++) {
       const int row = (pw + PW * i) * 8 + (lane >> 3);
-      const int seg = ((lane & 7) ^ row ^ (row >> 3)) & 7;
+      const int seg = ((lane & 7) ^ (row >> 1)) & 7;
       const uint32_t m = min(m0 + row, a.M - 1) - m0;
       off[i] = (m * (uint32_t)a.lda + seg * 8) * 2;
     }
@@ -1473,14 +1446,63 @@ struct ACopy {
     }
   }
 };
+
+// The A-tile copies issued by the 4 consumer waves instead (between their MFMAs, where the wave
+// has issue slots to spare): wave w copies the 8-row groups w, w + 4, ... of the tile.  Under the
+// segment swizzle those groups share one physical-slot assignment per lane, so a copy's source
+// offset is min(row, last row) * row bytes + that lane's segment: three VALU per copy, computed
+// when issued rather than held in registers the MFMA operands need.
+template <int BM>
+struct ACopyC {
+  static constexpr int N = BM / 32;  // copies per consumer wave per K-step
+  const char* base;   // A row m0 (uniform)
+  uint32_t lds;       // LDS byte address of this wave's first row group in ring slot 0 (uniform)
+  uint32_t rowbase;   // the lane's row within its wave's first group
+  uint32_t seg16;     // byte offset of the lane's logical segment within a row
+  uint32_t last;      // last valid row of the tile, relative to m0 (uniform)
+  uint32_t ldab;      // bytes per A row (uniform)
+
+  __device__ __forceinline__ void init(const GemmArgs& a, const _Float16* as, int w, int lane,
+                                       int m0) {
+    rowbase = w * 8 + (lane >> 3);
+    seg16 = (((lane & 7) ^ (rowbase >> 1)) & 7) * 16;
+    last = __builtin_amdgcn_readfirstlane((uint32_t)(min(m0 + BM, a.M) - 1 - m0));
+    ldab = __builtin_amdgcn_readfirstlane((uint32_t)a.lda * 2);
+    base = reinterpret_cast<const char*>(a.A + (int64_t)m0 * a.lda);
+    lds = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>(as + w * 8 * kBK)));
+  }
+
+  // copy i (0 <= i < N) of K-step kt into ring slot `slot_bytes`
+  __device__ __forceinline__ void copy(uint32_t slot_bytes, int kt, int i) const {
+    const char* src = base + (size_t)kt * kBK * sizeof(_Float16);
+    const uint32_t off = min(rowbase + 32u * i, last) * ldab + seg16;
+    const uint32_t dst = lds + slot_bytes + i * 32 * kBK * sizeof(_Float16);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(dst), "v"(off), "s"(src)
+                 : "memory", "m0");
+  }
+};
 #pragma clang diagnostic pop
 
+// Who issues the A-tile copies of a warp-specialized kernel: the consumer waves, between their
+// MFMAs, except in the 256-row tiles with 8 producer waves (12 waves per CU leave the consumers
+// too few registers: the copies' offsets spill there).  Measured at 1024 tokens against the
+// producers issuing them: 2-7 % faster on the gate/up forward, down_proj forward and dX and the
+// 128x128 dX; 3 % slower on the 256x96 8-producer dX, which keeps them on its producers.
+template <int BM, int PW>
+constexpr bool consumer_copies() {
+  return !(BM == 256 && PW == 8);
+}
+
 // Warp-specialized kernel: 4 consumer waves (one per SIMD, CWM x CWN over the BM x BN tile)
-// only read LDS fragments and issue MFMAs; 4 producer waves (the other wave of each SIMD) copy
-// the A tile of K-step kt+2 straight into a 3-deep LDS ring, and decode the NF4 of kt+1 into
-// the other half of a 2-deep B buffer while the consumers multiply kt.  Everything a producer
-// issues in one K-step is waited for at the start of the next, and one workgroup barrier per
-// K-step hands the buffers over.
+// read LDS fragments and issue MFMAs; PW producer waves decode the NF4 of K-step kt+1 into the
+// other half of a 2-deep B buffer while the consumers multiply kt.  The A tile of kt+2 goes
+// straight into a 3-deep LDS ring by direct-to-LDS copies, issued by the consumers between their
+// MFMAs or by the producers (consumer_copies).  Everything issued in one K-step is waited for
+// at the start of the next, and one workgroup barrier per K-step hands the buffers over.  Wave
+// roles are uniform branches, so neither side's registers live through the other's code.
 // One output tile (bx, by) of the warp-specialized GEMM; split index blockIdx.z.
 template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU>
 __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
@@ -1553,8 +1575,9 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
     // copies, would drain the copy of A(kt+1) along with B(kt+2).  Every issue is unconditional
     // (steps past the end re-load the last one), so the number of memory instructions in
     // flight is a constant and each wait names exactly the group it needs.
+    constexpr bool CC = consumer_copies<BM, PW>();
     using AC = ACopy<BM, PW>;
-    constexpr int LA = AC::N;  // A-tile copy instructions per producer wave and step
+    constexpr int LA = CC ? 0 : AC::N;  // A-tile copy instructions per producer wave and step
     constexpr uint32_t SLOT = LDS_A * sizeof(_Float16);
     const int last = kt1 - 1;
     // the branch is uniform and taken once; both paths pass the same barriers
@@ -1562,16 +1585,16 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
       constexpr int LB = B::VMEM;
       static_assert(NS >= 4 && NS * LB + 2 * LA <= 63, "stages: at least 4; waits fit vmcnt");
       AC ac;
-      ac.init(a, As, pw, lane, m0);
+      if constexpr (!CC) ac.init(a, As, pw, lane, m0);
       const typename B::Src src = B::setup(a, p, n0);
       typename B::Stage S[NS];
       typename B::Looked L;
       if (run) {
 #pragma unroll
         for (int u = 0; u < NS - 2; u++) B::issue(a, src, S[u], min(kt0 + u, last));
-        ac.copy(0, kt0);
+        if constexpr (!CC) ac.copy(0, kt0);
         B::issue(a, src, S[NS - 2], min(kt0 + NS - 2, last));
-        ac.copy(SLOT, min(kt0 + 1, last));
+        if constexpr (!CC) ac.copy(SLOT, min(kt0 + 1, last));
         B::issue(a, src, S[NS - 1], min(kt0 + NS - 1, last));
       }
       if (lora16 || kmask) {
@@ -1602,9 +1625,10 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
           wait_vmcnt<(NS - 3) * (LA + LB)>();
           B::ready(Sn);
           B::lookup(Sn, L, s_pair, s_code);
-          ac.copy(((r + 2) % 3) * SLOT, min(kt + 2, last));
+          if constexpr (!CC) ac.copy(((r + 2) % 3) * SLOT, min(kt + 2, last));
           B::issue(a, src, Si, min(kt + NS, last));
-          wait_vmcnt<2 * LB + LA>();  // A(kt+1); after it only B(kt+NS-1), A(kt+2), B(kt+NS)
+          // A(kt+1); after it only B(kt+NS-1), A(kt+2), B(kt+NS)
+          if constexpr (!CC) wait_vmcnt<2 * LB + LA>();
           lds_barrier();
           // nothing of the next step moves above this point (its arithmetic on the next stage
           // would then sit before the copies of this step in the schedule)
@@ -1627,6 +1651,18 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
         // allocated until the loads writing them have landed.
 #pragma unroll
         for (int u = 0; u < NS; u++) B::ready(S[u]);
+      }
+    } else if constexpr (CC) {
+      // no B items and no copies: the staged LoRA operands, then every barrier of the tile
+      if (lora16 || kmask) {
+        wait_vmem_all();  // the staged loads
+        if (lora16) lst.commit(a, Ls, p);
+        if (kmask) mst.commit(Ks, p);
+      }
+      lds_barrier();  // tables, LoRA operands
+      if (run) {
+        lds_barrier();  // K-step kt0 ready
+        for (int kt = kt0; kt < kt1; kt++) lds_barrier();
       }
     } else {
       AC ac;
@@ -1669,6 +1705,21 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
     lds_barrier();  // the A ring is free for the consumers' staged epilogue
   } else {
     // ---- consumers ----
+    constexpr bool CC = consumer_copies<BM, PW>();
+    using AC = ACopyC<BM>;
+    constexpr int LA = AC::N;
+    constexpr uint32_t SLOT = LDS_A * sizeof(_Float16);
+    const int lastk = kt1 - 1;
+    AC ac;
+    if constexpr (CC) {
+      ac.init(a, As, wave, lane, m0);
+      if (kt0 < kt1) {
+#pragma unroll
+        for (int i = 0; i < LA; i++) ac.copy(0, kt0, i);
+#pragma unroll
+        for (int i = 0; i < LA; i++) ac.copy(SLOT, min(kt0 + 1, lastk), i);
+      }
+    }
     AccStart<TM, TN, BWD> start;
     start.load(a, n0 + wn0, lseg);  // before the tables' loads
     fill_tables(a, s_pair, s_code, t, 256);
@@ -1682,14 +1733,101 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
       start.finish(a, acc, m0 + wm0, n0 + wn0, lrow, lseg, wm0, wn0, nullptr, 0,
                    kmask ? Ks : nullptr, MaskStage<BM, BN, NTP>::KST);
     if (kt0 < kt1) {
-      lds_barrier();  // K-step kt0 ready
+      if constexpr (CC) wait_vmcnt<LA>();  // A(kt0); after it only A(kt0+1)
+      lds_barrier();                        // K-step kt0 ready
+      // Operand fragments of one 16-deep sub-step in two register sets.  The last sub-step of
+      // each K-step is multiplied after the barrier that ends it (its fragments are read
+      // before), so the reads of the next step's first fragments overlap those MFMAs instead
+      // of leaving the MFMA pipe idle behind the barrier.
+      half8_t fa[2][TM], fb[2][TN];
+      // Per-lane fragment offsets, computed once.  Rows 32 apart share their swizzle
+      // ((row >> 1) & 7 with wm0, wn0 multiples of 32; in a backward tile, bt_off's unit XOR
+      // for reduction rows 16 apart and columns 32 apart), so the 32-row blocks and the
+      // sub-steps of a fragment read are compile-time offsets from one register per operand
+      // and sub-step, not one address register per fragment.
+      const int xs = (lrow >> 1) & 7;
+      int aoff[4], boff[4];  // halfs: lane's A / B (forward) fragment of sub-step kk, block 0
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++) {
+        const int seg = (((2 * kk + lseg) ^ xs) & 7) << 3;
+        aoff[kk] = (wm0 + lrow) * kBK + seg;
+        boff[kk] = (wn0 + lrow) * kBK + seg;
+      }
+      int btlo = 0, bthi = 0;  // backward tile: the lane's two 8-byte reads, block 0, kk 0
+      if constexpr (LDB > 0) {
+        const int g = lane >> 4, sl = lane & 15;
+        const int kl = 8 * (g >> 1) + (sl >> 2), nl = 16 * (g & 1) + 4 * (sl & 3);
+        btlo = bt_off(kl, wn0 + nl, LDB);
+        bthi = bt_off(kl + 4, wn0 + nl, LDB);
+      }
+      typedef __attribute__((address_space(3))) short4_t lds_short4;
+      auto load = [&](int set, const _Float16* as, const _Float16* bs, int kk) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+          fa[set][i] = *reinterpret_cast<const half8_t*>(as + aoff[kk] + i * 32 * kBK);
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+          if constexpr (LDB > 0) {
+            const _Float16* b = bs + 16 * kk * LDB + 32 * j;
+            const half4_t lo = __builtin_bit_cast(
+                half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(b + btlo)));
+            const half4_t hi = __builtin_bit_cast(
+                half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(b + bthi)));
+            fb[set][j] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          } else {
+            fb[set][j] = *reinterpret_cast<const half8_t*>(bs + boff[kk] + j * 32 * kBK);
+          }
+        }
+      };
+      auto mma = [&](int set) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[set][j], fa[set][i],
+                                                               acc[i][j], 0, 0, 0);
+      };
+      // Issue order of one sub-step: a fragment read of the next sub-step after each MFMA of
+      // this one.  Left alone, the scheduler puts every read right before the MFMA that uses
+      // it (fewer live registers) and the MFMA pipe idles through each read's latency.
+      constexpr int NRD = TM + TN * (LDB > 0 ? 2 : 1);  // LDS read instructions per sub-step
+      constexpr int NMF = TM * TN;                      // MFMAs per sub-step
+      auto interleave = [&]() {
+#pragma unroll
+        for (int q = 0; q < (NRD > NMF ? NRD : NMF); q++) {
+          if (q < NMF) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          if (q < NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+        }
+      };
+      load(0, As, bbuf(0), 0);
       for (int kt = kt0; kt < kt1; kt++) {
         const int r = kt - kt0;
-        mma_kstep<TM, TN, LDB>(acc, As + (r % 3) * LDS_A, bbuf(r), wm0, wn0, lrow, lseg);
-        lds_barrier();
+        const _Float16* as = As + (r % 3) * LDS_A;
+        const _Float16* bs = bbuf(r);
+#pragma unroll
+        for (int kk = 0; kk < 3; kk++) {
+          load((kk + 1) & 1, as, bs, kk + 1);
+          mma(kk & 1);
+          interleave();
+          __builtin_amdgcn_sched_barrier(0);
+          if constexpr (CC) {
+            // A(kt+2) into the ring slot step kt-1 used, spread over the sub-steps
+#pragma unroll
+            for (int i = kk * LA / 3; i < (kk + 1) * LA / 3; i++)
+              ac.copy(((r + 2) % 3) * SLOT, min(kt + 2, lastk), i);
+          }
+        }
+        if constexpr (CC) wait_vmcnt<LA>();  // A(kt+1); after it only A(kt+2)
+        lds_barrier();  // (its lgkmcnt(0) covers sub-step 3's fragments)
+        // step kt+1's first fragments (past the end: stale slots, read and never used)
+        load(0, As + ((r + 1) % 3) * LDS_A, bbuf(r + 1), 0);
+        mma(1);  // sub-step 3 of step kt
+        interleave();
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    lds_barrier();  // the producers' last copies have landed
+    if constexpr (CC) wait_vmem_all();  // no copy into the A ring may still be in flight
+    lds_barrier();  // the last copies have landed
     static_assert(4 * StagedStore<TM, TN>::AREA_DWORDS * 4 <= 3 * LDS_A * 2,
                   "staged epilogue areas fit in the A ring");
     if constexpr (GLU) {
