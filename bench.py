@@ -310,6 +310,49 @@ def layer_bwd(projs, saved, s=ALPHA / RANK):
     return grads
 
 
+class AutogradLayer:
+    """One layer's projections as a training step sees them: the four activations (q/k/v's,
+    o's, gate/up's, down's) as leaves that need their gradient, fp32 LoRA weights (peft keeps
+    them in fp32) and each projection's Proj record (packed weight, state, keep mask)."""
+
+    def __init__(self, projs, s=ALPHA / RANK):
+        from mindxsoup_amd.linear4bit import Proj
+
+        self.projs = projs
+        self.x = {i: projs[i]["x"].detach().requires_grad_(True) for i in (0, 3, 4, 6)}
+        self.a = [p["a"].float().requires_grad_(True) for p in projs]
+        self.b = [p["b"].float().requires_grad_(True) for p in projs]
+        self.rec = [Proj(p["packed"], p["st"], None, p["keep"], 1.0 / (1.0 - P_DROP), s)
+                    for p in projs]
+        self.dys = [p["dy"] for p in projs]
+        self.leaves = [*self.x.values(), *self.a, *self.b]
+
+    def forward(self):
+        """The 7 outputs in PROJ order: q/k/v in one siblings node (one grouped GEMM launch),
+        o, gate/up in one siblings node (each GEMM on its own plan), down."""
+        from mindxsoup_amd import linear4bit
+
+        r, a, b = self.rec, self.a, self.b
+        qkv = linear4bit.siblings_project(self.x[0], r[0:3], a[0:3], b[0:3], one_gemm=True)
+        o = linear4bit.lora_project(self.x[3], a[3], b[3], r[3].packed, r[3].state, None,
+                                    r[3].keep, r[3].mask_scale, r[3].s)
+        gu = linear4bit.siblings_project(self.x[4], r[4:6], a[4:6], b[4:6], one_gemm=False)
+        down = linear4bit.lora_project(self.x[6], a[6], b[6], r[6].packed, r[6].state, None,
+                                       r[6].keep, r[6].mask_scale, r[6].s)
+        return [*qkv, o, *gu, down]
+
+
+def autograd_step(alayers):
+    """Forward of every layer through the autograd ops, then one torch.autograd.grad over all
+    outputs: every input and LoRA weight gradient, as a training step's backward makes them."""
+    outs, dys, leaves = [], [], []
+    for L in alayers:
+        outs += L.forward()
+        dys += L.dys
+        leaves += L.leaves
+    return torch.autograd.grad(outs, leaves, dys)
+
+
 def graph_time(fn, steps, warmup):
     """Capture fn() in a HIP graph, replay: mean ms per replay (events on the capture stream's
     replay stream) and the wall-clock mean."""
@@ -641,9 +684,27 @@ def bench_fused(dev, steps, warmup):
             for p, ht in zip(reversed(projs), reversed(hts)):
                 proj_bwd(p, ht)
 
-    ms, wall = graph_time(step, max(3, steps // 5), max(2, warmup // 5))
-    ms_u, _ = graph_time(step_ungrouped, max(3, steps // 5), max(2, warmup // 5))
-    eager, host = eager_time(step, max(3, steps // 5), max(2, warmup // 5))
+    from mindxsoup_amd import ops
+
+    st_steps, st_warm = max(3, steps // 5), max(2, warmup // 5)
+    ms, wall = graph_time(step, st_steps, st_warm)
+    ms_u, _ = graph_time(step_ungrouped, st_steps, st_warm)
+    raw_eager, raw_host = eager_time(step, st_steps, st_warm)
+    # the same step as a training loop runs it: autograd nodes, eager launches
+    alayers = [AutogradLayer(projs) for projs in layers]
+    torch.cuda.synchronize()
+    print("bench: autograd step (torch.ops.mxs_nf4)", file=sys.stderr, flush=True)
+    prev = ops.ENABLED
+    try:
+        ops.ENABLED = True
+        eager, host = eager_time(lambda: autograd_step(alayers), st_steps, st_warm)
+        ag_ms, _ = graph_time(lambda: autograd_step(alayers), st_steps, st_warm)
+        ops.ENABLED = False  # the Python Functions over ctypes, for comparison
+        print("bench: autograd step (Python Functions)", file=sys.stderr, flush=True)
+        py_eager, py_host = eager_time(lambda: autograd_step(alayers), st_steps, st_warm)
+    finally:
+        ops.ENABLED = prev
+    per_dir = 2 * LAYERS * len(PROJ)
     fl = LAYERS * sum(proj_flops(n, k) for _, n, k in PROJ)
     tf = fl / ms / 1e9
     out["config5_stack"] = {"ms_per_step": round(ms, 4), "wall_ms_per_step": round(wall, 4),
@@ -653,10 +714,19 @@ def bench_fused(dev, steps, warmup):
                             "lora_rows": "q/k/v and gate/up grouped per launch",
                             "ungrouped_ms_per_step": round(ms_u, 4),
                             "eager_ms_per_step": round(eager, 4),
+                            "eager_over_graph": round(eager / ms, 3),
                             "eager_host_ms_per_step": round(host, 4),
                             "eager_host_us_per_projection_direction": round(
-                                host * 1e3 / (2 * LAYERS * len(PROJ)), 2)}
-    del layers
+                                host * 1e3 / per_dir, 2),
+                            "eager_path": "autograd step through torch.ops.mxs_nf4 (C++ nodes)",
+                            "autograd_graph_ms_per_step": round(ag_ms, 4),
+                            "eager_python_ms_per_step": round(py_eager, 4),
+                            "eager_python_host_us_per_projection_direction": round(
+                                py_host * 1e3 / per_dir, 2),
+                            "eager_raw_kernel_calls_ms_per_step": round(raw_eager, 4),
+                            "eager_raw_kernel_calls_host_us_per_projection_direction": round(
+                                raw_host * 1e3 / per_dir, 2)}
+    del layers, alayers
     return out
 
 

@@ -246,6 +246,20 @@ int mxs_lora_h_partials_group(int n, const void* const x[], int M, const int K[]
                               const void* const lora_b[], const int N[], void* const bt[],
                               float* const partials[], hipStream_t stream);
 
+/* mxs_lora_h_partials_group for LoRA weights kept in fp32 (peft keeps its adapter weights in
+ * fp32 and casts them for each fp16 forward, solution/attention.py:197-199 under autocast):
+ * lora_a[i] fp32 [r, K[i]] and lora_b[i] fp32 [N[i], r] are read in place and rounded to fp16
+ * (nearest even) where used, and the fp16 operands the GEMMs and the backward take come out as
+ * side outputs: at[i] = fp16(A)^T [K, r], bt[i] = fp16(B)^T [r, N], b16[i] = fp16(B) [N, r]
+ * (each array, or entry, may be NULL).  The same bits as casting the weights to fp16 first and
+ * calling mxs_lora_h_partials_group, without the two cast launches per projection. */
+int mxs_lora_h_partials_group_w32(int n, const void* const x[], int M, const int K[],
+                                  const float* const lora_a[], int r, const void* const mask[],
+                                  float mask_scale, float s, int ldt, void* const at[],
+                                  const float* const lora_b[], const int N[], void* const bt[],
+                                  void* const b16[], float* const partials[],
+                                  hipStream_t stream);
+
 /* mxs_lora_dh_partials for n (1..4) projections in ONE launch (their output gradients arrive
  * together: q/k/v from attention's backward, gate/up from the SwiGLU's); same bits as n calls. */
 int mxs_lora_dh_partials_group(int n, const void* const dy[], int M, const int N[],

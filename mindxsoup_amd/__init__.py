@@ -10,7 +10,7 @@ build).
     solution.apply()
 """
 
-from . import direct
+from . import direct, ops
 
 FEATURES = {
     # --- NF4 path (acted on) -------------------------------------------------------------
@@ -25,6 +25,8 @@ FEATURES = {
     "mlp_fused_swiglu": True,  # that MLP's SwiGLU in the up/down GEMM epilogues (LoRA layers)
     "attention_fp16": True,  # fp16 q/k/v from grouped NF4 + LoRA launches, one RoPE launch
     "stream_weights": False,  # decoder NF4 weights in pinned host memory, a layer at a time
+    "torch_ops": True,       # projections on the compiled torch.ops.mxs_nf4 operators (C++
+                             # host side and autograd); False: Python Functions over ctypes
     # --- reference switches outside the NF4 path (inert here) ------------------------------
     "startup_cache": False, "example_swiglu": False, "adam_host": False,
     "cublas_workspace": None, "fused_layer_input": False, "fused_head_acc": False,
@@ -56,6 +58,7 @@ def apply():
     from . import linear4bit, nf4, peft_lora, stream
 
     direct.enabled = FEATURES["direct_nograd"]
+    ops.ENABLED = FEATURES["torch_ops"]
     stream.LAYER_UNPACK = FEATURES["layer_unpack"]
     if FEATURES["stream_weights"]:
         stream.patch_stream_layers()  # stream.setup(model) then moves the weights

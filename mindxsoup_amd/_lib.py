@@ -71,6 +71,8 @@ _SIGNATURES = {
     "mxs_lora_h_partials": [P, I32, I32, P, I32, P, F32, F32, I32, P, P, I32, P, P, P],
     "mxs_lora_dh_partials": [P, I32, I32, P, I32, F32, I32, P, P],
     "mxs_lora_h_partials_group": [I32, P, I32, P, P, I32, P, F32, F32, I32, P, P, P, P, P, P],
+    "mxs_lora_h_partials_group_w32": [I32, P, I32, P, P, I32, P, F32, F32, I32, P, P, P, P, P, P,
+                                      P],
     "mxs_lora_dh_partials_group": [I32, P, I32, P, P, I32, F32, I32, P, P],
     "mxs_lora_dh_group": [I32, P, I32, P, P, I32, F32, I32, P, P, P],
     "mxs_lora_grads_group": [I32, P, P, I32, P, P, I32, P, P, I32, P, F32, P, P, P],

@@ -7,7 +7,7 @@ changes how q, k and v are made:
 
   1. the input is cast to fp16 once;
   2. when q, k and v are LoRA layers of one rank, scaling and dropout over NF4 bases (peft's
-     layout; peft_lora.adapter_of), all three run as one NF4LoraSiblingsFunction: one launch
+     layout; peft_lora.adapter_of), all three run as one siblings projection: one launch
      of LoRA row products and one launch of fused GEMMs forward, shared launches backward; any
      other mix of fp16 NF4 projections (bare or LoRA) runs projection by projection, each on
      the fused kernels;
@@ -65,7 +65,7 @@ def _route(proj, x16):
 
 
 def _siblings(ads, x2d):
-    """Proj records for NF4LoraSiblingsFunction, or None when the three adapters differ in
+    """Proj records for linear4bit.siblings_project, or None when the three adapters differ in
     rank, scaling or dropout (their row products could not share a launch)."""
     if len({(ad.rank, ad.s, ad.p, ad.dropping()) for ad in ads}) != 1:
         return None
@@ -94,8 +94,8 @@ def project_qkv(attn, x16):
         x2d = x16.reshape(-1, x16.shape[-1]).contiguous()
         projs = _siblings([ad for _, ad in routes], x2d)
         if projs is not None:
-            ab = [t for _, ad in routes for t in (ad.a, ad.b)]
-            outs = linear4bit.NF4LoraSiblingsFunction.apply(x2d, projs, *ab)
+            outs = linear4bit.siblings_project(x2d, projs, [ad.a for _, ad in routes],
+                                               [ad.b for _, ad in routes])
             return [y.view(*x16.shape[:-1], y.shape[-1]) for y in outs]
     return [peft_lora.fused_project(obj, x16) if kind == "lora" else obj(x16)
             for kind, obj in routes]

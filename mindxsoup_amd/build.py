@@ -6,6 +6,10 @@ Every csrc/*.hip file is compiled by hipcc to an object in csrc/_build/ (in para
 linked into mindxsoup_amd/libmxs_nf4.so.  No torch headers are involved: the library's
 interface is include/mxs_nf4.h.
 
+csrc/torch_ops.cpp (host C++ only, no device code) is compiled by g++ against torch's headers
+beside them and linked into mindxsoup_amd/libmxs_nf4_torch.so, which registers the
+torch.ops.mxs_nf4 operators and links libmxs_nf4.so from its own directory.
+
 Sources that issue global loads as inline asm (the ones calling vm_ready) are also compiled to
 device assembly, which isa_check verifies: no instruction may name a register whose load can
 still be in flight.  A finding fails the build.
@@ -21,6 +25,8 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(CSRC, "_build")
 LIB = os.path.join(PKG, "libmxs_nf4.so")
+TORCH_SRC = os.path.join(CSRC, "torch_ops.cpp")
+TORCH_LIB = os.path.join(PKG, "libmxs_nf4_torch.so")
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -71,24 +77,62 @@ def _check_asm(src):
     return out
 
 
+def _torch_flags():
+    import torch
+
+    tp = os.path.dirname(os.path.abspath(torch.__file__))
+    compile_flags = [
+        "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+        f"-I{os.path.join(tp, 'include')}",
+        f"-I{os.path.join(tp, 'include', 'torch', 'csrc', 'api', 'include')}",
+        "-I/opt/rocm/include", f"-I{os.path.join(ROOT, 'include')}",
+    ]
+    link_flags = [f"-L{PKG}", "-lmxs_nf4", f"-L{os.path.join(tp, 'lib')}", "-lc10", "-lc10_hip",
+                  "-ltorch_cpu", "-L/opt/rocm/lib", "-lamdhip64", "-Wl,-rpath,$ORIGIN"]
+    return compile_flags, link_flags
+
+
+def _compile_torch_ops():
+    obj = os.path.join(OBJ, "torch_ops.o")
+    r = subprocess.run(["g++", *_torch_flags()[0], "-c", TORCH_SRC, "-o", obj],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed on {TORCH_SRC}:\n{r.stderr}")
+    return obj
+
+
+def _link_torch_ops(obj):
+    tmp = TORCH_LIB + ".tmp"
+    r = subprocess.run(["g++", "-shared", obj, "-o", tmp, *_torch_flags()[1]],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link of {TORCH_LIB} failed:\n{r.stderr}")
+    os.replace(tmp, TORCH_LIB)
+
+
 def build(verbose=True):
     os.makedirs(OBJ, exist_ok=True)
     srcs = sources()
     asm_srcs = [s for s in srcs if "vm_ready(" in open(s).read()]
-    workers = min(len(srcs) + len(asm_srcs), max(1, (os.cpu_count() or 4)), 8)
+    workers = min(len(srcs) + len(asm_srcs) + 1, max(1, (os.cpu_count() or 4)), 8)
     with concurrent.futures.ThreadPoolExecutor(workers) as ex:
+        torch_obj = ex.submit(_compile_torch_ops)
         checks = [ex.submit(_check_asm, s) for s in asm_srcs]
         objs = list(ex.map(_compile, srcs))
         for c in checks:
             c.result()
+        torch_obj = torch_obj.result()
     tmp = LIB + ".tmp"
     r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp],
                        capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    _link_torch_ops(torch_obj)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources")
+        print(f"built {LIB} from {len(srcs)} sources and {TORCH_LIB}")
     return LIB
 
 

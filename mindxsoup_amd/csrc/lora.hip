@@ -58,12 +58,33 @@ struct RowsArgs {
   _Float16* bt;
   float* ws;              // fp32 partials [slices][ldt][r], times s (sliced or partial mode)
   int partial_out;        // write the partials even for one slice; no final fp16 outputs
+  // fp32 LoRA weights (the rows kernel's W32 form): R32 [r, K] and B32 [N, r] are read in place
+  // of R / B and rounded to fp16 (nearest even) where they are used, so the results are those of
+  // R and B cast first; b16 (optional) receives that fp16 copy of B [N, r].
+  const float* R32;
+  const float* B32;
+  _Float16* b16;
 };
+
+// 8 consecutive fp32 weights rounded to fp16 (round to nearest even, as a cast would).
+__device__ __forceinline__ half8_t f32x8_to_f16(const float* p) {
+  const float4_t lo = *reinterpret_cast<const float4_t*>(p);
+  const float4_t hi = *reinterpret_cast<const float4_t*>(p + 4);
+  half8_t h;
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    h[e] = (_Float16)lo[e];
+    h[4 + e] = (_Float16)hi[e];
+  }
+  return h;
+}
 
 // out[m][c] = fp16(s * sum_k drop(P)[m][k] * R[c][k]) for the 16 rows of row block rb, over
 // reduction slice `slice` of `slices`.  Waves [0, nw) reduce; any waves past nw (a grouped
 // launch sized for another problem) only take part in the barrier and the stores, so the result
 // is the same bits as a launch of exactly nw waves.  wg of n_wg places the side outputs.
+// W32: the weights come as fp32 (R32, B32).
+template <bool W32>
 __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice, int slices,
                                            int nw, int wg, int n_wg, float* red) {
   const int lane = threadIdx.x & 63;
@@ -97,12 +118,15 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
 #pragma unroll
     for (int b = 0; b < kMaxRB; b++) {
       if (b >= rbn) break;
-      const _Float16* rrow = a.R + (int64_t)(16 * b + (lane & 15)) * a.K + 8 * g;
+      const int64_t roff = (int64_t)(16 * b + (lane & 15)) * a.K + 8 * g;
       half8_t y[kChunksInFlight];
 #pragma unroll
       for (int u = 0; u < kChunksInFlight; u++) {
         const int c = c0 + u * nw;
-        y[u] = c < c_end ? *reinterpret_cast<const half8_t*>(rrow + 32 * c) : (half8_t){};
+        if constexpr (W32)
+          y[u] = c < c_end ? f32x8_to_f16(a.R32 + roff + 32 * c) : (half8_t){};
+        else
+          y[u] = c < c_end ? *reinterpret_cast<const half8_t*>(a.R + roff + 32 * c) : (half8_t){};
       }
 #pragma unroll
       for (int u = 0; u < kChunksInFlight; u++)
@@ -118,21 +142,32 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
     for (int v = 0; v < 4; v++)
       red[(wave * 16 + 4 * g + v) * ld + 16 * b + (lane & 15)] = acc[b][v];
   }
-  // side outputs, spread over the workgroups: R^T [K, r] and B^T [r, N]
+  // side outputs, spread over the workgroups: R^T [K, r], B^T [r, N] and (W32) fp16 B [N, r]
   if (a.rt) {
     const int span = ((a.K + n_wg - 1) / n_wg + 7) & ~7;
     const int k_beg = wg * span, k_end = min(a.K, k_beg + span);
     for (int i = threadIdx.x; i < (k_end - k_beg) * a.r; i += blockDim.x) {
       const int k = k_beg + i / a.r, c = i % a.r;
-      a.rt[(int64_t)k * a.r + c] = a.R[(int64_t)c * a.K + k];
+      if constexpr (W32)
+        a.rt[(int64_t)k * a.r + c] = (_Float16)a.R32[(int64_t)c * a.K + k];
+      else
+        a.rt[(int64_t)k * a.r + c] = a.R[(int64_t)c * a.K + k];
     }
   }
-  if (a.bt) {
+  if (a.bt || (W32 && a.b16)) {
     const int span = ((a.N + n_wg - 1) / n_wg + 7) & ~7;
     const int n_beg = wg * span, n_end = min(a.N, n_beg + span);
     for (int i = threadIdx.x; i < (n_end - n_beg) * a.r; i += blockDim.x) {
       const int n = n_beg + i / a.r, c = i % a.r;
-      a.bt[(int64_t)c * a.N + n] = a.B[(int64_t)n * a.r + c];
+      const int64_t src = (int64_t)n * a.r + c;
+      _Float16 v;
+      if constexpr (W32) {
+        v = (_Float16)a.B32[src];
+        if (a.b16) a.b16[src] = v;
+      } else {
+        v = a.B[src];
+      }
+      if (a.bt) a.bt[(int64_t)c * a.N + n] = v;
     }
   }
   __syncthreads();
@@ -154,7 +189,7 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
 
 __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
   extern __shared__ float red[];  // [waves][16][r + 1]
-  rows_block(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y, (int)blockDim.x >> 6,
+  rows_block<false>(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y, (int)blockDim.x >> 6,
              (int)(blockIdx.y * gridDim.x + blockIdx.x), (int)(gridDim.x * gridDim.y), red);
 }
 
@@ -169,14 +204,15 @@ struct RowsGroup {
   int n;
 };
 
+template <bool W32>
 __global__ __launch_bounds__(1024) void k_lora_rows_group(RowsGroup g) {
   extern __shared__ float red[];  // [waves][16][r + 1]
   const int bid = (int)blockIdx.x;
   int i = 0;
   while (i + 1 < g.n && bid >= g.start[i + 1]) i++;
   const int local = bid - g.start[i];
-  rows_block(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i], g.nw[i], local,
-             g.start[i + 1] - g.start[i], red);
+  rows_block<W32>(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i], g.nw[i], local,
+                  g.start[i + 1] - g.start[i], red);
 }
 
 // out[m][c] = fp16(sum of the slices' partials, in slice order) for m < M; outT [r, ldt]
@@ -313,8 +349,8 @@ static int rows_launch(RowsArgs a, void* workspace, hipStream_t stream) {
 
 // One launch for n rows problems: partial mode (a.ws = the problem's partials, sliced as a
 // single launch with that workspace would be) or finished mode (a.ws null: one slice, fp16
-// out / outT), each as its own launch would run.
-static int rows_group_launch(const RowsArgs* probs, int n, hipStream_t stream) {
+// out / outT), each as its own launch would run.  w32: every problem's weights are fp32.
+static int rows_group_launch(const RowsArgs* probs, int n, hipStream_t stream, bool w32 = false) {
   if (n < 1 || n > kMaxGroup) return MXS_ERR_ARG;
   RowsGroup g{};
   g.n = n;
@@ -329,7 +365,10 @@ static int rows_group_launch(const RowsArgs* probs, int n, hipStream_t stream) {
   }
   g.start[n] = total;
   const size_t lds = (size_t)nw_max * 16 * (probs[0].r + 1) * sizeof(float);
-  hipLaunchKernelGGL(k_lora_rows_group, dim3(total), dim3(64 * nw_max), lds, stream, g);
+  if (w32)
+    hipLaunchKernelGGL(k_lora_rows_group<true>, dim3(total), dim3(64 * nw_max), lds, stream, g);
+  else
+    hipLaunchKernelGGL(k_lora_rows_group<false>, dim3(total), dim3(64 * nw_max), lds, stream, g);
   return check_launch();
 }
 
@@ -528,6 +567,51 @@ int mxs_lora_h_partials_group(int n, const void* const x[], int M, const int K[]
     probs[i] = a;
   }
   return rows_group_launch(probs, n, stream);
+}
+
+int mxs_lora_h_partials_group_w32(int n, const void* const x[], int M, const int K[],
+                                  const float* const lora_a[], int r, const void* const mask[],
+                                  float mask_scale, float s, int ldt, void* const at[],
+                                  const float* const lora_b[], const int N[], void* const bt[],
+                                  void* const b16[], float* const partials[],
+                                  hipStream_t stream) {
+  if (n < 1 || n > kMaxGroup || M < 0 || r <= 0 || !x || !K || !lora_a || !partials)
+    return MXS_ERR_ARG;
+  if (M == 0) return MXS_OK;
+  if (r % 16 || r > 16 * kMaxRB || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  RowsArgs probs[kMaxGroup];
+  for (int i = 0; i < n; i++) {
+    const void* mk = mask ? mask[i] : nullptr;
+    void* at_i = at ? at[i] : nullptr;
+    const float* b_i = lora_b ? lora_b[i] : nullptr;
+    void* bt_i = bt ? bt[i] : nullptr;
+    void* b16_i = b16 ? b16[i] : nullptr;
+    const int n_i = N ? N[i] : 0;
+    if (K[i] < 0 || n_i < 0) return MXS_ERR_ARG;
+    if (!x[i] || !lora_a[i] || !partials[i] || ((bt_i || b16_i) && !b_i)) return MXS_ERR_ARG;
+    if (K[i] % 32) return MXS_ERR_SIZE;
+    if (((uintptr_t)x[i] % 16) || ((uintptr_t)lora_a[i] % 16) || (mk && ((uintptr_t)mk % 8)))
+      return MXS_ERR_ALIGN;
+    RowsArgs a{};
+    a.P = static_cast<const _Float16*>(x[i]);
+    a.M = M;
+    a.K = K[i];
+    a.mask = static_cast<const uint8_t*>(mk);
+    a.mscale = mask_scale;
+    a.R32 = lora_a[i];
+    a.r = r;
+    a.ldt = ldt;
+    a.s = s;
+    a.rt = static_cast<_Float16*>(at_i);
+    a.B32 = b_i;
+    a.N = n_i;
+    a.bt = static_cast<_Float16*>(bt_i);
+    a.b16 = static_cast<_Float16*>(b16_i);
+    a.partial_out = 1;
+    a.ws = partials[i];
+    probs[i] = a;
+  }
+  return rows_group_launch(probs, n, stream, true);
 }
 
 int mxs_lora_dh_partials_group(int n, const void* const dy[], int M, const int N[],

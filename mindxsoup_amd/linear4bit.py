@@ -18,7 +18,7 @@ import math
 
 import torch
 
-from . import direct, kernels, stream
+from . import direct, kernels, ops, stream
 from .nf4 import _supported, unpack_nf4
 from .quant import QuantState, quantize_4bit
 
@@ -330,21 +330,27 @@ class NF4LoraSiblingsFunction(torch.autograd.Function):
     GEMMs with their dA / dB, shared where the plans allow) and dx = the sum of the projections'
     input gradients.  Each output equals NF4LoraFunction on its projection to within the GEMM
     tolerance (the grouped GEMM runs every problem on one tile plan).
-    Inputs: x2d fp16 [M, K], `projs` (a tuple of Proj that siblings_ok accepts), then each
-    projection's lora_A [r, K] and lora_B [N, r] (their gradients come back in their dtypes).
+    Inputs: x2d fp16 [M, K], `projs` (a tuple of Proj that siblings_ok accepts), one_gemm (the
+    forward GEMMs in one grouped launch, else each on its own plan), then each projection's
+    lora_A [r, K] and lora_B [N, r] (their gradients come back in their dtypes).
     Outputs: one fp16 [M, N_i] per projection."""
 
     @staticmethod
-    def forward(ctx, x2d, projs, *ab):
+    def forward(ctx, x2d, projs, one_gemm, *ab):
         n = len(projs)
         a16 = [t.to(torch.float16).contiguous() for t in ab[0::2]]
         b16 = [t.to(torch.float16).contiguous() for t in ab[1::2]]
         s, mask_scale = projs[0].s, projs[0].mask_scale
         rows = kernels.lora_h_partials_group([x2d] * n, a16, s, [p.keep for p in projs],
                                              mask_scale, b16)
-        outs = kernels.nf4_linear_fwd_hp_group([x2d] * n, [p.packed for p in projs],
-                                               [p.state for p in projs], [r[0] for r in rows],
-                                               b16, [p.bias for p in projs])
+        if one_gemm:
+            outs = kernels.nf4_linear_fwd_hp_group([x2d] * n, [p.packed for p in projs],
+                                                   [p.state for p in projs],
+                                                   [r[0] for r in rows], b16,
+                                                   [p.bias for p in projs])
+        else:
+            outs = [kernels.nf4_linear_fwd_hp(x2d, p.packed, p.state, r[0], b, p.bias)
+                    for p, r, b in zip(projs, rows, b16)]
         ctx.save_for_backward(x2d, *[p.keep for p in projs], *[o[1] for o in outs],
                               *[r[1] for r in rows], *[r[2] for r in rows])
         ctx.projs = projs
@@ -368,7 +374,7 @@ class NF4LoraSiblingsFunction(torch.autograd.Function):
             items.append(dict(dy=dy.to(torch.float16).contiguous(), x2d=x2d, keep=keeps[i],
                               ht=hts[i], at=ats[i], bt=bts[i], packed=p.packed, state=p.state,
                               mask_scale=p.mask_scale, s=p.s,
-                              wants=(need[0], need[2 + 2 * i], need[3 + 2 * i])))
+                              wants=(need[0], need[3 + 2 * i], need[4 + 2 * i])))
         res = lora_backward_group(items)
         dx = None
         if need[0]:
@@ -379,7 +385,7 @@ class NF4LoraSiblingsFunction(torch.autograd.Function):
         for i, (_, da, db) in enumerate(res):
             grads += [None if da is None else da.to(ctx.dtypes[2 * i]),
                       None if db is None else db.to(ctx.dtypes[2 * i + 1])]
-        return (dx, None, *grads)
+        return (dx, None, None, *grads)
 
 
 class NF4LoraStreamFunction(NF4LoraFunction):
@@ -401,6 +407,32 @@ class NF4LoraStreamFunction(NF4LoraFunction):
         packed, absmax = stream.bytes_for(ctx.module)
         ctx.packed, ctx.state = packed.view(-1, 1), stream.state_with(ctx.base_state, absmax)
         return NF4LoraFunction.backward(ctx, dy)
+
+
+def linear_project(x, packed, state, bias):
+    """NF4LinearFunction on a resident weight: the compiled op (torch.ops.mxs_nf4.linear, its
+    backward in C++) when ops.ENABLED and the fused GEMM takes the shape, else the Python
+    Function (which also holds the unpack-then-F.linear branch)."""
+    if ops.ENABLED and _fused(state, x):
+        return ops.linear(x, packed, state, bias)
+    return direct.run(NF4LinearFunction, x, packed, state, bias)
+
+
+def lora_project(x2d, lora_a, lora_b, packed, state, bias, keep, mask_scale, s):
+    """NF4LoraFunction on a resident weight: torch.ops.mxs_nf4.lora_linear when ops.ENABLED,
+    else the Python Function; the same kernels in the same order, so the same bits."""
+    if ops.ENABLED:
+        return ops.lora_linear(x2d, lora_a, lora_b, packed, state, bias, keep, mask_scale, s)
+    return NF4LoraFunction.apply(x2d, lora_a, lora_b, packed, state, bias, keep, mask_scale, s)
+
+
+def siblings_project(x2d, projs, lora_as, lora_bs, one_gemm=True):
+    """NF4LoraSiblingsFunction: torch.ops.mxs_nf4.lora_siblings when ops.ENABLED, else the
+    Python Function.  Returns one fp16 [M, N_i] per projection."""
+    if ops.ENABLED:
+        return ops.lora_siblings(x2d, projs, lora_as, lora_bs, one_gemm)
+    ab = [t for pair in zip(lora_as, lora_bs) for t in pair]
+    return NF4LoraSiblingsFunction.apply(x2d, projs, bool(one_gemm), *ab)
 
 
 # ---------------------------------------------------------------------------------------------
@@ -480,7 +512,7 @@ def hip_forward(layer, x, original=None):
     if bias is not None:
         bias = bias.to(layer.compute_dtype)
     packed = layer.weight.data.view(-1, 1)  # canonical [(N*K+1)//2, 1]
-    return direct.run(NF4LinearFunction, x, packed, layer.weight.quant_state, bias)
+    return linear_project(x, packed, layer.weight.quant_state, bias)
 
 
 class Linear4bit(torch.nn.Module):
@@ -585,7 +617,7 @@ def _generic_forward(layer, x):
     state = layer.weight.quant_state
     bias = layer.bias.to(layer.compute_dtype) if layer.bias is not None else None
     packed = layer.weight.data.view(-1, 1)
-    return NF4LinearFunction.apply(x16, packed, state, bias).to(inp_dtype)
+    return linear_project(x16, packed, state, bias).to(inp_dtype)
 
 
 class LoraLinear4bit(torch.nn.Module):

@@ -11,7 +11,7 @@ first.
 import numpy as np
 import torch
 
-from . import _lib
+from . import _lib, ops
 
 # NF4 code values (QLoRA, arXiv 2305.14314, App. E); the kernels hold the same constants.
 NF4_VALUES = np.array([
@@ -64,6 +64,11 @@ def unpack_nf4(packed, shape, absmax, blocksize, dtype, absmax_8bit=None, code=N
     n_bytes = packed.numel()
     nested = absmax_8bit is not None
     dev = _check_device(packed, absmax, absmax_8bit, code, offset)
+    if out is None and ops.ENABLED:  # the compiled op: checks, allocation and launch in C++
+        if nested:
+            return ops.dequant(packed, shape, dtype, absmax_8bit=absmax_8bit, code=code,
+                               absmax2=absmax, offset=offset)
+        return ops.dequant(packed, shape, dtype, absmax=absmax)
     if out is None:
         out = torch.empty(shape, dtype=dtype, device=dev)
     elif out.dtype != dtype or not out.is_contiguous() or out.numel() != 2 * n_bytes:

@@ -155,8 +155,8 @@ def fused_project(ad, x16):
         y = linear4bit.NF4LoraStreamFunction.apply(x2d, ad.a, ad.b, base, state, bias, keep,
                                                    mask_scale, ad.s)
     else:
-        y = linear4bit.NF4LoraFunction.apply(x2d, ad.a, ad.b, base.weight.data.view(-1, 1),
-                                             state, bias, keep, mask_scale, ad.s)
+        y = linear4bit.lora_project(x2d, ad.a, ad.b, base.weight.data.view(-1, 1), state, bias,
+                                    keep, mask_scale, ad.s)
     return y if x16.dim() == 2 else y.view(*lead, y.shape[-1])
 
 

@@ -85,9 +85,9 @@ def test_matches_original_without_dropout(cuda, monkeypatch, batch, n_tokens, ma
     monkeypatch.setattr(attention, "qkv_rope", lambda *a: calls.append(1) or real(*a))
     attn = _attention(targets=targets).eval()  # LoRA dropout off
     sib = []
-    real_sib = linear4bit.NF4LoraSiblingsFunction.apply
-    monkeypatch.setattr(linear4bit.NF4LoraSiblingsFunction, "apply",
-                        lambda *a: sib.append(1) or real_sib(*a))
+    real_sib = linear4bit.siblings_project
+    monkeypatch.setattr(linear4bit, "siblings_project",
+                        lambda *a, **k: sib.append(1) or real_sib(*a, **k))
     torch.manual_seed(3)
     hidden = torch.randn(batch, n_tokens, HIDDEN, device="cuda")
     cos, sin = _cos_sin(n_tokens)

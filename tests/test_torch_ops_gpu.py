@@ -1,0 +1,263 @@
+"""The compiled operators (torch.ops.mxs_nf4, C++ host side and autograd over the C ABI) on the
+GPU: each against the Python Functions over ctypes, which launch the same kernels in the same
+order, bit for bit (torch.equal on every output and gradient), and against the CPU oracle
+(dequant bit-exact; projections within the north star's 1e-2 max relative error).  Host-side
+argument checks raise before anything is launched."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-2
+S, P = 2.0, 0.05
+
+
+def _layer(dev, n, k, seed, bias=False):
+    from mindxsoup_amd.linear4bit import Linear4bit
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    w = (torch.randn((n, k), device=dev, generator=g) * 0.02).half()
+    b = (torch.randn((n,), device=dev, generator=g) * 0.1).half() if bias else None
+    return Linear4bit.from_weight(w, b)
+
+
+def _w16(layer):
+    st = layer.weight.quant_state
+    q = O.NF4Weight(st.shape, layer.weight.data.view(-1).cpu().numpy(), st.absmax.cpu().numpy(),
+                    st.state2.code.cpu().numpy(), st.state2.absmax.cpu().numpy(),
+                    float(st.offset.item()))
+    return O.dequant(q)
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _inputs(dev, m, k, n, seed, lora_dtype=torch.float32):
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    x = torch.randn((m, k), device=dev, generator=g).half()
+    a = ((torch.rand((16, k), device=dev, generator=g) * 2 - 1) / k ** 0.5).to(lora_dtype)
+    b = (torch.randn((n, 16), device=dev, generator=g) * 0.01).to(lora_dtype)
+    dy = torch.randn((m, n), device=dev, generator=g).half()
+    keep = (torch.rand((m, k), device=dev, generator=g) >= P).to(torch.uint8)
+    return x, a, b, dy, keep
+
+
+def _run(fn, x, a, b, dy, wants=(True, True, True)):
+    """y and the gradients `wants` asks for (x, a, b) of y = fn(x, a, b) under dy."""
+    x, a, b = (t.detach().clone().requires_grad_(w) for t, w in zip((x, a, b), wants))
+    y = fn(x, a, b)
+    leaves = [t for t, w in zip((x, a, b), wants) if w]
+    grads = torch.autograd.grad(y, leaves, dy) if leaves else ()
+    return (y, *grads)
+
+
+def _same(got, want, what):
+    assert len(got) == len(want), what
+    for i, (g_, w_) in enumerate(zip(got, want)):
+        assert g_.dtype == w_.dtype and g_.shape == w_.shape, (what, i, g_.shape, w_.shape)
+        assert torch.equal(g_, w_), f"{what}: output {i} differs"
+
+
+@pytest.mark.parametrize("n,k,m,bias,dropout", [
+    (1536, 1536, 300, True, True), (8960, 1536, 1024, False, True),
+    (1536, 8960, 512, True, True), (256, 1536, 77, True, False), (1536, 1536, 1024, False, True)])
+def test_lora_linear_bits_equal_python_path(cuda, n, k, m, bias, dropout):
+    """lora_linear (one C++ node) and NF4LoraFunction (Python, ctypes): y, dx, dA, dB equal."""
+    from mindxsoup_amd import ops
+    from mindxsoup_amd.linear4bit import NF4LoraFunction
+
+    print(f"case op lora_linear n={n} k={k} m={m} bias={bias} dropout={dropout}", flush=True)
+    layer = _layer(cuda, n, k, 1, bias)
+    st, packed = layer.weight.quant_state, layer.weight.data.view(-1, 1)
+    x, a, b, dy, keep = _inputs(cuda, m, k, n, 2)
+    keep, ms = (keep, 1 / (1 - P)) if dropout else (None, 1.0)
+    got = _run(lambda x_, a_, b_: ops.lora_linear(x_, a_, b_, packed, st, layer.bias, keep, ms,
+                                                  S), x, a, b, dy)
+    assert "NF4LoraFunction" in got[0].grad_fn.name()
+    want = _run(lambda x_, a_, b_: NF4LoraFunction.apply(x_, a_, b_, packed, st, layer.bias,
+                                                         keep, ms, S), x, a, b, dy)
+    _same(got, want, "lora_linear")
+    if n == 1536 and k == 1536 and m == 300:  # and against the oracle
+        w, kp = _w16(layer), (keep.cpu().numpy() if dropout else None)
+        x16, a16, b16 = (_np(t).astype(np.float16) for t in (x, a, b))
+        ref_y = O.lora_fwd(x16, w, a16, b16, S, kp, P if dropout else 0.0,
+                           bias=_np(layer.bias))
+        ref = O.lora_bwd(_np(dy).astype(np.float16), x16, w, a16, b16, S, kp,
+                         P if dropout else 0.0)
+        errs = [O.max_rel(_np(got[0]), ref_y)] + [O.max_rel(_np(g_), r_)
+                                                 for g_, r_ in zip(got[1:], ref)]
+        assert max(errs) < TOL, errs
+
+
+@pytest.mark.parametrize("wants", [(True, False, False), (False, True, True),
+                                   (True, True, False), (False, False, True)])
+def test_lora_linear_partial_wants(cuda, wants):
+    """Frozen LoRA weights or a frozen input: only the wanted gradients, the same bits as the
+    Python Function (which takes the partials route for these)."""
+    from mindxsoup_amd import ops
+    from mindxsoup_amd.linear4bit import NF4LoraFunction
+
+    layer = _layer(cuda, 1536, 1536, 3)
+    st, packed = layer.weight.quant_state, layer.weight.data.view(-1, 1)
+    x, a, b, dy, keep = _inputs(cuda, 1024, 1536, 1536, 4)
+    got = _run(lambda x_, a_, b_: ops.lora_linear(x_, a_, b_, packed, st, None, keep, 1 / (1 - P),
+                                                  S), x, a, b, dy, wants)
+    want = _run(lambda x_, a_, b_: NF4LoraFunction.apply(x_, a_, b_, packed, st, None, keep,
+                                                         1 / (1 - P), S), x, a, b, dy, wants)
+    _same(got, want, f"wants={wants}")
+
+
+def test_lora_linear_nd_input_and_fp16_weights(cuda):
+    """[B, T, K] input with fp16 LoRA weights: output [B, T, N], dx in x's shape, dA / dB back in
+    fp16 -- the Python Function's results reshaped."""
+    from mindxsoup_amd import ops
+    from mindxsoup_amd.linear4bit import NF4LoraFunction
+
+    layer = _layer(cuda, 256, 1536, 5, bias=True)
+    st, packed = layer.weight.quant_state, layer.weight.data.view(-1, 1)
+    x, a, b, dy, keep = _inputs(cuda, 2 * 150, 1536, 256, 6, torch.float16)
+    x3, dy3 = x.view(2, 150, 1536), dy.view(2, 150, 256)
+    got = _run(lambda x_, a_, b_: ops.lora_linear(x_, a_, b_, packed, st, layer.bias, keep,
+                                                  1 / (1 - P), S), x3, a, b, dy3)
+    want = _run(lambda x_, a_, b_: NF4LoraFunction.apply(x_, a_, b_, packed, st, layer.bias,
+                                                         keep, 1 / (1 - P), S), x, a, b, dy)
+    assert got[0].shape == (2, 150, 256) and got[1].shape == (2, 150, 1536)
+    assert got[2].dtype == torch.float16 and got[3].dtype == torch.float16
+    _same([got[0].view(300, 256), got[1].view(300, 1536), got[2], got[3]], list(want), "N-D")
+
+
+@pytest.mark.parametrize("M", [300, 1024])
+@pytest.mark.parametrize("one_gemm", [True, False])
+def test_siblings_bits_equal_python_path(cuda, M, one_gemm):
+    """q, k, v in shared launches: lora_siblings (C++) and NF4LoraSiblingsFunction (Python) give
+    the same outputs, the same summed dx and the same LoRA gradients."""
+    from mindxsoup_amd import ops
+    from mindxsoup_amd.linear4bit import NF4LoraSiblingsFunction, Proj
+
+    print(f"case op lora_siblings M={M} one_gemm={one_gemm}", flush=True)
+    shapes = [(1536, 1536), (256, 1536), (256, 1536)]
+    layers = [_layer(cuda, n, k, 10 + i, bias=True) for i, (n, k) in enumerate(shapes)]
+    g = torch.Generator(device=cuda)
+    g.manual_seed(7)
+    x = torch.randn((M, 1536), device=cuda, generator=g).half()
+    projs, a_s, b_s = [], [], []
+    for lyr in layers:
+        n, k = lyr.weight.quant_state.shape
+        a_s.append((torch.rand((16, k), device=cuda, generator=g) * 2 - 1) / k ** 0.5)
+        b_s.append(torch.randn((n, 16), device=cuda, generator=g) * 0.01)
+        keep = (torch.rand((M, k), device=cuda, generator=g) >= P).to(torch.uint8)
+        projs.append(Proj(lyr.weight.data.view(-1, 1), lyr.weight.quant_state, lyr.bias, keep,
+                          1 / (1 - P), S))
+    dys = [torch.randn((M, n), device=cuda, generator=g).half() for n, _ in shapes]
+
+    def run(fn):
+        xl = x.clone().requires_grad_(True)
+        al = [t.clone().requires_grad_(True) for t in a_s]
+        bl = [t.clone().requires_grad_(True) for t in b_s]
+        ys = fn(xl, al, bl)
+        return [*ys, *torch.autograd.grad(ys, [xl, *al, *bl], dys)]
+
+    got = run(lambda x_, a_, b_: ops.lora_siblings(x_, projs, a_, b_, one_gemm))
+    ab = lambda a_, b_: [t for pair in zip(a_, b_) for t in pair]  # noqa: E731
+    want = run(lambda x_, a_, b_: NF4LoraSiblingsFunction.apply(x_, tuple(projs), one_gemm,
+                                                                *ab(a_, b_)))
+    _same(got, want, "lora_siblings")
+
+
+def test_linear_bits_equal_python_path(cuda):
+    """The base projection (no LoRA): linear (C++) and NF4LinearFunction, [B, T, K] input with
+    bias, y and dx equal; and the oracle's dequant-then-matmul within 1e-2."""
+    from mindxsoup_amd import ops
+    from mindxsoup_amd.linear4bit import NF4LinearFunction
+
+    layer = _layer(cuda, 8960, 1536, 8, bias=True)
+    st, packed = layer.weight.quant_state, layer.weight.data.view(-1, 1)
+    x = torch.randn((2, 200, 1536), device=cuda).half()
+    dy = torch.randn((2, 200, 8960), device=cuda).half()
+
+    def run(fn):
+        xl = x.clone().requires_grad_(True)
+        y = fn(xl)
+        return [y, *torch.autograd.grad(y, [xl], dy)]
+
+    got = run(lambda x_: ops.linear(x_, packed, st, layer.bias))
+    want = run(lambda x_: NF4LinearFunction.apply(x_, packed, st, layer.bias))
+    _same(got, want, "linear")
+    w = _w16(layer)
+    x16 = _np(x).reshape(-1, 1536).astype(np.float16)
+    assert O.max_rel(_np(got[0]).reshape(-1, 8960), O.linear_fwd(x16, w, _np(layer.bias))) < TOL
+
+
+def test_dequant_op_bit_exact(cuda):
+    """dequant (C++): nested scales and fp32 absmax, fp16 and fp32 outputs, bit-equal to the
+    oracle's decode and to the ctypes path."""
+    from mindxsoup_amd import nf4, ops
+
+    rng = np.random.default_rng(9)
+    q = O.quantize((rng.standard_normal((1536, 1536)) * 0.02).astype(np.float16))
+    t = lambda a_: torch.from_numpy(np.ascontiguousarray(a_)).to(cuda)  # noqa: E731
+    off = torch.tensor([q.offset], dtype=torch.float32, device=cuda)
+    want = O.dequant(q)
+    got = ops.dequant(t(q.packed), q.shape, torch.float16, absmax_8bit=t(q.absmax8),
+                      code=t(q.code), absmax2=t(q.absmax2), offset=off)
+    assert np.array_equal(got.cpu().numpy().view(np.int16), want.view(np.int16))
+    got32 = ops.dequant(t(q.packed), q.shape, torch.float32, absmax_8bit=t(q.absmax8),
+                        code=t(q.code), absmax2=t(q.absmax2), offset=off)
+    ctypes_path = nf4.unpack_nf4(t(q.packed), q.shape, t(q.absmax2), 64, torch.float32,
+                                 absmax_8bit=t(q.absmax8), code=t(q.code), offset=off,
+                                 out=torch.empty(q.shape, dtype=torch.float32, device=cuda))
+    assert torch.equal(got32, ctypes_path)
+    flat = ops.dequant(t(q.packed), q.shape, torch.float16, absmax=t(q.absmax_f32))
+    want_flat = O.dequant(packed=q.packed, absmax_f32=q.absmax_f32, shape=q.shape)
+    assert np.array_equal(flat.cpu().numpy().view(np.int16), want_flat.view(np.int16))
+
+
+def test_host_checks_raise(cuda):
+    """Shapes, dtypes and devices the kernels cannot take are refused on the host, by name."""
+    from mindxsoup_amd import ops
+
+    layer = _layer(cuda, 256, 1536, 11)
+    st, packed = layer.weight.quant_state, layer.weight.data.view(-1, 1)
+    x, a, b, _, keep = _inputs(cuda, 64, 1536, 256, 12)
+    with pytest.raises(RuntimeError, match="x must be fp16"):
+        ops.lora_linear(x.float(), a, b, packed, st, None, None, 1.0, S)
+    with pytest.raises(RuntimeError, match="keep must be a uint8"):
+        ops.lora_linear(x, a, b, packed, st, None, keep[:32], 1.0, S)
+    with pytest.raises(RuntimeError, match="packed must be contiguous uint8"):
+        ops.lora_linear(x, a, b, packed[: packed.numel() // 2], st, None, None, 1.0, S)
+    with pytest.raises(RuntimeError, match="lora_a must be"):
+        ops.lora_linear(x, a[:, :768], b, packed, st, None, None, 1.0, S)
+    with pytest.raises(RuntimeError, match="must be on"):
+        ops.lora_linear(x, a.cpu(), b, packed, st, None, None, 1.0, S)
+    with pytest.raises(RuntimeError, match="multiples of 64"):
+        ops.linear(x[:, :1500].contiguous(), packed, st, None)
+
+
+def test_modules_take_the_ops(cuda, monkeypatch):
+    """With ops.ENABLED (FEATURES["torch_ops"]) a LoRA layer's projection is one C++ node; with
+    it off, the Python Function: the same bits either way."""
+    from mindxsoup_amd import ops
+    from mindxsoup_amd.linear4bit import LoraLinear4bit
+
+    layer = LoraLinear4bit(_layer(cuda, 1536, 1536, 13, bias=True)).train()
+    torch.nn.init.normal_(layer.lora_B["default"].weight, std=0.02)
+    x, _, _, dy, keep = _inputs(cuda, 300, 1536, 1536, 14)
+    outs = {}
+    for enabled in (True, False):
+        monkeypatch.setattr(ops, "ENABLED", enabled)
+        layer.zero_grad(set_to_none=True)
+        layer.next_keep = keep
+        xl = x.clone().requires_grad_(True)
+        y = layer(xl)
+        assert (type(y.grad_fn).__name__ == "CppFunction") == enabled
+        y.backward(dy)
+        outs[enabled] = [y, xl.grad, layer.lora_A["default"].weight.grad,
+                         layer.lora_B["default"].weight.grad]
+    _same(outs[True], outs[False], "module")
