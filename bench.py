@@ -353,6 +353,34 @@ def autograd_step(alayers):
     return torch.autograd.grad(outs, leaves, dys)
 
 
+def stack_layers(dev, g):
+    """The 28 layers' projections: q/k/v share one activation, gate/up
+    another, o and down have their own; inputs resident before any timing."""
+    layers = []
+    for _ in range(LAYERS):
+        x_attn = torch.randn((M_TOKENS, 1536), device=dev, generator=g).half()
+        x_mlp = torch.randn((M_TOKENS, 1536), device=dev, generator=g).half()
+        projs = []
+        for name, n, k in PROJ:
+            x = x_attn if name in ("q", "k", "v") else x_mlp if name in ("gate", "up") else None
+            projs.append(make_proj(dev, g, n, k, x=x))
+        layers.append(projs)
+    torch.cuda.synchronize()
+    print("bench: projection stack inputs resident", file=sys.stderr, flush=True)
+    return layers
+
+
+def stack_step(layers):
+    """One step of the stack: every layer's forward, then every layer's backward in reverse."""
+    def step():
+        saved = []
+        for projs in layers:
+            saved.append(layer_fwd(projs)[1])
+        for projs, hts in zip(reversed(layers), reversed(saved)):
+            layer_bwd(projs, hts)
+    return step
+
+
 def graph_time(fn, steps, warmup):
     """Capture fn() in a HIP graph, replay: mean ms per replay (events on the capture stream's
     replay stream) and the wall-clock mean."""
@@ -657,24 +685,8 @@ def bench_fused(dev, steps, warmup):
     out["qkv_rope"] = bench_qkv_rope(dev, g, steps, warmup)
     out["stream_weights"] = bench_stream(dev, g, max(5, steps // 4), max(2, warmup // 4))
     # config 5: forward + backward of all 28 layers x 7 projections, M = 1024
-    layers = []
-    for _ in range(LAYERS):
-        x_attn = torch.randn((M_TOKENS, 1536), device=dev, generator=g).half()
-        x_mlp = torch.randn((M_TOKENS, 1536), device=dev, generator=g).half()
-        projs = []
-        for name, n, k in PROJ:
-            x = x_attn if name in ("q", "k", "v") else x_mlp if name in ("gate", "up") else None
-            projs.append(make_proj(dev, g, n, k, x=x))
-        layers.append(projs)
-    torch.cuda.synchronize()
-    print("bench: projection stack inputs resident", file=sys.stderr, flush=True)
-
-    def step():
-        saved = []
-        for projs in layers:
-            saved.append(layer_fwd(projs)[1])
-        for projs, hts in zip(reversed(layers), reversed(saved)):
-            layer_bwd(projs, hts)
+    layers = stack_layers(dev, g)
+    step = stack_step(layers)
 
     def step_ungrouped():  # each projection's LoRA row products in launches of their own
         saved = []
@@ -858,6 +870,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=M_TOKENS, help="M for --kernel")
     ap.add_argument("--cfg", type=int, default=-1, help="tile configuration for --kernel")
     ap.add_argument("--splits", type=int, default=1, help="split-K for --kernel with --cfg")
+    ap.add_argument("--stack", action="store_true",
+                    help="only the 28-layer projection stack as one HIP graph: one eager step, "
+                         "then --warmup and --steps replays (its JSON on stdout)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the hot path is "
@@ -872,6 +887,15 @@ def main():
     if args.kernel:
         print(json.dumps(bench_kernel(dev, args.kernel, args.tokens, args.steps, args.warmup,
                                       args.cfg, args.splits)), flush=True)
+        return
+    if args.stack:
+        g = torch.Generator(device=dev)
+        g.manual_seed(1)
+        ms, wall = graph_time(stack_step(stack_layers(dev, g)), args.steps, args.warmup)
+        fl = LAYERS * sum(proj_flops(n, k) for _, n, k in PROJ)
+        print(json.dumps({"config5_stack": {"ms_per_step": round(ms, 4),
+                                            "wall_ms_per_step": round(wall, 4),
+                                            "tflops": round(fl / ms / 1e9, 1)}}), flush=True)
         return
     if args.stream:
         g = torch.Generator(device=dev)
