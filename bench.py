@@ -259,6 +259,9 @@ def proj_bwd(p, saved, s=ALPHA / RANK):
 # the model produces together (q/k/v from attention's backward, gate/up from the SwiGLU's).
 FWD_GROUPS = [(0, 1, 2), (3,), (4, 5), (6,)]
 BWD_GROUPS = [(6,), (5, 4), (3,), (2, 1, 0)]
+# gate and up read one input: their input gradients, which a model adds, come from one summed
+# launch (the summed dX GEMM); q/k/v's stay separate here, as this step has no consumer for them
+SUM_DX_GROUPS = [(5, 4)]
 
 
 def layer_fwd(projs, s=ALPHA / RANK):
@@ -293,8 +296,9 @@ def layer_fwd(projs, s=ALPHA / RANK):
 
 def layer_bwd(projs, saved, s=ALPHA / RANK):
     """Backward of one layer's 7 projections in reverse order; each group's small launches
-    (dHs, dA / dB) and the v/k/q dX GEMMs shared (linear4bit.lora_backward_group).  Returns
-    each projection's (dX, dA, dB)."""
+    (dHs, dA / dB) and the v/k/q dX GEMMs shared, gate's and up's dX summed by one launch
+    (linear4bit.lora_backward_group).  Returns each projection's (dX, dA, dB) (up's dX is the
+    sum, gate's None)."""
     from mindxsoup_amd.linear4bit import lora_backward_group
 
     grads = [None] * len(projs)
@@ -304,7 +308,7 @@ def layer_bwd(projs, saved, s=ALPHA / RANK):
                                         bt=saved[i][2], packed=projs[i]["packed"],
                                         state=projs[i]["st"], mask_scale=1.0 / (1.0 - P_DROP),
                                         s=s, wants=(True, True, True)) for i in grp],
-                                  ws=projs[grp[0]]["ws"])
+                                  ws=projs[grp[0]]["ws"], sum_dx=grp in SUM_DX_GROUPS)
         for i, r in zip(grp, res):
             grads[i] = r
     return grads

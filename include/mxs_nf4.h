@@ -185,6 +185,34 @@ int mxs_nf4_linear_bwd_dx_hp(const void* dy, int M, int N, int K, const void* pa
                              void* lora_dht, void* dx, void* workspace, int cfg, int splits,
                              hipStream_t stream);
 
+/* The input gradient of two projections that read the same input, summed: dX = dX_0 + dX_1
+ * with dX_i = dY_i . W_i + mask_i * mask_scale * (fp16(sum of lora_dhp_i) . lora_at_i^T), as
+ * mxs_nf4_linear_bwd_dx_hp computes each.  These are the gate and up projections of the MLP
+ * (solution/mlp.py:42-43), whose input gradients autograd adds for their shared input.  ONE
+ * launch of the split-K kernel runs both reductions (each split two ways) and one reduce adds
+ * the four fp32 partial planes in order, so neither dX_i is rounded to fp16 on its own; the
+ * result equals the fp32 sum of the two GEMMs rounded once.  Arrays hold the per-projection
+ * arguments (N[i] = out_features; mask and lora_dht may be NULL, or any entry); the two share
+ * M, K, r, ldt, hp_slices and mask_scale.  workspace: at least
+ * mxs_nf4_linear_bwd_dx_pair_workspace_bytes(M, N[0], N[1], K) bytes.  Only where
+ * mxs_nf4_linear_bwd_dx_pair_ok(M, N[0], N[1], K) is 1 (both projections plan the narrow-output
+ * split-K kernel on their own), else MXS_ERR_SIZE. */
+int mxs_nf4_linear_bwd_dx_hp_pair(const void* const dy[2], int M, const int N[2], int K,
+                                  const void* const packed[2], const void* const absmax8[2],
+                                  const float* const code[2], const float* const absmax2[2],
+                                  const float* const offset[2], const float* const lora_dhp[2],
+                                  int hp_slices, int ldt, const void* const lora_at[2], int r,
+                                  const void* const mask[2], float mask_scale,
+                                  void* const lora_dht[2], void* dx, void* workspace,
+                                  hipStream_t stream);
+
+/* 1 when mxs_nf4_linear_bwd_dx_hp_pair takes two projections [K -> N0] and [K -> N1] at M
+ * tokens, else 0. */
+int mxs_nf4_linear_bwd_dx_pair_ok(int M, int N0, int N1, int K);
+
+/* Workspace bytes of mxs_nf4_linear_bwd_dx_hp_pair (0 where it does not apply). */
+int64_t mxs_nf4_linear_bwd_dx_pair_workspace_bytes(int M, int N0, int N1, int K);
+
 /* ---- LoRA side branch (peft lora.Linear around the 4-bit base, r % 16 == 0, r <= 128) ------
  * The transposed outputs/inputs (ht, dht) are fp16 [r, ldt] with ldt >= M, ldt % 8 == 0 (columns
  * past M hold zeros).  Results are deterministic (fixed summation order).  `workspace` may be

@@ -82,12 +82,17 @@ _SIGNATURES = {
     "mxs_nf4_linear_bwd_dx_hp": [P, I32, I32, I32, P, P, P, P, P, P, I32, I32, P, I32, P, F32, P,
                                  P, P, I32, I32, P],
     "mxs_transpose_f16": [P, I32, I32, P, P],
+    "mxs_nf4_linear_bwd_dx_hp_pair": [P, I32, P, I32, P, P, P, P, P, P, I32, I32, P, I32, P, F32,
+                                      P, P, P, P],
+    "mxs_nf4_linear_bwd_dx_pair_ok": [I32, I32, I32, I32],
+    "mxs_nf4_linear_bwd_dx_pair_workspace_bytes": [I32, I32, I32, I32],
 }
 
 
 _RESTYPES = {"mxs_nf4_dequant_layer_plan": ctypes.c_int64,
              "mxs_nf4_gemm_workspace_bytes": ctypes.c_int64,
-             "mxs_lora_workspace_bytes": ctypes.c_int64}
+             "mxs_lora_workspace_bytes": ctypes.c_int64,
+             "mxs_nf4_linear_bwd_dx_pair_workspace_bytes": ctypes.c_int64}
 
 
 def lib():

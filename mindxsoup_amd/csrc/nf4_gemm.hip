@@ -57,6 +57,8 @@ struct GemmArgs {
   int64_t ldc;
   float* ws;                // split-K partials [splits, M, Nc]
   int steps_per_split;
+  int zf;                   // grid z of this problem's first split (0, or the second problem's
+                            // first plane in a launch of two, k_nf4_gemm_ws_pair)
   // backward: the LoRA gradients dA (cp0) and dB (cp1), computed by cols_blocks extra
   // workgroups of the same launch in grid rows past the GEMM's (0: none).  They depend on
   // nothing the GEMM tiles write, so they run on the CUs the tiles leave idle.
@@ -139,7 +141,7 @@ struct AccStart {
 
   __device__ __forceinline__ void load(const GemmArgs& a, int nb, int lseg) {
     if constexpr (kBiasPre) {
-      if (blockIdx.z == 0 && a.bias) {
+      if ((int)blockIdx.z == a.zf && a.bias) {
 #pragma unroll
         for (int j = 0; j < TN; j++)
 #pragma unroll
@@ -152,7 +154,7 @@ struct AccStart {
   __device__ __forceinline__ float16_t base(const GemmArgs& a, int j, int nb, int lseg) const {
     float16_t c = {};
     if constexpr (!BWD) {
-      if (blockIdx.z == 0 && a.bias) {
+      if ((int)blockIdx.z == a.zf && a.bias) {
 #pragma unroll
         for (int g = 0; g < 4; g++) {
           half4_t b;
@@ -218,7 +220,7 @@ struct AccStart {
                                          int nb, int lrow, int lseg, int wr0, int wc0,
                                          const _Float16* ls = nullptr, int ls_cols = 0,
                                          const uint8_t* kls = nullptr, int kst = 0) {
-    if (blockIdx.z != 0 || !(a.lora_h || a.lora_hp)) {
+    if ((int)blockIdx.z != a.zf || !(a.lora_h || a.lora_hp)) {
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -935,7 +937,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void k_nf4_gemm(GemmArgs a)
   const int m0 = blockIdx.y * BM;
   const int n0 = blockIdx.x * BN;
   const int n_steps = a.Kr / kBK;
-  const int kt0 = blockIdx.z * a.steps_per_split;
+  const int kt0 = ((int)blockIdx.z - a.zf) * a.steps_per_split;
   const int kt1 = min(n_steps, kt0 + a.steps_per_split);
   const int lrow = lane & 31;
   const int lseg = lane >> 5;
@@ -1503,7 +1505,8 @@ constexpr bool consumer_copies() {
 // MFMAs or by the producers (consumer_copies).  Everything issued in one K-step is waited for
 // at the start of the next, and one workgroup barrier per K-step hands the buffers over.  Wave
 // roles are uniform branches, so neither side's registers live through the other's code.
-// One output tile (bx, by) of the warp-specialized GEMM; split index blockIdx.z.
+// One output tile (bx, by) of the warp-specialized GEMM; split index blockIdx.z - a.zf, partial
+// plane blockIdx.z.
 template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU>
 __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
   constexpr int WM = BM / CWM, WN = BN / CWN, TM = WM / 32, TN = WN / 32;
@@ -1532,10 +1535,10 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
   const int m0 = by * BM;
   const int n0 = bx * BN;
   const int n_steps = a.Kr / kBK;
-  const int kt0 = blockIdx.z * a.steps_per_split;
+  const int kt0 = ((int)blockIdx.z - a.zf) * a.steps_per_split;
   const int kt1 = min(n_steps, kt0 + a.steps_per_split);
   // the producers stage the LoRA operands (r = 16) and the keep mask in LDS for the consumers
-  const bool lora = blockIdx.z == 0 && (a.lora_hp || a.lora_h);
+  const bool lora = (int)blockIdx.z == a.zf && (a.lora_hp || a.lora_h);
   const bool lora16 = lora && a.r == 16;
   const bool kmask = BWD && lora && a.mask;
   // wave index as a scalar: the producer / consumer split below is a uniform branch, so neither
@@ -2167,6 +2170,77 @@ static int launch_ws_group(const GemmArgs* probs, int n, hipStream_t stream) {
   return e == hipSuccess ? MXS_OK : (int)e;
 }
 
+// Two problems of one output shape whose results are added (the gate and up projections' input
+// gradients: autograd sums them for the shared input) in ONE launch of the split-K kernel:
+// problem 0 owns grid z [0, sp), problem 1 [sp, 2 sp), each splitting its own reduction over
+// its z range; every split writes its fp32 partial plane (the plane index is the grid z) and
+// one reduce adds all 2 sp planes in order.  So neither projection's output is rounded to fp16
+// on its own, and the pair costs one launch and one reduce instead of two of each.
+struct GemmPair {
+  GemmArgs p[2];
+};
+
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS>
+__global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws_pair(GemmPair g) {
+  const int i = (int)blockIdx.z < g.p[1].zf ? 0 : 1;
+  ws_tile<BM, BN, CWM, CWN, BWD, PW, NS, false>(g.p[i], (int)blockIdx.x, (int)blockIdx.y);
+}
+
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS>
+static int launch_ws_pair(const GemmArgs& a0, const GemmArgs& a1, int sp, hipStream_t stream) {
+  if (sp < 1 || !a0.ws || a0.M != a1.M || a0.Nc != a1.Nc) return MXS_ERR_ARG;
+  GemmPair g{};
+  g.p[0] = a0;
+  g.p[1] = a1;
+  for (int i = 0; i < 2; i++) {
+    GemmArgs& a = g.p[i];
+    // the conditions under which launch_ws would keep this kernel; no fallback here
+    if ((int64_t)a.Nc * a.Kr >= (int64_t(1) << 32) || (int64_t)BM * a.lda * 2 >= (int64_t(1) << 32) ||
+        (BWD && a.Nc < (PW == 8 ? 16 : 32)) || a.glu || a.cols_blocks > 0)
+      return MXS_ERR_SIZE;
+    const int n_steps = a.Kr / kBK;
+    a.steps_per_split = (n_steps + sp - 1) / sp;
+    // every split of the z range has K-steps: its plane is written
+    if (n_steps < sp || (n_steps + a.steps_per_split - 1) / a.steps_per_split != sp)
+      return MXS_ERR_SIZE;
+    a.zf = i * sp;
+    a.ws = a0.ws;
+  }
+  const dim3 grid((a0.Nc + BN - 1) / BN, (a0.M + BM - 1) / BM, 2 * sp);
+  const size_t lds = (size_t)ws_lds_halfs<BM, BN, BWD>() * sizeof(_Float16);
+  static bool lds_set = false;  // idempotent attribute; a benign race between threads
+  if (!lds_set) {
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&k_nf4_gemm_ws_pair<BM, BN, CWM, CWN, BWD, PW, NS>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+    lds_set = true;
+  }
+  hipLaunchKernelGGL((k_nf4_gemm_ws_pair<BM, BN, CWM, CWN, BWD, PW, NS>), grid,
+                     dim3(64 * (4 + PW)), lds, stream, g);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  return launch_reduce(g.p[0], 2 * sp, stream);
+}
+
+// The pair's plan: both problems must plan the 256x96 split backward kernel (cfg 11) on their
+// own; the pair then splits each reduction kPairSplits ways.
+constexpr int kPairSplits = 2;
+
+static bool pair_plan_ok(int M, int N0, int N1, int K) {
+  if (M <= 0 || K <= 0 || N0 <= 0 || N1 <= 0 || N0 % kBK || N1 % kBK || K % kBK) return false;
+  for (int n : {N0, N1}) {
+    int cfg, sp;
+    choose(M, K, n, true, &cfg, &sp);
+    if (cfg != 11 || sp == 1) return false;
+    if ((int64_t)K * n >= (int64_t(1) << 32) || (int64_t)256 * n * 2 >= (int64_t(1) << 32))
+      return false;
+    const int steps = n / kBK, sps = (steps + kPairSplits - 1) / kPairSplits;
+    if (steps < kPairSplits || (steps + sps - 1) / sps != kPairSplits) return false;
+  }
+  return true;
+}
+
 // The arguments of a dX GEMM whose launch also computes the LoRA gradients (its workgroups past
 // the tiles): the gradients' checks (mxs_lora_grads); the GEMM's follow in check_gemm.
 static int dx_grads_args(const void* dy, int M, int N, int K, const void* packed,
@@ -2471,6 +2545,62 @@ int mxs_nf4_linear_bwd_dx_hp(const void* dy, int M, int N, int K, const void* pa
   a.ldc = K;
   set_workspace(a, workspace);
   return gemm_entry(true, a, cfg, splits, stream);
+}
+
+int mxs_nf4_linear_bwd_dx_pair_ok(int M, int N0, int N1, int K) {
+  return pair_plan_ok(M, N0, N1, K) ? 1 : 0;
+}
+
+int64_t mxs_nf4_linear_bwd_dx_pair_workspace_bytes(int M, int N0, int N1, int K) {
+  if (!pair_plan_ok(M, N0, N1, K)) return 0;
+  return (int64_t)2 * kPairSplits * M * K * (int64_t)sizeof(float);
+}
+
+int mxs_nf4_linear_bwd_dx_hp_pair(const void* const dy[2], int M, const int N[2], int K,
+                                  const void* const packed[2], const void* const absmax8[2],
+                                  const float* const code[2], const float* const absmax2[2],
+                                  const float* const offset[2], const float* const lora_dhp[2],
+                                  int hp_slices, int ldt, const void* const lora_at[2], int r,
+                                  const void* const mask[2], float mask_scale,
+                                  void* const lora_dht[2], void* dx, void* workspace,
+                                  hipStream_t stream) {
+  if (M < 0 || !dy || !N || !packed || !absmax8 || !code || !absmax2 || !offset || !lora_dhp ||
+      !lora_at)
+    return MXS_ERR_ARG;
+  if (M == 0) return MXS_OK;
+  if (!pair_plan_ok(M, N[0], N[1], K)) return MXS_ERR_SIZE;
+  if (!workspace) return MXS_ERR_ARG;
+  GemmArgs p[2];
+  for (int i = 0; i < 2; i++) {
+    GemmArgs a{};
+    a.A = static_cast<const _Float16*>(dy[i]);
+    a.lda = N[i];
+    a.packed = static_cast<const uint8_t*>(packed[i]);
+    a.absmax8 = static_cast<const uint8_t*>(absmax8[i]);
+    a.code = code[i];
+    a.absmax2 = absmax2[i];
+    a.offset = offset[i];
+    a.M = M;
+    a.Nc = K;
+    a.Kr = N[i];
+    a.Kw = K;
+    a.lora_hp = lora_dhp[i];
+    a.hp_slices = hp_slices;
+    a.ldt = ldt;
+    a.lora_ht = lora_dht ? static_cast<_Float16*>(lora_dht[i]) : nullptr;
+    a.lora_w = static_cast<const _Float16*>(lora_at[i]);
+    a.r = r;
+    a.mask = mask ? static_cast<const uint8_t*>(mask[i]) : nullptr;
+    a.mask_scale = mask_scale;
+    a.C = static_cast<_Float16*>(dx);
+    a.ldc = K;
+    set_workspace(a, workspace);
+    if (!a.lora_hp) return MXS_ERR_ARG;
+    const int c = check_gemm(true, a);
+    if (c != MXS_OK) return c == 1 ? MXS_OK : c;
+    p[i] = a;
+  }
+  return launch_ws_pair<256, 96, 4, 1, true, 8, 5>(p[0], p[1], kPairSplits, stream);
 }
 
 int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, const int N[],

@@ -608,12 +608,14 @@ using Lists3 = std::tuple<std::vector<Tensor>, std::vector<Tensor>, std::vector<
 // weight gradients in one launch where mxs_nf4_linear_bwd_dx_grads_group_ok allows, else each;
 // the others' dX GEMMs, then their dA / dB in one launch when all are wanted and the shapes are
 // equal.  wants: 3 per projection (dx, dA, dB).  Returns (dxs, das, dbs), undefined where not
-// wanted; the bits of lora_bwd on each.
+// wanted; the bits of lora_bwd on each.  sum_dx: dxs[0] is the sum of the projections' input
+// gradients (added in order; the others undefined), and two projections that
+// mxs_nf4_linear_bwd_dx_hp_pair takes (gate and up) get it from that one summed launch.
 Lists3 lora_bwd_group_cuda(TensorList dy, const Tensor& x, const OptTensorList& keep,
                            TensorList ht, TensorList at_, TensorList bt, TensorList packed,
                            TensorList absmax8, TensorList code, TensorList absmax2,
                            TensorList offset, double mask_scale, double s,
-                           at::IntArrayRef wants) {
+                           at::IntArrayRef wants, bool sum_dx) {
   const size_t n = dy.size();
   check_group(n, {ht.size(), at_.size(), bt.size(), packed.size(), absmax8.size(), code.size(),
                   absmax2.size(), offset.size()});
@@ -727,10 +729,45 @@ Lists3 lora_bwd_group_cuda(TensorList dy, const Tensor& x, const OptTensorList& 
   if (!grouped)
     for (size_t i : fin) bwd_finished(o[i], dh[i], dht[i], ms, dxs[i], das[i], dbs[i], ws, st);
 
-  // the "partials" projections: each dX GEMM, then the weight gradients
+  // the "partials" projections: each dX GEMM (or, summed, both in one launch), then the weight
+  // gradients
   std::vector<size_t> both;
   std::vector<Tensor> pend_dht(n);
+  const bool pair = sum_dx && n == 2 && fin.empty() && par.size() == 2 && want(0, 0) &&
+                    want(1, 0) && dhp[0].size(0) == dhp[1].size(0) &&
+                    mxs_nf4_linear_bwd_dx_pair_ok(M, o[0].N, o[1].N, K) != 0;
+  if (pair) {
+    const bool wt = want(0, 1) || want(0, 2) || want(1, 1) || want(1, 2);
+    std::array<const void*, 2> pdy{}, pk{}, pa8{}, pat{}, pm{};
+    std::array<const float*, 2> pc{}, pa2{}, po{}, php{};
+    std::array<void*, 2> pdht{};
+    std::array<int, 2> Ns{};
+    for (size_t i = 0; i < 2; ++i) {
+      if (wt) pend_dht[i] = at::empty({r, ldt}, f16);
+      pdy[i] = o[i].dy.data_ptr();
+      pk[i] = o[i].w.packed;
+      pa8[i] = o[i].w.absmax8;
+      pc[i] = o[i].w.code;
+      pa2[i] = o[i].w.absmax2;
+      po[i] = o[i].w.offset;
+      php[i] = dhp[i].data_ptr<float>();
+      pat[i] = o[i].at.data_ptr();
+      pm[i] = ptr(o[i].mask);
+      pdht[i] = ptr(pend_dht[i]);
+      Ns[i] = o[i].N;
+      if (want(i, 1) && want(i, 2)) both.push_back(i);
+    }
+    dxs[0] = at::empty({M, K}, f16);
+    const Tensor pws =
+        workspace(mxs_nf4_linear_bwd_dx_pair_workspace_bytes(M, Ns[0], Ns[1], K), o[0].x);
+    ok(mxs_nf4_linear_bwd_dx_hp_pair(pdy.data(), M, Ns.data(), K, pk.data(), pa8.data(),
+                                     pc.data(), pa2.data(), po.data(), php.data(),
+                                     (int)dhp[0].size(0), ldt, pat.data(), r, pm.data(), ms,
+                                     pdht.data(), dxs[0].data_ptr(), ptr(pws), st),
+       "mxs_nf4_linear_bwd_dx_hp_pair");
+  }
   for (size_t i : par) {
+    if (pair) break;
     const bool wa = want(i, 1), wb = want(i, 2), wg = wa || wb;
     dxs[i] = at::empty({M, K}, f16);
     if (wg) pend_dht[i] = at::empty({r, ldt}, f16);
@@ -778,17 +815,30 @@ Lists3 lora_bwd_group_cuda(TensorList dy, const Tensor& x, const OptTensorList& 
                       ptr<float>(dbs[i]), nullptr, st),
        "mxs_lora_grads");
   }
+  if (sum_dx && !pair) {  // in order, as autograd would add them
+    Tensor sum;
+    for (size_t i = 0; i < n; ++i) {
+      if (!dxs[i].defined()) continue;
+      sum = sum.defined() ? sum.add_(dxs[i]) : dxs[i];
+      dxs[i] = Tensor();
+    }
+    dxs[0] = sum;
+  }
   return {dxs, das, dbs};
 }
 
 Lists3 lora_bwd_group_meta(TensorList dy, const Tensor& x, const OptTensorList&, TensorList,
                            TensorList, TensorList bt, TensorList, TensorList, TensorList,
-                           TensorList, TensorList, double, double, at::IntArrayRef wants) {
+                           TensorList, TensorList, double, double, at::IntArrayRef wants,
+                           bool sum_dx) {
   const int64_t M = x.size(0), K = x.size(1);
   std::vector<Tensor> dxs, das, dbs;
+  bool any_x = false;
+  for (size_t i = 0; i < dy.size(); ++i) any_x = any_x || wants[3 * i];
   for (size_t i = 0; i < dy.size(); ++i) {
     const int64_t N = dy[i].size(1), r = bt[i].size(0);
-    dxs.push_back(wants[3 * i] ? at::empty({M, K}, x.options().dtype(at::kHalf)) : Tensor());
+    const bool wx = sum_dx ? (i == 0 && any_x) : wants[3 * i] != 0;
+    dxs.push_back(wx ? at::empty({M, K}, x.options().dtype(at::kHalf)) : Tensor());
     das.push_back(wants[3 * i + 1] ? at::empty({r, K}, x.options().dtype(at::kFloat))
                                    : Tensor());
     dbs.push_back(wants[3 * i + 2] ? at::empty({N, r}, x.options().dtype(at::kFloat))
@@ -928,7 +978,7 @@ using GroupFwdSig = Lists4(const Tensor&, TensorList, TensorList, TensorList, Te
                            const OptTensorList&, double, double, bool);
 using GroupBwdSig = Lists3(TensorList, const Tensor&, const OptTensorList&, TensorList,
                            TensorList, TensorList, TensorList, TensorList, TensorList,
-                           TensorList, TensorList, double, double, at::IntArrayRef);
+                           TensorList, TensorList, double, double, at::IntArrayRef, bool);
 
 // n NF4 + LoRA projections reading one input x fp16 [M, K] (a layer's q/k/v, or gate/up),
 // their launches shared (NF4LoraSiblingsFunction of the Python package): outputs fp16 [M, N_i];
@@ -998,14 +1048,10 @@ struct NF4LoraSiblingsFunction : public torch::autograd::Function<NF4LoraSibling
       std::tie(dxs, das, dbs) =
           bwd.call(dys, x, keep, slice(0), slice(1), slice(2), slice(3), slice(4), slice(5),
                    slice(6), slice(7), ctx->saved_data["mask_scale"].toDouble(),
-                   ctx->saved_data["s"].toDouble(), wants);
+                   ctx->saved_data["s"].toDouble(), wants, true);
     }
     variable_list out(7 * n + 6);
-    if (ctx->needs_input_grad(0)) {
-      Tensor dx = dxs[0];
-      for (int64_t i = 1; i < n; ++i) dx = dx.add_(dxs[i]);
-      out[0] = dx;
-    }
+    if (ctx->needs_input_grad(0)) out[0] = dxs[0];
     for (int64_t i = 0; i < n; ++i) {
       out[1 + i] = as_dtype(das[i], static_cast<at::ScalarType>(dts[2 * i]));
       out[1 + n + i] = as_dtype(dbs[i], static_cast<at::ScalarType>(dts[2 * i + 1]));
@@ -1077,7 +1123,7 @@ TORCH_LIBRARY(mxs_nf4, m) {
         "-> (Tensor[], Tensor[], Tensor[], Tensor[])");
   m.def("lora_bwd_group(Tensor[] dy, Tensor x, Tensor?[] keep, Tensor[] ht, Tensor[] at, "
         "Tensor[] bt, Tensor[] packed, Tensor[] absmax8, Tensor[] code, Tensor[] absmax2, "
-        "Tensor[] offset, float mask_scale, float s, int[] wants) "
+        "Tensor[] offset, float mask_scale, float s, int[] wants, bool sum_dx=False) "
         "-> (Tensor[], Tensor[], Tensor[])");
   m.def("linear(Tensor x, Tensor packed, Tensor absmax8, Tensor code, Tensor absmax2, "
         "Tensor offset, int out_features, Tensor? bias) -> Tensor");

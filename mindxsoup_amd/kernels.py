@@ -492,6 +492,54 @@ def nf4_linear_bwd_dx_hp(dy2d, packed, state, lora_dhp, lora_at, mask=None, mask
     return dx, dht
 
 
+def bwd_dx_pair_ok(M, N0, N1, K):
+    """True when nf4_linear_bwd_dx_hp_pair takes projections [K -> N0] and [K -> N1] at M tokens
+    (both plan the narrow-output split-K kernel on their own)."""
+    return bool(_lib.lib().mxs_nf4_linear_bwd_dx_pair_ok(M, N0, N1, K))
+
+
+def nf4_linear_bwd_dx_hp_pair(dys, packeds, states, lora_dhps, lora_ats, masks=None,
+                              mask_scale=1.0, want_t=True, ws=None):
+    """(dx, [dht0, dht1]): dX = the sum of nf4_linear_bwd_dx_hp's two input gradients, from ONE
+    split-K launch over both reductions and one reduce (each projection's part is never rounded
+    to fp16 on its own), and each projection's fp16 dHs^T (None unless want_t).  Only where
+    bwd_dx_pair_ok."""
+    masks = masks or [None, None]
+    (n0, k), (n1, k1) = states[0].shape, states[1].shape
+    dys = [d.contiguous() for d in dys]
+    M = dys[0].shape[0]
+    if k1 != k or dys[0].shape != (M, n0) or dys[1].shape != (M, n1) or \
+            any(d.dtype != torch.float16 for d in dys):
+        raise ValueError("dy_i must be fp16 [M, N_i] of two weights [N_i, K]")
+    if not bwd_dx_pair_ok(M, n0, n1, k):
+        raise ValueError(f"the pair does not take [{k} -> {n0}], [{k} -> {n1}] at {M} tokens")
+    S, ldt, r = lora_dhps[0].shape
+    for hp, at, mk in zip(lora_dhps, lora_ats, masks):
+        if hp.shape != (S, ldt, r) or hp.dtype != torch.float32 or ldt != _ldt(M) or \
+                at.shape != (k, r):
+            raise ValueError("lora_dhp [slices, ldt, r] fp32 (one shape) and lora_at [K, r]")
+        if mk is not None and (mk.dtype != torch.uint8 or mk.shape != (M, k)):
+            raise ValueError("mask must be uint8 [M, K]")
+    dev = dys[0].device
+    for pk, st in zip(packeds, states):
+        check_nf4_operands(pk, st, dev)
+    dx = torch.empty((M, k), dtype=torch.float16, device=dev)
+    dhts = [torch.empty((r, ldt), dtype=torch.float16, device=dev) if want_t else None
+            for _ in range(2)]
+    ws = _workspace(int(_lib.lib().mxs_nf4_linear_bwd_dx_pair_workspace_bytes(M, n0, n1, k)),
+                    dev, ws)
+    _lib.call("mxs_nf4_linear_bwd_dx_hp_pair", _ptr_array(dys), M, _int_array([n0, n1]), k,
+              _ptr_array(packeds), _ptr_array([st.absmax for st in states]),
+              _ptr_array([st.state2.code for st in states]),
+              _ptr_array([st.state2.absmax for st in states]),
+              _ptr_array([st.offset for st in states]),
+              _ptr_array([h.contiguous() for h in lora_dhps]), S, ldt,
+              _ptr_array([a.contiguous() for a in lora_ats]), r,
+              _ptr_array([_c(m) for m in masks]), float(mask_scale), _ptr_array(dhts),
+              _lib.ptr(dx), _lib.ptr(ws), _lib.stream_of(dev))
+    return dx, dhts
+
+
 def glu_fused(M, N, K, bwd):
     """True when the projection K -> N at M tokens takes the SwiGLU epilogue on its planned
     kernel: nf4_linear_fwd_glu (bwd False) or nf4_linear_bwd_dx_glu (bwd True)."""

@@ -195,14 +195,33 @@ def lora_backward(dy, x2d, keep, ht, at, bt, packed, state, mask_scale, s, want_
     return dx, da, db
 
 
-def lora_backward_group(items, ws=None):
+def _pair_takes(items, pre):
+    """Whether the two projections' input gradients go through one summed dX launch
+    (kernels.nf4_linear_bwd_dx_hp_pair): both take dHs partials, both want dX, one input
+    tensor, one dropout scale, and shapes the pair's plan takes."""
+    if len(items) != 2 or any("dhp" not in p for p in pre):
+        return False
+    a, b = items
+    x0, x1 = a["x2d"], b["x2d"]
+    return (a["wants"][0] and b["wants"][0] and a["mask_scale"] == b["mask_scale"]
+            and x0.shape == x1.shape and x0.data_ptr() == x1.data_ptr()
+            and pre[0]["dhp"].shape == pre[1]["dhp"].shape
+            and kernels.bwd_dx_pair_ok(x0.shape[0], a["dy"].shape[1], b["dy"].shape[1],
+                                       x0.shape[1]))
+
+
+def lora_backward_group(items, ws=None, sum_dx=False):
     """lora_backward for up to 4 projections over the same tokens whose output gradients arrive
     together (q/k/v from attention's backward, gate/up from the SwiGLU's), with their small
     launches shared: dHs in one launch per kind (prepare_dh); the dX GEMMs that carry the weight
     gradients in one launch where kernels.bwd_grads_group_ok allows; otherwise each dX GEMM,
     then dA and dB of all of them in one launch (equal shapes).  items: dicts with dy, x2d,
     keep, ht, at, bt, packed, state, mask_scale, s and wants = (want_x, want_a, want_b).
-    Returns [(dx, dA, dB)], the bits of lora_backward on each."""
+    Returns [(dx, dA, dB)], the bits of lora_backward on each.
+    sum_dx (projections over one input, whose input gradients autograd adds): the first item's
+    dx is the sum of all the items' (added in item order), the others' None; two projections
+    the summed launch takes (_pair_takes: gate and up) get their sum from that one launch, the
+    fp32 sum rounded once instead of each part rounded and added."""
     n = len(items)
     pre = prepare_dh([(it["dy"], it["bt"], it["x2d"].shape[1], it["s"], it["wants"])
                       for it in items])
@@ -230,6 +249,15 @@ def lora_backward_group(items, ws=None):
                                    it["packed"], it["state"], it["mask_scale"], it["s"],
                                    *it["wants"], ws=ws, **pre[i])
     pending = []
+    if sum_dx and not fused and _pair_takes(items, pre):
+        want_t = [it["wants"][1] or it["wants"][2] for it in items]
+        dx, dhts = kernels.nf4_linear_bwd_dx_hp_pair(
+            [it["dy"] for it in items], [it["packed"] for it in items],
+            [it["state"] for it in items], [p["dhp"] for p in pre], [it["at"] for it in items],
+            [it["keep"] for it in items], items[0]["mask_scale"], want_t=any(want_t), ws=ws)
+        out = [[dx, None, None], [None, None, None]]
+        pending = [(i, dhts[i]) for i in range(2) if want_t[i]]
+        sum_dx = False  # summed
     for i in range(n):
         if out[i] is not None:
             continue
@@ -262,6 +290,14 @@ def lora_backward_group(items, ws=None):
                                     it["mask_scale"], want_a=it["wants"][1],
                                     want_b=it["wants"][2], ws=ws)
         out[i][1], out[i][2] = da, db
+    out = [list(o) for o in out]
+    if sum_dx:
+        dx = None
+        for o in out:
+            if o[0] is not None:
+                dx = o[0] if dx is None else dx + o[0]
+            o[0] = None
+        out[0][0] = dx
     return [tuple(o) for o in out]
 
 
@@ -375,12 +411,8 @@ class NF4LoraSiblingsFunction(torch.autograd.Function):
                               ht=hts[i], at=ats[i], bt=bts[i], packed=p.packed, state=p.state,
                               mask_scale=p.mask_scale, s=p.s,
                               wants=(need[0], need[3 + 2 * i], need[4 + 2 * i])))
-        res = lora_backward_group(items)
-        dx = None
-        if need[0]:
-            dx = res[0][0]
-            for r in res[1:]:
-                dx = dx + r[0]
+        res = lora_backward_group(items, sum_dx=True)
+        dx = res[0][0] if need[0] else None
         grads = []
         for i, (_, da, db) in enumerate(res):
             grads += [None if da is None else da.to(ctx.dtypes[2 * i]),

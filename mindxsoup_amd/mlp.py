@@ -104,16 +104,15 @@ class NF4LoraMLPFunction(torch.autograd.Function):
                                          want_a=need[5], want_b=need[6])
         del h
         # up_proj and gate_proj with d(up) and d(gate) as their incoming gradients; their small
-        # launches (dHs, dA / dB) shared
-        (dx, dua, dub), (dxg, dga, dgb) = lora_backward_group([
+        # launches (dHs, dA / dB) shared, and their input gradients summed (in one launch where
+        # the summed dX GEMM takes them)
+        (dx, dua, dub), (_, dga, dgb) = lora_backward_group([
             dict(dy=up, x2d=x2d, keep=pu.keep, ht=ht_u, at=at_u, bt=bt_u, packed=pu.packed,
                  state=pu.state, mask_scale=pu.mask_scale, s=pu.s,
                  wants=(need[0], need[3], need[4])),
             dict(dy=gate, x2d=x2d, keep=pg.keep, ht=ht_g, at=at_g, bt=bt_g, packed=pg.packed,
                  state=pg.state, mask_scale=pg.mask_scale, s=pg.s,
-                 wants=(need[0], need[1], need[2]))])
-        if dx is not None:
-            dx += dxg
+                 wants=(need[0], need[1], need[2]))], sum_dx=True)
         grads = [dga, dgb, dua, dub, grads_d[0], grads_d[1]]
         grads = [None if g is None else g.to(t) for g, t in zip(grads, ctx.dtypes)]
         return (dx, *grads, None)

@@ -1,0 +1,126 @@
+"""The summed input gradient of two projections over one input (mxs_nf4_linear_bwd_dx_hp_pair:
+gate and up of the MLP in one split-K launch and one reduce) on the GPU.
+
+Bars: against the float64 oracle's dX_gate + dX_up within the north star's 1e-2; against the two
+separate launches (each dX rounded to fp16, then added in fp16) within their roundings (1.5 fp16
+ulps of the largest value); the dHs^T side outputs bit-equal to the separate launches'; and the
+group backward (linear4bit.lora_backward_group with sum_dx) taking it only where it applies."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+S, P = 2.0, 0.05
+
+
+def _proj(dev, n, k, M, seed, x):
+    from mindxsoup_amd.quant import quantize_4bit
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    w = (torch.randn((n, k), device=dev, generator=g) * 0.02).half()
+    packed, st = quantize_4bit(w)
+    a = ((torch.rand((16, k), device=dev, generator=g) * 2 - 1) / k ** 0.5).half()
+    b = (torch.randn((n, 16), device=dev, generator=g) * 0.01).half()
+    dy = torch.randn((M, n), device=dev, generator=g).half()
+    keep = (torch.rand((M, k), device=dev, generator=g) >= P).to(torch.uint8)
+    return dict(packed=packed, st=st, a=a, b=b, dy=dy, keep=keep, x=x, n=n, k=k)
+
+
+def _w(p):
+    st = p["st"]
+    return O.dequant(O.NF4Weight(st.shape, p["packed"].view(-1).cpu().numpy(),
+                                 st.absmax.cpu().numpy(), st.state2.code.cpu().numpy(),
+                                 st.state2.absmax.cpu().numpy(), float(st.offset.item())))
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+@pytest.mark.parametrize("M", [1024, 300, 37])
+def test_pair_sums_the_two_input_gradients(cuda, M):
+    from mindxsoup_amd import kernels
+
+    print(f"case dx pair M={M}", flush=True)
+    x = torch.randn((M, 1536), device=cuda).half()
+    ps = [_proj(cuda, 8960, 1536, M, 30 + i, x) for i in range(2)]
+    assert kernels.bwd_dx_pair_ok(M, 8960, 8960, 1536)
+    dhps = [kernels.lora_dh_partials(p["dy"], p["b"].t().contiguous(), S) for p in ps]
+    ats = [p["a"].t().contiguous() for p in ps]
+    dx, dhts = kernels.nf4_linear_bwd_dx_hp_pair(
+        [p["dy"] for p in ps], [p["packed"] for p in ps], [p["st"] for p in ps], dhps, ats,
+        [p["keep"] for p in ps], 1 / (1 - P))
+    sep = [kernels.nf4_linear_bwd_dx_hp(p["dy"], p["packed"], p["st"], dhp, at, p["keep"],
+                                        1 / (1 - P)) for p, dhp, at in zip(ps, dhps, ats)]
+    for (_, dht_sep), dht in zip(sep, dhts):
+        assert torch.equal(dht, dht_sep)
+    two = sep[0][0] + sep[1][0]
+    err_sep = ((dx.float() - two.float()).abs().max() / two.float().abs().max()).item()
+    assert 0 < err_sep < 2 ** -9, err_sep
+    x16 = _np(x).astype(np.float16)
+    ref = 0.0
+    for p in ps:
+        ref = ref + O.lora_bwd(_np(p["dy"]).astype(np.float16), x16, _w(p),
+                               _np(p["a"]).astype(np.float16), _np(p["b"]).astype(np.float16), S,
+                               p["keep"].cpu().numpy(), P)[0]
+    err = O.max_rel(_np(dx), ref)
+    print(f"  max_rel vs oracle {err:.2e}, vs separate {err_sep:.2e}", flush=True)
+    assert err < 1e-2
+    # the summed launch is no less accurate than the two rounded ones
+    assert err <= O.max_rel(_np(two), ref) * 1.05 + 1e-6
+
+
+def test_pair_refuses_other_plans(cuda):
+    """Shapes whose own plan is not the narrow-output split kernel (q/o: 1536 x 1536) are
+    refused on the host."""
+    from mindxsoup_amd import kernels
+
+    assert not kernels.bwd_dx_pair_ok(1024, 1536, 1536, 1536)
+    assert not kernels.bwd_dx_pair_ok(1024, 8960, 8960, 1000)
+    x = torch.randn((64, 1536), device=cuda).half()
+    ps = [_proj(cuda, 1536, 1536, 64, 40 + i, x) for i in range(2)]
+    dhps = [kernels.lora_dh_partials(p["dy"], p["b"].t().contiguous(), S) for p in ps]
+    with pytest.raises(ValueError, match="does not take"):
+        kernels.nf4_linear_bwd_dx_hp_pair([p["dy"] for p in ps], [p["packed"] for p in ps],
+                                          [p["st"] for p in ps], dhps,
+                                          [p["a"].t().contiguous() for p in ps])
+
+
+def test_group_backward_sums(cuda):
+    """lora_backward_group(sum_dx=True) on gate and up gives the pair's dx in the first item and
+    the separate launches' LoRA gradients; on q/k/v (no pair) the in-order fp16 sum of the
+    separate dx."""
+    from mindxsoup_amd import kernels
+    from mindxsoup_amd.linear4bit import lora_backward_group
+
+    M = 512
+    x = torch.randn((M, 1536), device=cuda).half()
+    for shapes, paired in (([8960, 8960], True), ([1536, 256, 256], False)):
+        ps = [_proj(cuda, n, 1536, M, 50 + i, x) for i, n in enumerate(shapes)]
+        items = []
+        for p in ps:
+            hp, at, bt = kernels.lora_h_partials(x, p["a"], S, p["keep"], 1 / (1 - P),
+                                                 lora_b=p["b"])
+            _, ht = kernels.nf4_linear_fwd_hp(x, p["packed"], p["st"], hp, p["b"])
+            items.append(dict(dy=p["dy"], x2d=x, keep=p["keep"], ht=ht, at=at, bt=bt,
+                              packed=p["packed"], state=p["st"], mask_scale=1 / (1 - P), s=S,
+                              wants=(True, True, True)))
+        summed = lora_backward_group(items, sum_dx=True)
+        apart = lora_backward_group(items)
+        assert all(r[0] is None for r in summed[1:])
+        for r_s, r_a in zip(summed, apart):
+            assert torch.equal(r_s[1], r_a[1]) and torch.equal(r_s[2], r_a[2])
+        two = apart[0][0]
+        for r in apart[1:]:
+            two = two + r[0]
+        if paired:
+            err = ((summed[0][0].float() - two.float()).abs().max()
+                   / two.float().abs().max()).item()
+            assert 0 < err < 2 ** -9, err
+        else:
+            assert torch.equal(summed[0][0], two)

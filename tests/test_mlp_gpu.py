@@ -5,7 +5,9 @@ Bars: the fused epilogues give the bits of the unfused sequence (the GEMM, then 
 mxs_silu_mul_bwd: the epilogue rounds the product to fp16 before the SwiGLU reads it, as the
 separate kernel does); the MLP block against a float64 composition of the oracle (NF4 decode,
 peft LoRA products, the SwiGLU restatement) within max relative error 1e-2; the fused block
-equal bit for bit to the three projections and silu_mul called one by one, forward and backward.
+equal bit for bit to the three projections and silu_mul called one by one, forward and backward,
+except the input gradient: the fused block adds gate's and up's parts in fp32 inside one launch
+and rounds once, where the composition rounds each part and adds them in fp16.
 """
 
 import numpy as np
@@ -185,8 +187,11 @@ def _run(mlp, x, dy, fused, seed):
 @pytest.mark.parametrize("fwd_tail", [False, True])
 def test_mlp_fused_equals_projections_and_silu_mul(cuda, M, fwd_tail, monkeypatch):
     """NF4LoraMLPFunction against the reference's composition through the same modules
-    (solution/mlp.py:42-44: down_proj(silu_mul(gate_proj(x16), up_proj(x16)))): output, input
-    gradient and all six LoRA gradients bit for bit, fp32 residual input as in the reference."""
+    (solution/mlp.py:42-44: down_proj(silu_mul(gate_proj(x16), up_proj(x16)))): output and all
+    six LoRA gradients bit for bit, fp32 residual input as in the reference; the input gradient
+    within the roundings of the composition's fp16 parts and their fp16 sum (at most 1.5 fp16
+    ulps of the largest value: max relative error below 2^-9), since the fused block sums them in
+    fp32 before its one rounding."""
     from mindxsoup_amd import mlp as mlp_mod
 
     print(f"case mlp fused/unfused M={M} fwd_tail={fwd_tail}", flush=True)
@@ -200,7 +205,9 @@ def test_mlp_fused_equals_projections_and_silu_mul(cuda, M, fwd_tail, monkeypatc
     y1, dx1, g1 = _run(mlp, x, dy, False, 5)
     y2, dx2, g2 = _run(mlp, x, dy, True, 5)
     assert y1.dtype == torch.float32 and dx1.dtype == torch.float32
-    assert torch.equal(y2, y1) and torch.equal(dx2, dx1)
+    assert torch.equal(y2, y1)
+    err = ((dx2 - dx1).abs().max() / dx1.abs().max()).item()
+    assert 0 < err < 2 ** -9, err  # 0 would mean the summed launch did not run
     assert sorted(g1) == sorted(g2) and len(g1) == 6
     for name in g1:
         assert torch.equal(g2[name], g1[name]), name

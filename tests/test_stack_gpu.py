@@ -32,6 +32,10 @@ def test_timed_layer_step_matches_oracle(cuda):
     grads = bench.layer_bwd(projs, saved)
     torch.cuda.synchronize()
     s, p = bench.ALPHA / bench.RANK, bench.P_DROP
+    names = [name for name, _, _ in bench.PROJ]
+    ig, iu = names.index("gate"), names.index("up")
+    assert grads[ig][0] is None and grads[iu][0] is not None
+    ref_dx_sum = 0.0
     for (name, n, k), pr, y, (dx, da, db) in zip(bench.PROJ, projs, ys, grads):
         st = pr["st"]
         w = O.dequant(O.NF4Weight(st.shape, pr["packed"].view(-1).cpu().numpy(),
@@ -41,8 +45,14 @@ def test_timed_layer_step_matches_oracle(cuda):
         kp, dy16 = pr["keep"].cpu().numpy(), _np(pr["dy"]).astype(np.float16)
         ref_y = O.lora_fwd(x16, w, a16, b16, s, kp, p)
         ref_dx, ref_da, ref_db = O.lora_bwd(dy16, x16, w, a16, b16, s, kp, p)
-        errs = {"y": O.max_rel(_np(y), ref_y), "dx": O.max_rel(_np(dx), ref_dx),
-                "dA": O.max_rel(_np(da), ref_da), "dB": O.max_rel(_np(db), ref_db)}
+        errs = {"y": O.max_rel(_np(y), ref_y), "dA": O.max_rel(_np(da), ref_da),
+                "dB": O.max_rel(_np(db), ref_db)}
+        if name in ("gate", "up"):
+            ref_dx_sum = ref_dx_sum + ref_dx
+            if name == "up":
+                errs["dx(gate+up)"] = O.max_rel(_np(dx), ref_dx_sum)
+        else:
+            errs["dx"] = O.max_rel(_np(dx), ref_dx)
         print(f"case stack layer {name}: " + " ".join(f"{k_}={v:.1e}" for k_, v in errs.items()),
               flush=True)
         assert max(errs.values()) < 1e-2, (name, errs)

@@ -133,16 +133,19 @@ def test_lora_linear_nd_input_and_fp16_weights(cuda):
     _same([got[0].view(300, 256), got[1].view(300, 1536), got[2], got[3]], list(want), "N-D")
 
 
-@pytest.mark.parametrize("M", [300, 1024])
-@pytest.mark.parametrize("one_gemm", [True, False])
-def test_siblings_bits_equal_python_path(cuda, M, one_gemm):
-    """q, k, v in shared launches: lora_siblings (C++) and NF4LoraSiblingsFunction (Python) give
-    the same outputs, the same summed dx and the same LoRA gradients."""
+@pytest.mark.parametrize("M,one_gemm,shapes", [
+    (300, True, "qkv"), (1024, True, "qkv"), (300, False, "qkv"), (1024, False, "qkv"),
+    (1024, False, "gateup"), (200, False, "gateup")])
+def test_siblings_bits_equal_python_path(cuda, M, one_gemm, shapes):
+    """q, k, v (or gate and up, whose input gradients come from one summed launch) in shared
+    launches: lora_siblings (C++) and NF4LoraSiblingsFunction (Python) give the same outputs,
+    the same summed dx and the same LoRA gradients."""
     from mindxsoup_amd import ops
     from mindxsoup_amd.linear4bit import NF4LoraSiblingsFunction, Proj
 
-    print(f"case op lora_siblings M={M} one_gemm={one_gemm}", flush=True)
-    shapes = [(1536, 1536), (256, 1536), (256, 1536)]
+    print(f"case op lora_siblings M={M} one_gemm={one_gemm} {shapes}", flush=True)
+    shapes = ([(1536, 1536), (256, 1536), (256, 1536)] if shapes == "qkv"
+              else [(8960, 1536), (8960, 1536)])
     layers = [_layer(cuda, n, k, 10 + i, bias=True) for i, (n, k) in enumerate(shapes)]
     g = torch.Generator(device=cuda)
     g.manual_seed(7)
