@@ -89,7 +89,7 @@ int mxs_nf4_quantize(const void* w_f16, int64_t n_values, const float* code, voi
                      void* workspace, hipStream_t stream);
 
 /* ---- Fused NF4 GEMMs (forward and input gradient of the frozen Linear4bit) ---------------
- * cfg: tile configuration id (0-4: all-wave kernels, 6-11: producer/consumer kernels; 5 is
+ * cfg: tile configuration id (0-4: all-wave kernels, 6-12: producer/consumer kernels; 5 is
  * invalid) or -1 to let the library choose tiles and split-K for the shape; splits: reduction
  * splits (used with cfg >= 0).  When the plan splits the reduction, `workspace` must hold
  * mxs_nf4_gemm_workspace_bytes(M, Nc, Kr, cfg, splits) bytes of device memory (fp32 partial
@@ -344,9 +344,11 @@ int mxs_silu_mul_bwd(const void* grad, void* gate, void* up, int64_t n, hipStrea
  * solution/attention.py:259-266): problem i has x[i] [M, K], out_features N[i], its NF4 weight
  * (packed[i] .. offset[i]), bias[i], LoRA partials lora_hp[i] (hp_slices, ldt, r shared),
  * lora_b[i] [N[i], r], lora_ht[i], output y[i] [M, N[i]]; the bias, lora_hp, lora_b and lora_ht
- * arrays may be NULL (or any entry: no bias / no LoRA term).  Every problem runs on 128x128
- * tiles with 8 producer waves, unsplit: the same bits as mxs_nf4_linear_fwd_hp with cfg 10 and
- * one split for each (the N = 256 projections alone would plan split-K tiles and a reduce). */
+ * arrays may be NULL (or any entry: no bias / no LoRA term).  Every problem runs unsplit on
+ * warp-specialized tiles with 8 producer waves, 128x64 when all the problems' tiles fit the CUs
+ * in one round (q, k and v at 1024 tokens), else 128x128: the same bits as mxs_nf4_linear_fwd_hp
+ * with one split for each (every warp-specialized configuration accumulates in one order; the
+ * N = 256 projections alone would plan split-K tiles and a reduce). */
 int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, const int N[],
                                 const void* const packed[], const void* const absmax8[],
                                 const float* const code[], const float* const absmax2[],

@@ -1992,11 +1992,25 @@ static int launch_by_id(int cfg, const GemmArgs& a, int splits, hipStream_t s) {
     case 9: return launch_ws<256, 96, 4, 1, BWD>(a, splits, s);
     case 10: return launch_ws<128, 128, 2, 2, BWD, 8>(a, splits, s);
     case 11: return launch_ws<256, 96, 4, 1, BWD, 8, 5>(a, splits, s);
+    case 12: return launch_ws<128, 64, 2, 2, BWD, 8>(a, splits, s);
     default: return MXS_ERR_ARG;
   }
 }
 
-constexpr int kNumCfg = 12;
+constexpr int kNumCfg = 13;
+
+// Compute units of the current device (queried once per device).
+static int cu_count() {
+  static int counts[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (counts[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    counts[dev] = n > 0 ? n : -1;
+  }
+  return counts[dev] > 0 ? counts[dev] : 0;
+}
 
 // Tile and split choice for one GEMM (M x Nc output, Kr reduction), from measured sweeps on
 // MI355X at the Qwen2.5-1.5B projection shapes (M = 1024):
@@ -2005,7 +2019,10 @@ constexpr int kNumCfg = 12;
 //   4 producer waves forward (46 against 51 us for down_proj at 1024 tokens) and 8 in the
 //   backward (49 against 51 us for gate/up dX); every ws configuration accumulates an output
 //   element in the same order, so for one split count the choice changes no result;
-//   mid outputs (Nc >= 1024): warp-specialized 128x128 with 8 producer waves, no split;
+//   mid outputs (Nc >= 1024): warp-specialized with 8 producer waves, no split, on 128x64 tiles
+//   when those fit the CUs in one round (the 1536-wide q/o shapes up to 1024 tokens: 192 tiles,
+//   13.6 against 18.9 us for 128x128 at 1024 tokens, 13.2 against 18.4 at 830), else 128x128
+//   (1430 tokens: 288 tiles of 128x64 would take two rounds, 25.6 against 19.2 us);
 //   small outputs: 64x128 all-wave tiles, split-K 4 when the reduction is long enough.
 // Splits keep at least 6 K-steps each.
 static void choose(int M, int Nc, int Kr, bool bwd, int* cfg, int* splits) {
@@ -2016,11 +2033,13 @@ static void choose(int M, int Nc, int Kr, bool bwd, int* cfg, int* splits) {
   } else if (Kr >= 4096) {
     c = bwd ? 11 : 9; sp = 4;
   } else if (Nc >= 1024) {
-    c = 10; sp = 1;
+    const int64_t tiles64 = (int64_t)((M + 127) / 128) * ((Nc + 63) / 64);
+    const int cus = cu_count();
+    c = (cus > 0 && tiles64 <= cus) ? 12 : 10;
+    sp = 1;
   } else {
     c = 4; sp = Kr >= 1024 ? 4 : 1;
   }
-  (void)M;
   while (sp > 1 && n_steps / sp < 6) sp >>= 1;
   *cfg = c;
   *splits = sp;
@@ -2069,19 +2088,6 @@ static int gemm_entry(bool bwd, const GemmArgs& a, int cfg, int splits, hipStrea
              : launch_by_id<false>(cfg, a, splits, stream);
 }
 
-// Compute units of the current device (queried once per device).
-static int cu_count() {
-  static int counts[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (counts[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
-    counts[dev] = n > 0 ? n : -1;
-  }
-  return counts[dev] > 0 ? counts[dev] : 0;
-}
-
 // The backward GEMM of a projection [K -> N] at M tokens and its LoRA gradient workgroups fit
 // one launch: the planned kernel is an unsplit warp-specialized one that takes the problem
 // (none of its fallback conditions holds) and its tiles plus the gradient workgroups fit the
@@ -2095,10 +2101,14 @@ static bool grads_fusable(int M, int N, int K, int r, int* cfg_out, int* nw_out)
   const int nw = cols_waves(M, r, kFusedColsCPL, cols_max_waves<kFusedColsCPL>());
   int cfg, sp;
   choose(M, K, N, true, &cfg, &sp);
+  // the 128x64 plan's tiles leave no CUs for the gradient workgroups at the sizes it is chosen
+  // for; the 128x128 tiles do (the q/o backward at 1024 tokens: 96 tiles + 96 gradient
+  // workgroups, one launch, against a dX launch of 128x64 tiles plus a gradient launch)
+  if (cfg == 12) cfg = 10;
   if (cfg < 6 || cfg >= kNumCfg || sp != 1) return false;
-  static const int kBM[] = {256, 256, 128, 256, 128, 256};  // cfg 6..11
-  static const int kBN[] = {128, 160, 128, 96, 128, 96};
-  static const int kPW[] = {4, 4, 4, 4, 8, 8};
+  static const int kBM[] = {256, 256, 128, 256, 128, 256, 128};  // cfg 6..12
+  static const int kBN[] = {128, 160, 128, 96, 128, 96, 64};
+  static const int kPW[] = {4, 4, 4, 4, 8, 8, 8};
   const int bm = kBM[cfg - 6], bn = kBN[cfg - 6], pw = kPW[cfg - 6];
   if (bm != 128) return false;  // only those kernels carry the gradient rows
   if (nw > 4 + pw) return false;
@@ -2123,19 +2133,20 @@ static bool glu_plan_ok(int M, int Nc, int Kr, bool bwd) {
   int cfg, sp;
   choose(M, Nc, Kr, bwd, &cfg, &sp);
   if (cfg < 6 || cfg >= kNumCfg) return false;
-  static const int kBM[] = {256, 256, 128, 256, 128, 256};  // cfg 6..11
-  static const int kPW[] = {4, 4, 4, 4, 8, 8};
+  static const int kBM[] = {256, 256, 128, 256, 128, 256, 128};  // cfg 6..12
+  static const int kPW[] = {4, 4, 4, 4, 8, 8, 8};
   const int bm = kBM[cfg - 6], pw = kPW[cfg - 6];
   return (int64_t)Nc * Kr < (int64_t(1) << 32) && (int64_t)bm * Kr * 2 < (int64_t(1) << 32) &&
          !(bwd && Nc < (pw == 8 ? 16 : 32));
 }
 
-// The GEMMs of several problems in one launch of 128x128 tiles with 8 producer waves, unsplit
-// (k_nf4_gemm_ws_group); in the backward each problem's LoRA gradient workgroups follow its
-// tiles.  Every problem must take that kernel (its 32-bit offsets, the backward's column clamp).
-template <bool BWD>
+// The GEMMs of several problems in one launch of one warp-specialized tile configuration with 8
+// producer waves, unsplit (k_nf4_gemm_ws_group): 128x128 tiles by default; in the backward each
+// problem's LoRA gradient workgroups follow its tiles.  Every problem must take that kernel (its
+// 32-bit offsets, the backward's column clamp).
+template <bool BWD, int BN = 128>
 static int launch_ws_group(const GemmArgs* probs, int n, hipStream_t stream) {
-  constexpr int BM = 128, BN = 128, PW = 8, NS = 4;
+  constexpr int BM = 128, PW = 8, NS = 4;
   if (n < 1 || n > kMaxGemmGroup) return MXS_ERR_ARG;
   GemmGroup g{};
   g.n = n;
@@ -2144,7 +2155,7 @@ static int launch_ws_group(const GemmArgs* probs, int n, hipStream_t stream) {
     GemmArgs a = probs[i];
     if ((int64_t)a.Nc * a.Kr >= (int64_t(1) << 32) ||
         (int64_t)BM * a.lda * 2 >= (int64_t(1) << 32) || (BWD && a.Nc < 16) ||
-        (!BWD && a.cols_blocks > 0))
+        (!BWD && a.cols_blocks > 0) || (a.cols_blocks > 0 && BN != 128))
       return MXS_ERR_SIZE;
     a.steps_per_split = a.Kr / kBK;
     g.p[i] = a;
@@ -2646,6 +2657,13 @@ int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, cons
     probs[live++] = a;
   }
   if (live == 0) return MXS_OK;
+  // 128x64 tiles when every problem's tiles together fit the CUs in one round (q, k and v at
+  // 1024 tokens: 192 + 32 + 32 = 256 tiles), as the planner does for one problem; else 128x128
+  int64_t tiles64 = 0;
+  for (int i = 0; i < live; i++)
+    tiles64 += (int64_t)((M + 127) / 128) * ((probs[i].Nc + 63) / 64);
+  const int cus = cu_count();
+  if (cus > 0 && tiles64 <= cus) return launch_ws_group<false, 64>(probs, live, stream);
   return launch_ws_group<false>(probs, live, stream);
 }
 

@@ -424,8 +424,9 @@ def nf4_linear_fwd_hp(x2d, packed, state, lora_hp, lora_b, bias=None, cfg=-1, sp
 
 def nf4_linear_fwd_hp_group(x2ds, packeds, states, lora_hps=None, lora_bs=None, biases=None):
     """nf4_linear_fwd_hp for up to 4 projections of one input width over the same tokens in one
-    launch (128x128 tiles, unsplit): a list of (y, ht) (ht None without LoRA), the bits of
-    nf4_linear_fwd_hp(..., cfg=10, splits=1) for each."""
+    launch (128x64 tiles when they fit the CUs in one round, else 128x128; unsplit): a list of
+    (y, ht) (ht None without LoRA), the bits of nf4_linear_fwd_hp(..., cfg=10, splits=1) for
+    each."""
     n = len(x2ds)
     lora_hps = lora_hps or [None] * n
     lora_bs = lora_bs or [None] * n

@@ -42,7 +42,8 @@ def _np(t):
 
 @pytest.mark.parametrize("n,k", [(256, 1536), (1536, 1536), (192, 128)])
 @pytest.mark.parametrize("cfg,splits", [(-1, 1), (0, 1), (1, 2), (2, 1), (4, 3), (6, 2), (7, 1),
-                                        (8, 1), (9, 1), (10, 1), (10, 2), (11, 1), (11, 3)])
+                                        (8, 1), (9, 1), (10, 1), (10, 2), (11, 1), (11, 3),
+                                        (12, 1), (12, 2)])
 def test_in_gemm_decode_is_bit_exact(cuda, n, k, cfg, splits):
     """One-hot rows: X = I gives Y = W^T and dY = I gives dX = W, each output a single exact
     product, so the fused kernels must reproduce the standalone dequant bit for bit (also with
@@ -88,7 +89,7 @@ def test_linear4bit_fwd_bwd_matches_oracle(cuda, out_features, bias, tokens):
 
 @pytest.mark.parametrize("cfg,splits", [(0, 1), (0, 4), (1, 1), (1, 3), (2, 2), (4, 1), (6, 1),
                                         (6, 3), (7, 2), (8, 1), (9, 4), (10, 1), (10, 3),
-                                        (11, 4)])
+                                        (11, 4), (12, 1), (12, 3)])
 def test_tile_configs_agree_with_oracle(cuda, cfg, splits):
     from mindxsoup_amd import kernels
 
