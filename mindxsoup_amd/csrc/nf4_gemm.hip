@@ -2101,10 +2101,6 @@ static bool grads_fusable(int M, int N, int K, int r, int* cfg_out, int* nw_out)
   const int nw = cols_waves(M, r, kFusedColsCPL, cols_max_waves<kFusedColsCPL>());
   int cfg, sp;
   choose(M, K, N, true, &cfg, &sp);
-  // the 128x64 plan's tiles leave no CUs for the gradient workgroups at the sizes it is chosen
-  // for; the 128x128 tiles do (the q/o backward at 1024 tokens: 96 tiles + 96 gradient
-  // workgroups, one launch, against a dX launch of 128x64 tiles plus a gradient launch)
-  if (cfg == 12) cfg = 10;
   if (cfg < 6 || cfg >= kNumCfg || sp != 1) return false;
   static const int kBM[] = {256, 256, 128, 256, 128, 256, 128};  // cfg 6..12
   static const int kBN[] = {128, 160, 128, 96, 128, 96, 64};
@@ -2118,9 +2114,21 @@ static bool grads_fusable(int M, int N, int K, int r, int* cfg_out, int* nw_out)
   constexpr int WC = 16 * kFusedColsCPL;
   const int64_t tiles = (int64_t)((K + bn - 1) / bn) * ((M + bm - 1) / bm);
   const int64_t cols = (K + WC - 1) / WC + (N + WC - 1) / WC;
-  // the gradient workgroups' cross-wave sums fit the kernel's LDS (at least 80 KB)
-  if ((int64_t)nw * r * (WC + 1) * 4 > 80 * 1024) return false;
-  if (tiles + cols > cu_count()) return false;
+  // The 128x64 plan (chosen where its tiles alone fill the CUs once) takes the gradient
+  // workgroups as a partial second round: they are short, and its tiles are (the q/o backward at
+  // 1024 tokens: 192 tiles + 96 gradient workgroups).  Otherwise 128x128 tiles, where tiles and
+  // gradient workgroups fit the CUs at once.
+  if (cfg == 12 && tiles + cols > 2 * (int64_t)cu_count()) {
+    cfg = 10;
+    const int64_t tiles128 = (int64_t)((K + 127) / 128) * ((M + 127) / 128);
+    if (tiles128 + cols > cu_count()) return false;
+  } else if (cfg != 12 && tiles + cols > cu_count()) {
+    return false;
+  }
+  // the gradient workgroups' cross-wave sums fit the kernel's LDS
+  const size_t lds = (cfg == 12 ? ws_lds_halfs<128, 64, true>() : ws_lds_halfs<128, 128, true>()) *
+                     sizeof(_Float16);
+  if ((size_t)nw * r * (WC + 1) * 4 > lds) return false;
   *cfg_out = cfg;
   *nw_out = nw;
   return true;
@@ -2155,7 +2163,7 @@ static int launch_ws_group(const GemmArgs* probs, int n, hipStream_t stream) {
     GemmArgs a = probs[i];
     if ((int64_t)a.Nc * a.Kr >= (int64_t(1) << 32) ||
         (int64_t)BM * a.lda * 2 >= (int64_t(1) << 32) || (BWD && a.Nc < 16) ||
-        (!BWD && a.cols_blocks > 0) || (a.cols_blocks > 0 && BN != 128))
+        (!BWD && a.cols_blocks > 0))
       return MXS_ERR_SIZE;
     a.steps_per_split = a.Kr / kBK;
     g.p[i] = a;
@@ -2311,7 +2319,7 @@ static bool dx_grads_group_ok(int n, int M, const int* N, int K, int r, int* nw)
   if (n < 1 || n > kMaxGemmGroup) return false;
   for (int i = 0; i < n; i++) {
     int cfg;
-    if (!grads_fusable(M, N[i], K, r, &cfg, &nw[i]) || cfg != 10) return false;
+    if (!grads_fusable(M, N[i], K, r, &cfg, &nw[i]) || (cfg != 10 && cfg != 12)) return false;
   }
   return true;
 }
@@ -2487,6 +2495,17 @@ int mxs_nf4_linear_bwd_dx_grads_group(int n, const void* const dy[], int M, cons
     e = check_gemm(true, probs[i]);
     if (e != MXS_OK) return e == 1 ? MXS_ERR_SIZE : e;  // grads_fusable admits no empty problem
   }
+  // 128x64 tiles where every problem plans them and all the tiles and gradient workgroups fill
+  // at most two rounds of the CUs (q, k and v at 1024 tokens), as for one problem; else 128x128
+  bool t64 = true;
+  int64_t wgs = 0;
+  for (int i = 0; i < n; i++) {
+    int cfg, sp;
+    choose(M, probs[i].Nc, probs[i].Kr, true, &cfg, &sp);
+    t64 = t64 && cfg == 12;
+    wgs += (int64_t)((M + 127) / 128) * ((probs[i].Nc + 63) / 64) + probs[i].cols_blocks;
+  }
+  if (t64 && wgs <= 2 * (int64_t)cu_count()) return launch_ws_group<true, 64>(probs, n, stream);
   return launch_ws_group<true>(probs, n, stream);
 }
 

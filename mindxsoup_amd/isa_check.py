@@ -92,7 +92,43 @@ def _blocks(ins, labels):
             succ.append([])
         else:
             succ.append(nxt)
+    _thread_known_conditions(ins, spans, succ)
     return spans, succ
+
+
+_ZERO_MASK = re.compile(r"^s_mov_b64\s+(s\[\d+:\d+\]),\s*0$")
+_TEST_MASK = re.compile(r"^s_and_b64\s+vcc,\s*exec,\s*(s\[\d+:\d+\])$")
+
+
+def _thread_known_conditions(ins, spans, succ):
+    """Drop the edges a zeroed lane mask rules out.
+
+    The compiler joins paths through a flag block: each predecessor sets a mask
+    (``s_mov_b64 s[a:b], 0`` or ``-1``) and jumps to ``s_and_b64 vcc, exec, s[a:b]`` +
+    ``s_cbranch_vccz``/``vccnz``.  Coming from a predecessor that wrote 0, vcc is 0 and only one
+    successor of the flag block is reachable; without this, that path would reach the other
+    successor too and carry its loads there.  The predecessor's edge goes straight to the one
+    successor (the flag block writes only scalar registers)."""
+    for n, (b, e) in enumerate(spans):
+        if len(succ[n]) != 1 or e - b < 1:
+            continue
+        last = ins[e - 1][0]
+        k = e - 2 if last.startswith("s_branch") else e - 1
+        m = _ZERO_MASK.match(ins[k][0]) if k >= b else None
+        if not m:
+            continue
+        fb, fe = spans[succ[n][0]]
+        if fe - fb != 2:
+            continue
+        t = _TEST_MASK.match(ins[fb][0])
+        br = ins[fb + 1][0].split()
+        if not t or t.group(1) != m.group(1) or br[0] not in ("s_cbranch_vccz", "s_cbranch_vccnz"):
+            continue
+        flag = succ[n][0]
+        taken, fall = succ[flag][0], (succ[flag][1:] or [None])[0]
+        nxt = taken if br[0] == "s_cbranch_vccz" else fall
+        if nxt is not None:
+            succ[n] = [nxt]
 
 
 def _step(state, ins, b, e, report=None):

@@ -80,6 +80,32 @@ def test_load_carried_around_a_loop_back_edge():
     assert findings(fixed) == []
 
 
+def test_zeroed_mask_path_skips_the_flag_blocks_other_successor():
+    # the compiler's join through a mask: coming from the loop (mask 0) vccz is taken, so the
+    # moves below are reached only from the path that set -1 and has nothing in flight
+    body = ("\ts_cbranch_scc1 .LBB0_3\n" + asm_load("v10", "global_load_dword") +
+            "\ts_mov_b64 s[0:1], 0\n"
+            "\ts_branch .LBB0_4\n"
+            ".LBB0_3:\n"
+            "\ts_mov_b64 s[0:1], -1\n"
+            ".LBB0_4:\n"
+            "\ts_and_b64 vcc, exec, s[0:1]\n"
+            "\ts_cbranch_vccz .LBB0_6\n"
+            "\tv_mov_b32 v10, v3\n"
+            ".LBB0_6:\n"
+            "\ts_waitcnt vmcnt(0)\n"
+            "\ts_endpgm\n")
+    assert findings(body) == []
+    # with the masks swapped the load's path reaches the move
+    swapped = body.replace("s_mov_b64 s[0:1], 0", "s_mov_b64 s[0:1], X").replace(
+        "s_mov_b64 s[0:1], -1", "s_mov_b64 s[0:1], 0").replace("s_mov_b64 s[0:1], X",
+                                                                "s_mov_b64 s[0:1], -1")
+    assert [r[2] for r in findings(swapped)] == [[10]]
+    # a different mask register decides nothing
+    other = body.replace("s_and_b64 vcc, exec, s[0:1]", "s_and_b64 vcc, exec, s[2:3]")
+    assert [r[2] for r in findings(other)] == [[10]]
+
+
 def test_dead_path_after_endpgm_is_not_followed():
     body = (asm_load("v10", "global_load_dword") + "\ts_waitcnt vmcnt(0)\n\ts_endpgm\n")
     assert findings(body) == []
