@@ -31,7 +31,11 @@
 namespace mxs {
 
 constexpr int kMaxRB = 8;            // r <= 128 (r / 16 accumulator blocks)
-constexpr int kChunksInFlight = 4;   // 32-wide reduction chunks loaded per rows-kernel iteration
+
+// 32-wide reduction chunks each wave of the rows kernel loads per iteration: 4 with one 16-row
+// block per workgroup, 3 with two (their loads share one register budget).
+template <int TB>
+constexpr int rows_chunks_in_flight() { return TB == 1 ? 4 : 3; }
 
 __device__ __forceinline__ half8_t drop8(half8_t x, u32x2 keep, float scale) {
 #pragma unroll
@@ -79,18 +83,22 @@ __device__ __forceinline__ half8_t f32x8_to_f16(const float* p) {
   return h;
 }
 
-// out[m][c] = fp16(s * sum_k drop(P)[m][k] * R[c][k]) for the 16 rows of row block rb, over
+// out[m][c] = fp16(s * sum_k drop(P)[m][k] * R[c][k]) for the 16*TB rows of row block rb, over
 // reduction slice `slice` of `slices`.  Waves [0, nw) reduce; any waves past nw (a grouped
 // launch sized for another problem) only take part in the barrier and the stores, so the result
 // is the same bits as a launch of exactly nw waves.  wg of n_wg places the side outputs.
-// W32: the weights come as fp32 (R32, B32).
-template <bool W32>
+// W32: the weights come as fp32 (R32, B32).  TB: 16-row blocks per workgroup; each R fragment
+// a wave loads feeds TB multiplies, so TB = 2 halves the re-reads of R (every row block reads
+// all of its slice of R).  Wave w takes chunks c_beg + w, c_beg + w + nw, ... and adds them in
+// that order whatever TB, so TB does not change the bits.  RB: the accumulator blocks compiled in
+// (1 for r = 16, kMaxRB for any r up to 128).
+template <bool W32, int TB, int RB>
 __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice, int slices,
                                            int nw, int wg, int n_wg, float* red) {
+  constexpr int CIF = rows_chunks_in_flight<TB>();
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int m0 = rb * 16;
-  const int row = m0 + (lane & 15);
+  const int m0 = rb * 16 * TB;
   const int g = lane >> 4;
   const int rbn = a.r >> 4;
   const int chunks = a.K >> 5;
@@ -98,30 +106,42 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
   const int cps = (chunks + slices - 1) / slices;
   const int c_beg = slice * cps;
   const int c_end = min(chunks, c_beg + cps);
-  const bool row_ok = row < a.M;
-  const int64_t prow = (int64_t)(row_ok ? row : 0) * a.K + 8 * g;
-  float4_t acc[kMaxRB];
+  bool row_ok[TB];
+  int64_t prow[TB];
 #pragma unroll
-  for (int b = 0; b < kMaxRB; b++) acc[b] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  for (int c0 = c_beg + wave; wave < nw && c0 < c_end; c0 += kChunksInFlight * nw) {
-    half8_t x[kChunksInFlight];
+  for (int t = 0; t < TB; t++) {
+    const int row = m0 + 16 * t + (lane & 15);
+    row_ok[t] = row < a.M;
+    prow[t] = (int64_t)(row_ok[t] ? row : 0) * a.K + 8 * g;
+  }
+  float4_t acc[TB][RB];
 #pragma unroll
-    for (int u = 0; u < kChunksInFlight; u++) {
+  for (int t = 0; t < TB; t++)
+#pragma unroll
+    for (int b = 0; b < RB; b++) acc[t][b] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  for (int c0 = c_beg + wave; wave < nw && c0 < c_end; c0 += CIF * nw) {
+    half8_t x[CIF][TB];
+#pragma unroll
+    for (int u = 0; u < CIF; u++) {
       const int c = c0 + u * nw;
-      half8_t v = {};
-      if (c < c_end && row_ok) {
-        v = *reinterpret_cast<const half8_t*>(a.P + prow + 32 * c);
-        if (a.mask) v = drop8(v, *reinterpret_cast<const u32x2*>(a.mask + prow + 32 * c), a.mscale);
+#pragma unroll
+      for (int t = 0; t < TB; t++) {
+        half8_t v = {};
+        if (c < c_end && row_ok[t]) {
+          v = *reinterpret_cast<const half8_t*>(a.P + prow[t] + 32 * c);
+          if (a.mask)
+            v = drop8(v, *reinterpret_cast<const u32x2*>(a.mask + prow[t] + 32 * c), a.mscale);
+        }
+        x[u][t] = v;
       }
-      x[u] = v;
     }
 #pragma unroll
-    for (int b = 0; b < kMaxRB; b++) {
+    for (int b = 0; b < RB; b++) {
       if (b >= rbn) break;
       const int64_t roff = (int64_t)(16 * b + (lane & 15)) * a.K + 8 * g;
-      half8_t y[kChunksInFlight];
+      half8_t y[CIF];
 #pragma unroll
-      for (int u = 0; u < kChunksInFlight; u++) {
+      for (int u = 0; u < CIF; u++) {
         const int c = c0 + u * nw;
         if constexpr (W32)
           y[u] = c < c_end ? f32x8_to_f16(a.R32 + roff + 32 * c) : (half8_t){};
@@ -129,18 +149,22 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
           y[u] = c < c_end ? *reinterpret_cast<const half8_t*>(a.R + roff + 32 * c) : (half8_t){};
       }
 #pragma unroll
-      for (int u = 0; u < kChunksInFlight; u++)
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[u], y[u], acc[b], 0, 0, 0);
+      for (int u = 0; u < CIF; u++)
+#pragma unroll
+        for (int t = 0; t < TB; t++)
+          acc[t][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x[u][t], y[u], acc[t][b], 0, 0, 0);
     }
   }
-  // acc[b][v] = C[row 4*g + v][column 16*b + lane%16]
+  // acc[t][b][v] = C[row 16*t + 4*g + v][column 16*b + lane%16]
   const int ld = a.r + 1;
 #pragma unroll
-  for (int b = 0; b < kMaxRB; b++) {
+  for (int b = 0; b < RB; b++) {
     if (b >= rbn || wave >= nw) break;
 #pragma unroll
-    for (int v = 0; v < 4; v++)
-      red[(wave * 16 + 4 * g + v) * ld + 16 * b + (lane & 15)] = acc[b][v];
+    for (int t = 0; t < TB; t++)
+#pragma unroll
+      for (int v = 0; v < 4; v++)
+        red[(wave * 16 * TB + 16 * t + 4 * g + v) * ld + 16 * b + (lane & 15)] = acc[t][b][v];
   }
   // side outputs, spread over the workgroups: R^T [K, r], B^T [r, N] and (W32) fp16 B [N, r]
   if (a.rt) {
@@ -171,12 +195,13 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < 16 * a.r; i += blockDim.x) {
-    const int c = i >> 4, rr = i & 15;  // consecutive threads: consecutive m of one outT row
+  for (int i = threadIdx.x; i < 16 * TB * a.r; i += blockDim.x) {
+    // consecutive threads: consecutive m of one outT row
+    const int c = i / (16 * TB), rr = i % (16 * TB);
     const int m = m0 + rr;
     if (m >= a.ldt) continue;
     float sum = 0.f;
-    for (int w = 0; w < nw; w++) sum += red[(w * 16 + rr) * ld + c];
+    for (int w = 0; w < nw; w++) sum += red[(w * 16 * TB + rr) * ld + c];
     if (slices > 1 || a.partial_out) {  // this slice's partial, times s
       a.ws[((int64_t)slice * a.ldt + m) * a.r + c] = a.s * sum;
       continue;
@@ -187,10 +212,12 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
   }
 }
 
+template <int TB, int RB>
 __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
-  extern __shared__ float red[];  // [waves][16][r + 1]
-  rows_block<false>(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y, (int)blockDim.x >> 6,
-             (int)(blockIdx.y * gridDim.x + blockIdx.x), (int)(gridDim.x * gridDim.y), red);
+  extern __shared__ float red[];  // [waves][16 * TB][r + 1]
+  rows_block<false, TB, RB>(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y,
+                            (int)blockDim.x >> 6, (int)(blockIdx.y * gridDim.x + blockIdx.x),
+                            (int)(gridDim.x * gridDim.y), red);
 }
 
 // Several rows problems over the same tokens in one launch (the q/k/v or gate/up projections
@@ -200,19 +227,19 @@ constexpr int kMaxGroup = 4;
 struct RowsGroup {
   RowsArgs p[kMaxGroup];
   int start[kMaxGroup + 1];
-  int rbs[kMaxGroup], slices[kMaxGroup], nw[kMaxGroup];
+  int rbs[kMaxGroup], slices[kMaxGroup], nw[kMaxGroup];  // rbs: blocks of 16 * TB rows
   int n;
 };
 
-template <bool W32>
+template <bool W32, int TB, int RB>
 __global__ __launch_bounds__(1024) void k_lora_rows_group(RowsGroup g) {
-  extern __shared__ float red[];  // [waves][16][r + 1]
+  extern __shared__ float red[];  // [waves][16 * TB][r + 1]
   const int bid = (int)blockIdx.x;
   int i = 0;
   while (i + 1 < g.n && bid >= g.start[i + 1]) i++;
   const int local = bid - g.start[i];
-  rows_block<W32>(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i], g.nw[i], local,
-                  g.start[i + 1] - g.start[i], red);
+  rows_block<W32, TB, RB>(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i], g.nw[i],
+                          local, g.start[i + 1] - g.start[i], red);
 }
 
 // out[m][c] = fp16(sum of the slices' partials, in slice order) for m < M; outT [r, ldt]
@@ -335,12 +362,29 @@ static void rows_plan(const RowsArgs& a, bool have_ws, int* slices, int* nw) {
   *nw = w;
 }
 
+// 16-row blocks per rows workgroup: two where r = 16 and the launch still has at least 256
+// workgroups and 16 waves per CU with them (each R fragment then feeds two multiplies; measured
+// at 1024 tokens: gate/up's dHs over N = 8960, 256 workgroups of 16 waves, 14.8 -> 12.4 us,
+// while the short reductions of K = 1536, 4 waves per workgroup, got slower), else one.  The
+// choice does not change the bits (rows_block).
+static int rows_tb(int r, int64_t workgroups_at_two, int64_t waves_at_two) {
+  return r == 16 && workgroups_at_two >= 256 && waves_at_two >= 16 * 256 ? 2 : 1;
+}
+
 static int rows_launch(RowsArgs a, void* workspace, hipStream_t stream) {
   int slices, nw;
   rows_plan(a, workspace != nullptr, &slices, &nw);
   a.ws = static_cast<float*>(workspace);
-  const size_t lds = (size_t)nw * 16 * (a.r + 1) * sizeof(float);
-  hipLaunchKernelGGL(k_lora_rows, dim3((a.ldt + 15) / 16, slices), dim3(64 * nw), lds, stream, a);
+  const int64_t at_two = (int64_t)((a.ldt + 31) / 32) * slices;
+  const int tb = rows_tb(a.r, at_two, at_two * nw);
+  const size_t lds = (size_t)nw * 16 * tb * (a.r + 1) * sizeof(float);
+  const dim3 grid((a.ldt + 16 * tb - 1) / (16 * tb), slices);
+  if (a.r != 16)
+    hipLaunchKernelGGL((k_lora_rows<1, kMaxRB>), grid, dim3(64 * nw), lds, stream, a);
+  else if (tb == 2)
+    hipLaunchKernelGGL((k_lora_rows<2, 1>), grid, dim3(64 * nw), lds, stream, a);
+  else
+    hipLaunchKernelGGL((k_lora_rows<1, 1>), grid, dim3(64 * nw), lds, stream, a);
   if (slices > 1 && !a.partial_out)
     hipLaunchKernelGGL(k_lora_rows_finish, dim3((a.ldt + 63) / 64), dim3(64), 0, stream, a,
                        slices);
@@ -354,21 +398,42 @@ static int rows_group_launch(const RowsArgs* probs, int n, hipStream_t stream, b
   if (n < 1 || n > kMaxGroup) return MXS_ERR_ARG;
   RowsGroup g{};
   g.n = n;
-  int total = 0, nw_max = 1;
+  int nw_max = 1;
+  int64_t at_two = 0, waves_at_two = 0;
+  const int r = probs[0].r;
   for (int i = 0; i < n; i++) {
     g.p[i] = probs[i];
     rows_plan(g.p[i], g.p[i].ws != nullptr, &g.slices[i], &g.nw[i]);
-    g.rbs[i] = (g.p[i].ldt + 15) / 16;
-    g.start[i] = total;
-    total += g.rbs[i] * g.slices[i];
+    const int64_t wgs = (int64_t)((g.p[i].ldt + 31) / 32) * g.slices[i];
+    at_two += wgs;
+    waves_at_two += wgs * g.nw[i];
     nw_max = g.nw[i] > nw_max ? g.nw[i] : nw_max;
   }
+  const int tb = rows_tb(r, at_two, waves_at_two);
+  int total = 0;
+  for (int i = 0; i < n; i++) {
+    g.rbs[i] = (g.p[i].ldt + 16 * tb - 1) / (16 * tb);
+    g.start[i] = total;
+    total += g.rbs[i] * g.slices[i];
+  }
   g.start[n] = total;
-  const size_t lds = (size_t)nw_max * 16 * (probs[0].r + 1) * sizeof(float);
-  if (w32)
-    hipLaunchKernelGGL(k_lora_rows_group<true>, dim3(total), dim3(64 * nw_max), lds, stream, g);
-  else
-    hipLaunchKernelGGL(k_lora_rows_group<false>, dim3(total), dim3(64 * nw_max), lds, stream, g);
+  const size_t lds = (size_t)nw_max * 16 * tb * (r + 1) * sizeof(float);
+  const dim3 grid(total), block(64 * nw_max);
+  if (w32) {
+    if (r != 16)
+      hipLaunchKernelGGL((k_lora_rows_group<true, 1, kMaxRB>), grid, block, lds, stream, g);
+    else if (tb == 2)
+      hipLaunchKernelGGL((k_lora_rows_group<true, 2, 1>), grid, block, lds, stream, g);
+    else
+      hipLaunchKernelGGL((k_lora_rows_group<true, 1, 1>), grid, block, lds, stream, g);
+  } else {
+    if (r != 16)
+      hipLaunchKernelGGL((k_lora_rows_group<false, 1, kMaxRB>), grid, block, lds, stream, g);
+    else if (tb == 2)
+      hipLaunchKernelGGL((k_lora_rows_group<false, 2, 1>), grid, block, lds, stream, g);
+    else
+      hipLaunchKernelGGL((k_lora_rows_group<false, 1, 1>), grid, block, lds, stream, g);
+  }
   return check_launch();
 }
 
