@@ -309,11 +309,13 @@ def test_lora_finish_and_backward_sequence(cuda, n, k, M):
 
 
 @pytest.mark.parametrize("n,k,M", [(1536, 1536, 1024), (256, 1536, 1024), (1536, 1536, 300),
-                                   (256, 1536, 37), (8960, 1536, 1024), (1536, 8960, 512)])
+                                   (256, 1536, 37), (8960, 1536, 1024), (1536, 8960, 512),
+                                   (1536, 1536, 1200), (1536, 1536, 1430), (1536, 1536, 2048)])
 def test_bwd_dx_grads_one_launch(cuda, n, k, M):
     """mxs_nf4_linear_bwd_dx_grads equals mxs_nf4_linear_bwd_dx followed by mxs_lora_grads bit
     for bit, whether it fuses them (1536-wide projections) or not, and its gradients match the
-    float64 products."""
+    float64 products.  1200 tokens: 128x64 tiles with the gradient workgroups in a second round;
+    1430: 128x128 tiles and gradient workgroups in one round; 2048: not fused."""
     from mindxsoup_amd import kernels
 
     print(f"case bwd_dx_grads n={n} k={k} M={M}", flush=True)

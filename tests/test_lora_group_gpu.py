@@ -133,7 +133,7 @@ def test_grouped_qkv_gemm_equals_separate(cuda, M, lora):
         assert err < 1e-2, (i, float(err))
 
 
-@pytest.mark.parametrize("M", [1024, 300])
+@pytest.mark.parametrize("M", [1024, 512, 300])
 def test_grouped_qkv_backward_equals_separate(cuda, M):
     """mxs_nf4_linear_bwd_dx_grads_group over v, k, q (K = 1536) against each projection's
     mxs_nf4_linear_bwd_dx_grads: dX, dA and dB bit for bit."""
