@@ -259,9 +259,10 @@ def proj_bwd(p, saved, s=ALPHA / RANK):
 # the model produces together (q/k/v from attention's backward, gate/up from the SwiGLU's).
 FWD_GROUPS = [(0, 1, 2), (3,), (4, 5), (6,)]
 BWD_GROUPS = [(6,), (5, 4), (3,), (2, 1, 0)]
-# gate and up read one input: their input gradients, which a model adds, come from one summed
-# launch (the summed dX GEMM); q/k/v's stay separate here, as this step has no consumer for them
-SUM_DX_GROUPS = [(5, 4)]
+# Projections over one input, whose input gradients a model adds: each group's sum comes from
+# one summed launch (q/k/v: one tile loop over the three reductions, their dA / dB in the same
+# launch; gate/up: split-K planes of both reductions and one reduce)
+SUM_DX_GROUPS = [(5, 4), (2, 1, 0)]
 
 
 def layer_fwd(projs, s=ALPHA / RANK):

@@ -377,6 +377,36 @@ int mxs_nf4_linear_bwd_dx_grads_group(int n, const void* const dy[], int M, cons
                                       const void* const x[], float* const da[],
                                       float* const db[], void* const dx[], hipStream_t stream);
 
+/* 1 when mxs_nf4_linear_bwd_dx_grads_sum takes these n (2..3) projections [K -> N[i]] of one
+ * input at M tokens: rank r = 16, K >= 1024 and a multiple of 64, each N[i] a multiple of 64
+ * whose own dX launch runs unsplit (q, k and v; not gate and up, whose long reductions take the
+ * split-K pair); with the LoRA gradients (grads != 0) also each projection's dA / dB workgroups as
+ * mxs_nf4_linear_bwd_dx_grads would run them (up to 1152 tokens). */
+int mxs_nf4_linear_bwd_dx_grads_sum_ok(int n, int M, const int N[], int K, int r, int grads);
+
+/* The q, k and v projections' backward as autograd needs it: ONE dX for their shared input x,
+ *   dx = sum_i ( dy[i] . W_i + mask[i] * mask_scale * (lora_dh[i] . lora_at[i]^T) )  [M, K],
+ * and every projection's dA[i] / dB[i] (as mxs_nf4_linear_bwd_dx_grads), in one launch: each
+ * output tile runs the projections' reductions back to back (K-steps of dy[0] . W_0, then
+ * dy[1] . W_1, ...) into one fp32 accumulator that started from all their LoRA terms (each
+ * masked by its own keep bytes), and is rounded to fp16 once; the gradient workgroups follow
+ * the tiles.  The sum of mxs_nf4_linear_bwd_dx_grads_group's dx[i] rounded each and added in
+ * fp16 differs from it by the roundings of the parts (a couple of fp16 ulps).  Every projection
+ * has a keep mask or none does.  da and db NULL: the summed dX alone (dht, ht and x unused, may
+ * be NULL), where mxs_nf4_linear_bwd_dx_grads_sum_ok(..., 0) says so; the caller then takes
+ * dA / dB from mxs_lora_grads.  Reference: the per-projection input gradient of
+ * solution/linear4bit.py:51-57 (plus peft's LoRA branch), added by autograd for the shared
+ * input.  Only where mxs_nf4_linear_bwd_dx_grads_sum_ok says so (else MXS_ERR_SIZE). */
+int mxs_nf4_linear_bwd_dx_grads_sum(int n, const void* const dy[], int M, const int N[], int K,
+                                    const void* const packed[], const void* const absmax8[],
+                                    const float* const code[], const float* const absmax2[],
+                                    const float* const offset[], const void* const lora_dh[],
+                                    const void* const lora_at[], int r, const void* const mask[],
+                                    float mask_scale, const void* const dht[],
+                                    const void* const ht[], int ldt, const void* x,
+                                    float* const da[], float* const db[], void* dx,
+                                    hipStream_t stream);
+
 /* The up projection's forward with the SwiGLU after it (solution/mlp.py:42-43:
  * silu_mul(gate_proj(x), up_proj(x))): mxs_nf4_linear_fwd_hp (lora_hp may be NULL: no LoRA
  * term) writing y = up_proj(x) [M, N] and h = silu(gate) * y [M, N] from the same tile, with

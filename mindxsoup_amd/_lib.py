@@ -63,6 +63,9 @@ _SIGNATURES = {
     "mxs_nf4_linear_bwd_dx_grads_group_ok": [I32, I32, P, I32, I32],
     "mxs_nf4_linear_bwd_dx_grads_group": [I32, P, I32, P, I32, P, P, P, P, P, P, P, I32, P, F32, P,
                                           P, I32, P, P, P, P, P],
+    "mxs_nf4_linear_bwd_dx_grads_sum_ok": [I32, I32, P, I32, I32, I32],
+    "mxs_nf4_linear_bwd_dx_grads_sum": [I32, P, I32, P, I32, P, P, P, P, P, P, P, I32, P, F32, P, P,
+                                        I32, P, P, P, P, P],
     "mxs_nf4_linear_fwd_hp_group": [I32, P, I32, I32, P, P, P, P, P, P, P, P, I32, I32, P, I32, P,
                                     P, P],
     "mxs_qkv_rope": [P, P, P, P, I64, I64, I32, I32, I32, I32, I32, I32, I32, F32, F32, P],

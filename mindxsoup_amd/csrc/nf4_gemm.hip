@@ -1477,8 +1477,14 @@ struct ACopyC {
 
   // copy i (0 <= i < N) of K-step kt into ring slot `slot_bytes`
   __device__ __forceinline__ void copy(uint32_t slot_bytes, int kt, int i) const {
-    const char* src = base + (size_t)kt * kBK * sizeof(_Float16);
-    const uint32_t off = min(rowbase + 32u * i, last) * ldab + seg16;
+    copy_from(base, ldab, slot_bytes, kt, i);
+  }
+
+  // the same from another problem's A (row m0 at base_, ldab_ bytes per row; same rows)
+  __device__ __forceinline__ void copy_from(const char* base_, uint32_t ldab_,
+                                            uint32_t slot_bytes, int kt, int i) const {
+    const char* src = base_ + (size_t)kt * kBK * sizeof(_Float16);
+    const uint32_t off = min(rowbase + 32u * i, last) * ldab_ + seg16;
     const uint32_t dst = lds + slot_bytes + i * 32 * kBK * sizeof(_Float16);
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                  :
@@ -1507,8 +1513,24 @@ constexpr bool consumer_copies() {
 // roles are uniform branches, so neither side's registers live through the other's code.
 // One output tile (bx, by) of the warp-specialized GEMM; split index blockIdx.z - a.zf, partial
 // plane blockIdx.z.
-template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU>
-__device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
+// Backward tiles whose output is the sum of up to kMaxSum problems' input gradients (autograd
+// adds them for their shared input): their reductions run back to back in one K loop into one
+// accumulator.  Problem q owns K-steps [end[q-1], end[q]); a[0] carries the output.
+constexpr int kMaxSum = 3;
+struct SumPlan {
+  int n;
+  int end[kMaxSum];
+};
+
+// The warp-specialized tile.  NSUM = 1: one problem `as[0]`.  NSUM > 1: the summed problems of
+// `plan` (as[0 .. plan->n)): every K-step takes its operands (dY, the NF4 weight, its code
+// table and offset) from its problem, and the accumulator starts from all their LoRA terms.
+// The problems share M, the output width and the weight row length, LoRA rank 16 and the keep
+// mask's presence; the A copies are the consumers' (consumer_copies).
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU, int NSUM>
+__device__ __forceinline__ void ws_tile_impl(const GemmArgs* as, const SumPlan* plan, int bx,
+                                             int by) {
+  const GemmArgs& a = as[0];
   constexpr int WM = BM / CWM, WN = BN / CWN, TM = WM / 32, TN = WN / 32;
   constexpr int NTP = 64 * PW;  // producer threads
   static_assert(CWM * CWN == 4 && WM % 32 == 0 && WN % 32 == 0, "consumer wave tiles");
@@ -1527,14 +1549,37 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
   auto bbuf = [&](int x) { return Bs + ((x & 1) ^ 1) * LDS_B; };
   uint8_t* Ks = reinterpret_cast<uint8_t*>(As + 2 * LDS_A);
   static_assert(BM * MaskStage<BM, BN, NTP>::KST <= (LDS_A + LDS_B) * 2, "staged keep mask fits");
+  static_assert(NSUM == 1 || (BWD && !GLU && consumer_copies<BM, PW>()), "summed tiles");
   __shared__ float2_t s_pair[256];
-  __shared__ float s_code[256];
+  __shared__ float s_code[256 * NSUM];  // problem q's code book at 256 q
+  __shared__ float s_off[NSUM];         // summed tiles: problem q's absmax offset
+  // summed problems: their count, the problem of K-step k and its first K-step
+  const int nsum = NSUM == 1 ? 1 : plan->n;
+  auto prob = [&](int k) -> int {
+    int q = 0;
+    if constexpr (NSUM > 1) {
+#pragma unroll
+      for (int i = 0; i + 1 < NSUM; i++) q += (i + 1 < nsum && k >= plan->end[i]) ? 1 : 0;
+    }
+    return q;
+  };
+  auto first = [&](int q) -> int {
+    if constexpr (NSUM == 1) return 0;
+    else return q == 0 ? 0 : plan->end[q - 1];
+  };
+  // the extra LoRA operand and keep mask areas of problems 1.. (after the single-problem LDS)
+  constexpr int KSTH = BM * MaskStage<BM, BN, NTP>::KST / 2;  // keep-mask halfs
+  constexpr int XTRA = (BM + BN) * 16 + KSTH;
+  static_assert(XTRA % 8 == 0 && ws_lds_halfs<BM, BN, BWD>() % 8 == 0, "16-byte areas");
+  auto ls_of = [&](int q) -> _Float16* {
+    return q == 0 ? Ls : smem + ws_lds_halfs<BM, BN, BWD>() + (q - 1) * XTRA;
+  };
 
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int m0 = by * BM;
   const int n0 = bx * BN;
-  const int n_steps = a.Kr / kBK;
+  const int n_steps = NSUM == 1 ? a.Kr / kBK : plan->end[nsum - 1];
   const int kt0 = ((int)blockIdx.z - a.zf) * a.steps_per_split;
   const int kt1 = min(n_steps, kt0 + a.steps_per_split);
   // the producers stage the LoRA operands (r = 16) and the keep mask in LDS for the consumers
@@ -1554,11 +1599,36 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
     const int p = t - 256;
     const int pw = p >> 6;
     const bool run = kt0 < kt1;
-    LoraStage<BM, BN, NTP> lst;
-    MaskStage<BM, BN, NTP> mst;
-    if (lora16) lst.issue(a, p, m0, n0);  // before the tiles: one round trip for all
-    if (kmask) mst.issue(a, p, m0, n0);
-    const float offset = a.offset[0];
+    LoraStage<BM, BN, NTP> lst[NSUM];
+    MaskStage<BM, BN, NTP> mst[NSUM];
+    if (lora16) lst[0].issue(a, p, m0, n0);  // before the tiles: one round trip for all
+    if (kmask) mst[0].issue(a, p, m0, n0);
+#pragma unroll
+    for (int q = 1; q < NSUM; q++) {
+      if (q >= nsum) break;
+      if (lora16) lst[q].issue(as[q], p, m0, n0);
+      if (kmask) mst[q].issue(as[q], p, m0, n0);
+    }
+    // the offset of K-step k's problem: a register with one problem; in a summed tile read
+    // from LDS (s_off, written with the tables), not an indexed register array (which would
+    // live in scratch memory and make the compiler wait for every load in flight)
+    const float off0 = NSUM == 1 ? a.offset[0] : 0.0f;
+    auto offset_at = [&](int k) -> float {
+      if constexpr (NSUM == 1) return off0;
+      else return s_off[prob(k)];
+    };
+    auto code_at = [&](int k) -> const float* { return s_code + 256 * prob(k); };
+    auto commit_staged = [&]() {
+      if (lora16) lst[0].commit(a, Ls, p);
+      if (kmask) mst[0].commit(Ks, p);
+#pragma unroll
+      for (int q = 1; q < NSUM; q++) {
+        if (q >= nsum) break;
+        _Float16* lq = ls_of(q);
+        if (lora16) lst[q].commit(as[q], lq, p);
+        if (kmask) mst[q].commit(reinterpret_cast<uint8_t*>(lq + (BM + BN) * 16), p);
+      }
+    };
     // NF4 tile of K-step kt is issued NS steps ahead into register stage (kt - kt0) % NS; its
     // table lookups are issued one step ahead, right after the previous tile is finished, so
     // their LDS latency overlaps the loads and barrier of that step; it is finished (scaled,
@@ -1592,29 +1662,37 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
       const typename B::Src src = B::setup(a, p, n0);
       typename B::Stage S[NS];
       typename B::Looked L;
+      // B of K-step k from its problem's weight
+      auto issue = [&](typename B::Stage& St, int k) {
+        if constexpr (NSUM == 1) {
+          B::issue(a, src, St, k);
+        } else {
+          const int q = prob(k);
+          B::issue(as[q], src, St, k - first(q));
+        }
+      };
       if (run) {
 #pragma unroll
-        for (int u = 0; u < NS - 2; u++) B::issue(a, src, S[u], min(kt0 + u, last));
+        for (int u = 0; u < NS - 2; u++) issue(S[u], min(kt0 + u, last));
         if constexpr (!CC) ac.copy(0, kt0);
-        B::issue(a, src, S[NS - 2], min(kt0 + NS - 2, last));
+        issue(S[NS - 2], min(kt0 + NS - 2, last));
         if constexpr (!CC) ac.copy(SLOT, min(kt0 + 1, last));
-        B::issue(a, src, S[NS - 1], min(kt0 + NS - 1, last));
+        issue(S[NS - 1], min(kt0 + NS - 1, last));
       }
       if (lora16 || kmask) {
         if (run) wait_vmcnt<NS * LB + 2 * LA>();  // the staged loads, issued before all of those
         else wait_vmem_all();
-        if (lora16) lst.commit(a, Ls, p);
-        if (kmask) mst.commit(Ks, p);
+        commit_staged();
       }
       lds_barrier();  // tables, LoRA operands
       if (run) {
         wait_vmcnt<(NS - 1) * LB + 2 * LA>();  // B(kt0)
         B::ready(S[0]);
-        B::lookup(S[0], L, s_pair, s_code);
-        B::finish(S[0], L, bbuf(0), p, offset);
+        B::lookup(S[0], L, s_pair, code_at(kt0));
+        B::finish(S[0], L, bbuf(0), p, offset_at(kt0));
         wait_vmcnt<2 * LB + LA>();  // A(kt0) and what precedes it (B(kt0+1) among them)
         B::ready(S[1]);
-        B::lookup(S[1], L, s_pair, s_code);
+        B::lookup(S[1], L, s_pair, code_at(min(kt0 + 1, last)));
         lds_barrier();  // K-step kt0 ready
         // Sc = B(kt+1) (looked up in L), Sn = B(kt+2), Si = the stage of B(kt), free for B(kt+NS)
         auto step = [&](int kt, typename B::Stage& Sc, typename B::Stage& Sn,
@@ -1623,13 +1701,13 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
           // Unconditional: past the end the stages hold the last K-step again and bbuf(r + 1) is
           // the buffer of step kt - 1, no longer read; branches here would only give the
           // compiler paths to merge.
-          B::finish(Sc, L, bbuf(r + 1), p, offset);
+          B::finish(Sc, L, bbuf(r + 1), p, offset_at(min(kt + 1, last)));
           // B(kt+2); after it A(kt+5-NS) .. A(kt+1) and B(kt+3) .. B(kt+NS-1)
           wait_vmcnt<(NS - 3) * (LA + LB)>();
           B::ready(Sn);
-          B::lookup(Sn, L, s_pair, s_code);
+          B::lookup(Sn, L, s_pair, code_at(min(kt + 2, last)));
           if constexpr (!CC) ac.copy(((r + 2) % 3) * SLOT, min(kt + 2, last));
-          B::issue(a, src, Si, min(kt + NS, last));
+          issue(Si, min(kt + NS, last));
           // A(kt+1); after it only B(kt+NS-1), A(kt+2), B(kt+NS)
           if constexpr (!CC) wait_vmcnt<2 * LB + LA>();
           lds_barrier();
@@ -1659,8 +1737,7 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
       // no B items and no copies: the staged LoRA operands, then every barrier of the tile
       if (lora16 || kmask) {
         wait_vmem_all();  // the staged loads
-        if (lora16) lst.commit(a, Ls, p);
-        if (kmask) mst.commit(Ks, p);
+        commit_staged();
       }
       lds_barrier();  // tables, LoRA operands
       if (run) {
@@ -1676,8 +1753,7 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
       }
       if (lora16 || kmask) {
         wait_vmem_all();  // the staged loads (issued before the copies)
-        if (lora16) lst.commit(a, Ls, p);
-        if (kmask) mst.commit(Ks, p);
+        commit_staged();
       }
       lds_barrier();  // tables, LoRA operands
       if (run) {
@@ -1714,18 +1790,58 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
     constexpr uint32_t SLOT = LDS_A * sizeof(_Float16);
     const int lastk = kt1 - 1;
     AC ac;
+    if constexpr (CC) ac.init(a, As, wave, lane, m0);
+    // the summed problems' dY rows m0 and row bytes (uniform), selected per K-step by constant
+    // indices (so the array stays in scalar registers)
+    const char* abase[NSUM];
+    uint32_t aldab[NSUM];
+    if constexpr (NSUM > 1) {
+#pragma unroll
+      for (int q = 0; q < NSUM; q++) {
+        if (q >= nsum) break;
+        abase[q] = reinterpret_cast<const char*>(as[q].A + (int64_t)m0 * as[q].lda);
+        aldab[q] = __builtin_amdgcn_readfirstlane((uint32_t)as[q].lda * 2);
+      }
+    }
+    // copy i of K-step k (in a summed tile, from its problem's dY)
+    auto acopy = [&](uint32_t slot, int k, int i) {
+      if constexpr (NSUM == 1) {
+        ac.copy(slot, k, i);
+      } else {
+        const int q = prob(k);
+        const char* b = abase[0];
+        uint32_t l = aldab[0];
+#pragma unroll
+        for (int j = 1; j < NSUM; j++) {
+          b = q == j ? abase[j] : b;
+          l = q == j ? aldab[j] : l;
+        }
+        ac.copy_from(b, l, slot, k - first(q), i);
+      }
+    };
     if constexpr (CC) {
-      ac.init(a, As, wave, lane, m0);
       if (kt0 < kt1) {
 #pragma unroll
-        for (int i = 0; i < LA; i++) ac.copy(0, kt0, i);
+        for (int i = 0; i < LA; i++) acopy(0, kt0, i);
 #pragma unroll
-        for (int i = 0; i < LA; i++) ac.copy(SLOT, min(kt0 + 1, lastk), i);
+        for (int i = 0; i < LA; i++) acopy(SLOT, min(kt0 + 1, lastk), i);
       }
     }
     AccStart<TM, TN, BWD> start;
     start.load(a, n0 + wn0, lseg);  // before the tables' loads
     fill_tables(a, s_pair, s_code, t, 256);
+#pragma unroll
+    for (int q = 1; q < NSUM; q++) {
+      if (q >= nsum) break;
+      for (int i = t; i < 256; i += 256) s_code[256 * q + i] = as[q].code[i];
+    }
+    if constexpr (NSUM > 1) {
+#pragma unroll
+      for (int q = 0; q < NSUM; q++) {
+        if (q >= nsum) break;
+        if (t == q) s_off[q] = as[q].offset[0];
+      }
+    }
     float16_t acc[TM][TN];
     lds_barrier();  // tables, LoRA operands
     // accumulator start (bias, LoRA) while the producers stage K-step kt0
@@ -1735,6 +1851,20 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
     else
       start.finish(a, acc, m0 + wm0, n0 + wn0, lrow, lseg, wm0, wn0, nullptr, 0,
                    kmask ? Ks : nullptr, MaskStage<BM, BN, NTP>::KST);
+    // the other summed problems' LoRA terms, each masked by its own keep bytes, added in order
+#pragma unroll
+    for (int q = 1; q < NSUM; q++) {
+      if (q >= nsum) break;
+      float16_t part[TM][TN];
+      const _Float16* lq = ls_of(q);
+      start.finish_staged(as[q], part, m0 + wm0, n0 + wn0, lrow, lseg, wm0, wn0, lq, BM,
+                          kmask ? reinterpret_cast<const uint8_t*>(lq + (BM + BN) * 16) : nullptr,
+                          MaskStage<BM, BN, NTP>::KST);
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] += part[i][j];
+    }
     if (kt0 < kt1) {
       if constexpr (CC) wait_vmcnt<LA>();  // A(kt0); after it only A(kt0+1)
       lds_barrier();                        // K-step kt0 ready
@@ -1817,7 +1947,7 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
             // A(kt+2) into the ring slot step kt-1 used, spread over the sub-steps
 #pragma unroll
             for (int i = kk * LA / 3; i < (kk + 1) * LA / 3; i++)
-              ac.copy(((r + 2) % 3) * SLOT, min(kt + 2, lastk), i);
+              acopy(((r + 2) % 3) * SLOT, min(kt + 2, lastk), i);
           }
         }
         if constexpr (CC) wait_vmcnt<LA>();  // A(kt+1); after it only A(kt+2)
@@ -1845,6 +1975,11 @@ __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
     epilogue_staged<TM, TN>(a, acc, m0 + wm0, n0 + wn0, lane,
                             reinterpret_cast<float*>(As) + wave * StagedStore<TM, TN>::AREA_DWORDS);
   }
+}
+
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU>
+__device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
+  ws_tile_impl<BM, BN, CWM, CWN, BWD, PW, NS, GLU, 1>(&a, nullptr, bx, by);
 }
 
 template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU>
@@ -2189,6 +2324,80 @@ static int launch_ws_group(const GemmArgs* probs, int n, hipStream_t stream) {
   return e == hipSuccess ? MXS_OK : (int)e;
 }
 
+// The summed backward (ws_tile_impl with NSUM > 1) in one launch with each problem's LoRA
+// gradient workgroups: workgroups [0, tiles) are the shared output's tiles in row-major order
+// over gx column tiles, then problem q's gradient workgroups from cstart[q].
+struct GemmSum {
+  GemmArgs p[kMaxSum];
+  SumPlan plan;
+  int gx, tiles;
+  int cstart[kMaxSum + 1];
+};
+
+template <int BM, int BN, int CWM, int CWN, int PW, int NS>
+__global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws_sum(GemmSum g) {
+  const int bid = (int)blockIdx.x;
+  if (bid >= g.tiles) {  // before any barrier of the tiles, as in k_nf4_gemm_ws
+    extern __shared__ __attribute__((aligned(16))) _Float16 smem[];
+    int q = 0;
+    while (q + 1 < g.plan.n && bid >= g.cstart[q + 1]) q++;
+    const GemmArgs& a = g.p[q];
+    const int id = bid - g.cstart[q];
+    if (id < a.cols_blocks)
+      lora_cols_block<kFusedColsCPL>(a.cp0, a.cp1, a.cols_cb0, a.M, a.cols_ldt, a.r, id,
+                                     a.cols_nw, reinterpret_cast<float*>(smem));
+    return;
+  }
+  ws_tile_impl<BM, BN, CWM, CWN, true, PW, NS, false, kMaxSum>(g.p, &g.plan, bid % g.gx,
+                                                               bid / g.gx);
+}
+
+// LDS halfs of the summed kernel: the single-problem layout, then problems 1 and 2's staged LoRA
+// operands ([BM][16] + [BN][16]) and keep bytes (BM rows of BN + 4)
+template <int BM, int BN>
+constexpr int ws_sum_lds_halfs() {
+  return ws_lds_halfs<BM, BN, true>() + (kMaxSum - 1) * ((BM + BN) * 16 + BM * (BN + 4) / 2);
+}
+
+template <int BN>
+static int launch_ws_sum(const GemmArgs* probs, int n, hipStream_t stream) {
+  constexpr int BM = 128, PW = 8, NS = 4;
+  if (n < 2 || n > kMaxSum) return MXS_ERR_ARG;
+  GemmSum g{};
+  g.plan.n = n;
+  int end = 0;
+  for (int q = 0; q < kMaxSum; q++) {
+    if (q < n) {
+      g.p[q] = probs[q];
+      end += probs[q].Kr / kBK;
+    }
+    g.plan.end[q] = end;
+  }
+  const GemmArgs& a = g.p[0];
+  g.p[0].steps_per_split = end;  // one split over the concatenated reduction
+  g.p[0].zf = 0;
+  g.gx = (a.Nc + BN - 1) / BN;
+  g.tiles = g.gx * ((a.M + BM - 1) / BM);
+  g.cstart[0] = g.tiles;
+  for (int q = 0; q < n; q++) g.cstart[q + 1] = g.cstart[q] + g.p[q].cols_blocks;
+  for (int q = n; q < kMaxSum; q++) g.cstart[q + 1] = g.cstart[q];
+  const int total = g.cstart[n];
+  if (total == 0) return MXS_OK;
+  const size_t lds = (size_t)ws_sum_lds_halfs<BM, BN>() * sizeof(_Float16);
+  static bool lds_set = false;  // idempotent attribute; a benign race between threads
+  if (!lds_set) {
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&k_nf4_gemm_ws_sum<BM, BN, 2, 2, PW, NS>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+    lds_set = true;
+  }
+  hipLaunchKernelGGL((k_nf4_gemm_ws_sum<BM, BN, 2, 2, PW, NS>), dim3(total), dim3(64 * (4 + PW)),
+                     lds, stream, g);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MXS_OK : (int)e;
+}
+
 // Two problems of one output shape whose results are added (the gate and up projections' input
 // gradients: autograd sums them for the shared input) in ONE launch of the split-K kernel:
 // problem 0 owns grid z [0, sp), problem 1 [sp, 2 sp), each splitting its own reduction over
@@ -2312,6 +2521,40 @@ static int dx_grads_args(const void* dy, int M, int N, int K, const void* packed
   a.cols_ldt = ldt;
   a.cols_nw = nw;
   return MXS_OK;
+}
+
+// Problems the summed dX launch takes (k_nf4_gemm_ws_sum: 2..3 problems over one input of
+// K >= 1024 columns, rank 16, 128-row tiles): the 32-bit offsets of the tile kernel and, with
+// the LoRA gradients (grads), each problem's gradient workgroups as its fused launch would run
+// them (same columns per lane and waves: up to 1152 tokens, where the sum over tokens needs at
+// most the kernel's 12 waves).  *bn: 64 where the output's 128x64 tiles fit the CUs once and,
+// with every gradient workgroup, twice; else 128.
+static bool dx_grads_sum_ok(int n, int M, const int* N, int K, int r, bool grads, int* bn,
+                            int* nw) {
+  if (n < 2 || n > kMaxSum || M <= 0 || K < 1024 || K % kBK != 0 || r != 16) return false;
+  *nw = grads ? cols_waves(M, r, kFusedColsCPL, cols_max_waves<kFusedColsCPL>()) : 0;
+  if (*nw > 12) return false;  // the 8-producer kernel's 12 waves
+  constexpr int WC = 16 * kFusedColsCPL;
+  int64_t cols = 0;
+  for (int i = 0; i < n; i++) {
+    if (N[i] <= 0 || N[i] % kBK != 0 || (int64_t)K * N[i] >= (int64_t(1) << 32) ||
+        (int64_t)128 * N[i] * 2 >= (int64_t(1) << 32))
+      return false;
+    // only reductions each problem's own launch runs unsplit (q, k, v): a long one (gate and up,
+    // N = 8960) re-reads dY from L2 for every column tile (154 against 101 us for the split-K
+    // pair at 1024 tokens)
+    int cfg, sp;
+    choose(M, K, N[i], true, &cfg, &sp);
+    if (sp != 1) return false;
+    if (grads && cols_cpl(K + N[i]) != kFusedColsCPL) return false;
+    if (grads) cols += (K + WC - 1) / WC + (N[i] + WC - 1) / WC;
+  }
+  if ((size_t)*nw * r * (WC + 1) * 4 > (size_t)ws_sum_lds_halfs<128, 64>() * sizeof(_Float16))
+    return false;
+  const int64_t tiles64 = (int64_t)((M + 127) / 128) * ((K + 63) / 64);
+  const int cus = cu_count();
+  *bn = (cus > 0 && tiles64 <= cus && tiles64 + cols <= 2 * (int64_t)cus) ? 64 : 128;
+  return true;
 }
 
 // Problems the grouped dX + LoRA-gradient launch takes: each fusable on the 128x128 tiles.
@@ -2507,6 +2750,48 @@ int mxs_nf4_linear_bwd_dx_grads_group(int n, const void* const dy[], int M, cons
   }
   if (t64 && wgs <= 2 * (int64_t)cu_count()) return launch_ws_group<true, 64>(probs, n, stream);
   return launch_ws_group<true>(probs, n, stream);
+}
+
+int mxs_nf4_linear_bwd_dx_grads_sum_ok(int n, int M, const int N[], int K, int r, int grads) {
+  int bn, nw;
+  return N && dx_grads_sum_ok(n, M, N, K, r, grads != 0, &bn, &nw) ? 1 : 0;
+}
+
+int mxs_nf4_linear_bwd_dx_grads_sum(int n, const void* const dy[], int M, const int N[], int K,
+                                    const void* const packed[], const void* const absmax8[],
+                                    const float* const code[], const float* const absmax2[],
+                                    const float* const offset[], const void* const lora_dh[],
+                                    const void* const lora_at[], int r, const void* const mask[],
+                                    float mask_scale, const void* const dht[],
+                                    const void* const ht[], int ldt, const void* x,
+                                    float* const da[], float* const db[], void* dx,
+                                    hipStream_t stream) {
+  if (n < 2 || n > kMaxSum || !dy || !N || !packed || !absmax8 || !code || !absmax2 || !offset ||
+      !lora_dh || !lora_at || !dx)
+    return MXS_ERR_ARG;
+  const bool grads = da != nullptr;  // dA and dB, or neither
+  if (grads != (db != nullptr) || (grads && (!dht || !ht || !x))) return MXS_ERR_ARG;
+  int bn, nw;
+  if (!dx_grads_sum_ok(n, M, N, K, r, grads, &bn, &nw)) return MXS_ERR_SIZE;
+  GemmArgs probs[kMaxSum];
+  const bool masked = mask && mask[0];
+  for (int i = 0; i < n; i++) {
+    if (!lora_dh[i] || !lora_at[i] || (grads && (!dht[i] || !ht[i] || !da[i] || !db[i])))
+      return MXS_ERR_ARG;
+    const void* mk = mask ? mask[i] : nullptr;
+    if ((mk != nullptr) != masked) return MXS_ERR_ARG;  // every problem masked, or none
+    // without the gradients the LoRA-gradient operands are stand-ins (the 16-byte aligned dY)
+    // that no workgroup reads: cols_blocks is zeroed below
+    int e = dx_grads_args(dy[i], M, N[i], K, packed[i], absmax8[i], code[i], absmax2[i],
+                          offset[i], lora_dh[i], lora_at[i], r, mk, mask_scale,
+                          grads ? dht[i] : dy[i], grads ? ht[i] : dy[i], ldt, grads ? x : dy[i],
+                          grads ? da[i] : nullptr, grads ? db[i] : nullptr, dx, nw, probs[i]);
+    if (e != MXS_OK) return e;
+    if (!grads) probs[i].cols_blocks = 0;
+    e = check_gemm(true, probs[i]);
+    if (e != MXS_OK) return e == 1 ? MXS_ERR_SIZE : e;
+  }
+  return bn == 64 ? launch_ws_sum<64>(probs, n, stream) : launch_ws_sum<128>(probs, n, stream);
 }
 
 int mxs_nf4_linear_fwd_hp(const void* x, int M, int K, int N, const void* packed,

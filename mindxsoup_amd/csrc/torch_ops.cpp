@@ -637,6 +637,96 @@ Lists3 lora_bwd_group_cuda(TensorList dy, const Tensor& x, const OptTensorList& 
   auto want = [&](size_t i, int j) { return wants[3 * i + j] != 0; };
 
   std::vector<Tensor> dxs(n), das(n), dbs(n), dh(n), dht(n), dhp(n);
+  // Summed (q, k and v over one input): every flag set, one keep-mask presence, and a plan the
+  // summed launch takes: dHs finished for all in one launch, then ONE launch for the summed dX
+  // and every dA / dB (the sum rounded once, not each part and then added).
+  if (sum_dx && n >= 2 && n <= 3) {
+    bool all = true;
+    std::array<int, kMaxGroup> Ns{};
+    for (size_t i = 0; i < n; ++i) {
+      all = all && want(i, 0) && want(i, 1) && want(i, 2) &&
+            o[i].mask.defined() == o[0].mask.defined();
+      Ns[i] = o[i].N;
+    }
+    if (all && mxs_nf4_linear_bwd_dx_grads_sum_ok((int)n, M, Ns.data(), K, r, 0)) {
+      // with the gradients in the same launch up to 1152 tokens; past that the summed dX alone,
+      // then dA / dB in one launch per weight height (k and v share one)
+      const bool fused = mxs_nf4_linear_bwd_dx_grads_sum_ok((int)n, M, Ns.data(), K, r, 1) != 0;
+      std::array<const void*, kMaxGroup> pdy{}, pbt{}, pk{}, pa8{}, pdhc{}, pat{}, pm{}, pdhtc{},
+          pht{};
+      std::array<void*, kMaxGroup> pdh{}, pdht{};
+      std::array<const float*, kMaxGroup> pc{}, pa2{}, po{};
+      std::array<float*, kMaxGroup> pda{}, pdb{};
+      for (size_t i = 0; i < n; ++i) {
+        const BwdOperands& q = o[i];
+        dh[i] = at::empty({M, r}, f16);
+        dht[i] = at::empty({r, ldt}, f16);
+        das[i] = at::empty({r, K}, f16.dtype(at::kFloat));
+        dbs[i] = at::empty({q.N, r}, f16.dtype(at::kFloat));
+        pdy[i] = q.dy.data_ptr();
+        pbt[i] = q.bt.data_ptr();
+        pdh[i] = dh[i].data_ptr();
+        pdht[i] = dht[i].data_ptr();
+        pdhc[i] = pdh[i];
+        pdhtc[i] = pdht[i];
+        pk[i] = q.w.packed;
+        pa8[i] = q.w.absmax8;
+        pc[i] = q.w.code;
+        pa2[i] = q.w.absmax2;
+        po[i] = q.w.offset;
+        pat[i] = q.at.data_ptr();
+        pm[i] = ptr(q.mask);
+        pht[i] = q.ht.data_ptr();
+        pda[i] = das[i].data_ptr<float>();
+        pdb[i] = dbs[i].data_ptr<float>();
+      }
+      ok(mxs_lora_dh_group((int)n, pdy.data(), M, Ns.data(), pbt.data(), r, sf, ldt, pdh.data(),
+                           pdht.data(), st),
+         "mxs_lora_dh_group");
+      dxs[0] = at::empty({M, K}, f16);
+      ok(mxs_nf4_linear_bwd_dx_grads_sum((int)n, pdy.data(), M, Ns.data(), K, pk.data(),
+                                         pa8.data(), pc.data(), pa2.data(), po.data(),
+                                         pdhc.data(), pat.data(), r, pm.data(), ms, pdhtc.data(),
+                                         pht.data(), ldt, o[0].x.data_ptr(),
+                                         fused ? pda.data() : nullptr,
+                                         fused ? pdb.data() : nullptr, dxs[0].data_ptr(), st),
+         "mxs_nf4_linear_bwd_dx_grads_sum");
+      if (!fused) {
+        std::vector<bool> done(n, false);
+        for (size_t i = 0; i < n; ++i) {
+          if (done[i]) continue;
+          std::array<const void*, kMaxGroup> gdht{}, ght{}, gx{}, gdy{}, gm{};
+          std::array<int, kMaxGroup> gK{}, gN{};
+          std::array<float*, kMaxGroup> gda{}, gdb{};
+          int cnt = 0;
+          for (size_t j = i; j < n; ++j) {
+            if (done[j] || o[j].N != o[i].N) continue;
+            done[j] = true;
+            gdht[cnt] = dht[j].data_ptr();
+            ght[cnt] = o[j].ht.data_ptr();
+            gx[cnt] = o[j].x.data_ptr();
+            gdy[cnt] = o[j].dy.data_ptr();
+            gm[cnt] = ptr(o[j].mask);
+            gK[cnt] = K;
+            gN[cnt] = o[j].N;
+            gda[cnt] = das[j].data_ptr<float>();
+            gdb[cnt] = dbs[j].data_ptr<float>();
+            ++cnt;
+          }
+          if (cnt > 1)
+            ok(mxs_lora_grads_group(cnt, gdht.data(), ght.data(), ldt, gx.data(), gdy.data(), M,
+                                    gK.data(), gN.data(), r, gm.data(), ms, gda.data(),
+                                    gdb.data(), st),
+               "mxs_lora_grads_group");
+          else
+            ok(mxs_lora_grads(gdht[0], ght[0], ldt, gx[0], gdy[0], M, K, gN[0], r, gm[0], ms,
+                              gda[0], gdb[0], nullptr, st),
+               "mxs_lora_grads");
+        }
+      }
+      return {dxs, das, dbs};
+    }
+  }
   std::vector<size_t> fin, par;
   for (size_t i = 0; i < n; ++i) {
     if (dh_finished(M, o[i].N, K, r, want(i, 0), want(i, 1), want(i, 2)))

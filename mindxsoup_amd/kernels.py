@@ -262,6 +262,52 @@ def nf4_linear_bwd_dx_grads_group(dys, packeds, states, dhs, ats, dhts, hts, x2d
     return list(zip(dx, da, db))
 
 
+def bwd_grads_sum_ok(M, Ns, K, r, grads=True):
+    """True when nf4_linear_bwd_dx_grads_sum takes projections [K -> N] for N in Ns (with their
+    LoRA gradients in the same launch, or, grads=False, the summed dX alone)."""
+    return bool(_lib.lib().mxs_nf4_linear_bwd_dx_grads_sum_ok(len(Ns), M, _int_array(Ns), K, r,
+                                                             int(bool(grads))))
+
+
+def nf4_linear_bwd_dx_grads_sum(dys, packeds, states, dhs, ats, dhts, hts, x2d, masks=None,
+                                mask_scale=1.0, grads=True):
+    """The backward of 2..3 projections over one input x2d in one launch: (dx, [(dA, dB), ..]),
+    dx = the sum of their input gradients (one fp32 accumulator, rounded once), dA / dB the bits
+    of nf4_linear_bwd_dx_grads (grads=False: (dx, None), the summed dX alone).  Only where
+    bwd_grads_sum_ok(..., grads); every projection has a keep mask or none does."""
+    n = len(dys)
+    masks = masks or [None] * n
+    if any(m is None for m in masks) and any(m is not None for m in masks):
+        raise ValueError("every projection has a keep mask, or none does")
+    dys = [d.contiguous() for d in dys]
+    x2d = x2d.contiguous()
+    M, K = x2d.shape
+    r = dhs[0].shape[1]
+    Ns = [st.shape[0] for st in states]
+    for d, st, dh, at, dht, ht in zip(dys, states, dhs, ats, dhts, hts):
+        if d.shape != (M, st.shape[0]) or st.shape[1] != K:
+            raise ValueError("dy [M, N], x [M, K] and the weight [N, K] disagree")
+        if dh.shape != (M, r) or at.shape != (K, r) or dht.shape[0] != r or ht.shape != dht.shape:
+            raise ValueError("LoRA operands disagree")
+    dev = x2d.device
+    for pk, st in zip(packeds, states):
+        check_nf4_operands(pk, st, dev)
+    dx = torch.empty((M, K), dtype=torch.float16, device=dev)
+    da = [torch.empty((r, K), dtype=torch.float32, device=dev) for _ in dys] if grads else None
+    db = [torch.empty((nn_, r), dtype=torch.float32, device=dev) for nn_ in Ns] if grads else None
+    masks = [_c(m) for m in masks]
+    _lib.call("mxs_nf4_linear_bwd_dx_grads_sum", n, _ptr_array(dys), M, _int_array(Ns), K,
+              _ptr_array(packeds), _ptr_array([st.absmax for st in states]),
+              _ptr_array([st.state2.code for st in states]),
+              _ptr_array([st.state2.absmax for st in states]),
+              _ptr_array([st.offset for st in states]), _ptr_array([_c(t) for t in dhs]),
+              _ptr_array([_c(t) for t in ats]), r, _ptr_array(masks), float(mask_scale),
+              _ptr_array([_c(t) for t in dhts]), _ptr_array([_c(t) for t in hts]),
+              dhts[0].shape[1], _lib.ptr(x2d), _ptr_array(da) if grads else None,
+              _ptr_array(db) if grads else None, _lib.ptr(dx), _lib.stream_of(dev))
+    return dx, list(zip(da, db)) if grads else None
+
+
 def lora_slices(M, Kr):
     """Reduction slices the partial-sum LoRA kernels use (1..4)."""
     return int(_lib.lib().mxs_lora_slices(M, Kr))

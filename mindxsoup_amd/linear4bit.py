@@ -210,6 +210,56 @@ def _pair_takes(items, pre):
                                        x0.shape[1]))
 
 
+def _sum_takes(items):
+    """The summed launch (kernels.nf4_linear_bwd_dx_grads_sum) takes these projections: 2..3 over
+    one input, every gradient wanted, one LoRA scaling and dropout scale, a keep mask for every
+    one or none, and a plan the library takes (q, k and v)."""
+    if not 2 <= len(items) <= 3:
+        return False
+    a = items[0]
+    x = a["x2d"]
+    masked = a["keep"] is not None
+    for it in items:
+        if (tuple(it["wants"]) != (True, True, True) or it["x2d"].data_ptr() != x.data_ptr()
+                or it["x2d"].shape != x.shape or it["s"] != a["s"]
+                or it["mask_scale"] != a["mask_scale"] or (it["keep"] is not None) != masked):
+            return False
+    return kernels.bwd_grads_sum_ok(x.shape[0], [it["state"].shape[0] for it in items],
+                                    x.shape[1], a["bt"].shape[0], grads=False)
+
+
+def _backward_summed(items):
+    """dHs of all items in one launch, then one launch for their summed dX and (up to 1152
+    tokens) every dA / dB; past that the summed dX alone, then dA / dB in one launch per
+    weight height (k and v share one)."""
+    a = items[0]
+    x = a["x2d"]
+    dhs = kernels.lora_dh_group([it["dy"] for it in items], [it["bt"] for it in items], a["s"])
+    Ns = [it["state"].shape[0] for it in items]
+    fused = kernels.bwd_grads_sum_ok(x.shape[0], Ns, x.shape[1], a["bt"].shape[0])
+    dx, grads = kernels.nf4_linear_bwd_dx_grads_sum(
+        [it["dy"] for it in items], [it["packed"] for it in items],
+        [it["state"] for it in items], [d[0] for d in dhs], [it["at"] for it in items],
+        [d[1] for d in dhs], [it["ht"] for it in items], x,
+        [it["keep"] for it in items], a["mask_scale"], grads=fused)
+    if grads is None:
+        grads = [None] * len(items)
+        for n_ in dict.fromkeys(Ns):
+            idx = [i for i, n2 in enumerate(Ns) if n2 == n_]
+            if len(idx) > 1:
+                res = kernels.lora_grads_group([dhs[i][1] for i in idx],
+                                               [items[i]["ht"] for i in idx], [x] * len(idx),
+                                               [items[i]["dy"] for i in idx],
+                                               [items[i]["keep"] for i in idx], a["mask_scale"])
+            else:
+                i = idx[0]
+                res = [kernels.lora_grads(dhs[i][1], items[i]["ht"], x, items[i]["dy"],
+                                          items[i]["keep"], a["mask_scale"])]
+            for i, r in zip(idx, res):
+                grads[i] = r
+    return [(dx if i == 0 else None, da, db) for i, (da, db) in enumerate(grads)]
+
+
 def lora_backward_group(items, ws=None, sum_dx=False):
     """lora_backward for up to 4 projections over the same tokens whose output gradients arrive
     together (q/k/v from attention's backward, gate/up from the SwiGLU's), with their small
@@ -219,10 +269,14 @@ def lora_backward_group(items, ws=None, sum_dx=False):
     keep, ht, at, bt, packed, state, mask_scale, s and wants = (want_x, want_a, want_b).
     Returns [(dx, dA, dB)], the bits of lora_backward on each.
     sum_dx (projections over one input, whose input gradients autograd adds): the first item's
-    dx is the sum of all the items' (added in item order), the others' None; two projections
-    the summed launch takes (_pair_takes: gate and up) get their sum from that one launch, the
-    fp32 sum rounded once instead of each part rounded and added."""
+    dx is the sum of all the items' (added in item order), the others' None; projections a
+    summed launch takes get their sum from that one launch, the fp32 sum rounded once instead
+    of each part rounded and added: q, k and v (_sum_takes: one tile loop over their three
+    reductions, with every dA / dB in the same launch), gate and up (_pair_takes: split-K
+    planes of both reductions and one reduce)."""
     n = len(items)
+    if sum_dx and _sum_takes(items):
+        return _backward_summed(items)
     pre = prepare_dh([(it["dy"], it["bt"], it["x2d"].shape[1], it["s"], it["wants"])
                       for it in items])
     out = [None] * n

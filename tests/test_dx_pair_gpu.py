@@ -92,9 +92,9 @@ def test_pair_refuses_other_plans(cuda):
 
 
 def test_group_backward_sums(cuda):
-    """lora_backward_group(sum_dx=True) on gate and up gives the pair's dx in the first item and
-    the separate launches' LoRA gradients; on q/k/v (no pair) the in-order fp16 sum of the
-    separate dx."""
+    """lora_backward_group(sum_dx=True) gives one dx in the first item, the separate launches'
+    sum within their roundings, and the separate launches' LoRA gradients: on gate and up from
+    the pair, on q/k/v from the summed tile loop (tests/test_dx_sum_gpu.py)."""
     from mindxsoup_amd import kernels
     from mindxsoup_amd.linear4bit import lora_backward_group
 
@@ -118,9 +118,5 @@ def test_group_backward_sums(cuda):
         two = apart[0][0]
         for r in apart[1:]:
             two = two + r[0]
-        if paired:
-            err = ((summed[0][0].float() - two.float()).abs().max()
-                   / two.float().abs().max()).item()
-            assert 0 < err < 2 ** -9, err
-        else:
-            assert torch.equal(summed[0][0], two)
+        err = ((summed[0][0].float() - two.float()).abs().max() / two.float().abs().max()).item()
+        assert 0 < err < 2 ** -9, (paired, err)

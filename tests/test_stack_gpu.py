@@ -1,7 +1,8 @@
 """The step bench.py times for BASELINE configs[4] (one decoder layer's 7 NF4 + LoRA projections,
 forward then backward, with the grouped launches the timed stack uses), checked projection by
 projection against the float64 oracle at M = 1024 tokens: y, dX, dA and dB within the north
-star's max relative error 1e-2."""
+star's max relative error 1e-2 (the summed dX of q/k/v and of gate/up against the oracle's
+sums)."""
 
 import numpy as np
 import pytest
@@ -35,7 +36,10 @@ def test_timed_layer_step_matches_oracle(cuda):
     names = [name for name, _, _ in bench.PROJ]
     ig, iu = names.index("gate"), names.index("up")
     assert grads[ig][0] is None and grads[iu][0] is not None
+    iq, ik, iv = names.index("q"), names.index("k"), names.index("v")
+    assert grads[iq][0] is None and grads[ik][0] is None and grads[iv][0] is not None
     ref_dx_sum = 0.0
+    ref_qkv = 0.0
     for (name, n, k), pr, y, (dx, da, db) in zip(bench.PROJ, projs, ys, grads):
         st = pr["st"]
         w = O.dequant(O.NF4Weight(st.shape, pr["packed"].view(-1).cpu().numpy(),
@@ -51,6 +55,10 @@ def test_timed_layer_step_matches_oracle(cuda):
             ref_dx_sum = ref_dx_sum + ref_dx
             if name == "up":
                 errs["dx(gate+up)"] = O.max_rel(_np(dx), ref_dx_sum)
+        elif name in ("q", "k", "v"):
+            ref_qkv = ref_qkv + ref_dx
+            if name == "v":
+                errs["dx(q+k+v)"] = O.max_rel(_np(dx), ref_qkv)
         else:
             errs["dx"] = O.max_rel(_np(dx), ref_dx)
         print(f"case stack layer {name}: " + " ".join(f"{k_}={v:.1e}" for k_, v in errs.items()),
