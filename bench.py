@@ -560,6 +560,50 @@ def bench_qkv_rope(dev, g, steps, warmup):
         us = ms * 1e3 / reps
         res[name] = {"us": round(us, 2), "bytes": nbytes, "GBps": round(nbytes / us / 1e3, 1),
                      "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 3)}
+    res["qkv_proj"] = bench_qkv_fold(dev, g, steps, warmup, cos, sin)
+    return res
+
+
+def bench_qkv_fold(dev, g, steps, warmup, cos, sin):
+    """The attention path's q/k/v forward at 1024 tokens (q 1536, k and v 256 over K = 1536,
+    LoRA partials and bias): the grouped GEMM followed by the rotation launch, against the
+    grouped GEMM with the rotation in its epilogue (the same bits).  Four weight sets rotated
+    so the weights come from HBM; us per layer."""
+    from mindxsoup_amd import kernels
+
+    s, T = ALPHA / RANK, M_TOKENS
+    sets = []
+    for _ in range(4):
+        ps = [make_proj(dev, g, n, 1536) for n in (1536, 256, 256)]
+        x = ps[0]["x"]
+        hps = [o[0] for o in kernels.lora_h_partials_group([x] * 3, [p["a"] for p in ps], s,
+                                                           None, 1.0, [p["b"] for p in ps])]
+        bias = [(torch.randn((p["n"],), device=dev, generator=g) * 0.1).half() for p in ps]
+        qo = torch.empty((1, T, 1536), device=dev, dtype=torch.float16)
+        ko = torch.empty((1, T, 256), device=dev, dtype=torch.float16)
+        sets.append((x, ps, hps, bias, qo, ko))
+
+    def heads(y, h):
+        return y.view(1, T, h, 128).transpose(1, 2)
+
+    def apart():
+        for x, ps, hps, bias, qo, ko in sets:
+            out = kernels.nf4_linear_fwd_hp_group([x] * 3, [p["packed"] for p in ps],
+                                                  [p["st"] for p in ps], hps,
+                                                  [p["b"] for p in ps], bias)
+            kernels.qkv_rope(heads(out[0][0], 12), None, heads(out[1][0], 2), None, None, cos,
+                             sin, heads(qo, 12), heads(ko, 2), None)
+
+    def folded():
+        for x, ps, hps, bias, _, _ in sets:
+            kernels.nf4_linear_fwd_hp_group([x] * 3, [p["packed"] for p in ps],
+                                            [p["st"] for p in ps], hps, [p["b"] for p in ps],
+                                            bias, rope=(2, cos, sin))
+
+    res = {}
+    for name, fn in (("gemm_then_rope_us", apart), ("gemm_rope_fused_us", folded)):
+        ms, _ = graph_time(fn, max(3, steps // 10), max(2, warmup // 5))
+        res[name] = round(ms * 1e3 / len(sets), 2)
     return res
 
 

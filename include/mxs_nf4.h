@@ -357,6 +357,25 @@ int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, cons
                                 const void* const lora_b[], int r, void* const lora_ht[],
                                 void* const y[], hipStream_t stream);
 
+/* mxs_nf4_linear_fwd_hp_group whose first n_rope (1..n) outputs are rotated as mxs_qkv_rope
+ * rotates q and k (solution/attention.py:28-82, qkv_rope_kernel, on the projections' own
+ * outputs; its caller solution/attention.py:259-271 projects q, k, v and then rotates): y[i]
+ * for i < n_rope holds rot(the fp16 projection output), each 128-column head rotated by the
+ * fp32 cos / sin row of its token (row m is token m % n_tokens of sequence m / n_tokens; rows
+ * at b * cos_stride_b + t * cos_stride_t, cos_stride_b may be 0; 16-byte aligned, strides
+ * multiples of 4).  The stored fp16 has the bits of mxs_nf4_linear_fwd_hp_group followed by
+ * mxs_qkv_rope (forward, no LoRA term) on those outputs; the remaining outputs (v) are
+ * unchanged.  N[i] of a rotated output: a multiple of 128; M a multiple of n_tokens. */
+int mxs_nf4_linear_fwd_hp_group_rope(int n, const void* const x[], int M, int K, const int N[],
+                                     const void* const packed[], const void* const absmax8[],
+                                     const float* const code[], const float* const absmax2[],
+                                     const float* const offset[], const void* const bias[],
+                                     const float* const lora_hp[], int hp_slices, int ldt,
+                                     const void* const lora_b[], int r, void* const lora_ht[],
+                                     void* const y[], int n_rope, const float* cos,
+                                     const float* sin, int64_t cos_stride_b,
+                                     int64_t cos_stride_t, int n_tokens, hipStream_t stream);
+
 /* 1 when mxs_nf4_linear_bwd_dx_grads_group takes these n (1..4) projections [K -> N[i]] at M
  * tokens: each one mxs_nf4_linear_bwd_grads_fused(M, N[i], K, r) would run as one launch on
  * 128x128 tiles. */

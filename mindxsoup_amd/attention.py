@@ -11,7 +11,10 @@ changes how q, k and v are made:
      of LoRA row products and one launch of fused GEMMs forward, shared launches backward; any
      other mix of fp16 NF4 projections (bare or LoRA) runs projection by projection, each on
      the fused kernels;
-  3. one launch rotates q and k (rope.qkv_rope); v goes to attention as a view, uncopied.
+  3. q and k are rotated: in the siblings projection's grouped GEMM (FOLD_ROPE: the epilogue
+     rotates before the fp16 store, the bits of a separate rotation launch; the backward's
+     inverse rotation is one launch, rope.RotatedHeads), else by one launch over both
+     (rope.qkv_rope); v goes to attention as a view, uncopied.
 
 The call takes the original forward when the path cannot serve it (a reason from
 `_refusal`): no GPU tensor, a KV cache or attention weights requested, no fp16 autocast (the
@@ -22,7 +25,9 @@ a projection that is not an fp16 NF4 layer the fused kernels take.
 import torch
 
 from . import linear4bit, peft_lora
-from .rope import HEAD_DIM, qkv_rope
+from .rope import HEAD_DIM, _angles, as_heads, qkv_rope, rotated_heads
+
+FOLD_ROPE = True  # rotate q and k in the siblings projection's GEMM when that path runs
 
 
 def _refusal(module, hidden, position_embeddings, past_key_values, kwargs):
@@ -83,9 +88,11 @@ def _siblings(ads, x2d):
     return projs if linear4bit.siblings_ok(projs, x2d.shape[1]) else None
 
 
-def project_qkv(attn, x16):
+def project_qkv(attn, x16, rope=None):
     """q, k, v fp16 [B, T, heads * 128] of the attention's projections on x16 [B, T, hidden],
-    or None when one of them is not an fp16 NF4 projection the fused kernels take."""
+    and whether q and k come rotated; None when one of them is not an fp16 NF4 projection the
+    fused kernels take.  rope = (cos, sin) fp32 [1 or B, T, 128]: the siblings projection
+    rotates q and k in its GEMM (the other paths return them unrotated)."""
     routes = [_route(getattr(attn, n, None), x16) for n in ("q_proj", "k_proj", "v_proj")]
     if any(r is None for r in routes):
         return None
@@ -94,11 +101,12 @@ def project_qkv(attn, x16):
         x2d = x16.reshape(-1, x16.shape[-1]).contiguous()
         projs = _siblings([ad for _, ad in routes], x2d)
         if projs is not None:
+            spec = None if rope is None else (2, *rope)
             outs = linear4bit.siblings_project(x2d, projs, [ad.a for _, ad in routes],
-                                               [ad.b for _, ad in routes])
-            return [y.view(*x16.shape[:-1], y.shape[-1]) for y in outs]
+                                               [ad.b for _, ad in routes], rope=spec)
+            return [y.view(*x16.shape[:-1], y.shape[-1]) for y in outs], rope is not None
     return [peft_lora.fused_project(obj, x16) if kind == "lora" else obj(x16)
-            for kind, obj in routes]
+            for kind, obj in routes], False
 
 
 def patch_qwen2_attention_fp16():
@@ -115,16 +123,21 @@ def patch_qwen2_attention_fp16():
 
     def forward(self, hidden_states, position_embeddings, attention_mask, past_key_values=None,
                 **kwargs):
-        qkv = None
+        got = None
         if _refusal(self, hidden_states, position_embeddings, past_key_values, kwargs) is None:
-            qkv = project_qkv(self, hidden_states.to(torch.float16))
-        if qkv is None:
+            cos, sin = position_embeddings
+            fold = _angles(cos, sin) if FOLD_ROPE else None
+            got = project_qkv(self, hidden_states.to(torch.float16), fold)
+        if got is None:
             return original(self, hidden_states, position_embeddings, attention_mask,
                             past_key_values, **kwargs)
-        q, k, v = qkv
-        cos, sin = position_embeddings
-        query, key, value = qkv_rope(q, None, k, v, None, cos, sin, q.shape[-1] // HEAD_DIM,
-                                     k.shape[-1] // HEAD_DIM)
+        (q, k, v), rotated = got
+        n_q, n_kv = q.shape[-1] // HEAD_DIM, k.shape[-1] // HEAD_DIM
+        if rotated:
+            query, key = rotated_heads(q, k, *fold, n_q, n_kv)
+            value = as_heads(v, n_kv)
+        else:
+            query, key, value = qkv_rope(q, None, k, v, None, cos, sin, n_q, n_kv)
         attend = modeling_qwen2.ALL_ATTENTION_FUNCTIONS.get_interface(
             self.config._attn_implementation, modeling_qwen2.eager_attention_forward)
         out, weights = attend(self, query, key, value, attention_mask,

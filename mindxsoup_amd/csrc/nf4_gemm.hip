@@ -72,7 +72,23 @@ struct GemmArgs {
   _Float16* glu_g;
   _Float16* glu_u;
   _Float16* glu_h;
+  // RoPE of attention's q / k on the fp16 output (forward, grouped launch; null: none): every
+  // 128-column head rotated by the (cos, sin) row of the output row's position, row m being
+  // token m % rope_T of sequence m / rope_T; cos / sin fp32 with unit stride along the head
+  const float* rope_cos;
+  const float* rope_sin;
+  int64_t rope_cs_b, rope_cs_t;
+  int rope_T;
 };
+
+// Column order of a RoPE tile: within each 128-column head, bits 5 and 6 of the column index
+// swap.  A consumer wave's 32-column blocks j = 0 and 1 (tile columns c and c + 32 of its
+// share) then hold head columns d and d + 64, the two halves one rotation pairs, in the same
+// lane and accumulator element.  Applied to the tile's column coordinate wherever it addresses
+// a column (the NF4 rows, lora_B's rows, the bias, the stores).
+__device__ __forceinline__ int rope_col(int v) {
+  return (v & ~96) | ((v & 32) << 1) | ((v & 64) >> 1);
+}
 
 // Columns per lane of the gradient workgroups inside the backward GEMM launch.
 constexpr int kFusedColsCPL = 2;
@@ -122,11 +138,18 @@ struct Tile {
 // warp-specialized kernel's producers staged (`ls`: [rows][16] fp16 operand of the workgroup's
 // rows then [cols][16] of lora_w, r = 16; `kls`: the workgroup's keep bytes, row stride `kst`)
 // or straight from memory.
-template <int TM, int TN, bool BWD>
+template <int TM, int TN, bool BWD, bool ROPE = false>
 struct AccStart {
   // the bias is prefetched only for narrow wave tiles (register budget of the wide ones)
   static constexpr bool kBiasPre = !BWD && TN <= 2;
   half4_t bias[kBiasPre ? TN : 1][4];  // 4 bias values per register group
+  bool swap = false;                   // ROPE kernels: the tile's columns in rope_col order
+
+  // output column of tile column coordinate n
+  __device__ __forceinline__ int col(int n) const {
+    if constexpr (ROPE) return swap ? rope_col(n) : n;
+    else return n;
+  }
 
   __device__ static __forceinline__ half4_t load_bias(const GemmArgs& a, int n) {
     half4_t b;
@@ -145,7 +168,8 @@ struct AccStart {
 #pragma unroll
         for (int j = 0; j < TN; j++)
 #pragma unroll
-          for (int g = 0; g < 4; g++) bias[j][g] = load_bias(a, nb + j * 32 + 8 * g + 4 * lseg);
+          for (int g = 0; g < 4; g++)
+            bias[j][g] = load_bias(a, col(nb + j * 32 + 8 * g + 4 * lseg));
       }
     }
   }
@@ -159,7 +183,7 @@ struct AccStart {
         for (int g = 0; g < 4; g++) {
           half4_t b;
           if constexpr (kBiasPre) b = bias[j][g];
-          else b = load_bias(a, nb + j * 32 + 8 * g + 4 * lseg);
+          else b = load_bias(a, col(nb + j * 32 + 8 * g + 4 * lseg));
 #pragma unroll
           for (int e = 0; e < 4; e++) c[4 * g + e] = (float)b[e];
         }
@@ -248,7 +272,7 @@ struct AccStart {
             wf = *reinterpret_cast<const half8_t*>(ls + (ls_cols + wc0 + j * 32 + lrow) * 16 +
                                                    8 * lseg);
           } else {
-            const int ncol = nb + j * 32 + lrow;
+            const int ncol = col(nb + j * 32 + lrow);
             wf = ncol < a.Nc
                 ? *reinterpret_cast<const half8_t*>(a.lora_w + (int64_t)ncol * a.r + r0 + 8 * lseg)
                 : (half8_t){};
@@ -385,7 +409,9 @@ struct LoraStage {
   u32x4 hv[NH];       // or the fp16 operand
   u32x4 w[NW];
 
-  __device__ __forceinline__ void issue(const GemmArgs& a, int p, int m0, int n0) {
+  // swap: the tile's columns in rope_col order (lora_B's rows follow them)
+  __device__ __forceinline__ void issue(const GemmArgs& a, int p, int m0, int n0,
+                                        bool swap = false) {
     if (a.lora_hp) {
 #pragma unroll
       for (int z = 0; z < 4; z++) {
@@ -406,11 +432,22 @@ struct LoraStage {
         hv[u] = c < BM * 2 && m0 + c / 2 < a.M ? src[c] : (u32x4){};
       }
     }
-    const u32x4* wsrc = reinterpret_cast<const u32x4*>(a.lora_w + (int64_t)n0 * 16);
+    if (swap) {
 #pragma unroll
-    for (int u = 0; u < NW; u++) {
-      const int c = p + NTP * u;
-      w[u] = c < BN * 2 && n0 + c / 2 < a.Nc ? wsrc[c] : (u32x4){};
+      for (int u = 0; u < NW; u++) {
+        const int c = p + NTP * u;
+        const int n = rope_col(n0 + c / 2);
+        w[u] = c < BN * 2 && n < a.Nc
+            ? *reinterpret_cast<const u32x4*>(a.lora_w + (int64_t)n * 16 + 8 * (c & 1))
+            : (u32x4){};
+      }
+    } else {
+      const u32x4* wsrc = reinterpret_cast<const u32x4*>(a.lora_w + (int64_t)n0 * 16);
+#pragma unroll
+      for (int u = 0; u < NW; u++) {
+        const int c = p + NTP * u;
+        w[u] = c < BN * 2 && n0 + c / 2 < a.Nc ? wsrc[c] : (u32x4){};
+      }
     }
   }
 
@@ -510,7 +547,41 @@ struct StagedStore {
   static constexpr int AREA_DWORDS = 32 * S32;
 };
 
-template <int TM, int TN>
+// RoPE of one lane's accumulators before the fp16 store (ROPE kernels): output row m, blocks
+// j = 0 / 1 holding head columns d / d + 64 (rope_col order; nb the wave's column coordinate).
+// Each value is first rounded to fp16, the unrotated projection output, then rotated in fp32
+// with every product and sum rounded once (no contraction): k_qkv_rope's arithmetic on that
+// output, so the stored fp16 has the bits of the projection followed by the rotation launch.
+// The cos / sin are read here, when every tile of the launch reaches its epilogue: staging them
+// in LDS earlier (in the prologue, or copied during the main loop by the producer waves without
+// NF4 items) measured no faster, the extra traffic then slowing the K-steps instead.
+template <int TN>
+__device__ __forceinline__ void rope_rotate(const GemmArgs& a, float16_t (&acc)[TN], int m,
+                                            int nb, int lseg) {
+#pragma clang fp contract(off)
+  static_assert(TN == 2, "a lane holds both halves of its head columns");
+  if (m >= a.M) return;
+  const int b = m / a.rope_T, t = m - b * a.rope_T;
+  const int64_t cr = (int64_t)b * a.rope_cs_b + (int64_t)t * a.rope_cs_t;
+  const int d0 = rope_col(nb) & 127;  // head column of block 0's first column (< 64)
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    const int d = d0 + 8 * g + 4 * lseg;
+    const float4_t c1 = *reinterpret_cast<const float4_t*>(a.rope_cos + cr + d);
+    const float4_t c2 = *reinterpret_cast<const float4_t*>(a.rope_cos + cr + d + 64);
+    const float4_t s1 = *reinterpret_cast<const float4_t*>(a.rope_sin + cr + d);
+    const float4_t s2 = *reinterpret_cast<const float4_t*>(a.rope_sin + cr + d + 64);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      const float x1 = (float)(_Float16)acc[0][4 * g + e];
+      const float x2 = (float)(_Float16)acc[1][4 * g + e];
+      acc[0][4 * g + e] = x1 * c1[e] + x2 * -s1[e];
+      acc[1][4 * g + e] = x2 * c2[e] + x1 * s2[e];
+    }
+  }
+}
+
+template <int TM, int TN, bool ROPE = false>
 __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, float16_t (&acc)[TM][TN],
                                                 int mb, int nb, int lane, float* area) {
   using SS = StagedStore<TM, TN>;
@@ -534,6 +605,9 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, float16_t (&a
           *reinterpret_cast<float4_t*>(area + lrow * SS::S32 + 32 * j + 8 * g + 4 * lseg) = v;
         }
     } else {
+      if constexpr (ROPE) {
+        if (a.rope_cos) rope_rotate<TN>(a, acc[i], row0 + lrow, nb, lseg);
+      }
       uint32_t* ar = reinterpret_cast<uint32_t*>(area);
 #pragma unroll
       for (int j = 0; j < TN; j++)
@@ -571,7 +645,9 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, float16_t (&a
       for (int q = 0; q < CPR / 2; q++) {
         const int c = q * 64 + lane;
         const int r = c / CPR, cc = c % CPR;
-        const int m = row0 + r, n = nb + 8 * cc;
+        const int m = row0 + r;
+        int n = nb + 8 * cc;
+        if constexpr (ROPE) n = a.rope_cos ? rope_col(n) : n;
         const u32x4 v = *reinterpret_cast<const u32x4*>(ar + r * SS::S16 + 4 * cc);
         if (m >= a.M || n >= a.Nc) continue;
         _Float16* dst = a.C + (int64_t)m * a.ldc + n;
@@ -1256,10 +1332,13 @@ struct BLoad8 {
     uint32_t w, blk;
   };
 
-  __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0) {
+  // swap: the tile's columns (W's rows) in rope_col order
+  __device__ static __forceinline__ Src setup(const GemmArgs& a, int p, int n0,
+                                              bool swap = false) {
     Src r;
     const int q = p;  // the caller runs only lanes with an item (p < TOTAL)
-    const uint32_t n = min(n0 + (q >> 2), a.Nc - 1);
+    const int c = n0 + (q >> 2);
+    const uint32_t n = min(swap ? rope_col(c) : c, a.Nc - 1);
     r.w = n * (uint32_t)(a.Kw / 2) + (q & 3) * 8;
     r.blk = n * (uint32_t)(a.Kw / 64);
     return r;
@@ -1527,11 +1606,18 @@ struct SumPlan {
 // table and offset) from its problem, and the accumulator starts from all their LoRA terms.
 // The problems share M, the output width and the weight row length, LoRA rank 16 and the keep
 // mask's presence; the A copies are the consumers' (consumer_copies).
-template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU, int NSUM>
+// ROPE: the forward tile of a grouped launch whose problems may ask for the RoPE of attention's
+// q / k (GemmArgs::rope_cos): such a tile's columns are in rope_col order and its epilogue
+// rotates (rope_rotate).
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU, int NSUM,
+          bool ROPE = false>
 __device__ __forceinline__ void ws_tile_impl(const GemmArgs* as, const SumPlan* plan, int bx,
                                              int by) {
   const GemmArgs& a = as[0];
   constexpr int WM = BM / CWM, WN = BN / CWN, TM = WM / 32, TN = WN / 32;
+  static_assert(!ROPE || (!BWD && !GLU && NSUM == 1 && PW == 8 && TN == 2),
+                "RoPE tiles: forward, 8 producer waves, two 32-column blocks per wave");
+  const bool swap = ROPE && a.rope_cos != nullptr;
   constexpr int NTP = 64 * PW;  // producer threads
   static_assert(CWM * CWN == 4 && WM % 32 == 0 && WN % 32 == 0, "consumer wave tiles");
   static_assert(PW == 4 || PW == 8, "4 or 8 producer waves");
@@ -1601,7 +1687,7 @@ __device__ __forceinline__ void ws_tile_impl(const GemmArgs* as, const SumPlan* 
     const bool run = kt0 < kt1;
     LoraStage<BM, BN, NTP> lst[NSUM];
     MaskStage<BM, BN, NTP> mst[NSUM];
-    if (lora16) lst[0].issue(a, p, m0, n0);  // before the tiles: one round trip for all
+    if (lora16) lst[0].issue(a, p, m0, n0, swap);  // before the tiles: one round trip for all
     if (kmask) mst[0].issue(a, p, m0, n0);
 #pragma unroll
     for (int q = 1; q < NSUM; q++) {
@@ -1659,7 +1745,10 @@ __device__ __forceinline__ void ws_tile_impl(const GemmArgs* as, const SumPlan* 
       static_assert(NS >= 4 && NS * LB + 2 * LA <= 63, "stages: at least 4; waits fit vmcnt");
       AC ac;
       if constexpr (!CC) ac.init(a, As, pw, lane, m0);
-      const typename B::Src src = B::setup(a, p, n0);
+      const typename B::Src src = [&] {
+        if constexpr (ROPE) return B::setup(a, p, n0, swap);
+        else return B::setup(a, p, n0);
+      }();
       typename B::Stage S[NS];
       typename B::Looked L;
       // B of K-step k from its problem's weight
@@ -1827,7 +1916,8 @@ __device__ __forceinline__ void ws_tile_impl(const GemmArgs* as, const SumPlan* 
         for (int i = 0; i < LA; i++) acopy(SLOT, min(kt0 + 1, lastk), i);
       }
     }
-    AccStart<TM, TN, BWD> start;
+    AccStart<TM, TN, BWD, ROPE> start;
+    start.swap = swap;
     start.load(a, n0 + wn0, lseg);  // before the tables' loads
     fill_tables(a, s_pair, s_code, t, 256);
 #pragma unroll
@@ -1972,14 +2062,16 @@ __device__ __forceinline__ void ws_tile_impl(const GemmArgs* as, const SumPlan* 
         return;
       }
     }
-    epilogue_staged<TM, TN>(a, acc, m0 + wm0, n0 + wn0, lane,
-                            reinterpret_cast<float*>(As) + wave * StagedStore<TM, TN>::AREA_DWORDS);
+    epilogue_staged<TM, TN, ROPE>(a, acc, m0 + wm0, n0 + wn0, lane,
+                                  reinterpret_cast<float*>(As) +
+                                      wave * StagedStore<TM, TN>::AREA_DWORDS);
   }
 }
 
-template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU>
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU,
+          bool ROPE = false>
 __device__ __forceinline__ void ws_tile(const GemmArgs& a, int bx, int by) {
-  ws_tile_impl<BM, BN, CWM, CWN, BWD, PW, NS, GLU, 1>(&a, nullptr, bx, by);
+  ws_tile_impl<BM, BN, CWM, CWN, BWD, PW, NS, GLU, 1, ROPE>(&a, nullptr, bx, by);
 }
 
 template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool GLU>
@@ -2016,7 +2108,7 @@ struct GemmGroup {
   int n;
 };
 
-template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS>
+template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS, bool ROPE = false>
 __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws_group(GemmGroup g) {
   const int bid = (int)blockIdx.x;
   int i = 0;
@@ -2033,7 +2125,8 @@ __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws_group(GemmGroup g
       return;
     }
   }
-  ws_tile<BM, BN, CWM, CWN, BWD, PW, NS, false>(g.p[i], local % g.gx[i], local / g.gx[i]);
+  ws_tile<BM, BN, CWM, CWN, BWD, PW, NS, false, ROPE>(g.p[i], local % g.gx[i],
+                                                     local / g.gx[i]);
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, bool BWD>
@@ -2287,7 +2380,7 @@ static bool glu_plan_ok(int M, int Nc, int Kr, bool bwd) {
 // producer waves, unsplit (k_nf4_gemm_ws_group): 128x128 tiles by default; in the backward each
 // problem's LoRA gradient workgroups follow its tiles.  Every problem must take that kernel (its
 // 32-bit offsets, the backward's column clamp).
-template <bool BWD, int BN = 128>
+template <bool BWD, int BN = 128, int CWM = 2, int CWN = 2, bool ROPE = false>
 static int launch_ws_group(const GemmArgs* probs, int n, hipStream_t stream) {
   constexpr int BM = 128, PW = 8, NS = 4;
   if (n < 1 || n > kMaxGemmGroup) return MXS_ERR_ARG;
@@ -2313,12 +2406,12 @@ static int launch_ws_group(const GemmArgs* probs, int n, hipStream_t stream) {
   static bool lds_set = false;  // idempotent attribute; a benign race between threads
   if (!lds_set) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&k_nf4_gemm_ws_group<BM, BN, 2, 2, BWD, PW, NS>),
+        reinterpret_cast<const void*>(&k_nf4_gemm_ws_group<BM, BN, CWM, CWN, BWD, PW, NS, ROPE>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return (int)e;
     lds_set = true;
   }
-  hipLaunchKernelGGL((k_nf4_gemm_ws_group<BM, BN, 2, 2, BWD, PW, NS>), dim3(total),
+  hipLaunchKernelGGL((k_nf4_gemm_ws_group<BM, BN, CWM, CWN, BWD, PW, NS, ROPE>), dim3(total),
                      dim3(64 * (4 + PW)), lds, stream, g);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MXS_OK : (int)e;
@@ -2918,16 +3011,34 @@ int mxs_nf4_linear_bwd_dx_hp_pair(const void* const dy[2], int M, const int N[2]
   return launch_ws_pair<256, 96, 4, 1, true, 8, 5>(p[0], p[1], kPairSplits, stream);
 }
 
-int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, const int N[],
-                                const void* const packed[], const void* const absmax8[],
-                                const float* const code[], const float* const absmax2[],
-                                const float* const offset[], const void* const bias[],
-                                const float* const lora_hp[], int hp_slices, int ldt,
-                                const void* const lora_b[], int r, void* const lora_ht[],
-                                void* const y[], hipStream_t stream) {
+// The rotation the grouped forward may apply to its first n_rope problems (attention's q / k).
+struct RopeSpec {
+  int n_rope;
+  const float* cos;
+  const float* sin;
+  int64_t cs_b, cs_t;
+  int T;
+};
+
+static int fwd_hp_group(int n, const void* const x[], int M, int K, const int N[],
+                        const void* const packed[], const void* const absmax8[],
+                        const float* const code[], const float* const absmax2[],
+                        const float* const offset[], const void* const bias[],
+                        const float* const lora_hp[], int hp_slices, int ldt,
+                        const void* const lora_b[], int r, void* const lora_ht[],
+                        void* const y[], const RopeSpec& rs, hipStream_t stream) {
   if (n < 1 || n > kMaxGemmGroup || !x || !N || !packed || !absmax8 || !code || !absmax2 ||
-      !offset || !y)
+      !offset || !y || rs.n_rope < 0 || rs.n_rope > n)
     return MXS_ERR_ARG;
+  if (rs.n_rope > 0) {
+    if (!rs.cos || !rs.sin || rs.T < 1 || M % rs.T != 0 || rs.cs_b < 0 || rs.cs_t < 0)
+      return MXS_ERR_ARG;
+    // float4 reads of cos / sin rows
+    if ((uintptr_t)rs.cos % 16 || (uintptr_t)rs.sin % 16 || rs.cs_b % 4 || rs.cs_t % 4)
+      return MXS_ERR_ALIGN;
+    for (int i = 0; i < rs.n_rope; i++)
+      if (N[i] % 128 != 0) return MXS_ERR_SIZE;  // whole 128-column heads
+  }
   GemmArgs probs[kMaxGemmGroup];
   int live = 0;
   for (int i = 0; i < n; i++) {
@@ -2955,6 +3066,13 @@ int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, cons
     }
     a.C = static_cast<_Float16*>(y[i]);
     a.ldc = N[i];
+    if (i < rs.n_rope) {
+      a.rope_cos = rs.cos;
+      a.rope_sin = rs.sin;
+      a.rope_cs_b = rs.cs_b;
+      a.rope_cs_t = rs.cs_t;
+      a.rope_T = rs.T;
+    }
     const int c = check_gemm(false, a);
     if (c == 1) continue;  // nothing to compute for this one
     if (c != MXS_OK) return c;
@@ -2962,13 +3080,45 @@ int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, cons
   }
   if (live == 0) return MXS_OK;
   // 128x64 tiles when every problem's tiles together fit the CUs in one round (q, k and v at
-  // 1024 tokens: 192 + 32 + 32 = 256 tiles), as the planner does for one problem; else 128x128
+  // 1024 tokens: 192 + 32 + 32 = 256 tiles), as the planner does for one problem; else 128x128.
+  // With the rotation the 128x64 tiles take 4 x 1 consumer waves (each wave's two 32-column
+  // blocks are one head's halves); the products, and so the bits, are those of the 2 x 2 layout.
   int64_t tiles64 = 0;
   for (int i = 0; i < live; i++)
     tiles64 += (int64_t)((M + 127) / 128) * ((probs[i].Nc + 63) / 64);
   const int cus = cu_count();
-  if (cus > 0 && tiles64 <= cus) return launch_ws_group<false, 64>(probs, live, stream);
+  const bool t64 = cus > 0 && tiles64 <= cus;
+  if (rs.n_rope > 0)
+    return t64 ? launch_ws_group<false, 64, 4, 1, true>(probs, live, stream)
+               : launch_ws_group<false, 128, 2, 2, true>(probs, live, stream);
+  if (t64) return launch_ws_group<false, 64>(probs, live, stream);
   return launch_ws_group<false>(probs, live, stream);
+}
+
+int mxs_nf4_linear_fwd_hp_group(int n, const void* const x[], int M, int K, const int N[],
+                                const void* const packed[], const void* const absmax8[],
+                                const float* const code[], const float* const absmax2[],
+                                const float* const offset[], const void* const bias[],
+                                const float* const lora_hp[], int hp_slices, int ldt,
+                                const void* const lora_b[], int r, void* const lora_ht[],
+                                void* const y[], hipStream_t stream) {
+  return fwd_hp_group(n, x, M, K, N, packed, absmax8, code, absmax2, offset, bias, lora_hp,
+                      hp_slices, ldt, lora_b, r, lora_ht, y, RopeSpec{}, stream);
+}
+
+int mxs_nf4_linear_fwd_hp_group_rope(int n, const void* const x[], int M, int K, const int N[],
+                                     const void* const packed[], const void* const absmax8[],
+                                     const float* const code[], const float* const absmax2[],
+                                     const float* const offset[], const void* const bias[],
+                                     const float* const lora_hp[], int hp_slices, int ldt,
+                                     const void* const lora_b[], int r, void* const lora_ht[],
+                                     void* const y[], int n_rope, const float* cos,
+                                     const float* sin, int64_t cos_stride_b,
+                                     int64_t cos_stride_t, int n_tokens, hipStream_t stream) {
+  if (n_rope < 1) return MXS_ERR_ARG;
+  const RopeSpec rs{n_rope, cos, sin, cos_stride_b, cos_stride_t, n_tokens};
+  return fwd_hp_group(n, x, M, K, N, packed, absmax8, code, absmax2, offset, bias, lora_hp,
+                      hp_slices, ldt, lora_b, r, lora_ht, y, rs, stream);
 }
 
 int mxs_nf4_linear_glu_fused(int M, int N, int K, int bwd) {

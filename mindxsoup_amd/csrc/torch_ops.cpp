@@ -318,10 +318,47 @@ Tensor lora_w(const Tensor& t, int64_t rows, int64_t cols, const at::Device& dev
 // (mxs_nf4_linear_fwd_hp), which finish Hs and compute Y = x W^T + bias + Hs B^T and write
 // Hs^T.  Returns (ys, hts, ats, bts).  For one projection this is lora_fwd: the grouped rows
 // launch of one problem gives the bits of mxs_lora_h_partials.
+// The RoPE the grouped forward may fold into its first n_rope outputs (attention's q / k):
+// cos / sin fp32 [1 or B, T, 128], one layout, unit last stride; x's rows B sequences of T.
+struct RopeOperands {
+  const float* cos = nullptr;
+  const float* sin = nullptr;
+  int64_t cs_b = 0, cs_t = 0;
+  int T = 0, n_rope = 0;
+};
+
+RopeOperands rope_operands(const OptTensor& cos, const OptTensor& sin, int64_t n_rope,
+                           int64_t M, size_t n, const at::Device& dev) {
+  RopeOperands r;
+  if (n_rope == 0) {
+    TORCH_CHECK(!cos.has_value() && !sin.has_value(), "cos / sin given without n_rope");
+    return r;
+  }
+  TORCH_CHECK(n_rope > 0 && n_rope <= (int64_t)n, "n_rope: 1 .. the number of projections");
+  TORCH_CHECK(cos.has_value() && sin.has_value(), "n_rope needs cos and sin");
+  const Tensor& c = *cos;
+  const Tensor& sn = *sin;
+  TORCH_CHECK(c.device() == dev && sn.device() == dev && c.scalar_type() == at::kFloat &&
+                  sn.scalar_type() == at::kFloat && c.dim() == 3 && c.sizes() == sn.sizes() &&
+                  c.strides() == sn.strides() && c.size(2) == 128 && c.stride(2) == 1,
+              "cos / sin must be fp32 [1 or B, T, 128] with one layout on x's device");
+  const int64_t T = c.size(1);
+  TORCH_CHECK(T >= 1 && M % T == 0 && (c.size(0) == 1 || c.size(0) == M / T),
+              "x's rows must be B whole sequences of cos / sin's T tokens");
+  r.cos = c.data_ptr<float>();
+  r.sin = sn.data_ptr<float>();
+  r.cs_b = c.size(0) > 1 ? c.stride(0) : 0;
+  r.cs_t = c.stride(1);
+  r.T = as_int(T, "T");
+  r.n_rope = static_cast<int>(n_rope);
+  return r;
+}
+
 Lists4 fwd_impl(const Tensor& x, TensorList lora_a, TensorList lora_b, TensorList packed,
                 TensorList absmax8, TensorList code, TensorList absmax2, TensorList offset,
                 const std::vector<OptTensor>& bias, const std::vector<OptTensor>& keep,
-                double mask_scale, double s, bool one_gemm) {
+                double mask_scale, double s, bool one_gemm, const OptTensor& cos = std::nullopt,
+                const OptTensor& sin = std::nullopt, int64_t n_rope = 0) {
   const size_t n = lora_a.size();
   check_group(n, {lora_b.size(), packed.size(), absmax8.size(), code.size(), absmax2.size(),
                   offset.size(), bias.size(), keep.size()});
@@ -380,6 +417,8 @@ Lists4 fwd_impl(const Tensor& x, TensorList lora_a, TensorList lora_b, TensorLis
     p_bt[i] = bts[i].data_ptr();
     p_b16[i] = b16[i].data_ptr();
   }
+  const RopeOperands rope = rope_operands(cos, sin, n_rope, M, n, dev);
+  TORCH_CHECK(rope.n_rope == 0 || one_gemm, "the RoPE rides on the grouped GEMM (one_gemm)");
   const hipStream_t st = stream_of(xc);
   const float ms = static_cast<float>(mask_scale), sf = static_cast<float>(s);
   if (w32) {
@@ -404,7 +443,14 @@ Lists4 fwd_impl(const Tensor& x, TensorList lora_a, TensorList lora_b, TensorLis
     p_y[i] = ys[i].data_ptr();
     p_ht[i] = hts[i].data_ptr();
   }
-  if (one_gemm) {
+  if (one_gemm && rope.n_rope > 0) {
+    ok(mxs_nf4_linear_fwd_hp_group_rope(
+           (int)n, xs.data(), m, k, Ns.data(), p_packed.data(), p_a8.data(), p_code.data(),
+           p_a2.data(), p_off.data(), pbias.data(), p_hp.data(), S, (int)ldt, pb.data(), rr,
+           p_ht.data(), p_y.data(), rope.n_rope, rope.cos, rope.sin, rope.cs_b, rope.cs_t,
+           rope.T, st),
+       "mxs_nf4_linear_fwd_hp_group_rope");
+  } else if (one_gemm) {
     ok(mxs_nf4_linear_fwd_hp_group((int)n, xs.data(), m, k, Ns.data(), p_packed.data(),
                                    p_a8.data(), p_code.data(), p_a2.data(), p_off.data(),
                                    pbias.data(), p_hp.data(), S, (int)ldt, pb.data(), rr,
@@ -428,12 +474,13 @@ Lists4 lora_fwd_group_cuda(const Tensor& x, TensorList lora_a, TensorList lora_b
                            TensorList packed, TensorList absmax8, TensorList code,
                            TensorList absmax2, TensorList offset, const OptTensorList& bias,
                            const OptTensorList& keep, double mask_scale, double s,
-                           bool one_gemm) {
+                           bool one_gemm, const OptTensor& cos, const OptTensor& sin,
+                           int64_t n_rope) {
   const size_t n = lora_a.size();
   TORCH_CHECK(bias.size() == 0 || bias.size() == n, "bias: none or one per projection");
   TORCH_CHECK(keep.size() == 0 || keep.size() == n, "keep: none or one per projection");
   return fwd_impl(x, lora_a, lora_b, packed, absmax8, code, absmax2, offset, entries(bias, n),
-                  entries(keep, n), mask_scale, s, one_gemm);
+                  entries(keep, n), mask_scale, s, one_gemm, cos, sin, n_rope);
 }
 
 // One projection (NF4LoraFunction.forward): fwd_impl of one.  Returns (y, ht, at, bt).
@@ -587,7 +634,8 @@ std::tuple<Tensor, Tensor, Tensor> lora_bwd_meta(
 
 Lists4 lora_fwd_group_meta(const Tensor& x, TensorList lora_a, TensorList lora_b, TensorList,
                            TensorList, TensorList, TensorList, TensorList, const OptTensorList&,
-                           const OptTensorList&, double, double, bool) {
+                           const OptTensorList&, double, double, bool, const OptTensor&,
+                           const OptTensor&, int64_t) {
   const int64_t M = x.size(0), K = x.size(1);
   const auto o = x.options().dtype(at::kHalf);
   std::vector<Tensor> ys, hts, ats, bts;
@@ -1065,7 +1113,8 @@ Tensor lora_linear_autograd(const Tensor& x, const Tensor& lora_a, const Tensor&
 
 using GroupFwdSig = Lists4(const Tensor&, TensorList, TensorList, TensorList, TensorList,
                            TensorList, TensorList, TensorList, const OptTensorList&,
-                           const OptTensorList&, double, double, bool);
+                           const OptTensorList&, double, double, bool, const OptTensor&,
+                           const OptTensor&, int64_t);
 using GroupBwdSig = Lists3(TensorList, const Tensor&, const OptTensorList&, TensorList,
                            TensorList, TensorList, TensorList, TensorList, TensorList,
                            TensorList, TensorList, double, double, at::IntArrayRef, bool);
@@ -1073,17 +1122,22 @@ using GroupBwdSig = Lists3(TensorList, const Tensor&, const OptTensorList&, Tens
 // n NF4 + LoRA projections reading one input x fp16 [M, K] (a layer's q/k/v, or gate/up),
 // their launches shared (NF4LoraSiblingsFunction of the Python package): outputs fp16 [M, N_i];
 // the backward returns dx = the sum of the projections' input gradients, in order.
+// With n_rope > 0 the first n_rope outputs come rotated (attention's q / k, the RoPE folded
+// into the grouped GEMM) while the backward stays that of the unrotated projections: the
+// caller applies the inverse rotation to their gradients first (rope.RotatedHeads).
 struct NF4LoraSiblingsFunction : public torch::autograd::Function<NF4LoraSiblingsFunction> {
   static variable_list forward(AutogradContext* ctx, const Tensor& x, TensorList lora_a,
                                TensorList lora_b, TensorList packed, TensorList absmax8,
                                TensorList code, TensorList absmax2, TensorList offset,
                                const OptTensorList& bias, const OptTensorList& keep,
-                               double mask_scale, double s, bool one_gemm) {
+                               double mask_scale, double s, bool one_gemm,
+                               const OptTensor& cos, const OptTensor& sin, int64_t n_rope) {
     static auto fwd = op<GroupFwdSig>("mxs_nf4::lora_fwd_group");
     at::AutoDispatchBelowADInplaceOrView below;
     const size_t n = lora_a.size();
     auto [ys, hts, ats, bts] = fwd.call(x, lora_a, lora_b, packed, absmax8, code, absmax2,
-                                        offset, bias, keep, mask_scale, s, one_gemm);
+                                        offset, bias, keep, mask_scale, s, one_gemm, cos, sin,
+                                        n_rope);
     variable_list saved{x};
     for (const TensorList& l : {TensorList(hts), TensorList(ats), TensorList(bts), packed,
                                 absmax8, code, absmax2, offset})
@@ -1140,7 +1194,7 @@ struct NF4LoraSiblingsFunction : public torch::autograd::Function<NF4LoraSibling
                    slice(6), slice(7), ctx->saved_data["mask_scale"].toDouble(),
                    ctx->saved_data["s"].toDouble(), wants, true);
     }
-    variable_list out(7 * n + 6);
+    variable_list out(7 * n + 9);
     if (ctx->needs_input_grad(0)) out[0] = dxs[0];
     for (int64_t i = 0; i < n; ++i) {
       out[1 + i] = as_dtype(das[i], static_cast<at::ScalarType>(dts[2 * i]));
@@ -1155,9 +1209,11 @@ std::vector<Tensor> lora_siblings_autograd(const Tensor& x, TensorList lora_a,
                                            TensorList absmax8, TensorList code,
                                            TensorList absmax2, TensorList offset,
                                            const OptTensorList& bias, const OptTensorList& keep,
-                                           double mask_scale, double s, bool one_gemm) {
+                                           double mask_scale, double s, bool one_gemm,
+                                           const OptTensor& cos, const OptTensor& sin,
+                                           int64_t n_rope) {
   return NF4LoraSiblingsFunction::apply(x, lora_a, lora_b, packed, absmax8, code, absmax2, offset, bias,
-                           keep, mask_scale, s, one_gemm);
+                           keep, mask_scale, s, one_gemm, cos, sin, n_rope);
 }
 
 // The autograd ops where no autograd key is dispatched (inference mode): the forward alone.
@@ -1185,10 +1241,12 @@ std::vector<Tensor> lora_siblings_plain(const Tensor& x, TensorList lora_a, Tens
                                         TensorList packed, TensorList absmax8, TensorList code,
                                         TensorList absmax2, TensorList offset,
                                         const OptTensorList& bias, const OptTensorList& keep,
-                                        double mask_scale, double s, bool one_gemm) {
+                                        double mask_scale, double s, bool one_gemm,
+                                        const OptTensor& cos, const OptTensor& sin,
+                                        int64_t n_rope) {
   static auto fwd = op<GroupFwdSig>("mxs_nf4::lora_fwd_group");
   return std::get<0>(fwd.call(x, lora_a, lora_b, packed, absmax8, code, absmax2, offset, bias,
-                              keep, mask_scale, s, one_gemm));
+                              keep, mask_scale, s, one_gemm, cos, sin, n_rope));
 }
 
 }  // namespace
@@ -1209,8 +1267,8 @@ TORCH_LIBRARY(mxs_nf4, m) {
         "-> (Tensor, Tensor, Tensor)");
   m.def("lora_fwd_group(Tensor x, Tensor[] lora_a, Tensor[] lora_b, Tensor[] packed, "
         "Tensor[] absmax8, Tensor[] code, Tensor[] absmax2, Tensor[] offset, Tensor?[] bias, "
-        "Tensor?[] keep, float mask_scale, float s, bool one_gemm) "
-        "-> (Tensor[], Tensor[], Tensor[], Tensor[])");
+        "Tensor?[] keep, float mask_scale, float s, bool one_gemm, Tensor? cos=None, "
+        "Tensor? sin=None, int n_rope=0) -> (Tensor[], Tensor[], Tensor[], Tensor[])");
   m.def("lora_bwd_group(Tensor[] dy, Tensor x, Tensor?[] keep, Tensor[] ht, Tensor[] at, "
         "Tensor[] bt, Tensor[] packed, Tensor[] absmax8, Tensor[] code, Tensor[] absmax2, "
         "Tensor[] offset, float mask_scale, float s, int[] wants, bool sum_dx=False) "
@@ -1222,7 +1280,8 @@ TORCH_LIBRARY(mxs_nf4, m) {
         "float mask_scale, float s) -> Tensor");
   m.def("lora_siblings(Tensor x, Tensor[] lora_a, Tensor[] lora_b, Tensor[] packed, "
         "Tensor[] absmax8, Tensor[] code, Tensor[] absmax2, Tensor[] offset, Tensor?[] bias, "
-        "Tensor?[] keep, float mask_scale, float s, bool one_gemm) -> Tensor[]");
+        "Tensor?[] keep, float mask_scale, float s, bool one_gemm, Tensor? cos=None, "
+        "Tensor? sin=None, int n_rope=0) -> Tensor[]");
 }
 
 TORCH_LIBRARY_IMPL(mxs_nf4, CUDA, m) {

@@ -468,11 +468,28 @@ def nf4_linear_fwd_hp(x2d, packed, state, lora_hp, lora_b, bias=None, cfg=-1, sp
     return y, ht
 
 
-def nf4_linear_fwd_hp_group(x2ds, packeds, states, lora_hps=None, lora_bs=None, biases=None):
+def rope_spec(n_rope, cos, sin, M):
+    """(cos stride b, cos stride t, tokens per sequence) for the RoPE of the grouped forward's
+    first n_rope outputs over M rows: cos / sin fp32 [1 or B, T, 128] of one layout with a unit
+    last stride, M = B * T."""
+    if cos.dtype != torch.float32 or sin.dtype != torch.float32 or cos.dim() != 3 \
+            or cos.shape != sin.shape or cos.stride() != sin.stride() or cos.stride(-1) != 1 \
+            or cos.shape[2] != 128:
+        raise ValueError("cos / sin must be fp32 [1 or B, T, 128] with one layout")
+    T = cos.shape[1]
+    if n_rope < 1 or T < 1 or M % T != 0 or cos.shape[0] not in (1, M // T):
+        raise ValueError("the rows must be B whole sequences of cos / sin's T tokens")
+    return (cos.stride(0) if cos.shape[0] > 1 else 0), cos.stride(1), T
+
+
+def nf4_linear_fwd_hp_group(x2ds, packeds, states, lora_hps=None, lora_bs=None, biases=None,
+                            rope=None):
     """nf4_linear_fwd_hp for up to 4 projections of one input width over the same tokens in one
     launch (128x64 tiles when they fit the CUs in one round, else 128x128; unsplit): a list of
     (y, ht) (ht None without LoRA), the bits of nf4_linear_fwd_hp(..., cfg=10, splits=1) for
-    each."""
+    each.  rope = (n_rope, cos, sin): the first n_rope outputs (attention's q and k, widths
+    multiples of 128) come rotated (mxs_nf4_linear_fwd_hp_group_rope), the bits of qkv_rope's
+    forward on the unrotated outputs; cos / sin as rope_spec takes them."""
     n = len(x2ds)
     lora_hps = lora_hps or [None] * n
     lora_bs = lora_bs or [None] * n
@@ -503,13 +520,22 @@ def nf4_linear_fwd_hp_group(x2ds, packeds, states, lora_hps=None, lora_bs=None, 
     hps = [None if hp is None else hp.contiguous() for hp in lora_hps]
     if any(hp is not None and hp.shape != (S, ldt, r) for hp in hps):
         raise ValueError("LoRA partials of one shape")
-    _lib.call("mxs_nf4_linear_fwd_hp_group", n, _ptr_array(x2ds), M, K,
-              _int_array([st.shape[0] for st in states]), _ptr_array(packeds),
-              _ptr_array([st.absmax for st in states]),
-              _ptr_array([st.state2.code for st in states]),
-              _ptr_array([st.state2.absmax for st in states]),
-              _ptr_array([st.offset for st in states]), _ptr_array(bias16), _ptr_array(hps), S,
-              ldt, _ptr_array(b16), r, _ptr_array(hts), _ptr_array(ys), _lib.stream_of(dev))
+    args = (n, _ptr_array(x2ds), M, K, _int_array([st.shape[0] for st in states]),
+            _ptr_array(packeds), _ptr_array([st.absmax for st in states]),
+            _ptr_array([st.state2.code for st in states]),
+            _ptr_array([st.state2.absmax for st in states]),
+            _ptr_array([st.offset for st in states]), _ptr_array(bias16), _ptr_array(hps), S,
+            ldt, _ptr_array(b16), r, _ptr_array(hts), _ptr_array(ys))
+    if rope is None:
+        _lib.call("mxs_nf4_linear_fwd_hp_group", *args, _lib.stream_of(dev))
+    else:
+        n_rope, cos, sin = rope
+        cs_b, cs_t, T = rope_spec(n_rope, cos, sin, M)
+        if n_rope > n or any(st.shape[0] % 128 for st in states[:n_rope]) \
+                or cos.device != dev or sin.device != dev:
+            raise ValueError("rotated outputs: whole 128-column heads on the input's device")
+        _lib.call("mxs_nf4_linear_fwd_hp_group_rope", *args, n_rope, _lib.ptr(cos),
+                  _lib.ptr(sin), cs_b, cs_t, T, _lib.stream_of(dev))
     return list(zip(ys, hts))
 
 

@@ -421,23 +421,29 @@ class NF4LoraSiblingsFunction(torch.autograd.Function):
     input gradients.  Each output equals NF4LoraFunction on its projection to within the GEMM
     tolerance (the grouped GEMM runs every problem on one tile plan).
     Inputs: x2d fp16 [M, K], `projs` (a tuple of Proj that siblings_ok accepts), one_gemm (the
-    forward GEMMs in one grouped launch, else each on its own plan), then each projection's
-    lora_A [r, K] and lora_B [N, r] (their gradients come back in their dtypes).
-    Outputs: one fp16 [M, N_i] per projection."""
+    forward GEMMs in one grouped launch, else each on its own plan), rope (None, or
+    (n_rope, cos, sin): the first n_rope outputs come rotated by the grouped GEMM, which needs
+    one_gemm), then each projection's lora_A [r, K] and lora_B [N, r] (their gradients come
+    back in their dtypes).
+    Outputs: one fp16 [M, N_i] per projection.  The backward is that of the unrotated outputs
+    whatever rope is: a rotated output's gradient must reach it rotated back (rope.RotatedHeads
+    does that between this node and attention)."""
 
     @staticmethod
-    def forward(ctx, x2d, projs, one_gemm, *ab):
+    def forward(ctx, x2d, projs, one_gemm, rope, *ab):
         n = len(projs)
         a16 = [t.to(torch.float16).contiguous() for t in ab[0::2]]
         b16 = [t.to(torch.float16).contiguous() for t in ab[1::2]]
         s, mask_scale = projs[0].s, projs[0].mask_scale
         rows = kernels.lora_h_partials_group([x2d] * n, a16, s, [p.keep for p in projs],
                                              mask_scale, b16)
+        if rope is not None and not one_gemm:
+            raise ValueError("the RoPE rides on the grouped GEMM (one_gemm)")
         if one_gemm:
             outs = kernels.nf4_linear_fwd_hp_group([x2d] * n, [p.packed for p in projs],
                                                    [p.state for p in projs],
                                                    [r[0] for r in rows], b16,
-                                                   [p.bias for p in projs])
+                                                   [p.bias for p in projs], rope=rope)
         else:
             outs = [kernels.nf4_linear_fwd_hp(x2d, p.packed, p.state, r[0], b, p.bias)
                     for p, r, b in zip(projs, rows, b16)]
@@ -464,14 +470,14 @@ class NF4LoraSiblingsFunction(torch.autograd.Function):
             items.append(dict(dy=dy.to(torch.float16).contiguous(), x2d=x2d, keep=keeps[i],
                               ht=hts[i], at=ats[i], bt=bts[i], packed=p.packed, state=p.state,
                               mask_scale=p.mask_scale, s=p.s,
-                              wants=(need[0], need[3 + 2 * i], need[4 + 2 * i])))
+                              wants=(need[0], need[4 + 2 * i], need[5 + 2 * i])))
         res = lora_backward_group(items, sum_dx=True)
         dx = res[0][0] if need[0] else None
         grads = []
         for i, (_, da, db) in enumerate(res):
             grads += [None if da is None else da.to(ctx.dtypes[2 * i]),
                       None if db is None else db.to(ctx.dtypes[2 * i + 1])]
-        return (dx, None, None, *grads)
+        return (dx, None, None, None, *grads)
 
 
 class NF4LoraStreamFunction(NF4LoraFunction):
@@ -512,13 +518,15 @@ def lora_project(x2d, lora_a, lora_b, packed, state, bias, keep, mask_scale, s):
     return NF4LoraFunction.apply(x2d, lora_a, lora_b, packed, state, bias, keep, mask_scale, s)
 
 
-def siblings_project(x2d, projs, lora_as, lora_bs, one_gemm=True):
+def siblings_project(x2d, projs, lora_as, lora_bs, one_gemm=True, rope=None):
     """NF4LoraSiblingsFunction: torch.ops.mxs_nf4.lora_siblings when ops.ENABLED, else the
-    Python Function.  Returns one fp16 [M, N_i] per projection."""
+    Python Function.  Returns one fp16 [M, N_i] per projection.  rope = (n_rope, cos, sin):
+    the first n_rope outputs come rotated (RoPE folded into the grouped GEMM), with the
+    backward of the unrotated outputs (see NF4LoraSiblingsFunction)."""
     if ops.ENABLED:
-        return ops.lora_siblings(x2d, projs, lora_as, lora_bs, one_gemm)
+        return ops.lora_siblings(x2d, projs, lora_as, lora_bs, one_gemm, rope)
     ab = [t for pair in zip(lora_as, lora_bs) for t in pair]
-    return NF4LoraSiblingsFunction.apply(x2d, projs, bool(one_gemm), *ab)
+    return NF4LoraSiblingsFunction.apply(x2d, projs, bool(one_gemm), rope, *ab)
 
 
 # ---------------------------------------------------------------------------------------------

@@ -58,18 +58,20 @@ def lora_linear(x, lora_a, lora_b, packed, state, bias, keep, mask_scale, s):
                               float(mask_scale), float(s))
 
 
-def lora_siblings(x2d, projs, lora_as, lora_bs, one_gemm=True):
+def lora_siblings(x2d, projs, lora_as, lora_bs, one_gemm=True, rope=None):
     """The projections `projs` (linear4bit.Proj, one scaling and dropout rate) over one input
     x2d fp16 [M, K], their launches shared (NF4LoraSiblingsFunction): a list of fp16 [M, N_i].
     one_gemm: the forward GEMMs in one grouped launch (128x128 tiles) rather than each on its
-    own plan."""
+    own plan.  rope = (n_rope, cos, sin): the first n_rope outputs come rotated, their
+    backward still that of the unrotated outputs (linear4bit.siblings_project)."""
     p0 = projs[0]
+    n_rope, cos, sin = rope if rope is not None else (0, None, None)
     return load().lora_siblings(
         x2d, list(lora_as), list(lora_bs), [p.packed for p in projs],
         [p.state.absmax for p in projs], [p.state.state2.code for p in projs],
         [p.state.state2.absmax for p in projs], [p.state.offset for p in projs],
         [p.bias for p in projs], [p.keep for p in projs], float(p0.mask_scale), float(p0.s),
-        bool(one_gemm))
+        bool(one_gemm), cos, sin, int(n_rope))
 
 
 def dequant(packed, shape, dtype, absmax_8bit=None, code=None, absmax2=None, offset=None,

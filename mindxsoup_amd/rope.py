@@ -118,6 +118,37 @@ class QKVRotary(torch.autograd.Function):
         return (None, None, None, None, None, None, *grads)
 
 
+class RotatedHeads(torch.autograd.Function):
+    """q and k that a projection already returns rotated (the RoPE folded into the grouped q/k/v
+    GEMM, kernels.nf4_linear_fwd_hp_group with rope): forward, the [B, heads, T, D] views of
+    those outputs, no launch; backward, the inverse rotation of dq and dk in one launch (the
+    backward half of QKVRotary), handed to the projection node, whose backward is that of the
+    unrotated outputs.  Forward and backward together are QKVRotary's."""
+
+    @staticmethod
+    def forward(ctx, n_q, n_kv, cos, sin, q_rot, k_rot):
+        cos, sin = _angles(cos, sin)
+        ctx.save_for_backward(cos, sin)
+        ctx.n = (n_q, n_kv)
+        return as_heads(q_rot, n_q), as_heads(k_rot, n_kv)
+
+    @staticmethod
+    def backward(ctx, dq, dk):
+        cos, sin = ctx.saved_tensors
+        n_q, n_kv = ctx.n
+        dq_h, dk_h = _one_dtype(as_heads(dq, n_q), as_heads(dk, n_kv))
+        gq = _new_heads(dq_h, n_q, torch.float16)
+        gk = _new_heads(dk_h, n_kv, torch.float16)
+        kernels.qkv_rope(dq_h, None, dk_h, None, None, cos, sin, gq, gk, None, backward=True)
+        return None, None, None, None, as_rows(gq), as_rows(gk)
+
+
+def rotated_heads(q_rot, k_rot, cos, sin, n_q, n_kv):
+    """(q, k) [B, heads, T, 128] for attention from projection outputs [B, T, heads * 128] that
+    are already rotated (RotatedHeads)."""
+    return direct.run(RotatedHeads, n_q, n_kv, cos, sin, q_rot, k_rot)
+
+
 def qkv_rope(q_base, q_lora, k, v_base, v_lora, cos, sin, n_q, n_kv, q_scale=1.0, v_scale=1.0):
     """(q, k, v) for attention, fp16 [B, heads, T, 128] (the reference's qkv_rope interface,
     solution/attention.py:169-171).  Inputs are the projections' [B, T, heads * 128] outputs (or

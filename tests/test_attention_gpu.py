@@ -67,8 +67,9 @@ def _max_rel(a, b):
     (4, 512, True, ("q_proj", "v_proj")), (2, 77, True, ("q_proj", "k_proj", "v_proj")),
     (4, 512, True, ("q_proj", "k_proj", "v_proj"))])
 def test_matches_original_without_dropout(cuda, monkeypatch, batch, n_tokens, masked, targets):
-    """LoRA on q and v: each projection on its own fused kernels; on q, k and v: the three in
-    shared launches (NF4LoraSiblingsFunction)."""
+    """LoRA on q and v: each projection on its own fused kernels, then the rotation launch; on
+    q, k and v: the three in shared launches (NF4LoraSiblingsFunction) with the rotation in
+    their GEMM."""
     from transformers.models.qwen2 import modeling_qwen2
 
     from mindxsoup_amd import attention, linear4bit
@@ -80,9 +81,12 @@ def test_matches_original_without_dropout(cuda, monkeypatch, batch, n_tokens, ma
     monkeypatch.setattr(cls, "forward", original)
     monkeypatch.setattr(cls, "_mindx_fp16", False, raising=False)
     assert attention.patch_qwen2_attention_fp16() and attention.patch_qwen2_attention_fp16()
-    calls = []
+    calls, folded = [], []
     real = attention.qkv_rope
     monkeypatch.setattr(attention, "qkv_rope", lambda *a: calls.append(1) or real(*a))
+    real_rot = attention.rotated_heads
+    monkeypatch.setattr(attention, "rotated_heads",
+                        lambda *a: folded.append(1) or real_rot(*a))
     attn = _attention(targets=targets).eval()  # LoRA dropout off
     sib = []
     real_sib = linear4bit.siblings_project
@@ -95,12 +99,46 @@ def test_matches_original_without_dropout(cuda, monkeypatch, batch, n_tokens, ma
         if masked else None
     ref = _run(attn, original, hidden, cos, sin, mask)
     ours = _run(attn, cls.forward, hidden, cos, sin, mask)
-    assert calls, "the fp16 path was not taken"
+    assert calls or folded, "the fp16 path was not taken"
     assert bool(sib) == (len(targets) == 3), "q/k/v in shared launches exactly when all have LoRA"
+    assert bool(folded) == bool(sib) and bool(calls) != bool(sib), "rotation in the GEMM"
     names = ["output", "grad input"] + [n for n, _ in attn.named_parameters() if "lora_" in n]
     assert len(ours) == len(ref) == 2 + 2 * len(targets)
     for name, a, b in zip(names, ours, ref):
         assert a.shape == b.shape and _max_rel(a, b) < 1e-2, f"{name}: {_max_rel(a, b):.2e}"
+
+
+@pytest.mark.parametrize("batch,n_tokens,masked", [(1, 1024, False), (2, 77, True),
+                                                   (4, 512, True)])
+def test_rope_in_the_gemm_gives_the_bits_of_the_rotation_launch(cuda, monkeypatch, batch,
+                                                                n_tokens, masked):
+    """q, k, v all with LoRA: the rotation folded into the siblings GEMM (attention.FOLD_ROPE)
+    against the same path with the rotation as its own launch: output, input gradient and
+    LoRA gradients bit for bit (1024 tokens: the 128x64 plan; 2048: 128x128)."""
+    from transformers.models.qwen2 import modeling_qwen2
+
+    from mindxsoup_amd import attention
+
+    print(f"case rope fold attention batch={batch} tokens={n_tokens}", flush=True)
+    cls = modeling_qwen2.Qwen2Attention
+    original = getattr(cls.forward, "_mindx_original", cls.forward)
+    monkeypatch.setattr(cls, "forward", original)
+    monkeypatch.setattr(cls, "_mindx_fp16", False, raising=False)
+    assert attention.patch_qwen2_attention_fp16()
+    attn = _attention(targets=("q_proj", "k_proj", "v_proj")).eval()
+    torch.manual_seed(4)
+    hidden = torch.randn(batch, n_tokens, HIDDEN, device="cuda")
+    cos, sin = _cos_sin(n_tokens)
+    mask = _padding_mask(batch, n_tokens, [n_tokens - 9 * i for i in range(batch)]) \
+        if masked else None
+    monkeypatch.setattr(attention, "FOLD_ROPE", False)
+    apart = _run(attn, cls.forward, hidden, cos, sin, mask)
+    monkeypatch.setattr(attention, "FOLD_ROPE", True)
+    folded = _run(attn, cls.forward, hidden, cos, sin, mask)
+    names = ["output", "grad input"] + [n for n, _ in attn.named_parameters() if "lora_" in n]
+    assert len(folded) == len(apart) == 8
+    for name, a, b in zip(names, folded, apart):
+        assert torch.equal(a, b), name
 
 
 def test_without_autocast_takes_original(cuda, monkeypatch):

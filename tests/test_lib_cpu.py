@@ -64,3 +64,28 @@ def test_layer_plan_marks_straddling_workgroups():
     assert L.mxs_nf4_dequant_layer_plan(block0.ctypes.data, 4, out.ctypes.data, n) == n
     assert out.tolist() == [0, 1, -1, 3, 3]  # workgroup 2 spans blocks 256..383: modules 1 and 3
     assert L.mxs_nf4_dequant_layer_plan(block0.ctypes.data, 4, out.ctypes.data, 2) < 0
+
+
+def test_group_rope_entry_checks_its_rotation_operands_on_the_host():
+    """mxs_nf4_linear_fwd_hp_group_rope refuses bad rotation operands before any device work:
+    a rotated output that is not whole 128-column heads, n_rope outside 1..n, missing or
+    misaligned cos / sin, and rows that are not whole sequences."""
+    import ctypes
+
+    from mindxsoup_amd import _lib
+
+    f = _lib.lib().mxs_nf4_linear_fwd_hp_group_rope
+    p = (ctypes.c_void_p * 2)(0x1000, 0x1000)  # stand-ins, never dereferenced on these paths
+
+    def call(N, n_rope=1, cos=0x1000, cs_t=128, T=64, M=128):
+        Ns = (ctypes.c_int * 2)(*N)
+        return f(2, p, M, 256, Ns, p, p, p, p, p, None, None, 0, 0, None, 16, None, p, n_rope,
+                 cos, 0x1000, 0, cs_t, T, None)
+
+    assert call((192, 128)) == -4  # MXS_ERR_SIZE
+    assert call((128, 128), n_rope=0) == -1  # MXS_ERR_ARG
+    assert call((128, 128), n_rope=3) == -1
+    assert call((128, 128), cos=None) == -1
+    assert call((128, 128), T=48) == -1
+    assert call((128, 128), cos=0x1004) == -3  # MXS_ERR_ALIGN
+    assert call((128, 128), cs_t=130) == -3

@@ -166,7 +166,7 @@ def test_siblings_function_matches_oracle(cuda, M):
         keeps.append(keep)
     projs = tuple(projs)
     assert siblings_ok(projs, 1536)
-    ys = NF4LoraSiblingsFunction.apply(x, projs, True, *ab)
+    ys = NF4LoraSiblingsFunction.apply(x, projs, True, None, *ab)
     dys = [torch.randn(y.shape, device=cuda, generator=g).half() for y in ys]
     torch.autograd.backward(ys, dys)
     x16 = _np(x).astype(np.float16)

@@ -170,8 +170,48 @@ def test_siblings_bits_equal_python_path(cuda, M, one_gemm, shapes):
     got = run(lambda x_, a_, b_: ops.lora_siblings(x_, projs, a_, b_, one_gemm))
     ab = lambda a_, b_: [t for pair in zip(a_, b_) for t in pair]  # noqa: E731
     want = run(lambda x_, a_, b_: NF4LoraSiblingsFunction.apply(x_, tuple(projs), one_gemm,
-                                                                *ab(a_, b_)))
+                                                                None, *ab(a_, b_)))
     _same(got, want, "lora_siblings")
+
+
+@pytest.mark.parametrize("M", [1024, 300])
+def test_siblings_with_folded_rope_bits_equal_python_path(cuda, M):
+    """lora_siblings with the RoPE of q and k folded into the grouped GEMM (n_rope = 2, one
+    sequence of M tokens): C++ and Python paths give the same rotated outputs, the same summed
+    dx and the same LoRA gradients (the backward is the unrotated projections')."""
+    from mindxsoup_amd import ops
+    from mindxsoup_amd.linear4bit import NF4LoraSiblingsFunction, Proj
+
+    print(f"case op lora_siblings rope M={M}", flush=True)
+    shapes = [(1536, 1536), (256, 1536), (256, 1536)]
+    layers = [_layer(cuda, n, k, 20 + i, bias=True) for i, (n, k) in enumerate(shapes)]
+    g = torch.Generator(device=cuda)
+    g.manual_seed(8)
+    x = torch.randn((M, 1536), device=cuda, generator=g).half()
+    projs, a_s, b_s = [], [], []
+    for lyr in layers:
+        n, k = lyr.weight.quant_state.shape
+        a_s.append((torch.rand((16, k), device=cuda, generator=g) * 2 - 1) / k ** 0.5)
+        b_s.append(torch.randn((n, 16), device=cuda, generator=g) * 0.01)
+        projs.append(Proj(lyr.weight.data.view(-1, 1), lyr.weight.quant_state, lyr.bias, None,
+                          1.0, S))
+    ang = torch.arange(M, device=cuda).float()[:, None] * torch.rand(128, device=cuda)
+    cos, sin = ang.cos()[None].contiguous(), ang.sin()[None].contiguous()
+    dys = [torch.randn((M, n), device=cuda, generator=g).half() for n, _ in shapes]
+
+    def run(fn):
+        xl = x.clone().requires_grad_(True)
+        al = [t.clone().requires_grad_(True) for t in a_s]
+        bl = [t.clone().requires_grad_(True) for t in b_s]
+        ys = fn(xl, al, bl)
+        return [*ys, *torch.autograd.grad(ys, [xl, *al, *bl], dys)]
+
+    rope = (2, cos, sin)
+    got = run(lambda x_, a_, b_: ops.lora_siblings(x_, projs, a_, b_, True, rope))
+    ab = lambda a_, b_: [t for pair in zip(a_, b_) for t in pair]  # noqa: E731
+    want = run(lambda x_, a_, b_: NF4LoraSiblingsFunction.apply(x_, tuple(projs), True, rope,
+                                                                *ab(a_, b_)))
+    _same(got, want, "lora_siblings rope")
 
 
 def test_linear_bits_equal_python_path(cuda):
