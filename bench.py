@@ -129,6 +129,41 @@ def bench_dequant(m, steps, warmup):
     return wall / steps * 1e3, float(np.mean(per_launch)), out
 
 
+def hbm_ceiling(packed, out, steps, warmup):
+    """What HBM delivers on this part (mxs_hbm_probe), timed like the dequant: pure 16-byte
+    load and store streams over the output's bytes, and the dequant's access pattern without
+    its arithmetic (4-byte non-temporal loads of the packed bytes, 16-byte non-temporal stores
+    over the fp16 output: 20 % reads, 80 % writes).  GB/s over the bytes each launch moves."""
+    from mindxsoup_amd import _lib
+
+    n = packed.numel() // 4             # dword chunks of the packed bytes
+    m = out.numel() * out.element_size() // 16  # 16-byte chunks of the output
+    sink = torch.empty(((m + 1023) // 1024) * 4, dtype=torch.int32, device=out.device)
+    cases = {"pattern": (0, packed, out, n, 20 * n),
+             "load_only": (1, out, sink, m, 16 * m),
+             "store_only": (2, None, out, m, 16 * m)}
+    stream = torch.cuda.current_stream()
+    res = {}
+    for name, (kind, src, dst, chunks, nbytes) in cases.items():
+        def launch():
+            _lib.call("mxs_hbm_probe", kind, _lib.ptr(src), _lib.ptr(dst), chunks,
+                      _lib.stream_of(dst.device))
+
+        for _ in range(warmup):
+            launch()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(steps):
+            launch()
+        b.record(stream)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / steps
+        res[name] = {"GBps": round(nbytes / ms / 1e6, 1), "bytes": nbytes,
+                     "ms": round(ms, 4)}
+    return res
+
+
 # The GPU box gives one GPU's job a share of 16 host cores (its OMP_NUM_THREADS), whatever its
 # affinity set shows; more threads would only oversubscribe that share.
 CPU_SHARE = 16
@@ -955,8 +990,11 @@ def main():
     torch.cuda.synchronize()
     print(f"bench: {len(m['nb'])} NF4 weights resident ({m['packed'].numel() / 1e9:.3f} GB packed)",
           file=sys.stderr, flush=True)
-    ms_step, ms_kernel, _ = bench_dequant(m, args.steps, args.warmup)
+    ms_step, ms_kernel, dq_out = bench_dequant(m, args.steps, args.warmup)
     print(f"bench: dequant timed, {ms_step:.4f} ms/step", file=sys.stderr, flush=True)
+    ceiling = hbm_ceiling(m["packed"], dq_out, args.steps, args.warmup)
+    del dq_out
+    nblocks = m["absmax8"].numel()
     cpu_baseline_dequant_cached = None
     if not args.no_cpu:
         print("bench: CPU baseline (oracle decode)", file=sys.stderr, flush=True)
@@ -978,7 +1016,15 @@ def main():
                      "traffic": measured_traffic(),
                      "kernel": "k_dequant_wide<nested, multi, f16>",
                      "kernel_ms": round(ms_kernel, 4)},
+        "hbm_ceiling": ceiling,
     }
+    # the dequant's own read / write mix at the pure streams' rates: the rate its bytes could
+    # move at if reads ran at load_only's and writes at store_only's
+    wbytes = 2 * 64 * nblocks
+    mix = nbytes / ((nbytes - wbytes) / ceiling["load_only"]["GBps"]
+                    + wbytes / ceiling["store_only"]["GBps"])
+    ceiling["mix_GBps"] = round(mix, 1)
+    ceiling["dequant_over_mix"] = round(achieved / mix, 4)
     del m
     torch.cuda.empty_cache()
     if not args.no_gemm:

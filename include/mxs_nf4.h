@@ -475,6 +475,14 @@ int mxs_nf4_linear_glu_fused(int M, int N, int K, int bwd);
 /* dst[cols, rows] = src[rows, cols]^T, fp16 (lora_A -> the [K, r] operand of the backward). */
 int mxs_transpose_f16(const void* src, int rows, int cols, void* dst, hipStream_t stream);
 
+/* Measurement only, no counterpart in the reference: streams over n_chunks 16-byte chunks that
+ * report what HBM delivers for an access pattern (bench.py's hbm_ceiling).  kind 0: the
+ * standalone dequant's pattern without its arithmetic (4-byte non-temporal loads from src,
+ * 16-byte non-temporal stores of the dword repeated to dst; 4 + 16 bytes per chunk); kind 1:
+ * 16-byte loads from src only (dst receives 4 bytes per 64 chunks); kind 2: 16-byte stores to
+ * dst only (src unused, may be NULL).  dst 16-byte aligned; src 16-byte aligned for kind 1. */
+int mxs_hbm_probe(int kind, const void* src, void* dst, int64_t n_chunks, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -71,6 +71,7 @@ _SIGNATURES = {
     "mxs_nf4_linear_fwd_hp_group_rope": [I32, P, I32, I32, P, P, P, P, P, P, P, P, I32, I32, P,
                                          I32, P, P, I32, P, P, I64, I64, I32, P],
     "mxs_qkv_rope": [P, P, P, P, I64, I64, I32, I32, I32, I32, I32, I32, I32, F32, F32, P],
+    "mxs_hbm_probe": [I32, P, P, I64, P],
     "mxs_silu_mul_bwd": [P, P, P, I64, P],
     "mxs_lora_slices": [I32, I32],
     "mxs_lora_h_partials": [P, I32, I32, P, I32, P, F32, F32, I32, P, P, I32, P, P, P],

@@ -240,3 +240,37 @@ def test_full_model_grouped_dequant_properties(cuda):
         n0 = int(block0[i].item()) * 64
         got = out[n0:n0 + s.shape[0] * s.shape[1]].cpu().view(torch.int16).numpy()
         assert np.array_equal(got, O.dequant(q).view(np.int16).reshape(-1))
+
+
+def test_hbm_probe_streams_what_it_reports(cuda):
+    """mxs_hbm_probe (bench.py's hbm_ceiling) moves the bytes it is timed on: the dequant's
+    pattern writes each loaded dword four times at its chunk, the store stream writes every
+    chunk, and the load stream reads every chunk (its per-wave XOR matches the host's), on a
+    chunk count that leaves a partial workgroup."""
+    from mindxsoup_amd import _lib
+
+    n = 5000
+    stream = _lib.stream_of(cuda)
+    src = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, 4), dtype=torch.int32, device=cuda)
+    dst = torch.zeros((n, 4), dtype=torch.int32, device=cuda)
+    _lib.call("mxs_hbm_probe", 0, _lib.ptr(src), _lib.ptr(dst), n, stream)
+    torch.cuda.synchronize()
+    words = src.view(-1)[:n]
+    assert torch.equal(dst, words[:, None].expand(n, 4))
+    _lib.call("mxs_hbm_probe", 2, None, _lib.ptr(dst), n, stream)
+    torch.cuda.synchronize()
+    idx = torch.arange(n, dtype=torch.int32, device=cuda)
+    assert torch.equal(dst, torch.stack([idx, idx ^ 1, idx ^ 2, idx ^ 3], 1))
+    blocks = (n + 1023) // 1024
+    sink = torch.zeros(blocks * 4, dtype=torch.int32, device=cuda)
+    _lib.call("mxs_hbm_probe", 1, _lib.ptr(src), _lib.ptr(sink), n, stream)
+    torch.cuda.synchronize()
+    x = src.cpu().numpy().view(np.uint32)
+    want = np.zeros(blocks * 4, dtype=np.uint32)
+    for b in range(blocks):
+        for t in range(256):
+            for u in range(4):
+                c = b * 1024 + u * 256 + t
+                if c < n:
+                    want[b * 4 + t // 64] ^= np.bitwise_xor.reduce(x[c])
+    assert np.array_equal(sink.cpu().numpy().view(np.uint32), want)
