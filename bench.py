@@ -947,6 +947,9 @@ def main():
     ap.add_argument("--no-gemm", action="store_true", help="dequant only")
     ap.add_argument("--stream", action="store_true",
                     help="only the host-streamed weights section (its JSON on stdout)")
+    ap.add_argument("--qkv", action="store_true",
+                    help="only the q/k/v RoPE section: the rotation kernel and the q/k/v "
+                         "projection with the rotation apart or folded (its JSON on stdout)")
     ap.add_argument("--calibrate", action="store_true",
                     help="only run a 1 GiB device copy (reference for the PMC byte counters)")
     ap.add_argument("--kernel", choices=sorted(KERNELS),
@@ -985,6 +988,12 @@ def main():
         g = torch.Generator(device=dev)
         g.manual_seed(1)
         print(json.dumps(bench_stream(dev, g, args.steps, args.warmup)), flush=True)
+        return
+    if args.qkv:
+        g = torch.Generator(device=dev)
+        g.manual_seed(1)
+        print(json.dumps({"qkv_rope": bench_qkv_rope(dev, g, args.steps, args.warmup)}),
+              flush=True)
         return
     m = model_weights(dev)
     torch.cuda.synchronize()
