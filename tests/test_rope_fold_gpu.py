@@ -51,6 +51,7 @@ def _heads(y, B, T, n):
 @pytest.mark.parametrize("B,T,cos_batch,lora", [
     (1, 1024, 1, True),    # 256 tiles of 128x64: the stack's shape
     (2, 1024, 2, True),    # 512 tiles: the 128x128 plan
+    (1, 1100, 1, True),    # 128x128 with a partial row tile
     (3, 100, 1, True),     # a partial row tile
     (3, 100, 3, False),
     (1, 37, 1, True),
