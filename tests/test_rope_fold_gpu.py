@@ -49,17 +49,18 @@ def _heads(y, B, T, n):
 
 
 @pytest.mark.parametrize("B,T,cos_batch,lora", [
-    (1, 1024, 1, True),    # 256 tiles of 128x64: the stack's shape
-    (2, 1024, 2, True),    # 512 tiles: the 128x128 plan
-    (1, 1100, 1, True),    # 128x128 with a partial row tile
-    (3, 100, 1, True),     # a partial row tile
-    (3, 100, 3, False),
-    (1, 37, 1, True),
+    (1, 1024, 1, 16),    # 256 tiles of 128x64: the stack's shape
+    (2, 1024, 2, 16),    # 512 tiles: the 128x128 plan
+    (1, 1100, 1, 16),    # 128x128 with a partial row tile
+    (3, 100, 1, 16),     # a partial row tile
+    (3, 100, 1, 32),     # rank 32: the LoRA operands read from memory, not staged
+    (3, 100, 3, 0),
+    (1, 37, 1, 16),
 ])
 def test_folded_rope_equals_the_rotation_of_the_projection(cuda, B, T, cos_batch, lora):
     from mindxsoup_amd import kernels
 
-    print(f"case rope fold B={B} T={T} cos_batch={cos_batch} lora={lora}", flush=True)
+    print(f"case rope fold B={B} T={T} cos_batch={cos_batch} rank={lora}", flush=True)
     M = B * T
     layers = [_nf4(cuda, n, K, 400 + i) for i, n in enumerate((1536, 256, 256))]
     packeds = [L.weight.data.view(-1, 1) for L in layers]
@@ -70,9 +71,9 @@ def test_folded_rope_equals_the_rotation_of_the_projection(cuda, B, T, cos_batch
     x = torch.randn((M, K), device=cuda, generator=g).half()
     hps = bs = None
     if lora:
-        As = [((torch.rand((16, K), device=cuda, generator=g) * 2 - 1) / np.sqrt(K)).half()
+        As = [((torch.rand((lora, K), device=cuda, generator=g) * 2 - 1) / np.sqrt(K)).half()
               for _ in layers]
-        bs = [(torch.randn((L.out_features, 16), device=cuda, generator=g) * 0.05).half()
+        bs = [(torch.randn((L.out_features, lora), device=cuda, generator=g) * 0.05).half()
               for L in layers]
         outs = kernels.lora_h_partials_group([x] * 3, As, 2.0, None, 1.0, bs)
         hps = [o[0] for o in outs]
