@@ -115,3 +115,39 @@ def test_folded_rope_refuses_partial_heads(cuda):
         kernels.nf4_linear_fwd_hp_group([x] * 2, [L.weight.data.view(-1, 1) for L in layers],
                                         [L.weight.quant_state for L in layers],
                                         rope=(1, cos[:, :48].contiguous(), sin[:, :48].contiguous()))
+
+
+def test_folded_rope_replays_in_a_graph(cuda):
+    """The grouped forward with the rotation captured in a HIP graph: every replay (eager work
+    and synchronizations between them, new inputs copied in before each) equals the eager
+    launch on the same inputs."""
+    from mindxsoup_amd import kernels
+
+    B, T = 1, 1024
+    layers = [_nf4(cuda, n, K, 470 + i) for i, n in enumerate((1536, 256, 256))]
+    packeds = [L.weight.data.view(-1, 1) for L in layers]
+    states = [L.weight.quant_state for L in layers]
+    biases = [L.bias for L in layers]
+    g = torch.Generator(device=cuda)
+    g.manual_seed(23)
+    x = torch.randn((B * T, K), device=cuda, generator=g).half()
+    cos, sin = _cos_sin(cuda, 1, T, 9)
+
+    def run():
+        return kernels.nf4_linear_fwd_hp_group([x] * 3, packeds, states, None, None, biases,
+                                               rope=(2, cos, sin))
+
+    run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = run()
+    for rep in range(3):
+        x.copy_(torch.randn((B * T, K), device=cuda, generator=g).half())
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [y.clone() for y, _ in outs]
+        want = [y for y, _ in run()]
+        torch.cuda.synchronize()
+        for a, b in zip(got, want):
+            assert torch.equal(a, b), rep
