@@ -130,10 +130,10 @@ def bench_dequant(m, steps, warmup):
 
 
 def hbm_ceiling(packed, out, steps, warmup):
-    """What HBM delivers on this part (mxs_hbm_probe), timed like the dequant: pure 16-byte
-    load and store streams over the output's bytes, and the dequant's access pattern without
-    its arithmetic (4-byte non-temporal loads of the packed bytes, 16-byte non-temporal stores
-    over the fp16 output: 20 % reads, 80 % writes).  GB/s over the bytes each launch moves."""
+    """What HBM delivers on this part (mxs_hbm_probe in libmxs_probe.so), timed like the
+    dequant: pure 16-byte load and store streams over the output's bytes, and the dequant's
+    access pattern without its arithmetic (4-byte non-temporal loads of the packed bytes,
+    16-byte non-temporal stores over the fp16 output: 20 % reads, 80 % writes).  GB/s over the bytes each launch moves."""
     from mindxsoup_amd import _lib
 
     n = packed.numel() // 4             # dword chunks of the packed bytes
@@ -146,8 +146,8 @@ def hbm_ceiling(packed, out, steps, warmup):
     res = {}
     for name, (kind, src, dst, chunks, nbytes) in cases.items():
         def launch():
-            _lib.call("mxs_hbm_probe", kind, _lib.ptr(src), _lib.ptr(dst), chunks,
-                      _lib.stream_of(dst.device))
+            _lib.hbm_probe(kind, _lib.ptr(src), _lib.ptr(dst), chunks,
+                           _lib.stream_of(dst.device))
 
         for _ in range(warmup):
             launch()

@@ -117,7 +117,9 @@ int mxs_nf4_linear_fwd(const void* x, int M, int K, int N, const void* packed,
  * memory: code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
  * No counterpart in the reference (its forward allocates through torch).  Nothing is allocated:
  * split-K partials go to a file-scope device array of MXS_NF4_SCRATCH_BYTES, whose address is
- * looked up once per device on the first call made with that device current.  A plan needing
+ * looked up once per device on the first call made with that device current.  That lookup is
+ * not a stream operation: under HIP graph capture, make one call on the device before the
+ * capture begins; the calls after it launch kernels only and are capturable.  A plan needing
  * more (splits * M * N * 4 bytes) returns MXS_ERR_SIZE with nothing launched.  Every call on
  * one GPU shares that array: calls that overlap in time on one GPU (other streams or threads)
  * race and must be serialized by the caller.  Same results as mxs_nf4_linear_fwd. */
@@ -474,14 +476,6 @@ int mxs_nf4_linear_glu_fused(int M, int N, int K, int bwd);
 
 /* dst[cols, rows] = src[rows, cols]^T, fp16 (lora_A -> the [K, r] operand of the backward). */
 int mxs_transpose_f16(const void* src, int rows, int cols, void* dst, hipStream_t stream);
-
-/* Measurement only, no counterpart in the reference: streams over n_chunks 16-byte chunks that
- * report what HBM delivers for an access pattern (bench.py's hbm_ceiling).  kind 0: the
- * standalone dequant's pattern without its arithmetic (4-byte non-temporal loads from src,
- * 16-byte non-temporal stores of the dword repeated to dst; 4 + 16 bytes per chunk); kind 1:
- * 16-byte loads from src only (dst receives 4 bytes per 64 chunks); kind 2: 16-byte stores to
- * dst only (src unused, may be NULL).  dst 16-byte aligned; src 16-byte aligned for kind 1. */
-int mxs_hbm_probe(int kind, const void* src, void* dst, int64_t n_chunks, hipStream_t stream);
 
 #ifdef __cplusplus
 }

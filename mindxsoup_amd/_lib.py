@@ -71,7 +71,6 @@ _SIGNATURES = {
     "mxs_nf4_linear_fwd_hp_group_rope": [I32, P, I32, I32, P, P, P, P, P, P, P, P, I32, I32, P,
                                          I32, P, P, I32, P, P, I64, I64, I32, P],
     "mxs_qkv_rope": [P, P, P, P, I64, I64, I32, I32, I32, I32, I32, I32, I32, F32, F32, P],
-    "mxs_hbm_probe": [I32, P, P, I64, P],
     "mxs_silu_mul_bwd": [P, P, P, I64, P],
     "mxs_lora_slices": [I32, I32],
     "mxs_lora_h_partials": [P, I32, I32, P, I32, P, F32, F32, I32, P, P, I32, P, P, P],
@@ -122,6 +121,29 @@ def lib():
 
 def exported_symbols():
     return list(_SIGNATURES)
+
+
+PROBE_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmxs_probe.so")
+_probe = None
+
+
+def probe_lib():
+    """libmxs_probe.so (include/mxs_probe.h): the HBM rate probes bench.py reports beside the
+    dequant.  Measurement only; the NF4 path never loads it."""
+    global _probe
+    if _probe is None:
+        if not os.path.exists(PROBE_PATH):
+            raise MxsLibraryError(
+                f"{PROBE_PATH} is not built: run `python -m mindxsoup_amd.build` (hipcc, gfx950)")
+        L = ctypes.CDLL(PROBE_PATH)
+        L.mxs_hbm_probe.argtypes = [I32, P, P, I64, P]
+        L.mxs_hbm_probe.restype = ctypes.c_int
+        _probe = L
+    return _probe
+
+
+def hbm_probe(kind, src, dst, n_chunks, stream):
+    check(probe_lib().mxs_hbm_probe(kind, src, dst, n_chunks, stream), "mxs_hbm_probe")
 
 
 def ptr(t):

@@ -6,6 +6,9 @@ Every csrc/*.hip file is compiled by hipcc to an object in csrc/_build/ (in para
 linked into mindxsoup_amd/libmxs_nf4.so.  No torch headers are involved: the library's
 interface is include/mxs_nf4.h.
 
+csrc/probe/hbm_probe.hip (HBM rate probes bench.py reports; include/mxs_probe.h) is linked
+apart into mindxsoup_amd/libmxs_probe.so, so the product library exports only the NF4 path.
+
 csrc/torch_ops.cpp (host C++ only, no device code) is compiled by g++ against torch's headers
 beside them and linked into mindxsoup_amd/libmxs_nf4_torch.so, which registers the
 torch.ops.mxs_nf4 operators and links libmxs_nf4.so from its own directory.
@@ -27,6 +30,8 @@ OBJ = os.path.join(CSRC, "_build")
 LIB = os.path.join(PKG, "libmxs_nf4.so")
 TORCH_SRC = os.path.join(CSRC, "torch_ops.cpp")
 TORCH_LIB = os.path.join(PKG, "libmxs_nf4_torch.so")
+PROBE_SRC = os.path.join(CSRC, "probe", "hbm_probe.hip")
+PROBE_LIB = os.path.join(PKG, "libmxs_probe.so")
 ARCH = "gfx950"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -112,27 +117,34 @@ def _link_torch_ops(obj):
     os.replace(tmp, TORCH_LIB)
 
 
+def _link_hip(objs, lib):
+    tmp = lib + ".tmp"
+    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link of {lib} failed:\n{r.stderr}")
+    os.replace(tmp, lib)
+
+
 def build(verbose=True):
     os.makedirs(OBJ, exist_ok=True)
     srcs = sources()
     asm_srcs = [s for s in srcs if "vm_ready(" in open(s).read()]
-    workers = min(len(srcs) + len(asm_srcs) + 1, max(1, (os.cpu_count() or 4)), 8)
+    workers = min(len(srcs) + len(asm_srcs) + 2, max(1, (os.cpu_count() or 4)), 8)
     with concurrent.futures.ThreadPoolExecutor(workers) as ex:
         torch_obj = ex.submit(_compile_torch_ops)
+        probe_obj = ex.submit(_compile, PROBE_SRC)
         checks = [ex.submit(_check_asm, s) for s in asm_srcs]
         objs = list(ex.map(_compile, srcs))
         for c in checks:
             c.result()
         torch_obj = torch_obj.result()
-    tmp = LIB + ".tmp"
-    r = subprocess.run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp],
-                       capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+        probe_obj = probe_obj.result()
+    _link_hip(objs, LIB)
+    _link_hip([probe_obj], PROBE_LIB)
     _link_torch_ops(torch_obj)
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources and {TORCH_LIB}")
+        print(f"built {LIB} from {len(srcs)} sources, {TORCH_LIB} and {PROBE_LIB}")
     return LIB
 
 

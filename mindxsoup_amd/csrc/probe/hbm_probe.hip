@@ -1,7 +1,8 @@
 // HBM rate probes for gfx950: what the memory delivers for the standalone dequant's access
 // pattern with none of its arithmetic, and for pure load and pure store streams.  bench.py
 // reports them beside the dequant so that its fraction of peak can be read against what this
-// part reaches for the same mix of reads and writes.
+// part reaches for the same mix of reads and writes.  Built into libmxs_probe.so, apart from the
+// product library.
 //
 //   kind 0, the dequant's pattern (k_dequant_wide): 256 lanes per workgroup, lane t loads the
 //     dwords c0 + t + 256 u (u < 4) non-temporally and stores 16 bytes per dword loaded at the
@@ -12,6 +13,7 @@
 //   kind 2, stores only: 16 bytes per chunk, as kind 0 stores.
 #include "common.h"
 #include "mxs_nf4.h"
+#include "mxs_probe.h"
 
 namespace mxs {
 

@@ -22,7 +22,10 @@ PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmxs_nf4_torc
 OPS = ("dequant", "linear_fwd", "linear_bwd_dx", "lora_fwd", "lora_bwd", "lora_fwd_group",
        "lora_bwd_group", "linear", "lora_linear", "lora_siblings")
 
-ENABLED = True  # set by apply() from FEATURES["torch_ops"]; False: the Python Functions
+# set by apply() from FEATURES["torch_ops"]; False: the Python Functions.  Off when MXS_NF4_LIB
+# names another build of the C-ABI library: this library links the package's own copy by file
+# name, so its ops would run that copy instead of the named one.
+ENABLED = not os.environ.get("MXS_NF4_LIB")
 
 _ops = None
 
@@ -31,6 +34,11 @@ def load():
     """torch.ops.mxs_nf4 with the library loaded (once)."""
     global _ops
     if _ops is None:
+        if os.environ.get("MXS_NF4_LIB"):
+            raise _lib.MxsLibraryError(
+                "MXS_NF4_LIB is set: the operator library links the package's own "
+                "libmxs_nf4.so, not the named build; use the Python Functions "
+                "(FEATURES['torch_ops'] = False) for A/B runs of another build")
         if not os.path.exists(PATH):
             raise _lib.MxsLibraryError(
                 f"{PATH} is not built: run `python -m mindxsoup_amd.build` (hipcc, gfx950)")

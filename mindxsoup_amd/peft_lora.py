@@ -12,7 +12,7 @@ in its accumulators, and the backward's dX / dA / dB in at most three launches.
 
 A layer is taken when it has exactly one plain adapter (no DoRA or other variant, no LoRA bias),
 is not merged or disabled, its base is an fp16 NF4 layer the fused kernels take, the rank is a
-multiple of 16, and the input is fp16 (or fp32 under fp16 autocast, where peft's branch
+multiple of 16 no larger than 128, and the input is fp16 (or fp32 under fp16 autocast, where peft's branch
 computes in fp16 as well).  Anything else runs the layer's own forward.
 """
 
@@ -127,13 +127,18 @@ def _fp16_input(x):
     return None
 
 
+MAX_RANK = 128
+
+
 def takes(ad, x16):
     """Whether NF4LoraFunction takes this adapter on this fp16 input."""
     if ad is None or x16 is None or not linear4bit.FUSED_LORA:
         return False
     base = ad.base
     state = base.weight.quant_state
-    if ad.rank % 16 != 0 or ad.a.shape[1] != state.shape[1] or ad.b.shape[0] != state.shape[0]:
+    # the LoRA row kernels hold r / 16 accumulator blocks, at most 8 (MXS_ERR_SIZE past r = 128)
+    if ad.rank % 16 != 0 or ad.rank > MAX_RANK or ad.a.shape[1] != state.shape[1] or \
+            ad.b.shape[0] != state.shape[0]:
         return False
     return linear4bit._direct_ok(base, x16, stream.offloaded(base)) and \
         kernels.fused_shape_ok(state)

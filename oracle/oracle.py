@@ -194,13 +194,16 @@ def dequant(wt: NF4Weight = None, *, packed=None, absmax8=None, code=None, absma
 # ---------------------------------------------------------------------------------------------
 
 def dropout_fp16(x_f16, keep_u8, p):
-    """solution/dropout.py:33-35: keep ? fp16(fp32(x) * fp32(1/(1-p))) : 0."""
+    """solution/dropout.py:33-35: keep ? fp16(fp32(x) * fp32(1/(1-p))) : 0.  Pinned in
+    tests/test_oracle.py by closed forms (p = 0.5, 0.75 give exactly 2x, 4x; dropped elements
+    +0.0) and by exact rational arithmetic over every finite fp16 value at p = 0.05."""
     x = np.asarray(x_f16, np.float16)
     if keep_u8 is None:
         return x
     scale = np.float32(1.0 / (1.0 - p))
-    return np.where(keep_u8 != 0, (x.astype(np.float32) * scale).astype(np.float16),
-                    np.float16(0))
+    with np.errstate(over="ignore"):  # products past fp16's range become ±inf, as in the kernel
+        kept = (x.astype(np.float32) * scale).astype(np.float16)
+    return np.where(keep_u8 != 0, kept, np.float16(0))
 
 
 def linear_fwd(x_f16, w_f16, bias=None):

@@ -253,17 +253,17 @@ def test_hbm_probe_streams_what_it_reports(cuda):
     stream = _lib.stream_of(cuda)
     src = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, 4), dtype=torch.int32, device=cuda)
     dst = torch.zeros((n, 4), dtype=torch.int32, device=cuda)
-    _lib.call("mxs_hbm_probe", 0, _lib.ptr(src), _lib.ptr(dst), n, stream)
+    _lib.hbm_probe(0, _lib.ptr(src), _lib.ptr(dst), n, stream)
     torch.cuda.synchronize()
     words = src.view(-1)[:n]
     assert torch.equal(dst, words[:, None].expand(n, 4))
-    _lib.call("mxs_hbm_probe", 2, None, _lib.ptr(dst), n, stream)
+    _lib.hbm_probe(2, None, _lib.ptr(dst), n, stream)
     torch.cuda.synchronize()
     idx = torch.arange(n, dtype=torch.int32, device=cuda)
     assert torch.equal(dst, torch.stack([idx, idx ^ 1, idx ^ 2, idx ^ 3], 1))
     blocks = (n + 1023) // 1024
     sink = torch.zeros(blocks * 4, dtype=torch.int32, device=cuda)
-    _lib.call("mxs_hbm_probe", 1, _lib.ptr(src), _lib.ptr(sink), n, stream)
+    _lib.hbm_probe(1, _lib.ptr(src), _lib.ptr(sink), n, stream)
     torch.cuda.synchronize()
     x = src.cpu().numpy().view(np.uint32)
     want = np.zeros(blocks * 4, dtype=np.uint32)

@@ -33,6 +33,19 @@ def test_library_exports_every_declared_symbol():
     assert sorted(_lib.exported_symbols()) == _declared()
 
 
+def test_probe_library_apart_from_the_product():
+    """The HBM probes bench.py reports live in libmxs_probe.so (include/mxs_probe.h), not in
+    the product library or its header."""
+    from mindxsoup_amd import _lib
+
+    text = open(os.path.join(ROOT, "include", "mxs_probe.h")).read()
+    names = re.findall(r"^int\s+(mxs_\w+)\s*\(", text, flags=re.M)
+    assert names == ["mxs_hbm_probe"]
+    assert "mxs_hbm_probe" not in _declared()
+    assert hasattr(_lib.probe_lib(), "mxs_hbm_probe")
+    assert not hasattr(ctypes.CDLL(_lib.LIB_PATH), "mxs_hbm_probe")
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     from mindxsoup_amd import _lib
 

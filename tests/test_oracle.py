@@ -223,6 +223,114 @@ def test_absmax_mean_close_to_exact_mean():
     assert abs(O.absmax_mean(a) - exact) <= 1e-7 * exact
 
 
+# --- LoRA dropout -------------------------------------------------------------------------
+
+def _round_binary(q, man_bits, emin, emax):
+    """Round the rational q to nearest even in a binary format with man_bits fraction bits,
+    smallest normal exponent emin and largest exponent emax (subnormals kept, overflow to an
+    infinity).  Returns a Fraction or ±math.inf; exact, independent of any float hardware."""
+    if q == 0:
+        return Fraction(0)
+    sign = -1 if q < 0 else 1
+    a = abs(q)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    quantum = Fraction(2) ** (max(e, emin) - man_bits)
+    n = a / quantum
+    whole = n.numerator // n.denominator
+    rest = n - whole
+    if rest > Fraction(1, 2) or (rest == Fraction(1, 2) and whole % 2 == 1):
+        whole += 1
+    r = whole * quantum
+    if r >= Fraction(2) ** (emax + 1):
+        return sign * math.inf
+    return sign * r
+
+
+def _rn_f64(q):
+    return _round_binary(q, 52, -1022, 1023)
+
+
+def _rn_f32(q):
+    return _round_binary(q, 23, -126, 127)
+
+
+def _rn_f16(q):
+    return _round_binary(q, 10, -14, 15)
+
+
+def _all_finite_f16():
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    x = bits.view(np.float16)
+    return x[np.isfinite(x)]
+
+
+def test_dropout_closed_forms():
+    """solution/dropout.py:33-35 with a scale of exactly 2 (p = 0.5) or 4 (p = 0.75): every kept
+    finite fp16 x becomes exactly 2x or 4x (±inf where that leaves fp16's range, sign of zero
+    kept); a dropped element is +0.0 whatever x is, -0.0 and negatives included."""
+    x = _all_finite_f16()
+    assert x.size == 63488
+    ones = np.ones(x.size, np.uint8)
+    for p, factor in ((0.5, 2), (0.75, 4)):
+        got = O.dropout_fp16(x, ones, p)
+        for xi, gi in zip(x.tolist(), got.tolist()):
+            want = Fraction(xi) * factor
+            if abs(want) > 65504:
+                assert gi == math.copysign(math.inf, xi), (p, xi, gi)
+            else:
+                assert Fraction(gi) == want, (p, xi, gi)
+                assert math.copysign(1.0, gi) == math.copysign(1.0, xi)
+        dropped = O.dropout_fp16(x, np.zeros(x.size, np.uint8), p)
+        assert np.all(dropped.view(np.uint16) == 0)
+
+
+def test_dropout_p005_is_two_roundings_of_the_exact_product():
+    """p = 0.05 (the BASELINE configs): the scale is the Python double 1/(1 - p) narrowed to the
+    fp32 kernel argument; each kept x is fp16_RN(fp32_RN(x * scale)), computed here in exact
+    rational arithmetic over all 63,488 finite fp16 values.  A missing fp32 step, a scale of
+    1 - p, or an fp16 scale fails it."""
+    p = 0.05
+    scale = _rn_f32(_rn_f64(1 / _rn_f64(1 - Fraction(p))))
+    assert float(scale) == float(np.float32(1.0 / (1.0 - p)))
+    assert scale != Fraction(20, 19)  # the narrowing is visible: not the exact 1/0.95
+    x = _all_finite_f16()
+    got = O.dropout_fp16(x, np.ones(x.size, np.uint8), p)
+    for xi, gi in zip(x.tolist(), got.tolist()):
+        want = _rn_f16(_rn_f32(Fraction(xi) * scale))
+        if want in (math.inf, -math.inf):
+            assert gi == want, (xi, gi)
+        else:
+            assert Fraction(gi) == want, (xi, gi)
+            if want == 0:
+                assert math.copysign(1.0, gi) == math.copysign(1.0, xi)
+    # a scale rounded to fp16 first (a plausible slip) gives other bits somewhere
+    s16 = _rn_f16(scale)
+    assert any(Fraction(g) != _rn_f16(_rn_f32(Fraction(xi) * s16))
+               for xi, g in zip(x.tolist(), got.tolist()) if abs(xi) < 30000)
+    # mixed mask: dropped elements are +0, kept ones as above
+    rng = np.random.default_rng(5)
+    keep = (rng.uniform(size=x.size) >= p).astype(np.uint8)
+    mixed = O.dropout_fp16(x, keep, p)
+    assert np.all(mixed.view(np.uint16)[keep == 0] == 0)
+    assert np.array_equal(mixed.view(np.uint16)[keep != 0], got.view(np.uint16)[keep != 0])
+
+
+def test_round_binary_pins():
+    """The exact rounding helper against known values: fp16's largest finite, the first value
+    that overflows, ties to even, the smallest subnormals."""
+    assert _rn_f16(Fraction(65504)) == 65504
+    assert _rn_f16(Fraction(65519)) == 65504
+    assert _rn_f16(Fraction(65520)) == math.inf
+    assert _rn_f16(1 + Fraction(1, 2 ** 11)) == 1  # tie, even stays
+    assert _rn_f16(1 + Fraction(3, 2 ** 11)) == 1 + Fraction(2, 2 ** 10)  # tie, rounds up
+    assert _rn_f16(Fraction(1, 2 ** 25)) == 0  # half the smallest subnormal: tie to even 0
+    assert _rn_f16(Fraction(3, 2 ** 26)) == Fraction(1, 2 ** 24)
+    assert _rn_f32(Fraction(1, 3)) == Fraction(float(np.float32(1 / 3)))
+    assert _rn_f64(Fraction(1, 10)) == Fraction(0.1)
+
+
 # --- GEMM / LoRA references ---------------------------------------------------------------
 
 def _lora_case(seed, m=24, k=64, n=40, r=16, p=0.25):

@@ -10,41 +10,7 @@ import types
 import pytest
 import torch
 
-
-class _Recorder:
-    def __init__(self, result="original"):
-        self.calls = []
-        self.result = result
-
-    def __call__(self, *args, **kwargs):
-        self.calls.append((args, kwargs))
-        return self.result
-
-
-@pytest.fixture
-def fake_bnb(monkeypatch):
-    """A bitsandbytes package with the three entry points the reference patches."""
-    bnb = types.ModuleType("bitsandbytes")
-    functional = types.ModuleType("bitsandbytes.functional")
-    backends = types.ModuleType("bitsandbytes.backends")
-    cuda = types.ModuleType("bitsandbytes.backends.cuda")
-    ops = types.ModuleType("bitsandbytes.backends.cuda.ops")
-    nn = types.ModuleType("bitsandbytes.nn")
-    functional.dequantize_4bit = _Recorder("dequantize_4bit")
-    ops._dequant_linear_fallback = _Recorder("fallback")
-
-    class Linear4bit(torch.nn.Module):
-        def forward(self, x):
-            return "bnb forward"
-
-    nn.Linear4bit = Linear4bit
-    bnb.functional, bnb.backends, bnb.nn = functional, backends, nn
-    backends.cuda, cuda.ops = cuda, ops
-    for name, mod in (("bitsandbytes", bnb), ("bitsandbytes.functional", functional),
-                      ("bitsandbytes.backends", backends), ("bitsandbytes.backends.cuda", cuda),
-                      ("bitsandbytes.backends.cuda.ops", ops), ("bitsandbytes.nn", nn)):
-        monkeypatch.setitem(sys.modules, name, mod)
-    return types.SimpleNamespace(bnb=bnb, functional=functional, ops=ops, nn=nn)
+from tests.conftest import _Recorder
 
 
 def _state(nested=True, shape=(64, 64)):
@@ -277,6 +243,21 @@ def test_adapter_resolution_declines_what_peft_composes_differently():
     plain.lora_dropout["default"] = torch.nn.Identity()
     assert peft_lora.adapter_of(plain).p == 0.0
     assert peft_lora.adapter_of(torch.nn.Linear(4, 4)) is None
+
+
+def test_takes_refuses_ranks_the_row_kernels_do_not_hold(monkeypatch):
+    """Ranks past 128 (the LoRA row kernels' eight 16-wide accumulator blocks) or not a multiple
+    of 16 take the layer's own forward instead of raising inside the fused one."""
+    from mindxsoup_amd import kernels, linear4bit, peft_lora
+
+    monkeypatch.setattr(linear4bit, "_direct_ok", lambda *a, **k: True)
+    monkeypatch.setattr(kernels, "fused_shape_ok", lambda *a, **k: True)
+    monkeypatch.setattr(linear4bit, "FUSED_LORA", True)
+    x16 = torch.zeros(4, 64, dtype=torch.float16)
+    for r, want in ((16, True), (128, True), (24, False), (144, False), (256, False)):
+        ad = peft_lora.adapter_of(_PeftLinear4bit(_nf4_base(), r=r, alpha=2 * r))
+        assert ad is not None and ad.rank == r
+        assert peft_lora.takes(ad, x16) is want, r
 
 
 def test_keep_mask_and_dropout_flag():

@@ -64,3 +64,62 @@ def test_timed_layer_step_matches_oracle(cuda):
         print(f"case stack layer {name}: " + " ".join(f"{k_}={v:.1e}" for k_, v in errs.items()),
               flush=True)
         assert max(errs.values()) < 1e-2, (name, errs)
+
+
+def _flat(ys, grads):
+    out = []
+    for y in ys:
+        out.append(y)
+    for grad in grads:
+        out.extend(t for t in grad if t is not None)
+    return out
+
+
+def test_graph_replayed_stack_step_equals_eager(cuda):
+    """The step as bench.py times it: layers sharing one workspace, forward of each then
+    backward in reverse, captured in one HIP graph.  Every replay's outputs (y, the summed and
+    single dX, dA, dB of every projection) equal the eager run's bit for bit, with eager steps
+    that overwrite the shared workspace run between the replays."""
+    import bench
+
+    g = torch.Generator(device=cuda)
+    g.manual_seed(12)
+    layers = []
+    for _ in range(2):
+        x_attn = torch.randn((bench.M_TOKENS, 1536), device=cuda, generator=g).half()
+        x_mlp = torch.randn((bench.M_TOKENS, 1536), device=cuda, generator=g).half()
+        projs = []
+        for name, n, k in bench.PROJ:
+            x = x_attn if name in ("q", "k", "v") else x_mlp if name in ("gate", "up") else None
+            projs.append(bench.make_proj(cuda, g, n, k, x=x))
+        layers.append(projs)
+
+    def step():
+        ys, saved = [], []
+        for projs in layers:
+            y, sv = bench.layer_fwd(projs)
+            ys += y
+            saved.append(sv)
+        grads = []
+        for projs, sv in zip(reversed(layers), reversed(saved)):
+            grads += bench.layer_bwd(projs, sv)
+        return _flat(ys, grads)
+
+    print("case stack graph replay: eager reference", flush=True)
+    eager = [t.clone() for t in step()]
+    torch.cuda.synchronize()
+    assert len(eager) == 2 * (7 + 7 * 2 + 4)  # dX of o, down and the two sums
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        static = step()
+    assert len(static) == len(eager)
+    for rep in range(3):
+        print(f"case stack graph replay {rep}", flush=True)
+        again = step()  # eager work on the same workspace between replays
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(again, eager))
+        graph.replay()
+        torch.cuda.synchronize()
+        bad = [i for i, (a, b) in enumerate(zip(static, eager)) if not torch.equal(a, b)]
+        assert not bad, (rep, bad)
+    del graph

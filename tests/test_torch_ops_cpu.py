@@ -102,3 +102,12 @@ def test_inference_mode_runs_forward_only(mx):
         y = mx.lora_linear(x, a, b, *_nf4(), None, None, 1.0, 2.0)
         assert y.shape == (M, N) and y.grad_fn is None
         assert mx.linear(x, *_nf4(), N, None).shape == (M, N)
+
+
+def test_ops_refuse_another_c_abi_build(monkeypatch):
+    """With MXS_NF4_LIB naming another build of libmxs_nf4.so, the operator library (which links
+    the package's own copy) refuses to load instead of mixing the two builds."""
+    monkeypatch.setenv("MXS_NF4_LIB", "/nonexistent/libmxs_nf4.so")
+    monkeypatch.setattr(ops, "_ops", None)
+    with pytest.raises(RuntimeError, match="MXS_NF4_LIB"):
+        ops.load()

@@ -75,3 +75,33 @@ def test_noalloc_refuses_plans_beyond_the_array(cuda):
     assert bool((y == 7.0).all())
     assert _lib.lib().mxs_nf4_linear_fwd_noalloc(None, -1, k, n, None, None, None, None, None,
                                                  None, None, None, 0, None, -1, 1, None) == -1
+
+
+def test_noalloc_replays_in_a_hip_graph(cuda):
+    """Captured in a HIP graph (after one call outside the capture has looked up the array's
+    address), the split-K down_proj forward replays to the workspace entry's bits, with eager
+    calls that reuse the array between the replays."""
+    n, k, r, M = 1536, 8960, 16, 1024
+    packed, st = _weight(cuda, n, k, 7)
+    x, h, b, bias = _inputs(cuda, M, k, n, r, 8)
+    want = kernels.nf4_linear_fwd(x, packed, st, bias, h, b)
+    y = torch.empty((M, n), dtype=torch.float16, device=cuda)
+    kernels.nf4_linear_fwd_noalloc(x, packed, st, y, bias, h, b)  # the address lookup
+    torch.cuda.synchronize()
+    assert _same(y, want)
+    y.fill_(float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        kernels.nf4_linear_fwd_noalloc(x, packed, st, y, bias, h, b)
+    x2, h2, b2, bias2 = _inputs(cuda, 300, k, n, r, 9)
+    other = torch.empty((300, n), dtype=torch.float16, device=cuda)
+    for rep in range(3):
+        print(f"noalloc graph replay {rep}", flush=True)
+        kernels.nf4_linear_fwd_noalloc(x2, packed, st, other, bias2, h2, b2)  # reuses the array
+        torch.cuda.synchronize()
+        y.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert _same(y, want), rep
+    assert _same(other, kernels.nf4_linear_fwd(x2, packed, st, bias2, h2, b2))
+    del graph
