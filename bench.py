@@ -236,6 +236,7 @@ def proj_flops(n, k, m=M_TOKENS, r=RANK, fwd=True, bwd=True):
 def make_proj(dev, g, n, k, x=None, x_kind="normal", dy_std=1.0):
     """One projection's synthetic inputs: NF4 weight N(0,0.02), LoRA A Kaiming-uniform, B
     N(0,0.01), fp16; X [M,K] ~ N(0,1) (or silu(g)*u), dY ~ N(0, dy_std); keep mask Bernoulli(0.95)."""
+    from mindxsoup_amd import kernels
     from mindxsoup_amd.quant import quantize_4bit
 
     w = (torch.randn((n, k), device=dev, generator=g) * 0.02).half()
@@ -253,8 +254,10 @@ def make_proj(dev, g, n, k, x=None, x_kind="normal", dy_std=1.0):
     la = ((torch.rand((RANK, k), device=dev, generator=g) * 2 - 1) * bound).half()
     lb = (torch.randn((n, RANK), device=dev, generator=g) * 0.01).half()
     dy = (torch.randn((M_TOKENS, n), device=dev, generator=g) * dy_std).half()
-    keep = (torch.rand((M_TOKENS, k), device=dev, generator=g) >= P_DROP).to(torch.uint8)
-    return dict(packed=packed, st=st, x=x, a=la, b=lb, dy=dy, keep=keep, n=n, k=k,
+    keep8 = (torch.rand((M_TOKENS, k), device=dev, generator=g) >= P_DROP).to(torch.uint8)
+    # the kernels' mask format: keep bits, drawn (packed) before any timing like x and dy
+    keep = kernels.keep_bits(keep8, M_TOKENS, k)
+    return dict(packed=packed, st=st, x=x, a=la, b=lb, dy=dy, keep=keep, keep8=keep8, n=n, k=k,
                 ws=shared_workspace(dev))
 
 
@@ -525,7 +528,8 @@ def swiglu_kernel_times(block, x, dy, steps, warmup):
     M = xs.shape[0]
     gate = torch.randn((M, 8960), device=xs.device).half()
     upv = torch.randn((M, 8960), device=xs.device).half()
-    keep = (torch.rand((M, 8960), device=xs.device) >= P_DROP).to(torch.uint8)
+    keep = kernels.keep_bits((torch.rand((M, 8960), device=xs.device) >= P_DROP).to(torch.uint8),
+                             M, 8960)
     hp, _, _ = kernels.lora_h_partials(xs, a_u, s, None, 1.0, lora_b=b_u)
     at_d, bt_d = a_d.t().contiguous(), b_d.t().contiguous()
     dhp = kernels.lora_dh_partials(dy, bt_d, s)
@@ -845,7 +849,7 @@ def cpu_baseline_layer(dev):
             code=st.state2.code.cpu().numpy(), absmax2=st.state2.absmax.cpu().numpy(),
             offset=float(st.offset.item()), shape=st.shape,
             x=p["x"].float().cpu(), a=p["a"].float().cpu(), b=p["b"].float().cpu(),
-            dy=p["dy"].float().cpu(), keep=p["keep"].cpu().bool()))
+            dy=p["dy"].float().cpu(), keep=p["keep8"].cpu().bool()))
     del projs
 
     def layer_pass():
@@ -898,7 +902,8 @@ def bench_kernel(dev, name, tokens, steps, warmup, cfg=-1, splits=1):
     p = make_proj(dev, g, n, k)
     x = torch.randn((tokens, k), device=dev, generator=g).half()
     dy = torch.randn((tokens, n), device=dev, generator=g).half()
-    keep = (torch.rand((tokens, k), device=dev, generator=g) >= P_DROP).to(torch.uint8)
+    keep = kernels.keep_bits((torch.rand((tokens, k), device=dev, generator=g) >= P_DROP)
+                             .to(torch.uint8), tokens, k)
     s, ms_ = ALPHA / RANK, 1.0 / (1.0 - P_DROP)
     nc, kr = (n, k) if direction == "fwd" else (k, n)
     ws = kernels.new_workspace(max(kernels.projection_workspace_bytes(tokens, k, n, RANK),

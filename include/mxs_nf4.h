@@ -14,6 +14,11 @@
  *   absmax2  f32 [ceil(N*K/64/256)]  second-level scale per 256 blocks (state2.absmax)
  *   offset   f32 [1]             mean added back (state.offset), a device pointer
  *   block scale = fma(code[absmax8[b]], absmax2[b >> 8], offset); value = fp16(NF4[q] * scale)
+ *
+ * Dropout keep masks (every `mask` argument) are bits: u32 [M, ceil(K/32)] for a mask over
+ * [M, K], bit k % 32 of word k / 32 of row m set where element (m, k) is kept, bits past K
+ * zero, 4-byte aligned.  mxs_keep_pack makes them from the reference's int8 keep mask
+ * (solution/dropout.py:64, `keep` [M, K], nonzero = kept).
  */
 #ifndef MXS_NF4_H
 #define MXS_NF4_H
@@ -134,8 +139,8 @@ int mxs_nf4_linear_fwd_noalloc(const void* x, int M, int K, int N, const void* p
  * (solution/linear4bit.py:51-57: unpack again, then grad @ W) plus the LoRA branch's input
  * gradient through the dropout (solution/dropout.py:62-69); lora_dh = s * dY . B from
  * mxs_lora_dh, lora_at = lora_A transposed ([K, r]: the `at` output of mxs_lora_h, or
- * mxs_transpose_f16).  mask: u8 keep mask
- * [M,K] or NULL (no dropout); mask_scale = 1/(1-p). */
+ * mxs_transpose_f16).  mask: keep bits of [M,K]
+ * or NULL (no dropout); mask_scale = 1/(1-p). */
 int mxs_nf4_linear_bwd_dx(const void* dy, int M, int N, int K, const void* packed,
                           const void* absmax8, const float* code, const float* absmax2,
                           const float* offset, const void* lora_dh, const void* lora_at, int r,
@@ -225,7 +230,7 @@ int64_t mxs_nf4_linear_bwd_dx_pair_workspace_bytes(int M, int N0, int N1, int K)
 int64_t mxs_lora_workspace_bytes(int M, int K, int N, int r);
 
 /* h = fp16(s * drop(x) . A^T) [M, r] and ht = its transpose: lora_A of peft's branch with the
- * reference's dropout (solution/dropout.py:33-35, mask u8 [M,K] or NULL) and the scaling s
+ * reference's dropout (solution/dropout.py:33-35, mask: keep bits of [M,K] or NULL) and the scaling s
  * folded in.  x [M,K] fp16, lora_a [r,K] fp16, K % 32 == 0.  Side outputs for the backward
  * (each optional, NULL to skip): at [K, r] = lora_a^T (the operand mxs_nf4_linear_bwd_dx takes)
  * and bt [r, N] = lora_b^T for lora_b [N, r] (the operand mxs_lora_dh takes). */
@@ -247,6 +252,12 @@ int mxs_lora_grad_a(const void* dht, int ldt, const void* x, int M, int K, int r
 /* dB[N,r] (fp32) = dY^T . h (h = s * H): lora_B's weight gradient. */
 int mxs_lora_grad_b(const void* ht, int ldt, const void* dy, int M, int N, int r, float* db,
                     void* workspace, hipStream_t stream);
+
+/* Keep bits (the mask format of every entry point) from a byte keep mask: keep [M, K] u8,
+ * nonzero = kept (the reference's int8 `keep` of PackedDropout, solution/dropout.py:47-69, drawn
+ * by F.dropout at :106-119); bits u32 [M, ceil(K/32)].  One launch; reads M*K bytes, writes
+ * M*K/8. */
+int mxs_keep_pack(const void* keep, int M, int K, void* bits, hipStream_t stream);
 
 /* Number of reduction slices (1..4) mxs_lora_h_partials / mxs_lora_dh_partials use for M tokens
  * and a reduction of length Kr: their partials buffer is fp32 [slices][ldt][r]. */
@@ -410,7 +421,7 @@ int mxs_nf4_linear_bwd_dx_grads_sum_ok(int n, int M, const int N[], int K, int r
  * and every projection's dA[i] / dB[i] (as mxs_nf4_linear_bwd_dx_grads), in one launch: each
  * output tile runs the projections' reductions back to back (K-steps of dy[0] . W_0, then
  * dy[1] . W_1, ...) into one fp32 accumulator that started from all their LoRA terms (each
- * masked by its own keep bytes), and is rounded to fp16 once; the gradient workgroups follow
+ * masked by its own keep bits), and is rounded to fp16 once; the gradient workgroups follow
  * the tiles.  The sum of mxs_nf4_linear_bwd_dx_grads_group's dx[i] rounded each and added in
  * fp16 differs from it by the roundings of the parts (a couple of fp16 ulps).  Every projection
  * has a keep mask or none does.  da and db NULL: the summed dX alone (dht, ht and x unused, may

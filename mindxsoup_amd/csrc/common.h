@@ -26,6 +26,12 @@ __device__ __constant__ static const float kNF4[16] = {
 constexpr int kBlock = 64;      // NF4 values per first-level absmax
 constexpr int kGroup = 256;     // first-level blocks per second-level absmax
 
+// Dropout keep masks travel as bits: row m of a mask over K columns is keep_words(K) 32-bit
+// words (keep_row_bytes(K) bytes), bit k % 32 of word k / 32 set where element (m, k) is kept;
+// bits past K are zero.  Byte k / 8 of a row holds columns k & ~7 .. +7, bit k % 8 for column k.
+__host__ __device__ constexpr int keep_words(int K) { return (K + 31) / 32; }
+__host__ __device__ constexpr int64_t keep_row_bytes(int K) { return 4 * (int64_t)keep_words(K); }
+
 // Two fp32 values -> two fp16 (round to nearest even) packed low-first in a dword.
 __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   float2_t v = {lo, hi};

@@ -17,7 +17,7 @@
 // v_mfma_f32_16x16x32_f16 accumulators in LDS in a fixed order (deterministic).  Summing partials
 // across workgroups would need a second launch or agent-scope fences (on the multi-XCD gfx950,
 // write-back and invalidation of whole L2s): both measured slower than these kernels.
-//   rows kernel: lane (row l%16, k-group l/16) loads 16-byte fragments of X (plus 8 mask bytes)
+//   rows kernel: lane (row l%16, k-group l/16) loads 16-byte fragments of X (plus a keep byte)
 //     and of the r x K operand (lora_A, or lora_B transposed), four 32-wide chunks in flight.
 //   cols kernel: each lane loads an 8-token x CPL-column block of the row-major fp16 input and
 //     regroups it in registers into CPL MFMA operands (one per column), so a wave covers 16*CPL
@@ -37,19 +37,18 @@ constexpr int kMaxRB = 8;            // r <= 128 (r / 16 accumulator blocks)
 template <int TB>
 constexpr int rows_chunks_in_flight() { return TB == 1 ? 4 : 3; }
 
-__device__ __forceinline__ half8_t drop8(half8_t x, u32x2 keep, float scale) {
+// 8 consecutive values through the dropout: bit e of `keep` set keeps value e (times scale).
+__device__ __forceinline__ half8_t drop8(half8_t x, uint32_t keep, float scale) {
 #pragma unroll
-  for (int e = 0; e < 8; e++) {
-    const uint32_t k = (keep[e >> 2] >> (8 * (e & 3))) & 0xFFu;
-    x[e] = k ? (_Float16)((float)x[e] * scale) : (_Float16)0.0f;
-  }
+  for (int e = 0; e < 8; e++)
+    x[e] = ((keep >> e) & 1u) ? (_Float16)((float)x[e] * scale) : (_Float16)0.0f;
   return x;
 }
 
 struct RowsArgs {
   const _Float16* P;      // [M, K] row-major
   int M, K;
-  const uint8_t* mask;    // [M, K] keep mask or null
+  const uint8_t* mask;    // keep bits of [M, K] (keep_row_bytes(K) per row) or null
   float mscale;
   const _Float16* R;      // [r, K] row-major
   int r, ldt;
@@ -107,12 +106,13 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
   const int c_beg = slice * cps;
   const int c_end = min(chunks, c_beg + cps);
   bool row_ok[TB];
-  int64_t prow[TB];
+  int64_t prow[TB], krow[TB];  // the lane's first value and its keep byte (chunk 0)
 #pragma unroll
   for (int t = 0; t < TB; t++) {
     const int row = m0 + 16 * t + (lane & 15);
     row_ok[t] = row < a.M;
     prow[t] = (int64_t)(row_ok[t] ? row : 0) * a.K + 8 * g;
+    krow[t] = (int64_t)(row_ok[t] ? row : 0) * keep_row_bytes(a.K) + g;
   }
   float4_t acc[TB][RB];
 #pragma unroll
@@ -129,8 +129,7 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
         half8_t v = {};
         if (c < c_end && row_ok[t]) {
           v = *reinterpret_cast<const half8_t*>(a.P + prow[t] + 32 * c);
-          if (a.mask)
-            v = drop8(v, *reinterpret_cast<const u32x2*>(a.mask + prow[t] + 32 * c), a.mscale);
+          if (a.mask) v = drop8(v, a.mask[krow[t] + 4 * c], a.mscale);
         }
         x[u][t] = v;
       }
@@ -309,6 +308,33 @@ __global__ __launch_bounds__(64 * cols_max_waves<CPL>()) void k_lora_cols_group(
                        (int)blockDim.x >> 6, red);
 }
 
+// Keep bits from a byte keep mask [M, K] (nonzero = kept; the reference's int8 `keep`): one
+// thread per 32-bit word, its 32 source bytes contiguous, consecutive threads' words contiguous.
+__global__ __launch_bounds__(256) void k_keep_pack(const uint8_t* __restrict__ keep, int M, int K,
+                                                  uint32_t* __restrict__ bits) {
+  const int kw = keep_words(K);
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)M * kw) return;
+  const int m = (int)(i / kw), w = (int)(i % kw);
+  const uint8_t* src = keep + (int64_t)m * K + 32 * w;
+  const int n = min(32, K - 32 * w);
+  uint32_t v = 0;
+  if (n == 32 && ((uintptr_t)src % 16) == 0) {
+    const u32x4 lo = *reinterpret_cast<const u32x4*>(src);
+    const u32x4 hi = *reinterpret_cast<const u32x4*>(src + 16);
+#pragma unroll
+    for (int d = 0; d < 4; d++)
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v |= (((lo[d] >> (8 * e)) & 0xffu) ? 1u : 0u) << (4 * d + e);
+        v |= (((hi[d] >> (8 * e)) & 0xffu) ? 1u : 0u) << (16 + 4 * d + e);
+      }
+  } else {
+    for (int e = 0; e < n; e++) v |= (src[e] ? 1u : 0u) << e;
+  }
+  bits[i] = v;
+}
+
 // dst[0, n) = 0 (a kernel, not hipMemsetAsync, so that the call can be captured in a graph).
 __global__ __launch_bounds__(256) void k_zero_f32(float* __restrict__ dst, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -484,6 +510,17 @@ using namespace mxs;
 
 extern "C" {
 
+int mxs_keep_pack(const void* keep, int M, int K, void* bits, hipStream_t stream) {
+  if (M < 0 || K < 0) return MXS_ERR_ARG;
+  if ((int64_t)M * K == 0) return MXS_OK;
+  if (!keep || !bits) return MXS_ERR_ARG;
+  if ((uintptr_t)bits % 4) return MXS_ERR_ALIGN;
+  const int64_t words = (int64_t)M * keep_words(K);
+  hipLaunchKernelGGL(k_keep_pack, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, stream,
+                     static_cast<const uint8_t*>(keep), M, K, static_cast<uint32_t*>(bits));
+  return check_launch();
+}
+
 int64_t mxs_lora_workspace_bytes(int M, int K, int N, int r) {
   const int ldt = (M + 7) / 8 * 8;
   const int sk = rows_slices(K, ldt), sn = rows_slices(N, ldt);
@@ -498,7 +535,7 @@ int mxs_lora_h(const void* x, int M, int K, const void* lora_a, int r, const voi
   if (M == 0) return MXS_OK;
   if (!x || !lora_a || !h || !ht || (bt && !lora_b)) return MXS_ERR_ARG;
   if (r % 16 || r > 16 * kMaxRB || K % 32 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
-  if (((uintptr_t)x % 16) || ((uintptr_t)lora_a % 16) || (mask && ((uintptr_t)mask % 8)))
+  if (((uintptr_t)x % 16) || ((uintptr_t)lora_a % 16) || (mask && ((uintptr_t)mask % 4)))
     return MXS_ERR_ALIGN;
   RowsArgs a{};
   a.P = static_cast<const _Float16*>(x);
@@ -552,7 +589,7 @@ int mxs_lora_h_partials(const void* x, int M, int K, const void* lora_a, int r, 
   if (M == 0) return MXS_OK;
   if (!x || !lora_a || !partials || (bt && !lora_b)) return MXS_ERR_ARG;
   if (r % 16 || r > 16 * kMaxRB || K % 32 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
-  if (((uintptr_t)x % 16) || ((uintptr_t)lora_a % 16) || (mask && ((uintptr_t)mask % 8)))
+  if (((uintptr_t)x % 16) || ((uintptr_t)lora_a % 16) || (mask && ((uintptr_t)mask % 4)))
     return MXS_ERR_ALIGN;
   RowsArgs a{};
   a.P = static_cast<const _Float16*>(x);
@@ -611,7 +648,7 @@ int mxs_lora_h_partials_group(int n, const void* const x[], int M, const int K[]
     if (K[i] < 0 || n_i < 0) return MXS_ERR_ARG;
     if (!x[i] || !lora_a[i] || !partials[i] || (bt_i && !b_i)) return MXS_ERR_ARG;
     if (K[i] % 32) return MXS_ERR_SIZE;
-    if (((uintptr_t)x[i] % 16) || ((uintptr_t)lora_a[i] % 16) || (mk && ((uintptr_t)mk % 8)))
+    if (((uintptr_t)x[i] % 16) || ((uintptr_t)lora_a[i] % 16) || (mk && ((uintptr_t)mk % 4)))
       return MXS_ERR_ALIGN;
     RowsArgs a{};
     a.P = static_cast<const _Float16*>(x[i]);
@@ -655,7 +692,7 @@ int mxs_lora_h_partials_group_w32(int n, const void* const x[], int M, const int
     if (K[i] < 0 || n_i < 0) return MXS_ERR_ARG;
     if (!x[i] || !lora_a[i] || !partials[i] || ((bt_i || b16_i) && !b_i)) return MXS_ERR_ARG;
     if (K[i] % 32) return MXS_ERR_SIZE;
-    if (((uintptr_t)x[i] % 16) || ((uintptr_t)lora_a[i] % 16) || (mk && ((uintptr_t)mk % 8)))
+    if (((uintptr_t)x[i] % 16) || ((uintptr_t)lora_a[i] % 16) || (mk && ((uintptr_t)mk % 4)))
       return MXS_ERR_ALIGN;
     RowsArgs a{};
     a.P = static_cast<const _Float16*>(x[i]);
@@ -768,7 +805,7 @@ int mxs_lora_grads(const void* dht, const void* ht, int ldt, const void* x, cons
   if ((da && (!dht || !x)) || (db && (!ht || !dy))) return MXS_ERR_ARG;
   if ((da && K % 8) || (db && N % 8) || ldt < M || ldt % 8) return MXS_ERR_SIZE;
   if ((da && ((uintptr_t)x % 16 || (uintptr_t)dht % 16)) ||
-      (db && ((uintptr_t)dy % 16 || (uintptr_t)ht % 16)) || (mask && ((uintptr_t)mask % 8)))
+      (db && ((uintptr_t)dy % 16 || (uintptr_t)ht % 16)) || (mask && ((uintptr_t)mask % 4)))
     return MXS_ERR_ALIGN;
   ColsProblem pa{}, pb{};
   pa.PT = static_cast<const _Float16*>(dht);
@@ -817,7 +854,7 @@ int mxs_lora_grads_group(int n, const void* const dht[], const void* const ht[],
     if (K[i] % 8 || N[i] % 8 || ldt < M || ldt % 8 || cols_cpl(K[i] + N[i]) != cpl)
       return MXS_ERR_SIZE;
     if ((uintptr_t)x[i] % 16 || (uintptr_t)dht[i] % 16 || (uintptr_t)dy[i] % 16 ||
-        (uintptr_t)ht[i] % 16 || (mk && ((uintptr_t)mk % 8)))
+        (uintptr_t)ht[i] % 16 || (mk && ((uintptr_t)mk % 4)))
       return MXS_ERR_ALIGN;
     ColsProblem& pa = g.pa[i];  // dA [r, K] = dHs^T . drop(X)
     pa.PT = static_cast<const _Float16*>(dht[i]);

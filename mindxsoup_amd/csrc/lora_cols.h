@@ -32,7 +32,7 @@ inline int cols_waves(int M, int r, int cpl, int max_waves) {
 struct ColsProblem {
   const _Float16* PT;     // [r, ldt] (transposed LoRA activations, zeros past M)
   const _Float16* Q;      // [M, Nq] row-major
-  const uint8_t* mask;    // [M, Nq] keep mask or null
+  const uint8_t* mask;    // keep bits of [M, Nq] (keep_row_bytes(Nq) per row) or null
   float mscale;
   int Nq;
   float* out;             // [r, Nq] (out_rn) or [Nq, r]
@@ -40,9 +40,9 @@ struct ColsProblem {
 };
 
 template <int CPL> struct ColsVec;
-template <> struct ColsVec<2> { typedef uint32_t T; typedef uint16_t MT; };
-template <> struct ColsVec<4> { typedef u32x2 T; typedef uint32_t MT; };
-template <> struct ColsVec<8> { typedef u32x4 T; typedef u32x2 MT; };
+template <> struct ColsVec<2> { typedef uint32_t T; };
+template <> struct ColsVec<4> { typedef u32x2 T; };
+template <> struct ColsVec<8> { typedef u32x4 T; };
 
 // out[j][n] = sum_m PT[j][m] * Q[m][n] over all tokens, for the 16*CPL columns of workgroup
 // `block`: block < cb0 is problem p0 (dA), the rest p1 (dB).  The first nw waves (at most
@@ -54,7 +54,6 @@ __device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const Col
                                                 int cb0, int M, int ldt, int r, int block,
                                                 int nw, float* red) {
   typedef typename ColsVec<CPL>::T VT;
-  typedef typename ColsVec<CPL>::MT MT;
   constexpr int WC = 16 * CPL;  // columns per workgroup
   const bool second = block >= cb0;
   const ColsProblem a = second ? p1 : p0;
@@ -65,6 +64,9 @@ __device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const Col
   const int lg = lane >> 4;  // tokens t0 + 8*lg .. +8
   const int col = nb + CPL * ln;
   const bool col_ok = col < a.Nq;
+  // the lane's CPL keep bits of a row: bits col % 8 .. of byte col / 8 (CPL divides 8)
+  const int64_t kst = keep_row_bytes(a.Nq);
+  const int kbyte = col >> 3, kshift = col & 7;
   const int ld = WC + 1;
   // U token blocks of 32 per batch, all loaded before any is multiplied (one memory round trip
   // per batch instead of one per block)
@@ -76,7 +78,7 @@ __device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const Col
     for (int t0 = wave * 32; t0 < M; t0 += nw * 32 * U) {
       half8_t av[U];
       VT rows[U][8];
-      MT mks[U][8];
+      uint32_t mks[U][8];
 #pragma unroll
       for (int u = 0; u < U; u++) {
         const int mb = t0 + u * nw * 32 + 8 * lg;
@@ -87,10 +89,10 @@ __device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const Col
         for (int e = 0; e < 8; e++) {
           const int m = mb + e;
           rows[u][e] = VT{};
-          mks[u][e] = MT{};
+          mks[u][e] = 0;
           if (m < M && col_ok) {
             rows[u][e] = *reinterpret_cast<const VT*>(a.Q + (int64_t)m * a.Nq + col);
-            if (a.mask) mks[u][e] = *reinterpret_cast<const MT*>(a.mask + (int64_t)m * a.Nq + col);
+            if (a.mask) mks[u][e] = a.mask[(int64_t)m * kst + kbyte];
           }
         }
       }
@@ -102,12 +104,9 @@ __device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const Col
           __builtin_memcpy(hv[e], &rows[u][e], sizeof(VT));
           if (a.mask) {
 #pragma unroll
-            for (int c = 0; c < CPL; c++) {
-              uint32_t kb;
-              if constexpr (CPL == 8) kb = (mks[u][e][c >> 2] >> (8 * (c & 3))) & 0xFFu;
-              else kb = ((uint32_t)mks[u][e] >> (8 * c)) & 0xFFu;
-              hv[e][c] = kb ? (_Float16)((float)hv[e][c] * a.mscale) : (_Float16)0.0f;
-            }
+            for (int c = 0; c < CPL; c++)
+              hv[e][c] = ((mks[u][e] >> (kshift + c)) & 1u) ? (_Float16)((float)hv[e][c] * a.mscale)
+                                                             : (_Float16)0.0f;
           }
         }
 #pragma unroll

@@ -45,7 +45,7 @@ struct GemmArgs {
   const _Float16* lora_h;   // [M, r]: s*H (forward) or s*dH (backward), or null
   const _Float16* lora_w;   // [Nc, r]: forward lora_B; backward lora_A transposed
   int r;
-  const uint8_t* mask;      // backward: dropout keep mask [M, Nc] or null
+  const uint8_t* mask;      // backward: dropout keep bits of [M, Nc] (keep_words(Nc) per row) or null
   float mask_scale;         // 1 / (1 - p)
   // LoRA activations given as fp32 partial sums instead of lora_h: [hp_slices][ldt][r], already
   // times s; the GEMM adds them in slice order and rounds to fp16 (the same value lora_h holds)
@@ -136,7 +136,8 @@ struct Tile {
 // that it shares the first round trip to memory with the first tiles' loads.  finish() builds
 // the accumulators.  The LoRA operands and the keep mask come either from LDS areas that the
 // warp-specialized kernel's producers staged (`ls`: [rows][16] fp16 operand of the workgroup's
-// rows then [cols][16] of lora_w, r = 16; `kls`: the workgroup's keep bytes, row stride `kst`)
+// rows then [cols][16] of lora_w, r = 16; `kls`: the workgroup's keep bits, row stride `kst`
+// bytes, a 32-bit word per 32 columns)
 // or straight from memory.
 template <int TM, int TN, bool BWD, bool ROPE = false>
 struct AccStart {
@@ -223,18 +224,21 @@ struct AccStart {
     return hf;
   }
 
-  // 4 keep bytes of row m, columns n..n+3, from memory
+  // the 32 keep bits of row m, columns n..n+31 (n a multiple of 32), from memory
   __device__ static __forceinline__ uint32_t keep_mem(const GemmArgs& a, int m, int n) {
-    uint32_t k = 0;
-    if (m >= a.M) return k;
-    if ((a.Nc % 4) == 0 && (a.ldc % 4) == 0 && n + 3 < a.Nc) {
-      k = *reinterpret_cast<const uint32_t*>(a.mask + (int64_t)m * a.Nc + n);
-    } else {
+    if (m >= a.M || n >= a.Nc) return 0u;
+    return reinterpret_cast<const uint32_t*>(a.mask)[(int64_t)m * keep_words(a.Nc) + (n >> 5)];
+  }
+
+  // acc (tile i, j) times the dropout: keep bits `kb` of the tile's 32 columns (bit c for column
+  // c of the tile; the lane's columns are 8g + 4 lseg + e) scaled by mask_scale, else 0
+  __device__ static __forceinline__ void drop_tile(const GemmArgs& a, float16_t& t, uint32_t kb,
+                                                   int lseg) {
+#pragma unroll
+    for (int g = 0; g < 4; g++)
 #pragma unroll
       for (int e = 0; e < 4; e++)
-        if (n + e < a.Nc) k |= (uint32_t)a.mask[(int64_t)m * a.Nc + n + e] << (8 * e);
-    }
-    return k;
+        t[4 * g + e] = ((kb >> (8 * g + 4 * lseg + e)) & 1u) ? t[4 * g + e] * a.mask_scale : 0.0f;
   }
 
   // Each tile's accumulator is born from its first LoRA MFMA (or its base value).  The first
@@ -284,18 +288,13 @@ struct AccStart {
       if constexpr (BWD) {
         if (a.mask) {
 #pragma unroll
-          for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-              const int c = j * 32 + 8 * g + 4 * lseg;
-              const uint32_t keep =
-                  kls ? *reinterpret_cast<const uint32_t*>(kls + (wr0 + i * 32 + lrow) * kst + wc0 + c)
-                      : keep_mem(a, m, nb + c);
-#pragma unroll
-              for (int e = 0; e < 4; e++)
-                acc[i][j][4 * g + e] =
-                    ((keep >> (8 * e)) & 0xffu) ? acc[i][j][4 * g + e] * a.mask_scale : 0.0f;
-            }
+          for (int j = 0; j < TN; j++) {
+            const uint32_t kb =
+                kls ? *reinterpret_cast<const uint32_t*>(kls + (wr0 + i * 32 + lrow) * kst +
+                                                         (wc0 + j * 32) / 8)
+                    : keep_mem(a, m, nb + j * 32);
+            drop_tile(a, acc[i][j], kb, lseg);
+          }
         }
       }
     }
@@ -303,7 +302,7 @@ struct AccStart {
 
   // finish() for operands staged in LDS (first split, r = 16): straight-line LDS reads and one
   // MFMA per tile; `ls`: [rows][16] operand then (at row ls_cols) [cols][16] of lora_w; `kls`
-  // (backward, may be null): keep bytes, row stride kst.
+  // (backward, may be null): keep bits, row stride kst bytes.
   __device__ __forceinline__ void finish_staged(const GemmArgs& a, float16_t (&acc)[TM][TN],
                                                 int mb, int nb, int lrow, int lseg, int wr0,
                                                 int wc0, const _Float16* ls, int ls_cols,
@@ -331,51 +330,36 @@ struct AccStart {
         if (kls) {
 #pragma unroll
           for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-              const uint32_t keep = *reinterpret_cast<const uint32_t*>(
-                  kls + (wr0 + i * 32 + lrow) * kst + wc0 + j * 32 + 8 * g + 4 * lseg);
-#pragma unroll
-              for (int e = 0; e < 4; e++)
-                acc[i][j][4 * g + e] =
-                    ((keep >> (8 * e)) & 0xffu) ? acc[i][j][4 * g + e] * a.mask_scale : 0.0f;
-            }
+            drop_tile(a, acc[i][j],
+                      *reinterpret_cast<const uint32_t*>(kls + (wr0 + i * 32 + lrow) * kst +
+                                                         (wc0 + j * 32) / 8),
+                      lseg);
         }
       }
     }
   }
 };
 
-// The backward pass's dropout keep bytes of the warp-specialized kernel's BM x BN tile, staged
-// by its producers in LDS (row stride BN + 4 bytes: an odd number of dwords, so the consumers'
-// 4-byte reads of one column over 32 rows hit distinct banks).  Rows are loaded 16 contiguous
-// bytes per lane, instead of 4 bytes from each of 32 rows per instruction.
+// The backward pass's dropout keep bits of the warp-specialized kernel's BM x BN tile, staged by
+// its producers in LDS: BN / 32 words per row at a row stride of an odd number of words, so the
+// consumers' word reads of one 32-column block over 32 rows hit distinct banks.  Producer thread
+// p loads words p, p + NTP, ... of the tile (row-major).
 template <int BM, int BN, int NTP>
 struct MaskStage {
-  static constexpr int KST = BN + 4;
-  static constexpr int CH = BN / 16;                // 16-byte chunks per row
-  static constexpr int N = (BM * CH + NTP - 1) / NTP;  // chunks per producer thread
-  u32x4 v[N];
+  static_assert(BN % 32 == 0, "whole keep words per tile row");
+  static constexpr int KW = BN / 32;                   // keep words per tile row
+  static constexpr int KST = 4 * (KW | 1);             // LDS row stride, bytes
+  static constexpr int N = (BM * KW + NTP - 1) / NTP;  // words per producer thread
+  uint32_t v[N];
 
   __device__ __forceinline__ void issue(const GemmArgs& a, int p, int m0, int n0) {
-    const bool vec = (a.Nc % 16) == 0 && ((uintptr_t)a.mask % 16) == 0;
+    const uint32_t* src = reinterpret_cast<const uint32_t*>(a.mask);
+    const int kw = keep_words(a.Nc);
 #pragma unroll
     for (int u = 0; u < N; u++) {
       const int c = p + NTP * u;
-      const int row = c / CH, cc = c % CH;
-      const int m = m0 + row, n = n0 + 16 * cc;
-      u32x4 x = {};
-      if (c < BM * CH && m < a.M) {
-        const uint8_t* src = a.mask + (int64_t)m * a.Nc + n;
-        if (vec && n + 15 < a.Nc) {
-          x = *reinterpret_cast<const u32x4*>(src);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 16; e++)
-            if (n + e < a.Nc) x[e >> 2] |= (uint32_t)src[e] << (8 * (e & 3));
-        }
-      }
-      v[u] = x;
+      const int m = m0 + c / KW, n = n0 + 32 * (c % KW);
+      v[u] = c < BM * KW && m < a.M && n < a.Nc ? src[(int64_t)m * kw + (n >> 5)] : 0u;
     }
   }
 
@@ -383,10 +367,8 @@ struct MaskStage {
 #pragma unroll
     for (int u = 0; u < N; u++) {
       const int c = p + NTP * u;
-      if (c >= BM * CH) break;
-      uint32_t* dst = reinterpret_cast<uint32_t*>(kls + (c / CH) * KST + 16 * (c % CH));
-#pragma unroll
-      for (int d = 0; d < 4; d++) dst[d] = v[u][d];
+      if (c >= BM * KW) break;
+      *reinterpret_cast<uint32_t*>(kls + (c / KW) * KST + 4 * (c % KW)) = v[u];
     }
   }
 };
@@ -1941,7 +1923,7 @@ __device__ __forceinline__ void ws_tile_impl(const GemmArgs* as, const SumPlan* 
     else
       start.finish(a, acc, m0 + wm0, n0 + wn0, lrow, lseg, wm0, wn0, nullptr, 0,
                    kmask ? Ks : nullptr, MaskStage<BM, BN, NTP>::KST);
-    // the other summed problems' LoRA terms, each masked by its own keep bytes, added in order
+    // the other summed problems' LoRA terms, each masked by its own keep bits, added in order
 #pragma unroll
     for (int q = 1; q < NSUM; q++) {
       if (q >= nsum) break;
@@ -2291,7 +2273,8 @@ static int check_gemm(bool bwd, const GemmArgs& a) {
   }
   if (a.Kr % kBK != 0 || a.Kw % kBK != 0) return MXS_ERR_SIZE;
   if (bwd && a.Nc % 8 != 0) return MXS_ERR_SIZE;
-  if (a.lda % 8 != 0 || ((uintptr_t)a.A % 16) != 0 || ((uintptr_t)a.packed % 16) != 0)
+  if (a.lda % 8 != 0 || ((uintptr_t)a.A % 16) != 0 || ((uintptr_t)a.packed % 16) != 0 ||
+      ((uintptr_t)a.mask % 4) != 0)
     return MXS_ERR_ALIGN;
   if (a.lora_h && (!a.lora_w || a.r <= 0 || a.r % 16 != 0)) return MXS_ERR_SIZE;
   if (a.lora_h && (((uintptr_t)a.lora_h % 16) != 0 || ((uintptr_t)a.lora_w % 16) != 0))
@@ -2446,10 +2429,11 @@ __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws_sum(GemmSum g) {
 }
 
 // LDS halfs of the summed kernel: the single-problem layout, then problems 1 and 2's staged LoRA
-// operands ([BM][16] + [BN][16]) and keep bytes (BM rows of BN + 4)
+// operands ([BM][16] + [BN][16]) and keep bits (BM rows of MaskStage's row stride)
 template <int BM, int BN>
 constexpr int ws_sum_lds_halfs() {
-  return ws_lds_halfs<BM, BN, true>() + (kMaxSum - 1) * ((BM + BN) * 16 + BM * (BN + 4) / 2);
+  return ws_lds_halfs<BM, BN, true>() +
+         (kMaxSum - 1) * ((BM + BN) * 16 + BM * MaskStage<BM, BN, 1>::KST / 2);
 }
 
 template <int BN>
@@ -2572,7 +2556,7 @@ static int dx_grads_args(const void* dy, int M, int N, int K, const void* packed
                          GemmArgs& a) {
   if (r % 16 || K % 8 || N % 8 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
   if (((uintptr_t)x % 16) || ((uintptr_t)dht % 16) || ((uintptr_t)dy % 16) ||
-      ((uintptr_t)ht % 16) || (mask && ((uintptr_t)mask % 8)))
+      ((uintptr_t)ht % 16) || (mask && ((uintptr_t)mask % 4)))
     return MXS_ERR_ALIGN;
   a = GemmArgs{};
   a.A = static_cast<const _Float16*>(dy);

@@ -108,14 +108,34 @@ Tensor lora16(const Tensor& t, int64_t rows, int64_t cols, const at::Device& dev
   return aligned(t.to(at::kHalf));
 }
 
+// The dropout keep mask as the kernels take it: keep bits, int32 [M, ceil(K/32)] (bit k % 32 of
+// word k / 32 of row m set where (m, k) is kept).  A byte mask [M, K] (uint8, int8 or bool,
+// nonzero = kept: the reference's int8 `keep`) is packed by one launch; bits pass through.
 Tensor keep_mask(const OptTensor& keep, int64_t M, int64_t K, const at::Device& dev) {
   if (!keep.has_value() || !keep->defined()) return Tensor();
   const Tensor& k = *keep;
-  TORCH_CHECK(k.scalar_type() == at::kByte && k.dim() == 2 && k.size(0) == M && k.size(1) == K,
-              "keep must be a uint8 [", M, ", ", K, "] dropout mask, got ", k.scalar_type(), " ",
-              k.sizes());
   TORCH_CHECK(k.device() == dev, "keep must be on ", dev);
-  return k.contiguous();
+  const int64_t kw = (K + 31) / 32;
+  if (k.scalar_type() == at::kInt && k.dim() == 2 && k.size(0) == M && k.size(1) == kw)
+    return k.contiguous();
+  const auto t = k.scalar_type();
+  TORCH_CHECK((t == at::kByte || t == at::kChar || t == at::kBool) && k.dim() == 2 &&
+                  k.size(0) == M && k.size(1) == K,
+              "keep must be a uint8 [", M, ", ", K, "] dropout mask or int32 [", M, ", ", kw,
+              "] keep bits, got ", t, " ", k.sizes());
+  const Tensor src = k.contiguous();
+  Tensor bits = at::empty({M, kw}, src.options().dtype(at::kInt));
+  if (src.is_meta()) return bits;  // fake tensors: the shape only
+  ok(mxs_keep_pack(src.data_ptr(), as_int(M, "M"), as_int(K, "K"), bits.data_ptr(),
+                   stream_of(src)),
+     "mxs_keep_pack");
+  return bits;
+}
+
+// keep_mask over the rows of x (a node packs once in its forward and saves the bits).
+OptTensor keep_bits_for(const OptTensor& keep, const Tensor& x2) {
+  const Tensor b = keep_mask(keep, x2.size(0), x2.size(1), x2.device());
+  return b.defined() ? OptTensor(b) : std::nullopt;
 }
 
 Tensor bias16(const OptTensor& bias, int64_t N, const at::Device& dev) {
@@ -1055,7 +1075,8 @@ using LoraBwdSig = std::tuple<Tensor, Tensor, Tensor>(
 
 // One NF4 + LoRA projection, y = base(x) + s * B(A(drop(x))) (NF4LoraFunction of the Python
 // package).  x fp16 [..., K]; lora_a [r, K], lora_b [N, r] in any float dtype (their gradients
-// come back in it); keep u8 [M, K] (M = rows of x) or None; mask_scale = 1/(1-p).
+// come back in it); keep u8 [M, K] (M = rows of x), keep bits int32 [M, ceil(K/32)] or None;
+// mask_scale = 1/(1-p).
 struct NF4LoraFunction : public torch::autograd::Function<NF4LoraFunction> {
   static Tensor forward(AutogradContext* ctx, const Tensor& x, const Tensor& lora_a,
                         const Tensor& lora_b, const Tensor& packed, const Tensor& absmax8,
@@ -1065,10 +1086,11 @@ struct NF4LoraFunction : public torch::autograd::Function<NF4LoraFunction> {
     static auto fwd = op<LoraFwdSig>("mxs_nf4::lora_fwd");
     at::AutoDispatchBelowADInplaceOrView below;
     const Tensor x2 = rows2d(x).contiguous();
+    const OptTensor kb = keep_bits_for(keep, x2);
     auto [y, ht, at_, bt] =
-        fwd.call(x2, lora_a, lora_b, packed, absmax8, code, absmax2, offset, bias, keep,
+        fwd.call(x2, lora_a, lora_b, packed, absmax8, code, absmax2, offset, bias, kb,
                  mask_scale, s);
-    ctx->save_for_backward({x2, keep.value_or(Tensor()), ht, at_, bt, packed, absmax8, code,
+    ctx->save_for_backward({x2, kb.value_or(Tensor()), ht, at_, bt, packed, absmax8, code,
                             absmax2, offset});
     ctx->saved_data["mask_scale"] = mask_scale;
     ctx->saved_data["s"] = s;
@@ -1135,15 +1157,17 @@ struct NF4LoraSiblingsFunction : public torch::autograd::Function<NF4LoraSibling
     static auto fwd = op<GroupFwdSig>("mxs_nf4::lora_fwd_group");
     at::AutoDispatchBelowADInplaceOrView below;
     const size_t n = lora_a.size();
+    OptTensorList kbs;
+    for (size_t i = 0; i < keep.size(); ++i) kbs.push_back(keep_bits_for(entry(keep, i), x));
     auto [ys, hts, ats, bts] = fwd.call(x, lora_a, lora_b, packed, absmax8, code, absmax2,
-                                        offset, bias, keep, mask_scale, s, one_gemm, cos, sin,
+                                        offset, bias, kbs, mask_scale, s, one_gemm, cos, sin,
                                         n_rope);
     variable_list saved{x};
     for (const TensorList& l : {TensorList(hts), TensorList(ats), TensorList(bts), packed,
                                 absmax8, code, absmax2, offset})
       saved.insert(saved.end(), l.begin(), l.end());
     for (size_t i = 0; i < n; ++i) {
-      const OptTensor k = entry(keep, i);
+      const OptTensor k = entry(kbs, i);
       saved.push_back(k.has_value() ? *k : Tensor());
     }
     ctx->save_for_backward(saved);

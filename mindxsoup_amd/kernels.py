@@ -36,6 +36,30 @@ def _c(t):
     return None if t is None else t.contiguous()
 
 
+def keep_words(K):
+    """32-bit words per row of a keep-bits mask over K columns."""
+    return (K + 31) // 32
+
+
+def keep_bits(mask, M, K):
+    """The dropout keep mask as every kernel takes it: bits, int32 [M, ceil(K/32)], bit k % 32 of
+    word k / 32 of row m set where element (m, k) is kept.  A byte mask [M, K] (uint8, int8 or
+    bool; nonzero = kept, the reference's int8 `keep`, solution/dropout.py:64) is packed by one
+    launch (mxs_keep_pack); a mask already in bits passes through; None stays None."""
+    if mask is None:
+        return None
+    kw = keep_words(K)
+    if mask.dtype == torch.int32 and tuple(mask.shape) == (M, kw):
+        return mask.contiguous()
+    if mask.dtype in (torch.uint8, torch.int8, torch.bool) and tuple(mask.shape) == (M, K):
+        src = mask.contiguous().view(torch.uint8)
+        bits = torch.empty((M, kw), dtype=torch.int32, device=mask.device)
+        _lib.call("mxs_keep_pack", _lib.ptr(src), M, K, _lib.ptr(bits), _lib.stream_of(mask.device))
+        return bits
+    raise ValueError(f"mask must be a uint8 [{M}, {K}] keep mask or int32 [{M}, {kw}] keep bits, "
+                     f"got {mask.dtype} {tuple(mask.shape)}")
+
+
 def check_nf4_operands(packed, state, device=None):
     """Raise ValueError unless the NF4 operands the kernels read through raw pointers hold what
     state.shape [N, K] says: packed contiguous uint8 with N*K/2 bytes, absmax contiguous uint8
@@ -171,10 +195,7 @@ def nf4_linear_bwd_dx(dy2d, packed, state, lora_dh=None, lora_a=None, mask=None,
         if lora_at.shape != (k, r) or lora_dh.shape[0] != M:
             raise ValueError("lora_dh [M, r] needs lora_at [K, r]")
         lora_dh, lora_at = lora_dh.contiguous(), lora_at.contiguous()
-    if mask is not None:
-        if mask.dtype != torch.uint8 or mask.shape != (M, k):
-            raise ValueError("mask must be uint8 [M, K]")
-        mask = mask.contiguous()
+    mask = keep_bits(mask, M, k)
     ws = _ws(M, k, n, dy2d.device, cfg, splits, ws)
     _lib.call("mxs_nf4_linear_bwd_dx", _lib.ptr(dy2d), M, n, k, *_nf4_args(packed, state),
               _lib.ptr(lora_dh), _lib.ptr(lora_at), r, _lib.ptr(mask), float(mask_scale),
@@ -204,10 +225,7 @@ def nf4_linear_bwd_dx_grads(dy2d, packed, state, lora_dh, lora_at, dht, ht, x2d,
         raise ValueError("x [M, K], lora_dh [M, r] and lora_at [K, r] disagree")
     if dht.shape[0] != r or ht.shape != dht.shape or dht.shape[1] < M:
         raise ValueError("dht and ht must be [r, ldt] with ldt >= M")
-    if mask is not None:
-        if mask.dtype != torch.uint8 or mask.shape != (M, k):
-            raise ValueError("mask must be uint8 [M, K]")
-        mask = mask.contiguous()
+    mask = keep_bits(mask, M, k)
     dev = dy2d.device
     dx = torch.empty((M, k), dtype=torch.float16, device=dev)
     da = torch.empty((r, k), dtype=torch.float32, device=dev)
@@ -249,7 +267,7 @@ def nf4_linear_bwd_dx_grads_group(dys, packeds, states, dhs, ats, dhts, hts, x2d
     dx = [torch.empty((M, K), dtype=torch.float16, device=dev) for _ in dys]
     da = [torch.empty((r, K), dtype=torch.float32, device=dev) for _ in dys]
     db = [torch.empty((nn_, r), dtype=torch.float32, device=dev) for nn_ in Ns]
-    masks = [_c(m) for m in masks]
+    masks = [keep_bits(m, M, K) for m in masks]
     _lib.call("mxs_nf4_linear_bwd_dx_grads_group", n, _ptr_array(dys), M, _int_array(Ns), K,
               _ptr_array(packeds), _ptr_array([st.absmax for st in states]),
               _ptr_array([st.state2.code for st in states]),
@@ -295,7 +313,7 @@ def nf4_linear_bwd_dx_grads_sum(dys, packeds, states, dhs, ats, dhts, hts, x2d, 
     dx = torch.empty((M, K), dtype=torch.float16, device=dev)
     da = [torch.empty((r, K), dtype=torch.float32, device=dev) for _ in dys] if grads else None
     db = [torch.empty((nn_, r), dtype=torch.float32, device=dev) for nn_ in Ns] if grads else None
-    masks = [_c(m) for m in masks]
+    masks = [keep_bits(m, M, K) for m in masks]
     _lib.call("mxs_nf4_linear_bwd_dx_grads_sum", n, _ptr_array(dys), M, _int_array(Ns), K,
               _ptr_array(packeds), _ptr_array([st.absmax for st in states]),
               _ptr_array([st.state2.code for st in states]),
@@ -330,7 +348,8 @@ def lora_h_partials(x2d, lora_a, s, mask=None, mask_scale=1.0, lora_b=None):
         if lora_b.shape != (N, r):
             raise ValueError("lora_b must be [N, r]")
         bt = torch.empty((r, N), dtype=torch.float16, device=dev)
-    _lib.call("mxs_lora_h_partials", _lib.ptr(x2d), M, K, _lib.ptr(lora_a), r, _lib.ptr(_c(mask)),
+    _lib.call("mxs_lora_h_partials", _lib.ptr(x2d), M, K, _lib.ptr(lora_a), r,
+              _lib.ptr(keep_bits(mask, M, K)),
               float(mask_scale), float(s), hp.shape[1], _lib.ptr(at), _lib.ptr(lora_b), N,
               _lib.ptr(bt), _lib.ptr(hp), _lib.stream_of(dev))
     return hp, at, bt
@@ -392,7 +411,7 @@ def lora_h_partials_group(xs, lora_as, s, masks=None, mask_scale=1.0, lora_bs=No
         outs.append((hp, at, bt))
         bts.append(bt)
         b16.append(b)
-    masks = [_c(m) for m in masks]
+    masks = [keep_bits(m, M, x.shape[1]) for m, x in zip(masks, xs)]
     _lib.call("mxs_lora_h_partials_group", n, _ptr_array(xs), M,
               _int_array([x.shape[1] for x in xs]), _ptr_array(a16), r, _ptr_array(masks),
               float(mask_scale), float(s), _ldt(M), _ptr_array([o[1] for o in outs]),
@@ -551,10 +570,7 @@ def nf4_linear_bwd_dx_hp(dy2d, packed, state, lora_dhp, lora_at, mask=None, mask
     S, ldt, r = lora_dhp.shape
     if ldt != _ldt(M) or lora_at.shape != (k, r) or lora_dhp.dtype != torch.float32:
         raise ValueError("lora_dhp [slices, ldt, r] fp32 needs lora_at [K, r]")
-    if mask is not None:
-        if mask.dtype != torch.uint8 or mask.shape != (M, k):
-            raise ValueError("mask must be uint8 [M, K]")
-        mask = mask.contiguous()
+    mask = keep_bits(mask, M, k)
     dx = torch.empty((M, k), dtype=torch.float16, device=dy2d.device)
     dht = torch.empty((r, ldt), dtype=torch.float16, device=dy2d.device) if want_t else None
     ws = _ws(M, k, n, dy2d.device, cfg, splits, ws)
@@ -591,8 +607,7 @@ def nf4_linear_bwd_dx_hp_pair(dys, packeds, states, lora_dhps, lora_ats, masks=N
         if hp.shape != (S, ldt, r) or hp.dtype != torch.float32 or ldt != _ldt(M) or \
                 at.shape != (k, r):
             raise ValueError("lora_dhp [slices, ldt, r] fp32 (one shape) and lora_at [K, r]")
-        if mk is not None and (mk.dtype != torch.uint8 or mk.shape != (M, k)):
-            raise ValueError("mask must be uint8 [M, K]")
+    masks = [keep_bits(mk, M, k) for mk in masks]
     dev = dys[0].device
     for pk, st in zip(packeds, states):
         check_nf4_operands(pk, st, dev)
@@ -608,7 +623,7 @@ def nf4_linear_bwd_dx_hp_pair(dys, packeds, states, lora_dhps, lora_ats, masks=N
               _ptr_array([st.offset for st in states]),
               _ptr_array([h.contiguous() for h in lora_dhps]), S, ldt,
               _ptr_array([a.contiguous() for a in lora_ats]), r,
-              _ptr_array([_c(m) for m in masks]), float(mask_scale), _ptr_array(dhts),
+              _ptr_array(masks), float(mask_scale), _ptr_array(dhts),
               _lib.ptr(dx), _lib.ptr(ws), _lib.stream_of(dev))
     return dx, dhts
 
@@ -681,10 +696,7 @@ def nf4_linear_bwd_dx_glu_(dy2d, packed, state, gate, up, lora_dhp=None, lora_at
                 or lora_dhp.dtype != torch.float32:
             raise ValueError("lora_dhp [slices, ldt, r] fp32 needs lora_at [K, r]")
         lora_dhp, lora_at = lora_dhp.contiguous(), lora_at.contiguous()
-        if mask is not None:
-            if mask.dtype != torch.uint8 or mask.shape != (M, k):
-                raise ValueError("mask must be uint8 [M, K]")
-            mask = mask.contiguous()
+        mask = keep_bits(mask, M, k)
         if want_t:
             dht = torch.empty((r, ldt), dtype=torch.float16, device=dev)
     ws = _ws(M, k, n, dev, -1, 1, ws)
@@ -746,7 +758,8 @@ def lora_h(x2d, lora_a, s, mask=None, mask_scale=1.0, ws=None, n_out=None, want_
             if lora_b.shape != (N, r):
                 raise ValueError("lora_b must be [N, r]")
             bt = torch.empty((r, N), dtype=torch.float16, device=dev)
-    _lib.call("mxs_lora_h", _lib.ptr(x2d), M, K, _lib.ptr(lora_a), r, _lib.ptr(_c(mask)),
+    _lib.call("mxs_lora_h", _lib.ptr(x2d), M, K, _lib.ptr(lora_a), r,
+              _lib.ptr(keep_bits(mask, M, K)),
               float(mask_scale), float(s), _lib.ptr(h), _lib.ptr(ht), ht.shape[1], _lib.ptr(at),
               _lib.ptr(lora_b if bt is not None else None), N, _lib.ptr(bt), _lib.ptr(ws),
               _lib.stream_of(dev))
@@ -789,7 +802,8 @@ def lora_grads(dht, ht, x2d, dy2d, mask=None, mask_scale=1.0, want_a=True, want_
     if da is None and db is None:
         return None, None
     _lib.call("mxs_lora_grads", _lib.ptr(dht), _lib.ptr(ht), dht.shape[1], _lib.ptr(x2d),
-              _lib.ptr(dy2d), M, K, N, r, _lib.ptr(_c(mask)), float(mask_scale), _lib.ptr(da),
+              _lib.ptr(dy2d), M, K, N, r, _lib.ptr(keep_bits(mask, M, K)), float(mask_scale),
+              _lib.ptr(da),
               _lib.ptr(db), _lib.ptr(ws), _lib.stream_of(x2d.device))
     return da, db
 
@@ -812,7 +826,8 @@ def lora_grads_group(dhts, hts, x2ds, dy2ds, masks=None, mask_scale=1.0):
     _lib.call("mxs_lora_grads_group", n, _ptr_array([_c(t) for t in dhts]),
               _ptr_array([_c(t) for t in hts]), ldt, _ptr_array(x2ds), _ptr_array(dy2ds), M,
               _int_array([x.shape[1] for x in x2ds]), _int_array([d.shape[1] for d in dy2ds]), r,
-              _ptr_array([_c(m) for m in masks]), float(mask_scale), _ptr_array(da),
+              _ptr_array([keep_bits(m, M, x.shape[1]) for m, x in zip(masks, x2ds)]),
+              float(mask_scale), _ptr_array(da),
               _ptr_array(db), _lib.stream_of(dev))
     return list(zip(da, db))
 
@@ -824,7 +839,7 @@ def lora_grad_a(dht, x2d, mask=None, mask_scale=1.0, ws=None):
     r = dht.shape[0]
     da = torch.empty((r, K), dtype=torch.float32, device=x2d.device)
     _lib.call("mxs_lora_grad_a", _lib.ptr(dht), dht.shape[1], _lib.ptr(x2d), M, K, r,
-              _lib.ptr(_c(mask)), float(mask_scale), _lib.ptr(da), _lib.ptr(ws),
+              _lib.ptr(keep_bits(mask, M, K)), float(mask_scale), _lib.ptr(da), _lib.ptr(ws),
               _lib.stream_of(x2d.device))
     return da
 

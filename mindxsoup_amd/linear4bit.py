@@ -362,13 +362,15 @@ class NF4LoraFunction(torch.autograd.Function):
     backward: dHs = s * dY B as slice partials (mxs_lora_dh_partials), then one fused GEMM
               that finishes dHs and computes dX = dY W + keep/(1-p) * dHs A (and writes dHs^T);
               dA = dHs^T drop(x) and dB = dY^T Hs in one launch.
-    `keep` is the u8 dropout mask [M, K] (None without dropout); mask_scale = 1/(1-p)."""
+    `keep` is the dropout keep mask: u8 [M, K] or keep bits (kernels.keep_bits; packed once in
+    the forward and saved so), None without dropout; mask_scale = 1/(1-p)."""
 
     @staticmethod
     def forward(ctx, x2d, lora_a, lora_b, packed, state, bias, keep, mask_scale, s):
         a16 = lora_a.to(torch.float16).contiguous()
         b16 = lora_b.to(torch.float16).contiguous()
         n, k = state.shape
+        keep = kernels.keep_bits(keep, x2d.shape[0], k)  # packed once, kept for the backward
         hp, at, bt = kernels.lora_h_partials(x2d, a16, s, keep, mask_scale, lora_b=b16)
         y, ht = kernels.nf4_linear_fwd_hp(x2d, packed, state, hp, b16, bias)
         ctx.save_for_backward(x2d, keep, ht, at, bt)
@@ -435,8 +437,8 @@ class NF4LoraSiblingsFunction(torch.autograd.Function):
         a16 = [t.to(torch.float16).contiguous() for t in ab[0::2]]
         b16 = [t.to(torch.float16).contiguous() for t in ab[1::2]]
         s, mask_scale = projs[0].s, projs[0].mask_scale
-        rows = kernels.lora_h_partials_group([x2d] * n, a16, s, [p.keep for p in projs],
-                                             mask_scale, b16)
+        keeps = [kernels.keep_bits(p.keep, x2d.shape[0], x2d.shape[1]) for p in projs]
+        rows = kernels.lora_h_partials_group([x2d] * n, a16, s, keeps, mask_scale, b16)
         if rope is not None and not one_gemm:
             raise ValueError("the RoPE rides on the grouped GEMM (one_gemm)")
         if one_gemm:
@@ -447,7 +449,7 @@ class NF4LoraSiblingsFunction(torch.autograd.Function):
         else:
             outs = [kernels.nf4_linear_fwd_hp(x2d, p.packed, p.state, r[0], b, p.bias)
                     for p, r, b in zip(projs, rows, b16)]
-        ctx.save_for_backward(x2d, *[p.keep for p in projs], *[o[1] for o in outs],
+        ctx.save_for_backward(x2d, *keeps, *[o[1] for o in outs],
                               *[r[1] for r in rows], *[r[2] for r in rows])
         ctx.projs = projs
         ctx.dtypes = [t.dtype for t in ab]

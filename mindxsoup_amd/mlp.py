@@ -158,7 +158,8 @@ def fused_forward(mlp, x16):
         keep, mask_scale = None, 1.0
         if ad.dropping():
             # gate and up read x; down reads hidden, [M, inter]
-            keep = ad.keep_mask(x2d, (x2d.shape[0], base.in_features))
+            keep = kernels.keep_bits(ad.keep_mask(x2d, (x2d.shape[0], base.in_features)),
+                                     x2d.shape[0], base.in_features)
             mask_scale = 1.0 / (1.0 - ad.p)
         projs.append(_Proj(base.weight.data.view(-1, 1), base.weight.quant_state,
                            _cast_bias_once(base, x16), keep, mask_scale, ad.s))

@@ -230,7 +230,8 @@ def test_lora_sliced_and_single_launch_reductions_agree(cuda):
     h, ht = kernels.lora_h(x, a, s, keep, 1 / (1 - p))            # sliced (workspace allocated)
     h1 = torch.empty_like(h)
     ht1 = torch.empty_like(ht)
-    _lib.call("mxs_lora_h", _lib.ptr(x), M, K, _lib.ptr(a), 16, _lib.ptr(keep), 1 / (1 - p), s,
+    _lib.call("mxs_lora_h", _lib.ptr(x), M, K, _lib.ptr(a), 16,
+              _lib.ptr(kernels.keep_bits(keep, M, K)), 1 / (1 - p), s,
               _lib.ptr(h1), _lib.ptr(ht1), ht1.shape[1], None, None, 0, None, None,
               _lib.stream_of(cuda))                                  # single launch
     bt = b.t().contiguous()

@@ -102,3 +102,21 @@ def test_group_rope_entry_checks_its_rotation_operands_on_the_host():
     assert call((128, 128), T=48) == -1
     assert call((128, 128), cos=0x1004) == -3  # MXS_ERR_ALIGN
     assert call((128, 128), cs_t=130) == -3
+
+
+def test_keep_bits_checks_shape_and_dtype():
+    """keep_bits passes int32 [M, ceil(K/32)] through untouched and refuses other shapes and
+    dtypes before anything is launched (no GPU needed)."""
+    import pytest
+    import torch
+
+    from mindxsoup_amd import kernels
+
+    assert kernels.keep_words(1) == 1 and kernels.keep_words(32) == 1 and kernels.keep_words(33) == 2
+    bits = torch.zeros((4, 3), dtype=torch.int32)
+    assert kernels.keep_bits(bits, 4, 96) is bits or kernels.keep_bits(bits, 4, 96).data_ptr() == bits.data_ptr()
+    assert kernels.keep_bits(None, 4, 96) is None
+    for bad in (torch.zeros((4, 4), dtype=torch.int32), torch.zeros((4, 95), dtype=torch.uint8),
+                torch.zeros((4, 96), dtype=torch.float16)):
+        with pytest.raises(ValueError):
+            kernels.keep_bits(bad, 4, 96)

@@ -46,7 +46,7 @@ def test_timed_layer_step_matches_oracle(cuda):
                                   st.absmax.cpu().numpy(), st.state2.code.cpu().numpy(),
                                   st.state2.absmax.cpu().numpy(), float(st.offset.item())))
         x16, a16, b16 = (_np(pr[key]).astype(np.float16) for key in ("x", "a", "b"))
-        kp, dy16 = pr["keep"].cpu().numpy(), _np(pr["dy"]).astype(np.float16)
+        kp, dy16 = pr["keep8"].cpu().numpy(), _np(pr["dy"]).astype(np.float16)
         ref_y = O.lora_fwd(x16, w, a16, b16, s, kp, p)
         ref_dx, ref_da, ref_db = O.lora_bwd(dy16, x16, w, a16, b16, s, kp, p)
         errs = {"y": O.max_rel(_np(y), ref_y), "dA": O.max_rel(_np(da), ref_da),
