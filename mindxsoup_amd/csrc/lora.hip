@@ -90,13 +90,13 @@ __device__ __forceinline__ half8_t f32x8_to_f16(const float* p) {
 // a wave loads feeds TB multiplies, so TB = 2 halves the re-reads of R (every row block reads
 // all of its slice of R).  Wave w takes chunks c_beg + w, c_beg + w + nw, ... and adds them in
 // that order whatever TB, so TB does not change the bits.  RB: the accumulator blocks compiled in
-// (1 for r = 16, kMaxRB for any r up to 128).
-template <bool W32, int TB, int RB>
+// (1 for r = 16, kMaxRB for any r up to 128).  MASK: a.mask is set (the dropout applies).
+template <bool W32, int TB, int RB, bool MASK>
 __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice, int slices,
                                            int nw, int wg, int n_wg, float* red) {
   constexpr int CIF = rows_chunks_in_flight<TB>();
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: chunk tests below
   const int m0 = rb * 16 * TB;
   const int g = lane >> 4;
   const int rbn = a.r >> 4;
@@ -120,33 +120,52 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
 #pragma unroll
     for (int b = 0; b < RB; b++) acc[t][b] = (float4_t){0.f, 0.f, 0.f, 0.f};
   for (int c0 = c_beg + wave; wave < nw && c0 < c_end; c0 += CIF * nw) {
-    half8_t x[CIF][TB];
+    // A batch's loads come first, each chunk's under its own wave-uniform test (rows past M are
+    // clamped to row 0 and zeroed after), and nothing uses a loaded value before the last load:
+    // one round trip per batch.  (A chunk's dropout right after its own load split the batch
+    // into a round trip per chunk.)
+    half8_t x[CIF][TB], y[CIF];
+    uint32_t kb[CIF][TB];
+    auto load_r = [&](int b) {
+      const int64_t roff = (int64_t)(16 * b + (lane & 15)) * a.K + 8 * g;
+#pragma unroll
+      for (int u = 0; u < CIF; u++) {
+        const int c = c0 + u * nw;
+        y[u] = (half8_t){};
+        if (c < c_end) {
+          if constexpr (W32)
+            y[u] = f32x8_to_f16(a.R32 + roff + 32 * c);
+          else
+            y[u] = *reinterpret_cast<const half8_t*>(a.R + roff + 32 * c);
+        }
+      }
+    };
 #pragma unroll
     for (int u = 0; u < CIF; u++) {
       const int c = c0 + u * nw;
 #pragma unroll
       for (int t = 0; t < TB; t++) {
-        half8_t v = {};
-        if (c < c_end && row_ok[t]) {
-          v = *reinterpret_cast<const half8_t*>(a.P + prow[t] + 32 * c);
-          if (a.mask) v = drop8(v, a.mask[krow[t] + 4 * c], a.mscale);
+        x[u][t] = (half8_t){};
+        kb[u][t] = 0;
+        if (c < c_end) {
+          x[u][t] = *reinterpret_cast<const half8_t*>(a.P + prow[t] + 32 * c);
+          if constexpr (MASK) kb[u][t] = a.mask[krow[t] + 4 * c];
         }
-        x[u][t] = v;
       }
     }
+    load_r(0);
+#pragma unroll
+    for (int u = 0; u < CIF; u++)
+#pragma unroll
+      for (int t = 0; t < TB; t++) {
+        half8_t v = x[u][t];
+        if constexpr (MASK) v = drop8(v, kb[u][t], a.mscale);
+        x[u][t] = row_ok[t] ? v : (half8_t){};
+      }
 #pragma unroll
     for (int b = 0; b < RB; b++) {
       if (b >= rbn) break;
-      const int64_t roff = (int64_t)(16 * b + (lane & 15)) * a.K + 8 * g;
-      half8_t y[CIF];
-#pragma unroll
-      for (int u = 0; u < CIF; u++) {
-        const int c = c0 + u * nw;
-        if constexpr (W32)
-          y[u] = c < c_end ? f32x8_to_f16(a.R32 + roff + 32 * c) : (half8_t){};
-        else
-          y[u] = c < c_end ? *reinterpret_cast<const half8_t*>(a.R + roff + 32 * c) : (half8_t){};
-      }
+      if (b > 0) load_r(b);
 #pragma unroll
       for (int u = 0; u < CIF; u++)
 #pragma unroll
@@ -214,9 +233,13 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
 template <int TB, int RB>
 __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
   extern __shared__ float red[];  // [waves][16 * TB][r + 1]
-  rows_block<false, TB, RB>(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y,
-                            (int)blockDim.x >> 6, (int)(blockIdx.y * gridDim.x + blockIdx.x),
-                            (int)(gridDim.x * gridDim.y), red);
+  const int wg = (int)(blockIdx.y * gridDim.x + blockIdx.x), n_wg = (int)(gridDim.x * gridDim.y);
+  if (a.mask)
+    rows_block<false, TB, RB, true>(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y,
+                                    (int)blockDim.x >> 6, wg, n_wg, red);
+  else
+    rows_block<false, TB, RB, false>(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y,
+                                     (int)blockDim.x >> 6, wg, n_wg, red);
 }
 
 // Several rows problems over the same tokens in one launch (the q/k/v or gate/up projections
@@ -237,8 +260,12 @@ __global__ __launch_bounds__(1024) void k_lora_rows_group(RowsGroup g) {
   int i = 0;
   while (i + 1 < g.n && bid >= g.start[i + 1]) i++;
   const int local = bid - g.start[i];
-  rows_block<W32, TB, RB>(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i], g.nw[i],
-                          local, g.start[i + 1] - g.start[i], red);
+  if (g.p[i].mask)
+    rows_block<W32, TB, RB, true>(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i],
+                                  g.nw[i], local, g.start[i + 1] - g.start[i], red);
+  else
+    rows_block<W32, TB, RB, false>(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i],
+                                   g.nw[i], local, g.start[i + 1] - g.start[i], red);
 }
 
 // out[m][c] = fp16(sum of the slices' partials, in slice order) for m < M; outT [r, ldt]

@@ -48,28 +48,27 @@ template <> struct ColsVec<8> { typedef u32x4 T; };
 // `block`: block < cb0 is problem p0 (dA), the rest p1 (dB).  The first nw waves (at most
 // blockDim.x / 64) take 32-token steps in turn and add their accumulators in LDS (`red`,
 // [nw][r][16*CPL + 1] floats) in wave order; further waves only help store.  Every thread of
-// the workgroup calls it (it synchronizes the workgroup once).
-template <int CPL>
-__device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const ColsProblem& p1,
-                                                int cb0, int M, int ldt, int r, int block,
-                                                int nw, float* red) {
+// the workgroup calls it (it synchronizes the workgroup once).  MASK: the problem has a keep
+// mask (uniform over the workgroup).
+template <int CPL, bool MASK>
+__device__ __forceinline__ void lora_cols_body(const ColsProblem& a, int nb, int M, int ldt,
+                                               int r, int nw, float* red) {
   typedef typename ColsVec<CPL>::T VT;
   constexpr int WC = 16 * CPL;  // columns per workgroup
-  const bool second = block >= cb0;
-  const ColsProblem a = second ? p1 : p0;
-  const int nb = (second ? block - cb0 : block) * WC;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int ln = lane & 15;  // columns nb + CPL*ln .. +CPL
   const int lg = lane >> 4;  // tokens t0 + 8*lg .. +8
   const int col = nb + CPL * ln;
   const bool col_ok = col < a.Nq;
+  const int ccol = col_ok ? col : 0;  // a column the loads may touch
   // the lane's CPL keep bits of a row: bits col % 8 .. of byte col / 8 (CPL divides 8)
   const int64_t kst = keep_row_bytes(a.Nq);
-  const int kbyte = col >> 3, kshift = col & 7;
+  const int kbyte = ccol >> 3, kshift = ccol & 7;
   const int ld = WC + 1;
   // U token blocks of 32 per batch, all loaded before any is multiplied (one memory round trip
-  // per batch instead of one per block)
+  // per batch instead of one per block).  The loads are unconditional (token and column clamped
+  // into the tensors) so that a batch issues back to back; values past M or Nq are zeroed after.
   constexpr int U = CPL == 8 ? 2 : 3;
   for (int b = 0; wave < nw && b < (r >> 4); b++) {  // r-blocks of 16 (input re-read per block)
     float4_t acc[CPL];
@@ -82,27 +81,27 @@ __device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const Col
 #pragma unroll
       for (int u = 0; u < U; u++) {
         const int mb = t0 + u * nw * 32 + 8 * lg;
-        av[u] = (half8_t){};
-        if (mb < ldt)
-          av[u] = *reinterpret_cast<const half8_t*>(a.PT + (int64_t)(16 * b + ln) * ldt + mb);
+        av[u] = *reinterpret_cast<const half8_t*>(a.PT + (int64_t)(16 * b + ln) * ldt +
+                                                  min(mb, ldt - 8));
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-          const int m = mb + e;
-          rows[u][e] = VT{};
-          mks[u][e] = 0;
-          if (m < M && col_ok) {
-            rows[u][e] = *reinterpret_cast<const VT*>(a.Q + (int64_t)m * a.Nq + col);
-            if (a.mask) mks[u][e] = a.mask[(int64_t)m * kst + kbyte];
-          }
+          const int64_t m = min(mb + e, M - 1);
+          rows[u][e] = *reinterpret_cast<const VT*>(a.Q + m * a.Nq + ccol);
+          if constexpr (MASK) mks[u][e] = a.mask[m * kst + kbyte];
         }
       }
+      // the whole batch issues before any of its values is used
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int u = 0; u < U; u++) {
+        const int mb = t0 + u * nw * 32 + 8 * lg;
+        if (mb >= ldt) av[u] = (half8_t){};
         _Float16 hv[8][CPL];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
+          if (!(mb + e < M && col_ok)) rows[u][e] = VT{};
           __builtin_memcpy(hv[e], &rows[u][e], sizeof(VT));
-          if (a.mask) {
+          if constexpr (MASK) {
 #pragma unroll
             for (int c = 0; c < CPL; c++)
               hv[e][c] = ((mks[u][e] >> (kshift + c)) & 1u) ? (_Float16)((float)hv[e][c] * a.mscale)
@@ -134,6 +133,17 @@ __device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const Col
     if (a.out_rn) a.out[(int64_t)j * a.Nq + n] = sum;
     else a.out[(int64_t)n * r + j] = sum;
   }
+}
+
+template <int CPL>
+__device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const ColsProblem& p1,
+                                                int cb0, int M, int ldt, int r, int block,
+                                                int nw, float* red) {
+  const bool second = block >= cb0;
+  const ColsProblem& a = second ? p1 : p0;
+  const int nb = (second ? block - cb0 : block) * 16 * CPL;
+  if (a.mask) lora_cols_body<CPL, true>(a, nb, M, ldt, r, nw, red);
+  else lora_cols_body<CPL, false>(a, nb, M, ldt, r, nw, red);
 }
 
 }  // namespace mxs
