@@ -326,6 +326,14 @@ def layer_fwd(projs, s=ALPHA / RANK):
             for i, (_, at, bt), (y, ht) in zip(grp, outs, res):
                 ys[i], saved[i] = y, (ht, at, bt)
             continue
+        if len(ps) == 2 and kernels.fwd_pair_ok(M_TOKENS, ps[0]["n"], ps[1]["n"], ps[0]["k"]):
+            # gate and up over one input: one launch (grid z selects the projection)
+            res = kernels.nf4_linear_fwd_hp_pair(ps[0]["x"], [p["packed"] for p in ps],
+                                                 [p["st"] for p in ps], [o[0] for o in outs],
+                                                 [p["b"] for p in ps])
+            for i, (_, at, bt), (y, ht) in zip(grp, outs, res):
+                ys[i], saved[i] = y, (ht, at, bt)
+            continue
         for i, p, (hp, at, bt) in zip(grp, ps, outs):
             ys[i], ht = kernels.nf4_linear_fwd_hp(p["x"], p["packed"], p["st"], hp, p["b"],
                                                   ws=p["ws"])

@@ -213,6 +213,27 @@ int mxs_nf4_linear_bwd_dx_hp_pair(const void* const dy[2], int M, const int N[2]
                                   void* const lora_dht[2], void* dx, void* workspace,
                                   hipStream_t stream);
 
+/* Two projections over the same input x [M, K] (the gate and up projections of the MLP,
+ * solution/mlp.py:42-43, each NF4LinearFunction.forward of solution/linear4bit.py:47-49 with
+ * peft's LoRA branch) in ONE launch: y[i] and lora_ht[i] as mxs_nf4_linear_fwd_hp computes them
+ * (the same bits), arrays of the per-projection arguments (bias and lora_ht may be NULL, or any
+ * entry); the two share M, K, r, ldt and hp_slices.  Grid z selects the projection, so their
+ * tiles share the GPU's rounds: at 1024 tokens 2 x 224 tiles of 256 x 160 take 1.75 rounds of
+ * 256 CUs, where two launches take one round each.  Only where mxs_nf4_linear_fwd_pair_ok(M,
+ * N[0], N[1], K) is 1 (both plan the unsplit 256 x 160 kernel: N[0] == N[1] >= 4096), else
+ * MXS_ERR_SIZE. */
+int mxs_nf4_linear_fwd_hp_pair(const void* x, int M, int K, const int N[2],
+                               const void* const packed[2], const void* const absmax8[2],
+                               const float* const code[2], const float* const absmax2[2],
+                               const float* const offset[2], const void* const bias[2],
+                               const float* const lora_hp[2], int hp_slices, int ldt,
+                               const void* const lora_b[2], int r, void* const lora_ht[2],
+                               void* const y[2], hipStream_t stream);
+
+/* 1 when mxs_nf4_linear_fwd_hp_pair takes two projections [K -> N0] and [K -> N1] at M tokens,
+ * else 0. */
+int mxs_nf4_linear_fwd_pair_ok(int M, int N0, int N1, int K);
+
 /* 1 when mxs_nf4_linear_bwd_dx_hp_pair takes two projections [K -> N0] and [K -> N1] at M
  * tokens, else 0. */
 int mxs_nf4_linear_bwd_dx_pair_ok(int M, int N0, int N1, int K);

@@ -52,6 +52,9 @@ _SIGNATURES = {
     "mxs_lora_grad_b": [P, I32, P, I32, I32, I32, P, P, P],
     "mxs_lora_grads": [P, P, I32, P, P, I32, I32, I32, I32, P, F32, P, P, P, P],
     "mxs_keep_pack": [P, I32, I32, P, P],
+    "mxs_nf4_linear_fwd_hp_pair": [P, I32, I32, P, P, P, P, P, P, P, P, I32, I32, P, I32, P, P,
+                                   P],
+    "mxs_nf4_linear_fwd_pair_ok": [I32, I32, I32, I32],
     "mxs_nf4_linear_bwd_dx_grads": [P, I32, I32, I32, P, P, P, P, P, P, P, I32, P, F32, P, P, I32,
                                     P, P, P, P, P, P],
     "mxs_nf4_linear_bwd_grads_fused": [I32, I32, I32, I32],

@@ -59,6 +59,8 @@ struct GemmArgs {
   int steps_per_split;
   int zf;                   // grid z of this problem's first split (0, or the second problem's
                             // first plane in a launch of two, k_nf4_gemm_ws_pair)
+  int unsplit;              // one split although gridDim.z > 1 (the z planes are problems): fp16
+                            // stores, no partials
   // backward: the LoRA gradients dA (cp0) and dB (cp1), computed by cols_blocks extra
   // workgroups of the same launch in grid rows past the GEMM's (0: none).  They depend on
   // nothing the GEMM tiles write, so they run on the CUs the tiles leave idle.
@@ -474,7 +476,7 @@ __device__ __forceinline__ void init_acc(const GemmArgs& a, float16_t (&acc)[TM]
 template <int TM, int TN, bool BWD>
 __device__ __forceinline__ void epilogue(const GemmArgs& a, float16_t (&acc)[TM][TN], int mb,
                                          int nb, int lrow, int lseg) {
-  const bool split = gridDim.z > 1;
+  const bool split = gridDim.z > 1 && !a.unsplit;
   const bool vec = (a.Nc % 4) == 0 && (a.ldc % 4) == 0;
 #pragma unroll
   for (int i = 0; i < TM; i++) {
@@ -569,7 +571,7 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& a, float16_t (&a
   using SS = StagedStore<TM, TN>;
   constexpr int WN = SS::WN;
   const int lrow = lane & 31, lseg = lane >> 5;
-  const bool split = gridDim.z > 1;
+  const bool split = gridDim.z > 1 && !a.unsplit;
   // whole 16-byte chunks can be stored when rows keep 16-byte alignment
   const bool vec = split ? (a.Nc % 4) == 0 : ((a.Nc % 8) == 0 && (a.ldc % 8) == 0 &&
                                                ((uintptr_t)a.C % 16) == 0);
@@ -2528,6 +2530,50 @@ static int launch_ws_pair(const GemmArgs& a0, const GemmArgs& a1, int sp, hipStr
   return launch_reduce(g.p[0], 2 * sp, stream);
 }
 
+// Two forward projections of one shape over the same input (gate and up, solution/mlp.py:42-43),
+// each unsplit, in ONE launch: grid z selects the problem.  Their 2 x 224 tiles of 256x160 at
+// 1024 tokens take 1.75 rounds of the 256 CUs instead of two launches of one round each that
+// leave 32 CUs idle.  Each tile runs exactly as in its own launch (the same bits).
+template <int BM, int BN, int CWM, int CWN, int PW, int NS>
+static int launch_ws_fwd_pair(const GemmArgs& a0, const GemmArgs& a1, hipStream_t stream) {
+  if (a0.M != a1.M || a0.Nc != a1.Nc || a0.Kr != a1.Kr) return MXS_ERR_ARG;
+  GemmPair g{};
+  g.p[0] = a0;
+  g.p[1] = a1;
+  for (int i = 0; i < 2; i++) {
+    GemmArgs& a = g.p[i];
+    if ((int64_t)a.Nc * a.Kr >= (int64_t(1) << 32) || (int64_t)BM * a.lda * 2 >= (int64_t(1) << 32) ||
+        a.glu || a.cols_blocks > 0)
+      return MXS_ERR_SIZE;
+    a.steps_per_split = a.Kr / kBK;
+    a.zf = i;
+    a.unsplit = 1;
+  }
+  const dim3 grid((a0.Nc + BN - 1) / BN, (a0.M + BM - 1) / BM, 2);
+  const size_t lds = (size_t)ws_lds_halfs<BM, BN, false>() * sizeof(_Float16);
+  static bool lds_set = false;  // idempotent attribute; a benign race between threads
+  if (!lds_set) {
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&k_nf4_gemm_ws_pair<BM, BN, CWM, CWN, false, PW, NS>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+    lds_set = true;
+  }
+  hipLaunchKernelGGL((k_nf4_gemm_ws_pair<BM, BN, CWM, CWN, false, PW, NS>), grid,
+                     dim3(64 * (4 + PW)), lds, stream, g);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MXS_OK : (int)e;
+}
+
+// The forward pair takes two problems [K -> N] that each plan the unsplit 256x160 kernel.
+static bool fwd_pair_plan_ok(int M, int N0, int N1, int K) {
+  if (M <= 0 || N0 != N1 || K <= 0 || K % kBK) return false;
+  int c, sp;
+  choose(M, N0, K, false, &c, &sp);
+  return c == 7 && sp == 1 && (int64_t)N0 * K < (int64_t(1) << 32) &&
+         (int64_t)256 * K * 2 < (int64_t(1) << 32);
+}
+
 // The pair's plan: both problems must plan the 256x96 split backward kernel (cfg 11) on their
 // own; the pair then splits each reduction kPairSplits ways.
 constexpr int kPairSplits = 2;
@@ -2937,6 +2983,53 @@ int mxs_nf4_linear_bwd_dx_hp(const void* dy, int M, int N, int K, const void* pa
   a.ldc = K;
   set_workspace(a, workspace);
   return gemm_entry(true, a, cfg, splits, stream);
+}
+
+int mxs_nf4_linear_fwd_pair_ok(int M, int N0, int N1, int K) {
+  return fwd_pair_plan_ok(M, N0, N1, K) ? 1 : 0;
+}
+
+int mxs_nf4_linear_fwd_hp_pair(const void* x, int M, int K, const int N[2],
+                               const void* const packed[2], const void* const absmax8[2],
+                               const float* const code[2], const float* const absmax2[2],
+                               const float* const offset[2], const void* const bias[2],
+                               const float* const lora_hp[2], int hp_slices, int ldt,
+                               const void* const lora_b[2], int r, void* const lora_ht[2],
+                               void* const y[2], hipStream_t stream) {
+  if (M < 0 || !x || !N || !packed || !absmax8 || !code || !absmax2 || !offset || !lora_hp ||
+      !lora_b || !y)
+    return MXS_ERR_ARG;
+  if (M == 0) return MXS_OK;
+  if (!fwd_pair_plan_ok(M, N[0], N[1], K)) return MXS_ERR_SIZE;
+  GemmArgs p[2];
+  for (int i = 0; i < 2; i++) {
+    GemmArgs a{};
+    a.A = static_cast<const _Float16*>(x);
+    a.lda = K;
+    a.packed = static_cast<const uint8_t*>(packed[i]);
+    a.absmax8 = static_cast<const uint8_t*>(absmax8[i]);
+    a.code = code[i];
+    a.absmax2 = absmax2[i];
+    a.offset = offset[i];
+    a.M = M;
+    a.Nc = N[i];
+    a.Kr = K;
+    a.Kw = K;
+    a.bias = bias ? static_cast<const _Float16*>(bias[i]) : nullptr;
+    a.lora_hp = lora_hp[i];
+    a.hp_slices = hp_slices;
+    a.ldt = ldt;
+    a.lora_ht = lora_ht ? static_cast<_Float16*>(lora_ht[i]) : nullptr;
+    a.lora_w = static_cast<const _Float16*>(lora_b[i]);
+    a.r = r;
+    a.C = static_cast<_Float16*>(y[i]);
+    a.ldc = N[i];
+    if (!a.lora_hp) return MXS_ERR_ARG;
+    const int c = check_gemm(false, a);
+    if (c != MXS_OK) return c == 1 ? MXS_OK : c;
+    p[i] = a;
+  }
+  return launch_ws_fwd_pair<256, 160, 4, 1, 4, 4>(p[0], p[1], stream);
 }
 
 int mxs_nf4_linear_bwd_dx_pair_ok(int M, int N0, int N1, int K) {

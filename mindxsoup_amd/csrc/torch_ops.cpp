@@ -476,6 +476,13 @@ Lists4 fwd_impl(const Tensor& x, TensorList lora_a, TensorList lora_b, TensorLis
                                    pbias.data(), p_hp.data(), S, (int)ldt, pb.data(), rr,
                                    p_ht.data(), p_y.data(), st),
        "mxs_nf4_linear_fwd_hp_group");
+  } else if (n == 2 && mxs_nf4_linear_fwd_pair_ok(m, Ns[0], Ns[1], k)) {
+    // gate and up: one launch, grid z selects the projection (the bits of two launches)
+    ok(mxs_nf4_linear_fwd_hp_pair(xc.data_ptr(), m, k, Ns.data(), p_packed.data(), p_a8.data(),
+                                  p_code.data(), p_a2.data(), p_off.data(), pbias.data(),
+                                  p_hp.data(), S, (int)ldt, pb.data(), rr, p_ht.data(),
+                                  p_y.data(), st),
+       "mxs_nf4_linear_fwd_hp_pair");
   } else {
     int64_t need = 0;
     for (size_t i = 0; i < n; ++i)

@@ -581,6 +581,45 @@ def nf4_linear_bwd_dx_hp(dy2d, packed, state, lora_dhp, lora_at, mask=None, mask
     return dx, dht
 
 
+def fwd_pair_ok(M, N0, N1, K):
+    """Whether nf4_linear_fwd_hp_pair takes two projections [K -> N0], [K -> N1] at M tokens."""
+    return bool(_lib.lib().mxs_nf4_linear_fwd_pair_ok(M, N0, N1, K))
+
+
+def nf4_linear_fwd_hp_pair(x2d, packeds, states, lora_hps, lora_bs, biases=None):
+    """nf4_linear_fwd_hp for two projections over the same x2d in one launch (grid z selects the
+    projection; the same bits as two calls): [(y, ht), (y, ht)].  Only where fwd_pair_ok."""
+    (n0, k), (n1, k1) = states[0].shape, states[1].shape
+    if x2d.dtype != torch.float16 or x2d.dim() != 2 or x2d.shape[1] != k or k1 != k:
+        raise ValueError("x must be fp16 [M, in_features] of two weights [N_i, K]")
+    x2d = x2d.contiguous()
+    M = x2d.shape[0]
+    if not fwd_pair_ok(M, n0, n1, k):
+        raise ValueError(f"the forward pair does not take [{k} -> {n0}], [{k} -> {n1}] at {M} "
+                         "tokens")
+    S, ldt, r = lora_hps[0].shape
+    for hp, b, n in zip(lora_hps, lora_bs, (n0, n1)):
+        if hp.shape != (S, ldt, r) or hp.dtype != torch.float32 or ldt != _ldt(M) or \
+                b.shape != (n, r):
+            raise ValueError("lora_hp [slices, ldt, r] fp32 (one shape) and lora_b [N, r]")
+    biases = biases or [None, None]
+    biases = [None if b is None else b.to(torch.float16).contiguous() for b in biases]
+    dev = x2d.device
+    for pk, st in zip(packeds, states):
+        check_nf4_operands(pk, st, dev)
+    ys = [torch.empty((M, n), dtype=torch.float16, device=dev) for n in (n0, n1)]
+    hts = [torch.empty((r, ldt), dtype=torch.float16, device=dev) for _ in range(2)]
+    _lib.call("mxs_nf4_linear_fwd_hp_pair", _lib.ptr(x2d), M, k, _int_array([n0, n1]),
+              _ptr_array(packeds), _ptr_array([st.absmax for st in states]),
+              _ptr_array([st.state2.code for st in states]),
+              _ptr_array([st.state2.absmax for st in states]),
+              _ptr_array([st.offset for st in states]), _ptr_array(biases),
+              _ptr_array([h.contiguous() for h in lora_hps]), S, ldt,
+              _ptr_array([b.contiguous() for b in lora_bs]), r, _ptr_array(hts), _ptr_array(ys),
+              _lib.stream_of(dev))
+    return list(zip(ys, hts))
+
+
 def bwd_dx_pair_ok(M, N0, N1, K):
     """True when nf4_linear_bwd_dx_hp_pair takes projections [K -> N0] and [K -> N1] at M tokens
     (both plan the narrow-output split-K kernel on their own)."""

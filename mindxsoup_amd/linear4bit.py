@@ -446,6 +446,12 @@ class NF4LoraSiblingsFunction(torch.autograd.Function):
                                                    [p.state for p in projs],
                                                    [r[0] for r in rows], b16,
                                                    [p.bias for p in projs], rope=rope)
+        elif n == 2 and kernels.fwd_pair_ok(x2d.shape[0], projs[0].state.shape[0],
+                                            projs[1].state.shape[0], x2d.shape[1]):
+            # gate and up: one launch (grid z selects the projection), the bits of two
+            outs = kernels.nf4_linear_fwd_hp_pair(x2d, [p.packed for p in projs],
+                                                  [p.state for p in projs], [r[0] for r in rows],
+                                                  b16, [p.bias for p in projs])
         else:
             outs = [kernels.nf4_linear_fwd_hp(x2d, p.packed, p.state, r[0], b, p.bias)
                     for p, r, b in zip(projs, rows, b16)]

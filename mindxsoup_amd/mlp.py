@@ -59,14 +59,24 @@ class NF4LoraMLPFunction(torch.autograd.Function):
                                                        lora_b=g_b)
             hp, at_u, bt_u = kernels.lora_h_partials(x2d, u_a, pu.s, pu.keep, pu.mask_scale,
                                                      lora_b=u_b)
-        gate, ht_g = kernels.nf4_linear_fwd_hp(x2d, pg.packed, pg.state, hp_g, g_b, pg.bias)
-        del hp_g
-        if GLU_FORWARD_TAIL and kernels.glu_fused(M, inter, hidden, False):
-            up, h, ht_u = kernels.nf4_linear_fwd_glu(x2d, pu.packed, pu.state, gate, hp, u_b,
-                                                     pu.bias)
-        else:
-            up, ht_u = kernels.nf4_linear_fwd_hp(x2d, pu.packed, pu.state, hp, u_b, pu.bias)
+        glu_tail = GLU_FORWARD_TAIL and kernels.glu_fused(M, inter, hidden, False)
+        if not glu_tail and kernels.fwd_pair_ok(M, pg.state.shape[0], inter, hidden) and \
+                hp_g.shape == hp.shape:
+            # gate and up in one launch (grid z selects the projection; the bits of two)
+            (gate, ht_g), (up, ht_u) = kernels.nf4_linear_fwd_hp_pair(
+                x2d, [pg.packed, pu.packed], [pg.state, pu.state], [hp_g, hp], [g_b, u_b],
+                [pg.bias, pu.bias])
+            del hp_g
             h = kernels.silu_mul(gate, up)
+        else:
+            gate, ht_g = kernels.nf4_linear_fwd_hp(x2d, pg.packed, pg.state, hp_g, g_b, pg.bias)
+            del hp_g
+            if glu_tail:
+                up, h, ht_u = kernels.nf4_linear_fwd_glu(x2d, pu.packed, pu.state, gate, hp, u_b,
+                                                         pu.bias)
+            else:
+                up, ht_u = kernels.nf4_linear_fwd_hp(x2d, pu.packed, pu.state, hp, u_b, pu.bias)
+                h = kernels.silu_mul(gate, up)
         hp, at_d, bt_d = kernels.lora_h_partials(h, d_a, pd.s, pd.keep, pd.mask_scale,
                                                  lora_b=d_b)
         y, ht_d = kernels.nf4_linear_fwd_hp(h, pd.packed, pd.state, hp, d_b, pd.bias)

@@ -120,3 +120,36 @@ def test_group_backward_sums(cuda):
             two = two + r[0]
         err = ((summed[0][0].float() - two.float()).abs().max() / two.float().abs().max()).item()
         assert 0 < err < 2 ** -9, (paired, err)
+
+
+
+@pytest.mark.parametrize("M", [1024, 300])
+def test_forward_pair_equals_two_launches(cuda, M):
+    """gate and up forward in one launch (mxs_nf4_linear_fwd_hp_pair, grid z selects the
+    projection) give the bits of two nf4_linear_fwd_hp launches, y and the transposed LoRA
+    operand, with a bias and without; within the north star's 1e-2 of the oracle."""
+    from mindxsoup_amd import kernels
+
+    print(f"case fwd pair M={M}", flush=True)
+    x = torch.randn((M, 1536), device=cuda).half()
+    ps = [_proj(cuda, 8960, 1536, M, 40 + i, x) for i in range(2)]
+    assert kernels.fwd_pair_ok(M, 8960, 8960, 1536)
+    assert not kernels.fwd_pair_ok(M, 1536, 1536, 1536) and not kernels.fwd_pair_ok(M, 8960, 256, 1536)
+    rows = kernels.lora_h_partials_group([x, x], [p["a"] for p in ps], S, [p["keep"] for p in ps],
+                                         1 / (1 - P), [p["b"] for p in ps])
+    bias = [torch.randn((8960,), device=cuda).half(), None]
+    for biases in (None, bias):
+        two = [kernels.nf4_linear_fwd_hp(x, p["packed"], p["st"], r[0], p["b"],
+                                         None if biases is None else biases[i])
+               for i, (p, r) in enumerate(zip(ps, rows))]
+        pair = kernels.nf4_linear_fwd_hp_pair(x, [p["packed"] for p in ps], [p["st"] for p in ps],
+                                              [r[0] for r in rows], [p["b"] for p in ps], biases)
+        for (y2, t2), (y1, t1) in zip(two, pair):
+            assert torch.equal(y1, y2) and torch.equal(t1, t2)
+    x16 = _np(x).astype(np.float16)
+    for p, (y, _) in zip(ps, pair):
+        ref = O.lora_fwd(x16, _w(p), _np(p["a"]).astype(np.float16),
+                         _np(p["b"]).astype(np.float16), S, p["keep"].cpu().numpy(), P)
+        if p is ps[0]:
+            ref = ref + _np(bias[0])
+        assert O.max_rel(_np(y), ref) < 1e-2
