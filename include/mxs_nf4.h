@@ -213,6 +213,24 @@ int mxs_nf4_linear_bwd_dx_hp_pair(const void* const dy[2], int M, const int N[2]
                                   void* const lora_dht[2], void* dx, void* workspace,
                                   hipStream_t stream);
 
+/* mxs_nf4_linear_bwd_dx_hp_pair and, in the same calls' stream order, both projections' LoRA
+ * gradients as mxs_lora_grads_group computes them from the dHs^T the pair writes (lora_dht,
+ * required here), ht[i] = Hs_i^T [r, ldt] and the shared input x [M, K] (dA_i [r, K], dB_i
+ * [N[i], r], fp32): the bits of those two calls.  The backward of the gate and up projections'
+ * LoRA branches (peft's lora_A / lora_B under solution/mlp.py:42-43) with their summed input
+ * gradient.  Two launches instead of three: the pair GEMM, then one launch for its split-K
+ * reduce and the gradients (independent of each other), the reduce's workgroups filling the
+ * CUs the gradients' last partial round leaves idle.  Same conditions as
+ * mxs_nf4_linear_bwd_dx_hp_pair, and the two projections share their gradients' columns per
+ * lane (as mxs_lora_grads_group requires). */
+int mxs_nf4_linear_bwd_dx_hp_pair_grads(
+    const void* const dy[2], int M, const int N[2], int K, const void* const packed[2],
+    const void* const absmax8[2], const float* const code[2], const float* const absmax2[2],
+    const float* const offset[2], const float* const lora_dhp[2], int hp_slices, int ldt,
+    const void* const lora_at[2], int r, const void* const mask[2], float mask_scale,
+    void* const lora_dht[2], const void* const ht[2], const void* x, float* const da[2],
+    float* const db[2], void* dx, void* workspace, hipStream_t stream);
+
 /* Two projections over the same input x [M, K] (the gate and up projections of the MLP,
  * solution/mlp.py:42-43, each NF4LinearFunction.forward of solution/linear4bit.py:47-49 with
  * peft's LoRA branch) in ONE launch: y[i] and lora_ht[i] as mxs_nf4_linear_fwd_hp computes them

@@ -93,6 +93,8 @@ _SIGNATURES = {
     "mxs_transpose_f16": [P, I32, I32, P, P],
     "mxs_nf4_linear_bwd_dx_hp_pair": [P, I32, P, I32, P, P, P, P, P, P, I32, I32, P, I32, P, F32,
                                       P, P, P, P],
+    "mxs_nf4_linear_bwd_dx_hp_pair_grads": [P, I32, P, I32, P, P, P, P, P, P, I32, I32, P, I32,
+                                            P, F32, P, P, P, P, P, P, P, P],
     "mxs_nf4_linear_bwd_dx_pair_ok": [I32, I32, I32, I32],
     "mxs_nf4_linear_bwd_dx_pair_workspace_bytes": [I32, I32, I32, I32],
 }

@@ -313,26 +313,12 @@ __global__ __launch_bounds__(64 * cols_max_waves<CPL>()) void k_lora_cols(ColsPr
   lora_cols_block<CPL>(p0, p1, cb0, M, ldt, r, (int)blockIdx.x, (int)blockDim.x >> 6, red);
 }
 
-// dA / dB of several projections in one launch (gate's and up's arrive together): pair i owns
-// workgroups [start[i], start[i+1]), laid out as its own launch's grid (dA blocks, then dB).
-// All pairs share the columns per lane and the waves, which is what their own launches would
-// use when their shapes agree.
-struct ColsGroup {
-  ColsProblem pa[kMaxGroup], pb[kMaxGroup];
-  int start[kMaxGroup + 1];
-  int cb0[kMaxGroup];
-  int n;
-};
-
+// dA / dB of several projections in one launch (ColsGroup).
 template <int CPL>
 __global__ __launch_bounds__(64 * cols_max_waves<CPL>()) void k_lora_cols_group(ColsGroup g, int M,
                                                                                int ldt, int r) {
   extern __shared__ float red[];  // [waves][r][16 * CPL + 1]
-  const int bid = (int)blockIdx.x;
-  int i = 0;
-  while (i + 1 < g.n && bid >= g.start[i + 1]) i++;
-  lora_cols_block<CPL>(g.pa[i], g.pb[i], g.cb0[i], M, ldt, r, bid - g.start[i],
-                       (int)blockDim.x >> 6, red);
+  lora_cols_group_block<CPL>(g, M, ldt, r, (int)blockIdx.x, (int)blockDim.x >> 6, red);
 }
 
 // Keep bits from a byte keep mask [M, K] (nonzero = kept; the reference's int8 `keep`): one
@@ -506,13 +492,7 @@ static int cols_launch_t(const ColsProblem& p0, const ColsProblem& p1, int nprob
 template <int CPL>
 static int cols_group_launch_t(ColsGroup g, int M, int ldt, int r, hipStream_t stream) {
   constexpr int WC = 16 * CPL;
-  int total = 0;
-  for (int i = 0; i < g.n; i++) {
-    g.cb0[i] = (g.pa[i].Nq + WC - 1) / WC;
-    g.start[i] = total;
-    total += g.cb0[i] + (g.pb[i].Nq + WC - 1) / WC;
-  }
-  g.start[g.n] = total;
+  const int total = cols_group_layout(g, CPL);
   const int nw = cols_waves(M, r, CPL, cols_max_waves<CPL>());
   const int per_wave = r * (WC + 1) * (int)sizeof(float);
   if (nw * per_wave > kColsLds) return MXS_ERR_SIZE;
@@ -875,29 +855,10 @@ int mxs_lora_grads_group(int n, const void* const dht[], const void* const ht[],
   g.n = n;
   const int cpl = cols_cpl(K[0] + N[0]);
   for (int i = 0; i < n; i++) {
-    const void* mk = mask ? mask[i] : nullptr;
-    if (K[i] <= 0 || N[i] <= 0 || !dht[i] || !ht[i] || !x[i] || !dy[i] || !da[i] || !db[i])
-      return MXS_ERR_ARG;
-    if (K[i] % 8 || N[i] % 8 || ldt < M || ldt % 8 || cols_cpl(K[i] + N[i]) != cpl)
-      return MXS_ERR_SIZE;
-    if ((uintptr_t)x[i] % 16 || (uintptr_t)dht[i] % 16 || (uintptr_t)dy[i] % 16 ||
-        (uintptr_t)ht[i] % 16 || (mk && ((uintptr_t)mk % 4)))
-      return MXS_ERR_ALIGN;
-    ColsProblem& pa = g.pa[i];  // dA [r, K] = dHs^T . drop(X)
-    pa.PT = static_cast<const _Float16*>(dht[i]);
-    pa.Q = static_cast<const _Float16*>(x[i]);
-    pa.mask = static_cast<const uint8_t*>(mk);
-    pa.mscale = mask_scale;
-    pa.Nq = K[i];
-    pa.out = da[i];
-    pa.out_rn = 1;
-    ColsProblem& pb = g.pb[i];  // dB [N, r] = dY^T . Hs
-    pb.PT = static_cast<const _Float16*>(ht[i]);
-    pb.Q = static_cast<const _Float16*>(dy[i]);
-    pb.mscale = 1.0f;
-    pb.Nq = N[i];
-    pb.out = db[i];
-    pb.out_rn = 0;
+    const int e = cols_group_set(g, i, dht[i], ht[i], ldt, x[i], dy[i], M, K[i], N[i],
+                                 mask ? mask[i] : nullptr, mask_scale, da[i], db[i]);
+    if (e != MXS_OK) return e;
+    if (cols_cpl(K[i] + N[i]) != cpl) return MXS_ERR_SIZE;
   }
   if (cpl == 8) return cols_group_launch_t<8>(g, M, ldt, r, stream);
   if (cpl == 4) return cols_group_launch_t<4>(g, M, ldt, r, stream);

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "common.h"
+#include "mxs_nf4.h"
 
 namespace mxs {
 
@@ -144,6 +145,71 @@ __device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const Col
   const int nb = (second ? block - cb0 : block) * 16 * CPL;
   if (a.mask) lora_cols_body<CPL, true>(a, nb, M, ldt, r, nw, red);
   else lora_cols_body<CPL, false>(a, nb, M, ldt, r, nw, red);
+}
+
+// dA / dB of several projections in one launch (gate's and up's arrive together): pair i owns
+// workgroups [start[i], start[i+1]), laid out as its own launch's grid (dA blocks, then dB).
+// All pairs share the columns per lane and the waves, which is what their own launches would
+// use when their shapes agree.
+constexpr int kMaxColsGroup = 4;
+struct ColsGroup {
+  ColsProblem pa[kMaxColsGroup], pb[kMaxColsGroup];
+  int start[kMaxColsGroup + 1];
+  int cb0[kMaxColsGroup];
+  int n;
+};
+
+// Pair i of a gradient group: dA [r, K] = dHs^T . drop(X) from dht [r, ldt], x [M, K] and the
+// keep bits (or null), dB [N, r] = dY^T . Hs from ht [r, ldt] and dy [M, N], with the checks of
+// mxs_lora_grads.  MXS_OK or an error code.
+inline int cols_group_set(ColsGroup& g, int i, const void* dht, const void* ht, int ldt,
+                          const void* x, const void* dy, int M, int K, int N, const void* mask,
+                          float mask_scale, float* da, float* db) {
+  if (K <= 0 || N <= 0 || !dht || !ht || !x || !dy || !da || !db) return MXS_ERR_ARG;
+  if (K % 8 || N % 8 || ldt < M || ldt % 8) return MXS_ERR_SIZE;
+  if ((uintptr_t)x % 16 || (uintptr_t)dht % 16 || (uintptr_t)dy % 16 || (uintptr_t)ht % 16 ||
+      (mask && ((uintptr_t)mask % 4)))
+    return MXS_ERR_ALIGN;
+  ColsProblem& pa = g.pa[i];
+  pa.PT = static_cast<const _Float16*>(dht);
+  pa.Q = static_cast<const _Float16*>(x);
+  pa.mask = static_cast<const uint8_t*>(mask);
+  pa.mscale = mask_scale;
+  pa.Nq = K;
+  pa.out = da;
+  pa.out_rn = 1;
+  ColsProblem& pb = g.pb[i];
+  pb.PT = static_cast<const _Float16*>(ht);
+  pb.Q = static_cast<const _Float16*>(dy);
+  pb.mask = nullptr;
+  pb.mscale = 1.0f;
+  pb.Nq = N;
+  pb.out = db;
+  pb.out_rn = 0;
+  return MXS_OK;
+}
+
+// Lays out the group's workgroups for CPL columns per lane (16 * CPL columns a workgroup);
+// returns their number.
+inline int cols_group_layout(ColsGroup& g, int cpl) {
+  const int wc = 16 * cpl;
+  int total = 0;
+  for (int i = 0; i < g.n; i++) {
+    g.cb0[i] = (g.pa[i].Nq + wc - 1) / wc;
+    g.start[i] = total;
+    total += g.cb0[i] + (g.pb[i].Nq + wc - 1) / wc;
+  }
+  g.start[g.n] = total;
+  return total;
+}
+
+// Workgroup `bid` (< g.start[g.n]) of a gradient group, with nw summing waves.
+template <int CPL>
+__device__ __forceinline__ void lora_cols_group_block(const ColsGroup& g, int M, int ldt, int r,
+                                                      int bid, int nw, float* red) {
+  int i = 0;
+  while (i + 1 < g.n && bid >= g.start[i + 1]) i++;
+  lora_cols_block<CPL>(g.pa[i], g.pb[i], g.cb0[i], M, ldt, r, bid - g.start[i], nw, red);
 }
 
 }  // namespace mxs

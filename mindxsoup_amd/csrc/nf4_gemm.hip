@@ -755,15 +755,14 @@ struct GluTail {
   }
 };
 
+// The split-K reduce of elements e .. e + 3 (one thread).
 template <int GLU>
-__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int splits,
-                                                      int M, int Nc, _Float16* __restrict__ C,
-                                                      int64_t ldc,
-                                                      _Float16* __restrict__ glu_g,
-                                                      _Float16* __restrict__ glu_u,
-                                                      _Float16* __restrict__ glu_h) {
+__device__ __forceinline__ void splitk_reduce_quad(const float* __restrict__ ws, int splits,
+                                                   int M, int Nc, _Float16* __restrict__ C,
+                                                   int64_t ldc, _Float16* __restrict__ glu_g,
+                                                   _Float16* __restrict__ glu_u,
+                                                   _Float16* __restrict__ glu_h, int64_t e) {
   const int64_t plane = (int64_t)M * Nc;
-  const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (e >= plane) return;
   const int m = (int)(e / Nc), n = (int)(e % Nc);
   if ((Nc % 4) == 0 && (ldc % 4) == 0) {
@@ -822,6 +821,38 @@ __global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__
       if constexpr (GLU == 1) glu_h[o] = swiglu_fwd((float)glu_g[o], (float)h);
     }
   }
+}
+
+template <int GLU>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ ws, int splits,
+                                                      int M, int Nc, _Float16* __restrict__ C,
+                                                      int64_t ldc,
+                                                      _Float16* __restrict__ glu_g,
+                                                      _Float16* __restrict__ glu_u,
+                                                      _Float16* __restrict__ glu_h) {
+  splitk_reduce_quad<GLU>(ws, splits, M, Nc, C, ldc, glu_g, glu_u, glu_h,
+                          ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4);
+}
+
+// The split-K reduce (no SwiGLU) and a LoRA gradient group in ONE launch: they are independent
+// (the gradients read the dHs^T the GEMM wrote, not its output).  Workgroups [0, cols) are the
+// gradient group's, as its own launch lays them out (same waves, so the same bits); the nred
+// after them reduce quads bid - cols, + nred * blockDim.x, ...  Dispatched after the gradient
+// workgroups, the reduce fills the CUs their last partial round leaves idle.
+template <int CPL>
+__global__ __launch_bounds__(64 * cols_max_waves<CPL>()) void k_splitk_reduce_cols(
+    const float* __restrict__ ws, int splits, int Mc, int Nc, _Float16* __restrict__ C,
+    int64_t ldc, ColsGroup g, int M, int ldt, int r, int nw, int nred) {
+  extern __shared__ float red[];  // [nw][r][16 * CPL + 1]
+  const int bid = (int)blockIdx.x, cols = g.start[g.n];
+  if (bid < cols) {
+    lora_cols_group_block<CPL>(g, M, ldt, r, bid, nw, red);
+    return;
+  }
+  const int64_t quads = ((int64_t)Mc * Nc + 3) / 4;
+  for (int64_t q = (int64_t)(bid - cols) * blockDim.x + threadIdx.x; q < quads;
+       q += (int64_t)nred * blockDim.x)
+    splitk_reduce_quad<0>(ws, splits, Mc, Nc, C, ldc, nullptr, nullptr, nullptr, 4 * q);
 }
 
 static int launch_reduce(const GemmArgs& a, int splits, hipStream_t stream) {
@@ -2493,8 +2524,10 @@ __global__ __launch_bounds__(64 * (4 + PW)) void k_nf4_gemm_ws_pair(GemmPair g) 
   ws_tile<BM, BN, CWM, CWN, BWD, PW, NS, false>(g.p[i], (int)blockIdx.x, (int)blockIdx.y);
 }
 
+// reduce: false leaves the 2 sp planes for the caller's reduce (k_splitk_reduce_cols).
 template <int BM, int BN, int CWM, int CWN, bool BWD, int PW, int NS>
-static int launch_ws_pair(const GemmArgs& a0, const GemmArgs& a1, int sp, hipStream_t stream) {
+static int launch_ws_pair(const GemmArgs& a0, const GemmArgs& a1, int sp, hipStream_t stream,
+                          bool reduce = true) {
   if (sp < 1 || !a0.ws || a0.M != a1.M || a0.Nc != a1.Nc) return MXS_ERR_ARG;
   GemmPair g{};
   g.p[0] = a0;
@@ -2527,7 +2560,7 @@ static int launch_ws_pair(const GemmArgs& a0, const GemmArgs& a1, int sp, hipStr
                      dim3(64 * (4 + PW)), lds, stream, g);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  return launch_reduce(g.p[0], 2 * sp, stream);
+  return reduce ? launch_reduce(g.p[0], 2 * sp, stream) : MXS_OK;
 }
 
 // Two forward projections of one shape over the same input (gate and up, solution/mlp.py:42-43),
@@ -2737,6 +2770,73 @@ static int scratch_address(void** out) {
   }
   *out = p;
   return MXS_OK;
+}
+
+// The two problems of the summed dX pair (mxs_nf4_linear_bwd_dx_hp_pair's checks): MXS_OK,
+// 1 when there is nothing to compute, or an error code.
+static int dx_pair_args(const void* const dy[2], int M, const int N[2], int K,
+                        const void* const packed[2], const void* const absmax8[2],
+                        const float* const code[2], const float* const absmax2[2],
+                        const float* const offset[2], const float* const lora_dhp[2],
+                        int hp_slices, int ldt, const void* const lora_at[2], int r,
+                        const void* const mask[2], float mask_scale, void* const lora_dht[2],
+                        void* dx, void* workspace, GemmArgs p[2]) {
+  if (M < 0 || !dy || !N || !packed || !absmax8 || !code || !absmax2 || !offset || !lora_dhp ||
+      !lora_at)
+    return MXS_ERR_ARG;
+  if (M == 0) return 1;
+  if (!pair_plan_ok(M, N[0], N[1], K)) return MXS_ERR_SIZE;
+  if (!workspace) return MXS_ERR_ARG;
+  for (int i = 0; i < 2; i++) {
+    GemmArgs a{};
+    a.A = static_cast<const _Float16*>(dy[i]);
+    a.lda = N[i];
+    a.packed = static_cast<const uint8_t*>(packed[i]);
+    a.absmax8 = static_cast<const uint8_t*>(absmax8[i]);
+    a.code = code[i];
+    a.absmax2 = absmax2[i];
+    a.offset = offset[i];
+    a.M = M;
+    a.Nc = K;
+    a.Kr = N[i];
+    a.Kw = K;
+    a.lora_hp = lora_dhp[i];
+    a.hp_slices = hp_slices;
+    a.ldt = ldt;
+    a.lora_ht = lora_dht ? static_cast<_Float16*>(lora_dht[i]) : nullptr;
+    a.lora_w = static_cast<const _Float16*>(lora_at[i]);
+    a.r = r;
+    a.mask = mask ? static_cast<const uint8_t*>(mask[i]) : nullptr;
+    a.mask_scale = mask_scale;
+    a.C = static_cast<_Float16*>(dx);
+    a.ldc = K;
+    set_workspace(a, workspace);
+    if (!a.lora_hp) return MXS_ERR_ARG;
+    const int c = check_gemm(true, a);
+    if (c != MXS_OK) return c;
+    p[i] = a;
+  }
+  return MXS_OK;
+}
+
+template <int CPL>
+static int reduce_cols_launch(const GemmArgs& a, int splits, ColsGroup g, int M, int ldt, int r,
+                              hipStream_t stream) {
+  constexpr int WC = 16 * CPL;
+  const int cols = cols_group_layout(g, CPL);
+  const int nw = cols_waves(M, r, CPL, cols_max_waves<CPL>());
+  const size_t lds = (size_t)nw * r * (WC + 1) * sizeof(float);
+  if (lds > (size_t)kColsLds) return MXS_ERR_SIZE;
+  // reduce workgroups: the CUs the gradient workgroups' last partial round leaves idle, at
+  // least a quarter of the CUs
+  const int cus = cu_count() > 0 ? cu_count() : 256;
+  const int tail = cols % cus;
+  int nred = tail == 0 ? cus : cus - tail;
+  if (nred < cus / 4) nred = cus / 4;
+  hipLaunchKernelGGL(k_splitk_reduce_cols<CPL>, dim3(cols + nred), dim3(64 * nw), lds, stream,
+                     a.ws, splits, a.M, a.Nc, a.C, (int64_t)a.ldc, g, M, ldt, r, nw, nred);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MXS_OK : (int)e;
 }
 
 extern "C" {
@@ -3049,43 +3149,50 @@ int mxs_nf4_linear_bwd_dx_hp_pair(const void* const dy[2], int M, const int N[2]
                                   const void* const mask[2], float mask_scale,
                                   void* const lora_dht[2], void* dx, void* workspace,
                                   hipStream_t stream) {
-  if (M < 0 || !dy || !N || !packed || !absmax8 || !code || !absmax2 || !offset || !lora_dhp ||
-      !lora_at)
-    return MXS_ERR_ARG;
-  if (M == 0) return MXS_OK;
-  if (!pair_plan_ok(M, N[0], N[1], K)) return MXS_ERR_SIZE;
-  if (!workspace) return MXS_ERR_ARG;
   GemmArgs p[2];
-  for (int i = 0; i < 2; i++) {
-    GemmArgs a{};
-    a.A = static_cast<const _Float16*>(dy[i]);
-    a.lda = N[i];
-    a.packed = static_cast<const uint8_t*>(packed[i]);
-    a.absmax8 = static_cast<const uint8_t*>(absmax8[i]);
-    a.code = code[i];
-    a.absmax2 = absmax2[i];
-    a.offset = offset[i];
-    a.M = M;
-    a.Nc = K;
-    a.Kr = N[i];
-    a.Kw = K;
-    a.lora_hp = lora_dhp[i];
-    a.hp_slices = hp_slices;
-    a.ldt = ldt;
-    a.lora_ht = lora_dht ? static_cast<_Float16*>(lora_dht[i]) : nullptr;
-    a.lora_w = static_cast<const _Float16*>(lora_at[i]);
-    a.r = r;
-    a.mask = mask ? static_cast<const uint8_t*>(mask[i]) : nullptr;
-    a.mask_scale = mask_scale;
-    a.C = static_cast<_Float16*>(dx);
-    a.ldc = K;
-    set_workspace(a, workspace);
-    if (!a.lora_hp) return MXS_ERR_ARG;
-    const int c = check_gemm(true, a);
-    if (c != MXS_OK) return c == 1 ? MXS_OK : c;
-    p[i] = a;
-  }
+  const int c = dx_pair_args(dy, M, N, K, packed, absmax8, code, absmax2, offset, lora_dhp,
+                             hp_slices, ldt, lora_at, r, mask, mask_scale, lora_dht, dx,
+                             workspace, p);
+  if (c != MXS_OK) return c == 1 ? MXS_OK : c;
   return launch_ws_pair<256, 96, 4, 1, true, 8, 5>(p[0], p[1], kPairSplits, stream);
+}
+
+int mxs_nf4_linear_bwd_dx_hp_pair_grads(
+    const void* const dy[2], int M, const int N[2], int K, const void* const packed[2],
+    const void* const absmax8[2], const float* const code[2], const float* const absmax2[2],
+    const float* const offset[2], const float* const lora_dhp[2], int hp_slices, int ldt,
+    const void* const lora_at[2], int r, const void* const mask[2], float mask_scale,
+    void* const lora_dht[2], const void* const ht[2], const void* x, float* const da[2],
+    float* const db[2], void* dx, void* workspace, hipStream_t stream) {
+  if (!lora_dht || !ht || !x || !da || !db) return MXS_ERR_ARG;
+  GemmArgs p[2];
+  const int c = dx_pair_args(dy, M, N, K, packed, absmax8, code, absmax2, offset, lora_dhp,
+                             hp_slices, ldt, lora_at, r, mask, mask_scale, lora_dht, dx,
+                             workspace, p);
+  if (c == 1) {  // no tokens: dX is empty, dA and dB are empty reductions (zeros)
+    for (int i = 0; i < 2; i++) {
+      const int e = mxs_lora_grads(nullptr, nullptr, ldt, nullptr, nullptr, 0, K, N[i], r,
+                                   nullptr, mask_scale, da[i], db[i], nullptr, stream);
+      if (e != MXS_OK) return e;
+    }
+    return MXS_OK;
+  }
+  if (c != MXS_OK) return c;
+  if (r % 16) return MXS_ERR_SIZE;
+  ColsGroup g{};
+  g.n = 2;
+  const int cpl = cols_cpl(K + N[0]);
+  for (int i = 0; i < 2; i++) {
+    const int e = cols_group_set(g, i, lora_dht[i], ht[i], ldt, x, dy[i], M, K, N[i],
+                                 mask ? mask[i] : nullptr, mask_scale, da[i], db[i]);
+    if (e != MXS_OK) return e;
+    if (cols_cpl(K + N[i]) != cpl) return MXS_ERR_SIZE;
+  }
+  const int e = launch_ws_pair<256, 96, 4, 1, true, 8, 5>(p[0], p[1], kPairSplits, stream, false);
+  if (e != MXS_OK) return e;
+  if (cpl == 8) return reduce_cols_launch<8>(p[0], 2 * kPairSplits, g, M, ldt, r, stream);
+  if (cpl == 4) return reduce_cols_launch<4>(p[0], 2 * kPairSplits, g, M, ldt, r, stream);
+  return reduce_cols_launch<2>(p[0], 2 * kPairSplits, g, M, ldt, r, stream);
 }
 
 // The rotation the grouped forward may apply to its first n_rope problems (attention's q / k).

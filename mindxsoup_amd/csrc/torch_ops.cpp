@@ -901,6 +901,7 @@ Lists3 lora_bwd_group_cuda(TensorList dy, const Tensor& x, const OptTensorList& 
   const bool pair = sum_dx && n == 2 && fin.empty() && par.size() == 2 && want(0, 0) &&
                     want(1, 0) && dhp[0].size(0) == dhp[1].size(0) &&
                     mxs_nf4_linear_bwd_dx_pair_ok(M, o[0].N, o[1].N, K) != 0;
+  bool pair_grads = false;  // the pair's launches computed both projections' dA and dB
   if (pair) {
     const bool wt = want(0, 1) || want(0, 2) || want(1, 1) || want(1, 2);
     std::array<const void*, 2> pdy{}, pk{}, pa8{}, pat{}, pm{};
@@ -925,11 +926,32 @@ Lists3 lora_bwd_group_cuda(TensorList dy, const Tensor& x, const OptTensorList& 
     dxs[0] = at::empty({M, K}, f16);
     const Tensor pws =
         workspace(mxs_nf4_linear_bwd_dx_pair_workspace_bytes(M, Ns[0], Ns[1], K), o[0].x);
-    ok(mxs_nf4_linear_bwd_dx_hp_pair(pdy.data(), M, Ns.data(), K, pk.data(), pa8.data(),
-                                     pc.data(), pa2.data(), po.data(), php.data(),
-                                     (int)dhp[0].size(0), ldt, pat.data(), r, pm.data(), ms,
-                                     pdht.data(), dxs[0].data_ptr(), ptr(pws), st),
-       "mxs_nf4_linear_bwd_dx_hp_pair");
+    if (both.size() == 2 && Ns[0] == Ns[1]) {
+      // every weight gradient wanted: the pair's reduce and the gradients in one launch
+      std::array<const void*, 2> pht{};
+      std::array<float*, 2> pda{}, pdb{};
+      for (size_t i = 0; i < 2; ++i) {
+        das[i] = at::empty({r, K}, f16.dtype(at::kFloat));
+        dbs[i] = at::empty({o[i].N, r}, f16.dtype(at::kFloat));
+        pht[i] = o[i].ht.data_ptr();
+        pda[i] = das[i].data_ptr<float>();
+        pdb[i] = dbs[i].data_ptr<float>();
+      }
+      ok(mxs_nf4_linear_bwd_dx_hp_pair_grads(
+             pdy.data(), M, Ns.data(), K, pk.data(), pa8.data(), pc.data(), pa2.data(),
+             po.data(), php.data(), (int)dhp[0].size(0), ldt, pat.data(), r, pm.data(), ms,
+             pdht.data(), pht.data(), o[0].x.data_ptr(), pda.data(), pdb.data(),
+             dxs[0].data_ptr(), ptr(pws), st),
+         "mxs_nf4_linear_bwd_dx_hp_pair_grads");
+      both.clear();
+      pair_grads = true;
+    } else {
+      ok(mxs_nf4_linear_bwd_dx_hp_pair(pdy.data(), M, Ns.data(), K, pk.data(), pa8.data(),
+                                       pc.data(), pa2.data(), po.data(), php.data(),
+                                       (int)dhp[0].size(0), ldt, pat.data(), r, pm.data(), ms,
+                                       pdht.data(), dxs[0].data_ptr(), ptr(pws), st),
+         "mxs_nf4_linear_bwd_dx_hp_pair");
+    }
   }
   for (size_t i : par) {
     if (pair) break;
@@ -972,7 +994,7 @@ Lists3 lora_bwd_group_cuda(TensorList dy, const Tensor& x, const OptTensorList& 
   }
   for (size_t i : par) {
     const bool wa = want(i, 1), wb = want(i, 2);
-    if (!(wa || wb) || (same && wa && wb)) continue;
+    if (!(wa || wb) || (same && wa && wb) || pair_grads) continue;
     if (wa) das[i] = at::empty({r, K}, f16.dtype(at::kFloat));
     if (wb) dbs[i] = at::empty({o[i].N, r}, f16.dtype(at::kFloat));
     ok(mxs_lora_grads(pend_dht[i].data_ptr(), o[i].ht.data_ptr(), ldt, o[i].x.data_ptr(),

@@ -626,12 +626,9 @@ def bwd_dx_pair_ok(M, N0, N1, K):
     return bool(_lib.lib().mxs_nf4_linear_bwd_dx_pair_ok(M, N0, N1, K))
 
 
-def nf4_linear_bwd_dx_hp_pair(dys, packeds, states, lora_dhps, lora_ats, masks=None,
-                              mask_scale=1.0, want_t=True, ws=None):
-    """(dx, [dht0, dht1]): dX = the sum of nf4_linear_bwd_dx_hp's two input gradients, from ONE
-    split-K launch over both reductions and one reduce (each projection's part is never rounded
-    to fp16 on its own), and each projection's fp16 dHs^T (None unless want_t).  Only where
-    bwd_dx_pair_ok."""
+def _dx_pair_operands(dys, packeds, states, lora_dhps, lora_ats, masks):
+    """The checked operands of the summed dX pair: (dys, M, N0, N1, K, slices, ldt, r, keep bits,
+    device)."""
     masks = masks or [None, None]
     (n0, k), (n1, k1) = states[0].shape, states[1].shape
     dys = [d.contiguous() for d in dys]
@@ -642,7 +639,7 @@ def nf4_linear_bwd_dx_hp_pair(dys, packeds, states, lora_dhps, lora_ats, masks=N
     if not bwd_dx_pair_ok(M, n0, n1, k):
         raise ValueError(f"the pair does not take [{k} -> {n0}], [{k} -> {n1}] at {M} tokens")
     S, ldt, r = lora_dhps[0].shape
-    for hp, at, mk in zip(lora_dhps, lora_ats, masks):
+    for hp, at in zip(lora_dhps, lora_ats):
         if hp.shape != (S, ldt, r) or hp.dtype != torch.float32 or ldt != _ldt(M) or \
                 at.shape != (k, r):
             raise ValueError("lora_dhp [slices, ldt, r] fp32 (one shape) and lora_at [K, r]")
@@ -650,21 +647,64 @@ def nf4_linear_bwd_dx_hp_pair(dys, packeds, states, lora_dhps, lora_ats, masks=N
     dev = dys[0].device
     for pk, st in zip(packeds, states):
         check_nf4_operands(pk, st, dev)
+    return dys, M, n0, n1, k, S, ldt, r, masks, dev
+
+
+def _dx_pair_args(dys, M, n0, n1, k, packeds, states, lora_dhps, S, ldt, lora_ats, r, masks,
+                  mask_scale, dhts):
+    return (_ptr_array(dys), M, _int_array([n0, n1]), k,
+            _ptr_array(packeds), _ptr_array([st.absmax for st in states]),
+            _ptr_array([st.state2.code for st in states]),
+            _ptr_array([st.state2.absmax for st in states]),
+            _ptr_array([st.offset for st in states]),
+            _ptr_array([h.contiguous() for h in lora_dhps]), S, ldt,
+            _ptr_array([a.contiguous() for a in lora_ats]), r,
+            _ptr_array(masks), float(mask_scale), _ptr_array(dhts))
+
+
+def nf4_linear_bwd_dx_hp_pair(dys, packeds, states, lora_dhps, lora_ats, masks=None,
+                              mask_scale=1.0, want_t=True, ws=None):
+    """(dx, [dht0, dht1]): dX = the sum of nf4_linear_bwd_dx_hp's two input gradients, from ONE
+    split-K launch over both reductions and one reduce (each projection's part is never rounded
+    to fp16 on its own), and each projection's fp16 dHs^T (None unless want_t).  Only where
+    bwd_dx_pair_ok."""
+    dys, M, n0, n1, k, S, ldt, r, masks, dev = _dx_pair_operands(dys, packeds, states, lora_dhps,
+                                                                 lora_ats, masks)
     dx = torch.empty((M, k), dtype=torch.float16, device=dev)
     dhts = [torch.empty((r, ldt), dtype=torch.float16, device=dev) if want_t else None
             for _ in range(2)]
     ws = _workspace(int(_lib.lib().mxs_nf4_linear_bwd_dx_pair_workspace_bytes(M, n0, n1, k)),
                     dev, ws)
-    _lib.call("mxs_nf4_linear_bwd_dx_hp_pair", _ptr_array(dys), M, _int_array([n0, n1]), k,
-              _ptr_array(packeds), _ptr_array([st.absmax for st in states]),
-              _ptr_array([st.state2.code for st in states]),
-              _ptr_array([st.state2.absmax for st in states]),
-              _ptr_array([st.offset for st in states]),
-              _ptr_array([h.contiguous() for h in lora_dhps]), S, ldt,
-              _ptr_array([a.contiguous() for a in lora_ats]), r,
-              _ptr_array(masks), float(mask_scale), _ptr_array(dhts),
+    _lib.call("mxs_nf4_linear_bwd_dx_hp_pair",
+              *_dx_pair_args(dys, M, n0, n1, k, packeds, states, lora_dhps, S, ldt, lora_ats, r,
+                             masks, mask_scale, dhts),
               _lib.ptr(dx), _lib.ptr(ws), _lib.stream_of(dev))
     return dx, dhts
+
+
+def nf4_linear_bwd_dx_hp_pair_grads(dys, packeds, states, lora_dhps, lora_ats, hts, x2d,
+                                    masks=None, mask_scale=1.0, ws=None):
+    """(dx, [dht0, dht1], [(dA0, dB0), (dA1, dB1)]): nf4_linear_bwd_dx_hp_pair and then both
+    projections' lora_grads_group from its dHs^T, the shared input x2d [M, K] and their Hs^T
+    (hts), in two launches (the pair GEMM; its reduce and the gradients together); the bits of
+    those two calls."""
+    dys, M, n0, n1, k, S, ldt, r, masks, dev = _dx_pair_operands(dys, packeds, states, lora_dhps,
+                                                                 lora_ats, masks)
+    x2d = x2d.contiguous()
+    if x2d.shape != (M, k) or any(tuple(ht.shape) != (r, ldt) for ht in hts):
+        raise ValueError("x [M, K] and ht [r, ldt] disagree with the pair")
+    dx = torch.empty((M, k), dtype=torch.float16, device=dev)
+    dhts = [torch.empty((r, ldt), dtype=torch.float16, device=dev) for _ in range(2)]
+    da = [torch.empty((r, k), dtype=torch.float32, device=dev) for _ in range(2)]
+    db = [torch.empty((n, r), dtype=torch.float32, device=dev) for n in (n0, n1)]
+    ws = _workspace(int(_lib.lib().mxs_nf4_linear_bwd_dx_pair_workspace_bytes(M, n0, n1, k)),
+                    dev, ws)
+    _lib.call("mxs_nf4_linear_bwd_dx_hp_pair_grads",
+              *_dx_pair_args(dys, M, n0, n1, k, packeds, states, lora_dhps, S, ldt, lora_ats, r,
+                             masks, mask_scale, dhts),
+              _ptr_array([_c(t) for t in hts]), _lib.ptr(x2d), _ptr_array(da), _ptr_array(db),
+              _lib.ptr(dx), _lib.ptr(ws), _lib.stream_of(dev))
+    return dx, dhts, list(zip(da, db))
 
 
 def glu_fused(M, N, K, bwd):

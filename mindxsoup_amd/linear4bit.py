@@ -273,7 +273,8 @@ def lora_backward_group(items, ws=None, sum_dx=False):
     summed launch takes get their sum from that one launch, the fp32 sum rounded once instead
     of each part rounded and added: q, k and v (_sum_takes: one tile loop over their three
     reductions, with every dA / dB in the same launch), gate and up (_pair_takes: split-K
-    planes of both reductions and one reduce)."""
+    planes of both reductions, then one launch for their reduce and, where every weight
+    gradient is wanted, both projections' dA / dB)."""
     n = len(items)
     if sum_dx and _sum_takes(items):
         return _backward_summed(items)
@@ -305,12 +306,22 @@ def lora_backward_group(items, ws=None, sum_dx=False):
     pending = []
     if sum_dx and not fused and _pair_takes(items, pre):
         want_t = [it["wants"][1] or it["wants"][2] for it in items]
-        dx, dhts = kernels.nf4_linear_bwd_dx_hp_pair(
-            [it["dy"] for it in items], [it["packed"] for it in items],
-            [it["state"] for it in items], [p["dhp"] for p in pre], [it["at"] for it in items],
-            [it["keep"] for it in items], items[0]["mask_scale"], want_t=any(want_t), ws=ws)
-        out = [[dx, None, None], [None, None, None]]
-        pending = [(i, dhts[i]) for i in range(2) if want_t[i]]
+        pair_args = ([it["dy"] for it in items], [it["packed"] for it in items],
+                     [it["state"] for it in items], [p["dhp"] for p in pre],
+                     [it["at"] for it in items])
+        if all(it["wants"][1] and it["wants"][2] for it in items) and \
+                items[0]["dy"].shape == items[1]["dy"].shape:
+            # the pair's reduce and both projections' dA / dB in one launch
+            dx, _, grads = kernels.nf4_linear_bwd_dx_hp_pair_grads(
+                *pair_args, [it["ht"] for it in items], items[0]["x2d"],
+                [it["keep"] for it in items], items[0]["mask_scale"], ws=ws)
+            out = [[dx, *grads[0]], [None, *grads[1]]]
+        else:
+            dx, dhts = kernels.nf4_linear_bwd_dx_hp_pair(
+                *pair_args, [it["keep"] for it in items], items[0]["mask_scale"],
+                want_t=any(want_t), ws=ws)
+            out = [[dx, None, None], [None, None, None]]
+            pending = [(i, dhts[i]) for i in range(2) if want_t[i]]
         sum_dx = False  # summed
     for i in range(n):
         if out[i] is not None:

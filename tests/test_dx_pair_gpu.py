@@ -153,3 +153,40 @@ def test_forward_pair_equals_two_launches(cuda, M):
         if p is ps[0]:
             ref = ref + _np(bias[0])
         assert O.max_rel(_np(y), ref) < 1e-2
+
+
+@pytest.mark.parametrize("M", [1024, 300, 37])
+def test_pair_with_gradients_equals_pair_then_grads(cuda, M):
+    """mxs_nf4_linear_bwd_dx_hp_pair_grads (the pair GEMM, then its reduce and both projections'
+    dA / dB in one launch) gives the bits of mxs_nf4_linear_bwd_dx_hp_pair followed by
+    mxs_lora_grads_group: dX, the dHs^T side outputs and the four gradients; the gradients within
+    the north star's 1e-2 of float64 products of the same operands."""
+    from mindxsoup_amd import kernels
+
+    print(f"case dx pair grads M={M}", flush=True)
+    x = torch.randn((M, 1536), device=cuda).half()
+    ps = [_proj(cuda, 8960, 1536, M, 60 + i, x) for i in range(2)]
+    rows = kernels.lora_h_partials_group([x, x], [p["a"] for p in ps], S, [p["keep"] for p in ps],
+                                         1 / (1 - P), [p["b"] for p in ps])
+    hts = [kernels.nf4_linear_fwd_hp(x, p["packed"], p["st"], r[0], p["b"])[1]
+           for p, r in zip(ps, rows)]
+    dhps = [kernels.lora_dh_partials(p["dy"], p["b"].t().contiguous(), S) for p in ps]
+    ats = [p["a"].t().contiguous() for p in ps]
+    args = ([p["dy"] for p in ps], [p["packed"] for p in ps], [p["st"] for p in ps], dhps, ats)
+    keeps = [p["keep"] for p in ps]
+    dx, dhts, grads = kernels.nf4_linear_bwd_dx_hp_pair_grads(*args, hts, x, keeps, 1 / (1 - P))
+    dx1, dhts1 = kernels.nf4_linear_bwd_dx_hp_pair(*args, keeps, 1 / (1 - P))
+    grads1 = kernels.lora_grads_group(dhts1, hts, [x, x], [p["dy"] for p in ps], keeps,
+                                      1 / (1 - P))
+    torch.cuda.synchronize()
+    assert torch.equal(dx, dx1)
+    for t, t1 in zip(dhts, dhts1):
+        assert torch.equal(t, t1)
+    for (da, db), (da1, db1) in zip(grads, grads1):
+        assert torch.equal(da, da1) and torch.equal(db, db1)
+    for p, (da, db), dht, ht in zip(ps, grads, dhts, hts):
+        xk = O.dropout_fp16(_np(x).astype(np.float16), p["keep"].cpu().numpy(), P)
+        ref_a = _np(dht[:, :M]).astype(np.float64) @ xk.astype(np.float64)
+        ref_b = _np(p["dy"]).astype(np.float64).T @ _np(ht[:, :M]).astype(np.float64).T
+        assert O.max_rel(_np(da), ref_a) < 1e-2
+        assert O.max_rel(_np(db), ref_b) < 1e-2
