@@ -235,9 +235,11 @@ int mxs_nf4_linear_bwd_dx_hp_pair_grads(
  * solution/mlp.py:42-43, each NF4LinearFunction.forward of solution/linear4bit.py:47-49 with
  * peft's LoRA branch) in ONE launch: y[i] and lora_ht[i] as mxs_nf4_linear_fwd_hp computes them
  * (the same bits), arrays of the per-projection arguments (bias and lora_ht may be NULL, or any
- * entry); the two share M, K, r, ldt and hp_slices.  Grid z selects the projection, so their
- * tiles share the GPU's rounds: at 1024 tokens 2 x 224 tiles of 256 x 160 take 1.75 rounds of
- * 256 CUs, where two launches take one round each.  Only where mxs_nf4_linear_fwd_pair_ok(M,
+ * entry); the two share M, K, r, ldt and hp_slices.  Their tiles share the GPU's rounds: at
+ * 1024 tokens 2 x 224 tiles of 256 x 160 would take 1.75 rounds of 256 CUs, so where it fills
+ * the CUs better the launch cuts the columns into 256 x 160 tiles and narrower 256 x 128 ones
+ * (at 1024 tokens: 192 + 320 tiles, each CU running one of each or two narrow ones).  Only
+ * where mxs_nf4_linear_fwd_pair_ok(M,
  * N[0], N[1], K) is 1 (both plan the unsplit 256 x 160 kernel: N[0] == N[1] >= 4096), else
  * MXS_ERR_SIZE. */
 int mxs_nf4_linear_fwd_hp_pair(const void* x, int M, int K, const int N[2],

@@ -18,8 +18,11 @@
 // epilogue stores fp16.  With split-K (gridDim.z > 1) each split writes fp32 partials and
 // k_splitk_reduce sums them (split 0 carries bias and LoRA).
 #include <atomic>
+#include <functional>
 #include <mutex>
+#include <queue>
 #include <type_traits>
+#include <vector>
 
 #include "common.h"
 #include "lora_cols.h"
@@ -2598,6 +2601,131 @@ static int launch_ws_fwd_pair(const GemmArgs& a0, const GemmArgs& a1, hipStream_
   return e == hipSuccess ? MXS_OK : (int)e;
 }
 
+// The forward pair with two tile widths in ONE launch, so that the CUs end together: 2 x 224
+// tiles of 256x160 at 1024 tokens take 1.75 rounds of 256 CUs, i.e. two tile times with 64 CUs
+// idle in the second.  Each projection's columns split at ncut (a multiple of 160): [0, ncut)
+// in 256x160 tiles (w[i]), [ncut, N) in 256x128 tiles (n[i]: the same problem viewed from
+// column ncut, its weight rows, scales, bias and lora_B rows offset, no dHs^T writes).  The
+// wide tiles come first in the grid, one per CU; the narrow ones (0.86 of a wide tile's time,
+// measured) fill the rest, so that a CU runs one of each or two narrow ones.  Every output
+// element is computed as either tile computes it (the same K-steps, MFMAs and epilogue), so the
+// results are the bits of the one-width launch.
+struct GemmMixed {
+  GemmArgs w[2], n[2];
+  int gxw, gxn, gy, nwide;
+};
+
+template <int NS>
+__global__ __launch_bounds__(64 * 8) void k_nf4_gemm_ws_pair_mixed(GemmMixed g) {
+  const int bid = (int)blockIdx.x;
+  if (bid < g.nwide) {
+    const int per = g.gxw * g.gy, i = bid / per, l = bid % per;
+    ws_tile<256, 160, 4, 1, false, 4, NS, false>(g.w[i], l % g.gxw, l / g.gxw);
+  } else {
+    const int b = bid - g.nwide, per = g.gxn * g.gy, i = b / per, l = b % per;
+    ws_tile<256, 128, 2, 2, false, 4, NS, false>(g.n[i], l % g.gxn, l / g.gxn);
+  }
+}
+
+// Time of a narrow (256x128) tile against a wide (256x160) one, measured at one round
+// (1536-long reduction: 25.3 against 29.2 us).
+constexpr double kNarrowTile = 0.86;
+
+// Makespan, in wide-tile times, of W wide then Nn narrow tiles taken in that order by `cus`
+// CUs, each tile by the CU that frees first.
+static double list_makespan(int W, int Nn, int cus) {
+  std::priority_queue<double, std::vector<double>, std::greater<double>> free_at(
+      std::greater<double>(), std::vector<double>(cus, 0.0));
+  double end = 0.0;
+  for (int t = 0; t < W + Nn; t++) {
+    const double f = free_at.top() + (t < W ? 1.0 : kNarrowTile);
+    free_at.pop();
+    free_at.push(f);
+    end = f > end ? f : end;
+  }
+  return end;
+}
+
+// The column split of the mixed forward pair for two problems [K -> N] at M tokens (0: the
+// one-width launch is as fast).  ncut: a multiple of 160 that leaves a multiple of 128, and a
+// whole number of second-level scale groups (256 blocks of 64) before it.
+static int fwd_pair_mixed_cut(int M, int N, int K) {
+  const int cus = cu_count();
+  if (cus <= 0 || N % 32 || (K % 64)) return 0;
+  static std::mutex mu;
+  static int key[3] = {-1, -1, -1}, cached = 0, cached_cus = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  if (key[0] == M && key[1] == N && key[2] == K && cached_cus == cus) return cached;
+  const int gy = (M + 255) / 256;
+  const double plain = list_makespan(2 * gy * ((N + 159) / 160), 0, cus);
+  double best = plain * 0.97;  // worth a second kernel only where it gains
+  int cut = 0;
+  for (int a = 1; 160 * a < N; a++) {
+    const int rest = N - 160 * a;
+    if (rest % 128 || ((int64_t)160 * a * K / 64) % 256) continue;
+    const double t = list_makespan(2 * gy * a, 2 * gy * (rest / 128), cus);
+    if (t < best) {
+      best = t;
+      cut = 160 * a;
+    }
+  }
+  key[0] = M, key[1] = N, key[2] = K, cached = cut, cached_cus = cus;
+  return cut;
+}
+
+static int launch_ws_fwd_pair_mixed(const GemmArgs& a0, const GemmArgs& a1, int ncut,
+                                    hipStream_t stream) {
+  constexpr int NS = 4;
+  if (a0.M != a1.M || a0.Nc != a1.Nc || a0.Kr != a1.Kr || ncut <= 0 || ncut >= a0.Nc ||
+      ncut % 160 || (a0.Nc - ncut) % 128)
+    return MXS_ERR_ARG;
+  GemmMixed g{};
+  const GemmArgs* src[2] = {&a0, &a1};
+  for (int i = 0; i < 2; i++) {
+    GemmArgs a = *src[i];
+    if ((int64_t)a.Nc * a.Kr >= (int64_t(1) << 32) || (int64_t)256 * a.lda * 2 >= (int64_t(1) << 32) ||
+        a.glu || a.cols_blocks > 0 || a.rope_cos)
+      return MXS_ERR_SIZE;
+    const int64_t blk0 = (int64_t)ncut * a.Kw / 64;  // first scale block of the narrow view
+    if (blk0 % 256) return MXS_ERR_SIZE;
+    a.steps_per_split = a.Kr / kBK;
+    a.zf = 0;
+    a.unsplit = 0;
+    GemmArgs w = a;
+    w.Nc = ncut;  // the wide tiles' columns: [0, ncut) of the same buffers
+    GemmArgs n = a;
+    n.Nc = a.Nc - ncut;
+    n.packed = a.packed + (int64_t)ncut * (a.Kw / 2);
+    n.absmax8 = a.absmax8 + blk0;
+    n.absmax2 = a.absmax2 + blk0 / 256;
+    if (a.bias) n.bias = a.bias + ncut;
+    if (a.lora_w) n.lora_w = a.lora_w + (int64_t)ncut * a.r;
+    n.lora_ht = nullptr;  // the wide tiles of column 0 write dHs^T
+    n.C = a.C + ncut;
+    g.w[i] = w;
+    g.n[i] = n;
+  }
+  g.gxw = ncut / 160;
+  g.gxn = (a0.Nc - ncut) / 128;
+  g.gy = (a0.M + 255) / 256;
+  g.nwide = 2 * g.gxw * g.gy;
+  const int total = g.nwide + 2 * g.gxn * g.gy;
+  const size_t lds = (size_t)(ws_lds_halfs<256, 160, false>() > ws_lds_halfs<256, 128, false>()
+                                  ? ws_lds_halfs<256, 160, false>()
+                                  : ws_lds_halfs<256, 128, false>()) *
+                     sizeof(_Float16);
+  static bool lds_set = false;  // idempotent attribute; a benign race between threads
+  if (!lds_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_nf4_gemm_ws_pair_mixed<NS>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return (int)e;
+    lds_set = true;
+  }
+  hipLaunchKernelGGL((k_nf4_gemm_ws_pair_mixed<NS>), dim3(total), dim3(64 * 8), lds, stream, g);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? MXS_OK : (int)e;
+}
+
 // The forward pair takes two problems [K -> N] that each plan the unsplit 256x160 kernel.
 static bool fwd_pair_plan_ok(int M, int N0, int N1, int K) {
   if (M <= 0 || N0 != N1 || K <= 0 || K % kBK) return false;
@@ -3129,6 +3257,8 @@ int mxs_nf4_linear_fwd_hp_pair(const void* x, int M, int K, const int N[2],
     if (c != MXS_OK) return c == 1 ? MXS_OK : c;
     p[i] = a;
   }
+  const int ncut = fwd_pair_mixed_cut(M, N[0], K);
+  if (ncut > 0) return launch_ws_fwd_pair_mixed(p[0], p[1], ncut, stream);
   return launch_ws_fwd_pair<256, 160, 4, 1, 4, 4>(p[0], p[1], stream);
 }
 

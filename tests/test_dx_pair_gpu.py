@@ -123,11 +123,13 @@ def test_group_backward_sums(cuda):
 
 
 
-@pytest.mark.parametrize("M", [1024, 300])
+@pytest.mark.parametrize("M", [1024, 300, 768, 900])
 def test_forward_pair_equals_two_launches(cuda, M):
-    """gate and up forward in one launch (mxs_nf4_linear_fwd_hp_pair, grid z selects the
-    projection) give the bits of two nf4_linear_fwd_hp launches, y and the transposed LoRA
-    operand, with a bias and without; within the north star's 1e-2 of the oracle."""
+    """gate and up forward in one launch (mxs_nf4_linear_fwd_hp_pair) give the bits of two
+    nf4_linear_fwd_hp launches, y and the transposed LoRA operand, with a bias and without;
+    within the north star's 1e-2 of the oracle.  300 tokens: one width (grid z selects the
+    projection); 1024 and 900 (a partial last row band): 256x160 tiles up to column 3840 and
+    256x128 tiles past it in one launch; 768: the split at column 640."""
     from mindxsoup_amd import kernels
 
     print(f"case fwd pair M={M}", flush=True)
