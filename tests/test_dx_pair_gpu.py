@@ -192,3 +192,36 @@ def test_pair_with_gradients_equals_pair_then_grads(cuda, M):
         ref_b = _np(p["dy"]).astype(np.float64).T @ _np(ht[:, :M]).astype(np.float64).T
         assert O.max_rel(_np(da), ref_a) < 1e-2
         assert O.max_rel(_np(db), ref_b) < 1e-2
+
+
+def test_pair_with_gradients_without_masks_and_refused_shapes(cuda):
+    """No dropout (masks None): the pair with gradients still gives the bits of the pair then the
+    gradient group; two projections whose gradients would take different columns per lane
+    (8960 and 4096 outputs over 1536 inputs) are refused by the library, not computed."""
+    from mindxsoup_amd import kernels
+
+    M = 512
+    x = torch.randn((M, 1536), device=cuda).half()
+    ps = [_proj(cuda, 8960, 1536, M, 70 + i, x) for i in range(2)]
+    rows = kernels.lora_h_partials_group([x, x], [p["a"] for p in ps], S, None, 1.0,
+                                         [p["b"] for p in ps])
+    hts = [kernels.nf4_linear_fwd_hp(x, p["packed"], p["st"], r[0], p["b"])[1]
+           for p, r in zip(ps, rows)]
+    dhps = [kernels.lora_dh_partials(p["dy"], p["b"].t().contiguous(), S) for p in ps]
+    args = ([p["dy"] for p in ps], [p["packed"] for p in ps], [p["st"] for p in ps], dhps,
+            [p["a"].t().contiguous() for p in ps])
+    dx, dhts, grads = kernels.nf4_linear_bwd_dx_hp_pair_grads(*args, hts, x)
+    dx1, dhts1 = kernels.nf4_linear_bwd_dx_hp_pair(*args)
+    grads1 = kernels.lora_grads_group(dhts1, hts, [x, x], [p["dy"] for p in ps])
+    torch.cuda.synchronize()
+    assert torch.equal(dx, dx1)
+    for (da, db), (da1, db1) in zip(grads, grads1):
+        assert torch.equal(da, da1) and torch.equal(db, db1)
+    q = [ps[0], _proj(cuda, 4096, 1536, M, 72, x)]
+    if kernels.bwd_dx_pair_ok(M, 8960, 4096, 1536):
+        dhq = [kernels.lora_dh_partials(p["dy"], p["b"].t().contiguous(), S) for p in q]
+        htq = [torch.zeros_like(hts[0]) for _ in q]
+        with pytest.raises(RuntimeError):
+            kernels.nf4_linear_bwd_dx_hp_pair_grads(
+                [p["dy"] for p in q], [p["packed"] for p in q], [p["st"] for p in q], dhq,
+                [p["a"].t().contiguous() for p in q], htq, x)
