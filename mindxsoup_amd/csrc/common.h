@@ -39,6 +39,23 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, h);
 }
 
+// fp16 of an fp32 value computed as it is: a product rounded to fp32 and then to fp16, as the
+// reference's kernels compute in fp32 and cast.  Left alone the compiler contracts a multiply
+// and the conversion into one mixed-precision FMA (whatever the contract pragma says), which
+// rounds the exact product once: one fp16 ulp off where the fp32 product lands on an fp16
+// rounding tie.  The empty asm keeps the fp32 value.
+__device__ __forceinline__ _Float16 f16_of(float p) {
+  __asm__("" : "+v"(p));
+  return (_Float16)p;
+}
+
+// fp16(fp32(x) * s), the reference's dropout (solution/dropout.py:33-35).  Rounded once instead,
+// hundreds of the 63 488 finite inputs come out one ulp off at some rates (over 700 at p = 0.04;
+// none at p = 0.05).
+__device__ __forceinline__ _Float16 scale_round2(_Float16 x, float s) {
+  return f16_of((float)x * s);
+}
+
 // Decoded block scale of the double-quantized absmax: code[q8] * absmax2 + offset, one fused
 // multiply-add in fp32 (the contraction Triton applies to the reference kernel).
 __device__ __forceinline__ float nested_scale(float code_q8, float absmax2, float offset) {

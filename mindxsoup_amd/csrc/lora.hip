@@ -38,10 +38,14 @@ template <int TB>
 constexpr int rows_chunks_in_flight() { return TB == 1 ? 4 : 3; }
 
 // 8 consecutive values through the dropout: bit e of `keep` set keeps value e (times scale).
+// R2: each product rounded to fp32 and then to fp16 (scale_round2), else in one mixed-precision
+// FMA (where that is the same: round_once_exact).
+template <bool R2>
 __device__ __forceinline__ half8_t drop8(half8_t x, uint32_t keep, float scale) {
 #pragma unroll
   for (int e = 0; e < 8; e++)
-    x[e] = ((keep >> e) & 1u) ? (_Float16)((float)x[e] * scale) : (_Float16)0.0f;
+    x[e] = ((keep >> e) & 1u) ? (R2 ? scale_round2(x[e], scale) : (_Float16)((float)x[e] * scale))
+                              : (_Float16)0.0f;
   return x;
 }
 
@@ -50,6 +54,7 @@ struct RowsArgs {
   int M, K;
   const uint8_t* mask;    // keep bits of [M, K] (keep_row_bytes(K) per row) or null
   float mscale;
+  int round2;             // dropout rounded twice (round_once_exact(mscale) is false)
   const _Float16* R;      // [r, K] row-major
   int r, ldt;
   float s;
@@ -90,8 +95,9 @@ __device__ __forceinline__ half8_t f32x8_to_f16(const float* p) {
 // a wave loads feeds TB multiplies, so TB = 2 halves the re-reads of R (every row block reads
 // all of its slice of R).  Wave w takes chunks c_beg + w, c_beg + w + nw, ... and adds them in
 // that order whatever TB, so TB does not change the bits.  RB: the accumulator blocks compiled in
-// (1 for r = 16, kMaxRB for any r up to 128).  MASK: a.mask is set (the dropout applies).
-template <bool W32, int TB, int RB, bool MASK>
+// (1 for r = 16, kMaxRB for any r up to 128).  MASK: a.mask is set (the dropout applies).  R2:
+// the dropout rounds twice (a kernel of its own, so that the other keeps its registers).
+template <bool W32, int TB, int RB, bool MASK, bool R2>
 __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice, int slices,
                                            int nw, int wg, int n_wg, float* red) {
   constexpr int CIF = rows_chunks_in_flight<TB>();
@@ -159,7 +165,7 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
 #pragma unroll
       for (int t = 0; t < TB; t++) {
         half8_t v = x[u][t];
-        if constexpr (MASK) v = drop8(v, kb[u][t], a.mscale);
+        if constexpr (MASK) v = drop8<R2>(v, kb[u][t], a.mscale);
         x[u][t] = row_ok[t] ? v : (half8_t){};
       }
 #pragma unroll
@@ -230,16 +236,16 @@ __device__ __forceinline__ void rows_block(const RowsArgs& a, int rb, int slice,
   }
 }
 
-template <int TB, int RB>
+template <int TB, int RB, bool R2>
 __global__ __launch_bounds__(1024) void k_lora_rows(RowsArgs a) {
   extern __shared__ float red[];  // [waves][16 * TB][r + 1]
   const int wg = (int)(blockIdx.y * gridDim.x + blockIdx.x), n_wg = (int)(gridDim.x * gridDim.y);
   if (a.mask)
-    rows_block<false, TB, RB, true>(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y,
-                                    (int)blockDim.x >> 6, wg, n_wg, red);
+    rows_block<false, TB, RB, true, R2>(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y,
+                                        (int)blockDim.x >> 6, wg, n_wg, red);
   else
-    rows_block<false, TB, RB, false>(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y,
-                                     (int)blockDim.x >> 6, wg, n_wg, red);
+    rows_block<false, TB, RB, false, false>(a, (int)blockIdx.x, (int)blockIdx.y, (int)gridDim.y,
+                                            (int)blockDim.x >> 6, wg, n_wg, red);
 }
 
 // Several rows problems over the same tokens in one launch (the q/k/v or gate/up projections
@@ -253,7 +259,7 @@ struct RowsGroup {
   int n;
 };
 
-template <bool W32, int TB, int RB>
+template <bool W32, int TB, int RB, bool R2>
 __global__ __launch_bounds__(1024) void k_lora_rows_group(RowsGroup g) {
   extern __shared__ float red[];  // [waves][16 * TB][r + 1]
   const int bid = (int)blockIdx.x;
@@ -261,10 +267,10 @@ __global__ __launch_bounds__(1024) void k_lora_rows_group(RowsGroup g) {
   while (i + 1 < g.n && bid >= g.start[i + 1]) i++;
   const int local = bid - g.start[i];
   if (g.p[i].mask)
-    rows_block<W32, TB, RB, true>(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i],
+    rows_block<W32, TB, RB, true, R2>(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i],
                                   g.nw[i], local, g.start[i + 1] - g.start[i], red);
   else
-    rows_block<W32, TB, RB, false>(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i],
+    rows_block<W32, TB, RB, false, false>(g.p[i], local % g.rbs[i], local / g.rbs[i], g.slices[i],
                                    g.nw[i], local, g.start[i + 1] - g.start[i], red);
 }
 
@@ -410,6 +416,28 @@ static int rows_tb(int r, int64_t workgroups_at_two, int64_t waves_at_two) {
   return r == 16 && workgroups_at_two >= 256 && waves_at_two >= 16 * 256 ? 2 : 1;
 }
 
+// The row-product kernel with the dropout rounding the launch needs: twice (R2) where some
+// problem has a keep mask and rounding once is not the same for its scale.
+static bool rows_round2(const RowsArgs& a) { return a.mask && !round_once_exact(a.mscale); }
+
+template <int TB, int RB>
+static void launch_rows_k(bool r2, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                          const RowsArgs& a) {
+  if (r2)
+    hipLaunchKernelGGL((k_lora_rows<TB, RB, true>), grid, block, lds, stream, a);
+  else
+    hipLaunchKernelGGL((k_lora_rows<TB, RB, false>), grid, block, lds, stream, a);
+}
+
+template <bool W32, int TB, int RB>
+static void launch_rows_group_k(bool r2, dim3 grid, dim3 block, size_t lds, hipStream_t stream,
+                                const RowsGroup& g) {
+  if (r2)
+    hipLaunchKernelGGL((k_lora_rows_group<W32, TB, RB, true>), grid, block, lds, stream, g);
+  else
+    hipLaunchKernelGGL((k_lora_rows_group<W32, TB, RB, false>), grid, block, lds, stream, g);
+}
+
 static int rows_launch(RowsArgs a, void* workspace, hipStream_t stream) {
   int slices, nw;
   rows_plan(a, workspace != nullptr, &slices, &nw);
@@ -418,12 +446,13 @@ static int rows_launch(RowsArgs a, void* workspace, hipStream_t stream) {
   const int tb = rows_tb(a.r, at_two, at_two * nw);
   const size_t lds = (size_t)nw * 16 * tb * (a.r + 1) * sizeof(float);
   const dim3 grid((a.ldt + 16 * tb - 1) / (16 * tb), slices);
+  const bool r2 = rows_round2(a);
   if (a.r != 16)
-    hipLaunchKernelGGL((k_lora_rows<1, kMaxRB>), grid, dim3(64 * nw), lds, stream, a);
+    launch_rows_k<1, kMaxRB>(r2, grid, dim3(64 * nw), lds, stream, a);
   else if (tb == 2)
-    hipLaunchKernelGGL((k_lora_rows<2, 1>), grid, dim3(64 * nw), lds, stream, a);
+    launch_rows_k<2, 1>(r2, grid, dim3(64 * nw), lds, stream, a);
   else
-    hipLaunchKernelGGL((k_lora_rows<1, 1>), grid, dim3(64 * nw), lds, stream, a);
+    launch_rows_k<1, 1>(r2, grid, dim3(64 * nw), lds, stream, a);
   if (slices > 1 && !a.partial_out)
     hipLaunchKernelGGL(k_lora_rows_finish, dim3((a.ldt + 63) / 64), dim3(64), 0, stream, a,
                        slices);
@@ -458,20 +487,22 @@ static int rows_group_launch(const RowsArgs* probs, int n, hipStream_t stream, b
   g.start[n] = total;
   const size_t lds = (size_t)nw_max * 16 * tb * (r + 1) * sizeof(float);
   const dim3 grid(total), block(64 * nw_max);
+  bool r2 = false;
+  for (int i = 0; i < n; i++) r2 = r2 || rows_round2(g.p[i]);
   if (w32) {
     if (r != 16)
-      hipLaunchKernelGGL((k_lora_rows_group<true, 1, kMaxRB>), grid, block, lds, stream, g);
+      launch_rows_group_k<true, 1, kMaxRB>(r2, grid, block, lds, stream, g);
     else if (tb == 2)
-      hipLaunchKernelGGL((k_lora_rows_group<true, 2, 1>), grid, block, lds, stream, g);
+      launch_rows_group_k<true, 2, 1>(r2, grid, block, lds, stream, g);
     else
-      hipLaunchKernelGGL((k_lora_rows_group<true, 1, 1>), grid, block, lds, stream, g);
+      launch_rows_group_k<true, 1, 1>(r2, grid, block, lds, stream, g);
   } else {
     if (r != 16)
-      hipLaunchKernelGGL((k_lora_rows_group<false, 1, kMaxRB>), grid, block, lds, stream, g);
+      launch_rows_group_k<false, 1, kMaxRB>(r2, grid, block, lds, stream, g);
     else if (tb == 2)
-      hipLaunchKernelGGL((k_lora_rows_group<false, 2, 1>), grid, block, lds, stream, g);
+      launch_rows_group_k<false, 2, 1>(r2, grid, block, lds, stream, g);
     else
-      hipLaunchKernelGGL((k_lora_rows_group<false, 1, 1>), grid, block, lds, stream, g);
+      launch_rows_group_k<false, 1, 1>(r2, grid, block, lds, stream, g);
   }
   return check_launch();
 }
@@ -819,6 +850,7 @@ int mxs_lora_grads(const void* dht, const void* ht, int ldt, const void* x, cons
   pa.Q = static_cast<const _Float16*>(x);
   pa.mask = static_cast<const uint8_t*>(mask);
   pa.mscale = mask_scale;
+  pa.round2 = mask && !round_once_exact(mask_scale);
   pa.Nq = K;
   pa.out = da;
   pa.out_rn = 1;

@@ -3,6 +3,10 @@
 // (nf4_gemm.hip), which then computes dX and both gradients in one launch.
 #pragma once
 
+#include <string.h>
+
+#include <mutex>
+
 #include "common.h"
 #include "mxs_nf4.h"
 
@@ -30,11 +34,41 @@ inline int cols_waves(int M, int r, int cpl, int max_waves) {
   return w;
 }
 
+// Whether rounding the exact product x * s once to fp16 gives the reference's dropout,
+// fp16(fp32(x) * s), for every finite fp16 x (so at p = 0.05, not at p = 0.04).  Where it does,
+// the kernels let the compiler fuse the multiply and the conversion (one mixed-precision FMA);
+// where it does not they round twice (scale_round2), at a few more instructions and registers.
+// Checked on the host once per scale (63 488 products), the last few scales kept.
+inline bool round_once_exact(float s) {
+  static std::mutex mu;
+  static float seen[4];
+  static bool exact[4];
+  static int n = 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < n; i++)
+    if (memcmp(&seen[i], &s, sizeof s) == 0) return exact[i];
+  bool ok = true;
+  for (uint32_t b = 0; b < 65536 && ok; b++) {
+    const uint16_t bits = (uint16_t)b;
+    _Float16 x;
+    memcpy(&x, &bits, sizeof x);
+    if (!__builtin_isfinite((float)x)) continue;
+    const _Float16 twice = (_Float16)((float)x * s);
+    const _Float16 once = (_Float16)((double)x * (double)s);  // the product is exact in double
+    ok = memcmp(&twice, &once, sizeof once) == 0;
+  }
+  const int slot = n < 4 ? n++ : 3;
+  seen[slot] = s;
+  exact[slot] = ok;
+  return ok;
+}
+
 struct ColsProblem {
   const _Float16* PT;     // [r, ldt] (transposed LoRA activations, zeros past M)
   const _Float16* Q;      // [M, Nq] row-major
   const uint8_t* mask;    // keep bits of [M, Nq] (keep_row_bytes(Nq) per row) or null
   float mscale;
+  int round2;             // dropout rounded twice (round_once_exact(mscale) is false)
   int Nq;
   float* out;             // [r, Nq] (out_rn) or [Nq, r]
   int out_rn;
@@ -50,8 +84,10 @@ template <> struct ColsVec<8> { typedef u32x4 T; };
 // blockDim.x / 64) take 32-token steps in turn and add their accumulators in LDS (`red`,
 // [nw][r][16*CPL + 1] floats) in wave order; further waves only help store.  Every thread of
 // the workgroup calls it (it synchronizes the workgroup once).  MASK: the problem has a keep
-// mask (uniform over the workgroup).
-template <int CPL, bool MASK>
+// mask (uniform over the workgroup).  R2: the dropout's product is rounded to fp32 and then to
+// fp16 (scale_round2), else in one mixed-precision FMA (where that is the same:
+// round_once_exact).
+template <int CPL, bool MASK, bool R2 = false>
 __device__ __forceinline__ void lora_cols_body(const ColsProblem& a, int nb, int M, int ldt,
                                                int r, int nw, float* red) {
   typedef typename ColsVec<CPL>::T VT;
@@ -105,8 +141,10 @@ __device__ __forceinline__ void lora_cols_body(const ColsProblem& a, int nb, int
           if constexpr (MASK) {
 #pragma unroll
             for (int c = 0; c < CPL; c++)
-              hv[e][c] = ((mks[u][e] >> (kshift + c)) & 1u) ? (_Float16)((float)hv[e][c] * a.mscale)
-                                                             : (_Float16)0.0f;
+              hv[e][c] = ((mks[u][e] >> (kshift + c)) & 1u)
+                             ? (R2 ? scale_round2(hv[e][c], a.mscale)
+                                   : (_Float16)((float)hv[e][c] * a.mscale))
+                             : (_Float16)0.0f;
           }
         }
 #pragma unroll
@@ -143,8 +181,9 @@ __device__ __forceinline__ void lora_cols_block(const ColsProblem& p0, const Col
   const bool second = block >= cb0;
   const ColsProblem& a = second ? p1 : p0;
   const int nb = (second ? block - cb0 : block) * 16 * CPL;
-  if (a.mask) lora_cols_body<CPL, true>(a, nb, M, ldt, r, nw, red);
-  else lora_cols_body<CPL, false>(a, nb, M, ldt, r, nw, red);
+  if (!a.mask) lora_cols_body<CPL, false>(a, nb, M, ldt, r, nw, red);
+  else if (a.round2) lora_cols_body<CPL, true, true>(a, nb, M, ldt, r, nw, red);
+  else lora_cols_body<CPL, true, false>(a, nb, M, ldt, r, nw, red);
 }
 
 // dA / dB of several projections in one launch (gate's and up's arrive together): pair i owns
@@ -175,6 +214,7 @@ inline int cols_group_set(ColsGroup& g, int i, const void* dht, const void* ht, 
   pa.Q = static_cast<const _Float16*>(x);
   pa.mask = static_cast<const uint8_t*>(mask);
   pa.mscale = mask_scale;
+  pa.round2 = mask && !round_once_exact(mask_scale);
   pa.Nq = K;
   pa.out = da;
   pa.out_rn = 1;
@@ -183,6 +223,7 @@ inline int cols_group_set(ColsGroup& g, int i, const void* dht, const void* ht, 
   pb.Q = static_cast<const _Float16*>(dy);
   pb.mask = nullptr;
   pb.mscale = 1.0f;
+  pb.round2 = 0;
   pb.Nq = N;
   pb.out = db;
   pb.out_rn = 0;

@@ -2789,6 +2789,7 @@ static int dx_grads_args(const void* dy, int M, int N, int K, const void* packed
   pa.Q = static_cast<const _Float16*>(x);
   pa.mask = static_cast<const uint8_t*>(mask);
   pa.mscale = mask_scale;
+  pa.round2 = mask && !round_once_exact(mask_scale);
   pa.Nq = K;
   pa.out = da;
   pa.out_rn = 1;
@@ -2796,6 +2797,7 @@ static int dx_grads_args(const void* dy, int M, int N, int K, const void* packed
   pb.PT = static_cast<const _Float16*>(ht);
   pb.Q = static_cast<const _Float16*>(dy);
   pb.mscale = 1.0f;
+  pb.round2 = 0;
   pb.Nq = N;
   pb.out = db;
   pb.out_rn = 0;

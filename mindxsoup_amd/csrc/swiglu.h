@@ -1,6 +1,6 @@
 // SwiGLU of the fp16 MLP (solution/silu_mul.py:26-44): values are computed in fp32 from the
 // fp16 inputs and rounded to fp16 once, in the kernel's order, with no fused multiply-adds
-// (the contract pragma).  sigmoid(g) = 1 / (1 + exp(-g)) uses the hardware's exp2 and
+// (the contract pragma; the last product is kept in fp32 before its fp16 cast, f16_of).  sigmoid(g) = 1 / (1 + exp(-g)) uses the hardware's exp2 and
 // reciprocal (v_exp_f32 on log2(e) * x, v_rcp_f32: each within about 1 ulp), the class of
 // approximation the reference's tl.sigmoid compiles to (approximate exp2 and division).  An
 // accurate expf and an IEEE division take about four times the vector instructions (forward
@@ -24,7 +24,7 @@ __device__ __forceinline__ _Float16 swiglu_fwd(float g, float u) {
 #pragma clang fp contract(off)
   const float s = sigmoid_hw(g);
   const float silu = g * s;
-  return (_Float16)(u * silu);
+  return f16_of(u * silu);
 }
 
 // For the incoming d(out) = dh: d(gate) = fp16((dh * up) * (s + silu * (1 - s))),
@@ -34,8 +34,8 @@ __device__ __forceinline__ void swiglu_bwd(float dh, float g, float u, _Float16&
 #pragma clang fp contract(off)
   const float s = sigmoid_hw(g);
   const float silu = g * s;
-  d_gate = (_Float16)((dh * u) * (s + silu * (1.0f - s)));
-  d_up = (_Float16)(dh * silu);
+  d_gate = f16_of((dh * u) * (s + silu * (1.0f - s)));
+  d_up = f16_of(dh * silu);
 }
 
 }  // namespace mxs

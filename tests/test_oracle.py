@@ -520,3 +520,28 @@ def test_qkv_rope_oracle_against_transformers_and_properties():
     a1 = O.qkv_rope(qa, qb, k, va, vb, c1, s1, nq, nkv, 2.0, 2.0)
     a2 = O.qkv_rope(qa, qb, k, va, vb, cb, sb, nq, nkv, 2.0, 2.0)
     assert all(np.array_equal(x_, y_) for x_, y_ in zip(a1, a2))
+
+
+def _finite_f16():
+    v = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    return v[np.isfinite(v)]
+
+
+def _single_rounding_mismatches(p):
+    """Finite fp16 inputs whose exact product with fp32(1/(1-p)), rounded once to fp16 (what a
+    mixed-precision FMA computes), differs from dropout_fp16's two roundings."""
+    x = _finite_f16()
+    s = np.float32(1.0 / (1.0 - p))
+    with np.errstate(over="ignore"):
+        once = (x.astype(np.float64) * np.float64(s)).astype(np.float16)  # exact in float64
+    twice = O.dropout_fp16(x, np.ones(x.size, np.uint8), p)
+    return int(np.sum(twice.view(np.uint16) != once.view(np.uint16)))
+
+
+def test_dropout_rates_that_tell_one_rounding_from_two():
+    """tests/test_dropout_bits_gpu.py pins the kernels' dropout at p = 0.05, 0.04 and 0.4: the
+    workload's rate, where one rounding equals two for every input, and two rates where they
+    differ for hundreds of inputs (so a kernel that rounds once fails there)."""
+    assert _single_rounding_mismatches(0.05) == 0
+    assert _single_rounding_mismatches(0.04) > 100
+    assert _single_rounding_mismatches(0.4) > 1000
