@@ -225,3 +225,24 @@ def test_pair_with_gradients_without_masks_and_refused_shapes(cuda):
             kernels.nf4_linear_bwd_dx_hp_pair_grads(
                 [p["dy"] for p in q], [p["packed"] for p in q], [p["st"] for p in q], dhq,
                 [p["a"].t().contiguous() for p in q], htq, x)
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 6144, 1536), (512, 11008, 4096), (1024, 14336, 4096)])
+def test_forward_pair_mixed_widths_other_shapes(cuda, M, N, K):
+    """Other MLP widths: where the launch cuts the columns into 256x160 and 256x128 tiles (at
+    column 640, or 10240 for 14336 outputs at 1024 tokens) the results are still the bits of two
+    one-projection launches."""
+    from mindxsoup_amd import kernels
+
+    print(f"case fwd pair mixed M={M} N={N} K={K}", flush=True)
+    x = torch.randn((M, K), device=cuda).half()
+    ps = [_proj(cuda, N, K, M, 80 + i, x) for i in range(2)]
+    assert kernels.fwd_pair_ok(M, N, N, K)
+    rows = kernels.lora_h_partials_group([x, x], [p["a"] for p in ps], S, [p["keep"] for p in ps],
+                                         1 / (1 - P), [p["b"] for p in ps])
+    two = [kernels.nf4_linear_fwd_hp(x, p["packed"], p["st"], r[0], p["b"])
+           for p, r in zip(ps, rows)]
+    pair = kernels.nf4_linear_fwd_hp_pair(x, [p["packed"] for p in ps], [p["st"] for p in ps],
+                                          [r[0] for r in rows], [p["b"] for p in ps])
+    for (y2, t2), (y1, t1) in zip(two, pair):
+        assert torch.equal(y1, y2) and torch.equal(t1, t2)
